@@ -1,0 +1,430 @@
+// Ragged verify / decode attention over the static KV cache (solutions/packed.py:142-166).
+//
+// Rule (solutions/packed.py:6-8): a query token at position p of cache row r attends to the
+// cached positions 0..p of row r (this call's K/V already appended), for every block kind:
+// decode (T = 1), verification (T = d + 1) and prefill chunks.
+//
+// Layouts
+//   q      [N, Hq, D]            (packed token axis; RoPE applied)
+//   cache  [B, Hkv, S, D]        (per layer; KVCache of common/model.py:171-183)
+//   out    [N, Hq * D]
+//   blocks int32 [nb][4] = {q_start, pos0, T, row}
+//   works  int32 [n_work][8] = {blk, row0, nrows, kv_lo, kv_hi, part, 0, 0}
+//   groups int32 [n_group][8] = {blk, row0, nrows, part_first, n_split, 0, 0, 0}
+// The G query heads of a KV head are folded into query rows: row = t * G + g (t = token of the
+// block, g = head within the group), so one workgroup reads each KV tile once for all G*T rows.
+//
+// bf16 path (MFMA, gfx950): a workgroup = 4 waves, one 16-row query tile per wave, the 64-position
+// K/V tiles are staged once in LDS for the four waves.  Scores are computed transposed,
+// S^T[pos][q] = K Q^T with v_mfma_f32_16x16x32_bf16, so every lane owns one query column: the
+// online softmax state (running max, row sum) is lane-local and only needs xor shuffles across the
+// four 16-lane groups.  O^T[d][q] = V^T P^T with v_mfma_f32_16x16x16_bf16 takes P^T straight from
+// the score registers (same lane layout), V^T fragments are read from LDS.
+//
+// Long contexts are split into fixed, position-aligned chunks of LSK_ATTN_SPLIT positions
+// (flash-decoding).  Because split boundaries, tile boundaries and the combine order depend only on
+// absolute positions, the result for a query never depends on which other tokens share its block
+// or batch (batch invariance: a T = 1 decode query and the same query inside a T = 9 verify block
+// give bitwise identical outputs).
+#include "lsk_common.h"
+#include "../include/lsk.h"
+
+#define ATTN_TILE 64
+#define ATTN_ROWS 64  // query rows per workgroup (4 waves x 16)
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int D>
+__global__ __launch_bounds__(256) void attn_bf16_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const int32_t* __restrict__ blocks, const int32_t* __restrict__ works, uint16_t* __restrict__ out,
+    float* __restrict__ o_part, float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
+  constexpr int KSTEPS = D / 32;   // 16x16x32 k-steps over the head dim
+  constexpr int CT = D / 16;       // 16-wide d tiles of O^T
+  constexpr int LDS_STRIDE = D + 8;  // bf16 elements per staged row (16 B pad against bank conflicts)
+  constexpr int CHUNKS = ATTN_TILE * D / 8;  // 16-byte chunks per K (or V) tile
+  constexpr int PER_THREAD = CHUNKS / 256;
+  static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
+
+  __shared__ __attribute__((aligned(16))) uint16_t sK[ATTN_TILE * LDS_STRIDE];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[ATTN_TILE * LDS_STRIDE];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63;
+  const int l16 = lane & 15, lg = lane >> 4;
+  const int kvh = blockIdx.y;
+  const int Hq = Hkv * G;
+
+  const int32_t* wk = works + (long)blockIdx.x * 8;
+  const int blk = wk[0], row0 = wk[1], nrows = wk[2], kv_lo = wk[3], kv_hi = wk[4], part = wk[5];
+  const int32_t* bm = blocks + (long)blk * 4;
+  const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
+
+  // ---- this lane's query column
+  const int rloc = wave * 16 + l16;  // row within the group
+  const bool qvalid = rloc < nrows;
+  const int r = row0 + (qvalid ? rloc : 0);
+  const int t = r / G, g = r - t * G;
+  const int qpos = pos0 + t;
+  const int hq = kvh * G + g;
+  const bool wave_active = wave * 16 < nrows;
+
+  lsk_bf16x8 qf[KSTEPS];
+  {
+    const uint16_t* qrow = q + ((long)(q_start + t) * Hq + hq) * D;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j) {
+      if (qvalid) {
+        qf[j] = *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg);
+      } else {
+        qf[j] = (lsk_bf16x8){};
+      }
+    }
+  }
+
+  lsk_f32x4 oacc[CT];
+#pragma unroll
+  for (int c = 0; c < CT; ++c) oacc[c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const long head_base = ((long)crow * Hkv + kvh) * (long)S * D;
+  const uint16_t* kbase = kc + head_base;
+  const uint16_t* vbase = vc + head_base;
+
+  uint4 kreg[PER_THREAD], vreg[PER_THREAD];
+  auto load_tile = [&](int tb) {
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+      const int c = tid + 256 * u;
+      const int p = c / (D / 8), d8 = c - p * (D / 8);
+      if (tb + p < kv_hi) {
+        const long off = (long)(tb + p) * D + d8 * 8;
+        kreg[u] = *(const uint4*)(kbase + off);
+        vreg[u] = *(const uint4*)(vbase + off);
+      } else {
+        kreg[u] = make_uint4(0, 0, 0, 0);
+        vreg[u] = make_uint4(0, 0, 0, 0);
+      }
+    }
+  };
+
+  load_tile(kv_lo);
+  for (int tb = kv_lo; tb < kv_hi; tb += ATTN_TILE) {
+    __syncthreads();  // previous tile fully consumed
+#pragma unroll
+    for (int u = 0; u < PER_THREAD; ++u) {
+      const int c = tid + 256 * u;
+      const int p = c / (D / 8), d8 = c - p * (D / 8);
+      *(uint4*)(sK + p * LDS_STRIDE + d8 * 8) = kreg[u];
+      *(uint4*)(sV + p * LDS_STRIDE + d8 * 8) = vreg[u];
+    }
+    __syncthreads();
+    if (tb + ATTN_TILE < kv_hi) load_tile(tb + ATTN_TILE);  // in flight during the compute below
+
+    if (wave_active) {
+      // ---- S^T tile: 4 sub-tiles of 16 positions x 16 queries
+      lsk_f32x4 sacc[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        sacc[p] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+        const uint16_t* krow = sK + (16 * p + l16) * LDS_STRIDE + 8 * lg;
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j) {
+          const lsk_bf16x8 kf = *(const lsk_bf16x8*)(krow + 32 * j);
+          sacc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[j], sacc[p], 0, 0, 0);
+        }
+      }
+      // ---- online softmax (log2 domain), lane-local per query column
+      float sv[4][4];
+      float mt = -INFINITY;
+#pragma unroll
+      for (int p = 0; p < 4; ++p)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int kp = tb + 16 * p + 4 * lg + i;
+          const bool ok = qvalid && kp < kv_hi && kp <= qpos;
+          const float s = ok ? sacc[p][i] * scale_log2 : -INFINITY;
+          sv[p][i] = s;
+          mt = fmaxf(mt, s);
+        }
+      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
+      float rs = 0.f;
+      lsk_s16x4 pb[4];
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float e = (sv[p][i] == -INFINITY) ? 0.f : fast_exp2(sv[p][i] - m_new);
+          rs += e;
+          pb[p][i] = (short)f2bf(e);
+        }
+      }
+      rs += __shfl_xor(rs, 16, 64);
+      rs += __shfl_xor(rs, 32, 64);
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+#pragma unroll
+      for (int c = 0; c < CT; ++c) {
+        oacc[c][0] *= alpha;
+        oacc[c][1] *= alpha;
+        oacc[c][2] *= alpha;
+        oacc[c][3] *= alpha;
+      }
+      // ---- O^T += V^T P^T
+#pragma unroll
+      for (int p = 0; p < 4; ++p) {
+        const uint16_t* vcol = sV + (16 * p + 4 * lg) * LDS_STRIDE + l16;
+#pragma unroll
+        for (int c = 0; c < CT; ++c) {
+          lsk_s16x4 va;
+          va[0] = (short)vcol[0 * LDS_STRIDE + 16 * c];
+          va[1] = (short)vcol[1 * LDS_STRIDE + 16 * c];
+          va[2] = (short)vcol[2 * LDS_STRIDE + 16 * c];
+          va[3] = (short)vcol[3 * LDS_STRIDE + 16 * c];
+          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[p], oacc[c], 0, 0, 0);
+        }
+      }
+    }
+  }
+
+  if (!wave_active || !qvalid) return;
+  if (part < 0) {
+    uint16_t* orow = out + (long)(q_start + t) * Hq * D + (long)hq * D;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      ushort4 o;
+      o.x = f2bf(oacc[c][0] / l_run);
+      o.y = f2bf(oacc[c][1] / l_run);
+      o.z = f2bf(oacc[c][2] / l_run);
+      o.w = f2bf(oacc[c][3] / l_run);
+      *(ushort4*)(orow + 16 * c + 4 * lg) = o;
+    }
+  } else {
+    const long slot = ((long)part * Hkv + kvh) * ATTN_ROWS + rloc;
+    float* op = o_part + slot * D;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) *(float4*)(op + 16 * c + 4 * lg) = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+    if (lg == 0) {
+      ml_part[slot * 2 + 0] = m_run;
+      ml_part[slot * 2 + 1] = l_run;
+    }
+  }
+}
+
+// Merge the splits of one query group in split order:
+//   M = max_s m_s, w_s = exp2(m_s - M) (0 for an empty split, 1 when m_s == M),
+//   out = (sum_s w_s O_s) / (sum_s w_s l_s).
+// A group with a single non-empty split reduces to O_0 / l_0, exactly what the direct path stores.
+template <typename T, int D>
+__global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __restrict__ blocks,
+                                                           const int32_t* __restrict__ groups,
+                                                           const float* __restrict__ o_part,
+                                                           const float* __restrict__ ml_part, T* __restrict__ out,
+                                                           int G, int Hkv) {
+  const int32_t* gp = groups + (long)blockIdx.x * 8;
+  const int blk = gp[0], row0 = gp[1], nrows = gp[2], pf = gp[3], ns = gp[4];
+  const int kvh = blockIdx.y;
+  const int Hq = Hkv * G;
+  const int q_start = blocks[(long)blk * 4 + 0];
+  for (int e = threadIdx.x; e < nrows * D; e += blockDim.x) {
+    const int rl = e / D, d = e - rl * D;
+    float M = -INFINITY;
+    for (int s = 0; s < ns; ++s) M = fmaxf(M, ml_part[(((long)(pf + s) * Hkv + kvh) * ATTN_ROWS + rl) * 2]);
+    float L = 0.f, O = 0.f;
+    for (int s = 0; s < ns; ++s) {
+      const long slot = ((long)(pf + s) * Hkv + kvh) * ATTN_ROWS + rl;
+      const float ms = ml_part[slot * 2], ls = ml_part[slot * 2 + 1];
+      const float w = (ms == -INFINITY) ? 0.f : ((ms == M) ? 1.f : fast_exp2(ms - M));
+      L = L + w * ls;
+      O = O + w * o_part[slot * D + d];
+    }
+    const int r = row0 + rl;
+    const int t = r / G, g = r - t * G;
+    Elem<T>::st(out + (long)(q_start + t) * Hq * D + (long)(kvh * G + g) * D + d, O / L);
+  }
+}
+
+// ----------------------------------------------------------------------------- fp32 path
+// Straightforward per-query kernel for fp32 models (parity runs): one wave per query row, the
+// row's positions 0..qpos in 64-position chunks (lane = position), online softmax with exact expf,
+// O[d] accumulated over the chunk's positions in order.  Fixed order per query -> batch invariant.
+template <int D>
+__global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
+                                                       const float* __restrict__ vc,
+                                                       const int32_t* __restrict__ blocks,
+                                                       const int32_t* __restrict__ works, float* __restrict__ out,
+                                                       int G, int Hkv, int S, float scale) {
+  constexpr int DPL = (D + 63) / 64;  // d values per lane
+  __shared__ float sp[4][64];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int kvh = blockIdx.y;
+  const int Hq = Hkv * G;
+  const int32_t* wk = works + (long)blockIdx.x * 8;
+  const int blk = wk[0], row0 = wk[1], nrows = wk[2];
+  const int32_t* bm = blocks + (long)blk * 4;
+  const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
+  const long head_base = ((long)crow * Hkv + kvh) * (long)S * D;
+  for (int rl = wave; rl < nrows; rl += 4) {
+    const int r = row0 + rl;
+    const int t = r / G, g = r - t * G;
+    const int qpos = pos0 + t;
+    const float* qv = q + ((long)(q_start + t) * Hq + kvh * G + g) * D;
+    float m_run = -INFINITY, l_run = 0.f;
+    float o[DPL];
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) o[i] = 0.f;
+    for (int base = 0; base <= qpos; base += 64) {
+      const int kp = base + lane;
+      float s = -INFINITY;
+      if (kp <= qpos) {
+        const float* kr = kc + head_base + (long)kp * D;
+        float acc = 0.f;
+        for (int d = 0; d < D; ++d) acc += qv[d] * kr[d];
+        s = acc * scale;
+      }
+      float mt = s;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = (m_new == m_run) ? 1.f : expf(m_run - m_new);
+      const float p = (s == -INFINITY) ? 0.f : expf(s - m_new);
+      float rs = p;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) rs += __shfl_xor(rs, off, 64);
+      l_run = l_run * alpha + rs;
+      m_run = m_new;
+      sp[wave][lane] = p;
+      __builtin_amdgcn_wave_barrier();
+      const int nvalid = min(64, qpos + 1 - base);
+#pragma unroll
+      for (int i = 0; i < DPL; ++i) {
+        const int d = lane + 64 * i;
+        if (d < D) {
+          float acc = o[i] * alpha;
+          for (int j = 0; j < nvalid; ++j) acc += sp[wave][j] * vc[head_base + (long)(base + j) * D + d];
+          o[i] = acc;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    float* orow = out + (long)(q_start + t) * Hq * D + (long)(kvh * G + g) * D;
+#pragma unroll
+    for (int i = 0; i < DPL; ++i) {
+      const int d = lane + 64 * i;
+      if (d < D) orow[d] = o[i] / l_run;
+    }
+  }
+}
+
+// ----------------------------------------------------------------------------- host planner
+
+extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
+                             int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts) {
+  LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
+  LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && split % ATTN_TILE == 0, LSK_ESHAPE,
+              "lsk_attn_plan: bad arguments (split must be a positive multiple of %d)", ATTN_TILE);
+  int nw = 0, ng = 0, np = 0;
+  for (int b = 0; b < nb; ++b) {
+    const int pos0 = blocks[b * 4 + 1], T = blocks[b * 4 + 2];
+    LSK_REQUIRE(T >= 0 && pos0 >= 0, LSK_ESHAPE, "lsk_attn_plan: block %d has T=%d pos0=%d", b, T, pos0);
+    const int rows = T * group;
+    for (int row0 = 0; row0 < rows; row0 += ATTN_ROWS) {
+      const int nrows = (rows - row0) < ATTN_ROWS ? (rows - row0) : ATTN_ROWS;
+      const int t_last = (row0 + nrows - 1) / group;
+      const long kv_end = (long)pos0 + t_last + 1;
+      const int ns = (int)((kv_end + split - 1) / split);
+      if (ns > 1) {
+        LSK_REQUIRE(groups != nullptr && ng < max_groups, LSK_EWORKSPACE, "lsk_attn_plan: too many combine groups");
+        int32_t* gp = groups + (long)ng * 8;
+        gp[0] = b; gp[1] = row0; gp[2] = nrows; gp[3] = np; gp[4] = ns; gp[5] = gp[6] = gp[7] = 0;
+        ++ng;
+      }
+      for (int s = 0; s < ns; ++s) {
+        LSK_REQUIRE(nw < max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
+        int32_t* wp = works + (long)nw * 8;
+        const long lo = (long)s * split;
+        const long hi = (lo + split < kv_end) ? lo + split : kv_end;
+        wp[0] = b; wp[1] = row0; wp[2] = nrows; wp[3] = (int32_t)lo; wp[4] = (int32_t)hi;
+        wp[5] = ns > 1 ? np + s : -1; wp[6] = wp[7] = 0;
+        ++nw;
+      }
+      if (ns > 1) np += ns;
+    }
+  }
+  *n_works = nw;
+  *n_groups = ng;
+  *n_parts = np;
+  return 0;
+}
+
+extern "C" size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim) {
+  // o_part [n_parts][Hkv][64][D] fp32, ml_part [n_parts][Hkv][64][2] fp32
+  const size_t rows = (size_t)n_parts * n_kv_heads * ATTN_ROWS;
+  return lsk_align_up(rows * head_dim * sizeof(float), 256) + lsk_align_up(rows * 2 * sizeof(float), 256);
+}
+
+extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache,
+                               const int32_t* blocks, const int32_t* works, int n_works, const int32_t* groups,
+                               int n_groups, int n_parts, void* out, int n_heads, int n_kv_heads, int head_dim,
+                               int max_seq, float scale, void* workspace, size_t ws_bytes, void* stream) {
+  LSK_REQUIRE(q && kcache && vcache && blocks && works && out, LSK_EARG, "lsk_ragged_attn: null pointer");
+  LSK_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && max_seq > 0 && n_works >= 0,
+              LSK_ESHAPE, "lsk_ragged_attn: bad shape");
+  if (n_works == 0) return 0;
+  const int G = n_heads / n_kv_heads;
+  hipStream_t s = (hipStream_t)stream;
+  dim3 grid(n_works, n_kv_heads);
+  if (dtype == LSK_DTYPE_BF16) {
+    LSK_REQUIRE(head_dim == 64 || head_dim == 128, LSK_EUNSUPPORTED,
+                "lsk_ragged_attn: bf16 head_dim %d (supported: 64, 128)", head_dim);
+    LSK_REQUIRE(max_seq % ATTN_TILE == 0, LSK_ESHAPE, "lsk_ragged_attn: max_seq must be a multiple of %d", ATTN_TILE);
+    float* o_part = nullptr;
+    float* ml_part = nullptr;
+    if (n_parts > 0) {
+      const size_t need = lsk_attn_workspace_bytes(n_parts, n_kv_heads, head_dim);
+      LSK_REQUIRE(workspace != nullptr && ws_bytes >= need && groups != nullptr, LSK_EWORKSPACE,
+                  "lsk_ragged_attn: workspace of %zu bytes needed, %zu given", need, ws_bytes);
+      const size_t rows = (size_t)n_parts * n_kv_heads * ATTN_ROWS;
+      o_part = (float*)workspace;
+      ml_part = (float*)((char*)workspace + lsk_align_up(rows * head_dim * sizeof(float), 256));
+    }
+    const float scale_log2 = scale * 1.4426950408889634f;
+    if (head_dim == 128)
+      attn_bf16_kernel<128><<<grid, 256, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
+                                                  (const uint16_t*)vcache, blocks, works, (uint16_t*)out, o_part,
+                                                  ml_part, G, n_kv_heads, max_seq, scale_log2);
+    else
+      attn_bf16_kernel<64><<<grid, 256, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
+                                                 (const uint16_t*)vcache, blocks, works, (uint16_t*)out, o_part,
+                                                 ml_part, G, n_kv_heads, max_seq, scale_log2);
+    int rc = lsk_check_launch("lsk_ragged_attn");
+    if (rc) return rc;
+    if (n_groups > 0) {
+      dim3 cg(n_groups, n_kv_heads);
+      if (head_dim == 128)
+        attn_combine_kernel<uint16_t, 128><<<cg, 256, 0, s>>>(blocks, groups, o_part, ml_part, (uint16_t*)out, G,
+                                                               n_kv_heads);
+      else
+        attn_combine_kernel<uint16_t, 64><<<cg, 256, 0, s>>>(blocks, groups, o_part, ml_part, (uint16_t*)out, G,
+                                                              n_kv_heads);
+      return lsk_check_launch("lsk_ragged_attn(combine)");
+    }
+    return 0;
+  }
+  if (dtype == LSK_DTYPE_F32) {
+    LSK_REQUIRE(n_parts == 0, LSK_EARG, "lsk_ragged_attn: the fp32 path takes unsplit plans");
+    switch (head_dim) {
+      case 16: attn_f32_kernel<16><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 32: attn_f32_kernel<32><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 64: attn_f32_kernel<64><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 128: attn_f32_kernel<128><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      default: LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_ragged_attn: fp32 head_dim %d", head_dim);
+    }
+    return lsk_check_launch("lsk_ragged_attn(f32)");
+  }
+  LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_ragged_attn: dtype %d", dtype);
+  return LSK_EUNSUPPORTED;
+}

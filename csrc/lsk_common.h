@@ -1,0 +1,66 @@
+// Shared device/host helpers for the packed ragged LayerSkip-Llama kernels (gfx950).
+//
+// Storage types: bf16 is carried as uint16_t (torch.bfloat16 bit layout), fp32 as float.
+// Every conversion float -> bf16 rounds to nearest even with NaN -> 0x7FC0, which is the rule
+// torch's CPU kernels apply when a float intermediate is stored into a bfloat16 tensor; the
+// elementwise kernels rely on it to reproduce the reference's rounding points bit for bit.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#define LSK_DTYPE_F32 0
+#define LSK_DTYPE_BF16 1
+
+typedef __bf16 lsk_bf16x8 __attribute__((ext_vector_type(8)));
+typedef short lsk_s16x4 __attribute__((ext_vector_type(4)));
+typedef float lsk_f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
+
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)0x7fc0;
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Round a float through bf16 and back (value of the float once stored in a bf16 tensor).
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
+
+// Loads/stores of "dtype T" elements expressed as float.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float ld(const float* p) { return *p; }
+  static __device__ __forceinline__ void st(float* p, float v) { *p = v; }
+  // value after being stored in a tensor of this dtype
+  static __device__ __forceinline__ float round(float v) { return v; }
+};
+template <> struct Elem<uint16_t> {
+  static __device__ __forceinline__ float ld(const uint16_t* p) { return bf2f(*p); }
+  static __device__ __forceinline__ void st(uint16_t* p, float v) { *p = f2bf(v); }
+  static __device__ __forceinline__ float round(float v) { return rbf(v); }
+};
+
+// ----------------------------------------------------------------------------- host side
+// Error reporting: every C-ABI entry returns 0 on success, a negative code for an argument
+// error detected on the host before any launch, or a positive hipError_t.  The text of the
+// last error of the calling thread is kept for lsk_last_error().
+#define LSK_EARG -1
+#define LSK_ESHAPE -2
+#define LSK_EUNSUPPORTED -3
+#define LSK_EWORKSPACE -4
+
+void lsk_set_error(const char* fmt, ...);
+int lsk_check_launch(const char* what);
+
+#define LSK_REQUIRE(cond, code, ...)      \
+  do {                                    \
+    if (!(cond)) {                        \
+      lsk_set_error(__VA_ARGS__);         \
+      return (code);                      \
+    }                                     \
+  } while (0)
+
+static inline size_t lsk_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

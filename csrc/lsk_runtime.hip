@@ -1,0 +1,174 @@
+// Native layer-range runner of the packed forward (solutions/packed.py:169-196: packed_layer /
+// packed_layers).  One call issues every kernel of layers [start, end) on one stream, so the host
+// pays one C call per segment instead of ~9 launches per layer from Python.
+//
+// Per layer (same op order and rounding points as solutions/packed.py:175-185):
+//   xn   = rmsnorm(x, attn_norm)                      lsk_rmsnorm
+//   qkv  = xn Wqkv^T                                  lsk_gemm NONE
+//   q, cache[k, v] = rope(q), rope(k), v              lsk_rope_append
+//   attn = ragged attention(q, cache)                 lsk_ragged_attn (+ split combine)
+//   x    = x + attn Wo^T                              lsk_gemm RESIDUAL
+//   xn   = rmsnorm(x, ffn_norm)                       lsk_rmsnorm
+//   h    = silu(g) * u, [g; u] = xn W13^T             lsk_gemm SILU_MUL
+//   x    = x + h W2^T                                 lsk_gemm RESIDUAL (in place)
+#include <math.h>
+#include <mutex>
+#include <vector>
+
+#include "lsk_common.h"
+#include "../include/lsk.h"
+
+namespace {
+
+struct Model {
+  int dtype, n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab;
+  float eps;
+  std::vector<const void*> wqkv, wo, w13, w2, attn_norm, ffn_norm;
+  std::vector<void*> kc, vc;
+  int max_batch, max_seq;
+  const float* cos_tab;
+  const float* sin_tab;
+  int tab_len;
+};
+
+std::mutex g_mu;
+std::vector<Model*> g_models;  // handle = index + 1
+
+Model* get(long h) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (h <= 0 || h > (long)g_models.size()) return nullptr;
+  return g_models[h - 1];
+}
+
+size_t elem_size(int dtype) { return dtype == LSK_DTYPE_BF16 ? 2 : 4; }
+
+struct Layout {
+  size_t xn, qkv, q, attn, h, part, total;
+};
+
+Layout layout(const Model& m, int N, int n_parts) {
+  const size_t es = elem_size(m.dtype);
+  const int qd = m.n_heads * m.head_dim, kvd = m.n_kv_heads * m.head_dim;
+  Layout L;
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    size_t o = off;
+    off += lsk_align_up(bytes, 256);
+    return o;
+  };
+  L.xn = take((size_t)N * m.dim * es);
+  L.qkv = take((size_t)N * (qd + 2 * kvd) * es);
+  L.q = take((size_t)N * qd * es);
+  L.attn = take((size_t)N * qd * es);
+  L.h = take((size_t)N * m.ffn * es);
+  L.part = take(n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, m.n_kv_heads, m.head_dim) : 0);
+  L.total = off;
+  return L;
+}
+
+}  // namespace
+
+extern "C" long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, int n_kv_heads, int head_dim, int ffn,
+                                 int vocab, float eps, const void* const* wqkv, const void* const* wo,
+                                 const void* const* w13, const void* const* w2, const void* const* attn_norm,
+                                 const void* const* ffn_norm, void* const* kcache, void* const* vcache, int max_batch,
+                                 int max_seq, const float* cos_tab, const float* sin_tab, int tab_len) {
+  LSK_REQUIRE(dtype == LSK_DTYPE_BF16 || dtype == LSK_DTYPE_F32, LSK_EUNSUPPORTED, "lsk_model_create: dtype %d", dtype);
+  LSK_REQUIRE(n_layers > 0 && dim > 0 && n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && head_dim > 0 &&
+                  ffn > 0 && vocab > 0 && max_batch > 0 && max_seq > 0 && tab_len > 0,
+              LSK_ESHAPE, "lsk_model_create: bad dimensions");
+  LSK_REQUIRE(wqkv && wo && w13 && w2 && attn_norm && ffn_norm && kcache && vcache && cos_tab && sin_tab, LSK_EARG,
+              "lsk_model_create: null pointer");
+  Model* m = new Model();
+  m->dtype = dtype; m->n_layers = n_layers; m->dim = dim; m->n_heads = n_heads; m->n_kv_heads = n_kv_heads;
+  m->head_dim = head_dim; m->ffn = ffn; m->vocab = vocab; m->eps = eps;
+  m->wqkv.assign(wqkv, wqkv + n_layers); m->wo.assign(wo, wo + n_layers);
+  m->w13.assign(w13, w13 + n_layers); m->w2.assign(w2, w2 + n_layers);
+  m->attn_norm.assign(attn_norm, attn_norm + n_layers); m->ffn_norm.assign(ffn_norm, ffn_norm + n_layers);
+  m->kc.assign(kcache, kcache + n_layers); m->vc.assign(vcache, vcache + n_layers);
+  m->max_batch = max_batch; m->max_seq = max_seq;
+  m->cos_tab = cos_tab; m->sin_tab = sin_tab; m->tab_len = tab_len;
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_models.push_back(m);
+  return (long)g_models.size();
+}
+
+extern "C" int lsk_model_destroy(long handle) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  LSK_REQUIRE(handle > 0 && handle <= (long)g_models.size() && g_models[handle - 1], LSK_EARG,
+              "lsk_model_destroy: bad handle %ld", handle);
+  delete g_models[handle - 1];
+  g_models[handle - 1] = nullptr;
+  return 0;
+}
+
+extern "C" size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts) {
+  Model* m = get(handle);
+  if (!m) return 0;
+  return layout(*m, n_tokens, n_parts).total;
+}
+
+// meta (device int32): [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8]
+// capture (host array of n_layers device pointers or NULL): capture[i] != NULL receives the output of
+// layer i (the hidden state entering exit layer i + 1; solutions/packed.py:190-195).
+extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
+                                  const int32_t* meta, int nb, int n_works, int n_groups, int n_parts,
+                                  void* workspace, size_t ws_bytes, void* const* capture, void* stream) {
+  Model* m = get(handle);
+  LSK_REQUIRE(m != nullptr, LSK_EARG, "lsk_forward_layers: bad handle %ld", handle);
+  LSK_REQUIRE(0 <= start && start <= end && end <= m->n_layers, LSK_ESHAPE, "lsk_forward_layers: bad range [%d, %d)",
+              start, end);
+  LSK_REQUIRE(x_in && x_out && x_in != x_out, LSK_EARG, "lsk_forward_layers: x_in / x_out");
+  const int N = n_tokens;
+  const size_t es = elem_size(m->dtype);
+  hipStream_t s = (hipStream_t)stream;
+  if (N == 0) return 0;
+  if (start == end) {
+    hipError_t e = hipMemcpyAsync(x_out, x_in, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: copy %s", hipGetErrorString(e)); return (int)e; }
+    return 0;
+  }
+  LSK_REQUIRE(meta != nullptr, LSK_EARG, "lsk_forward_layers: meta missing");
+  const Layout L = layout(*m, N, n_parts);
+  LSK_REQUIRE(workspace != nullptr && ws_bytes >= L.total, LSK_EWORKSPACE,
+              "lsk_forward_layers: workspace of %zu bytes needed, %zu given", L.total, ws_bytes);
+  char* ws = (char*)workspace;
+  void* xn = ws + L.xn;
+  void* qkv = ws + L.qkv;
+  void* q = ws + L.q;
+  void* attn = ws + L.attn;
+  void* h = ws + L.h;
+  void* part = n_parts > 0 ? (void*)(ws + L.part) : nullptr;
+  const size_t part_bytes = n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, m->n_kv_heads, m->head_dim) : 0;
+  const int32_t* rows = meta;
+  const int32_t* pos = meta + N;
+  const int32_t* blocks = pos + N;
+  const int32_t* works = blocks + (size_t)nb * 4;
+  const int32_t* groups = works + (size_t)n_works * 8;
+  const int qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
+  const float scale = (float)(1.0 / sqrt((double)m->head_dim));
+  int rc;
+  for (int i = start; i < end; ++i) {
+    const void* xi = (i == start) ? x_in : x_out;
+    if ((rc = lsk_rmsnorm(m->dtype, xi, m->attn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream))) return rc;
+    if ((rc = lsk_gemm(m->dtype, xn, m->dim, m->wqkv[i], m->dim, qkv, qd + 2 * kvd, nullptr, 0, N, qd + 2 * kvd,
+                       m->dim, LSK_EPI_NONE, 0, stream))) return rc;
+    if ((rc = lsk_rope_append(m->dtype, qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab, m->tab_len, rows, pos, N,
+                              m->n_heads, m->n_kv_heads, m->head_dim, m->max_batch, m->max_seq, stream))) return rc;
+    if ((rc = lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts,
+                              attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes,
+                              stream))) return rc;
+    if ((rc = lsk_gemm(m->dtype, attn, qd, m->wo[i], qd, x_out, m->dim, xi, m->dim, N, m->dim, qd, LSK_EPI_RESIDUAL, 0,
+                       stream))) return rc;
+    if ((rc = lsk_rmsnorm(m->dtype, x_out, m->ffn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream))) return rc;
+    if ((rc = lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
+                       LSK_EPI_SILU_MUL, m->ffn, stream))) return rc;
+    if ((rc = lsk_gemm(m->dtype, h, m->ffn, m->w2[i], m->ffn, x_out, m->dim, x_out, m->dim, N, m->dim, m->ffn,
+                       LSK_EPI_RESIDUAL, 0, stream))) return rc;
+    if (capture && capture[i]) {
+      hipError_t e = hipMemcpyAsync(capture[i], x_out, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }
+    }
+  }
+  return 0;
+}

@@ -1,0 +1,139 @@
+/* liblsk: C ABI of the MI355X (gfx950) kernels behind the packed ragged LayerSkip-Llama forward.
+ *
+ * The reference (hsungo/thesis) is pure PyTorch; it has no native ABI.  Each entry point below
+ * replaces the eager torch ops of one step of its hot path, cited as file:line of the reference.
+ *
+ * Conventions
+ *   - dtype codes: LSK_DTYPE_F32 (0) and LSK_DTYPE_BF16 (1); bf16 is torch.bfloat16 storage.
+ *   - All pointers are device pointers unless stated; the library never allocates or frees
+ *     device memory: tensors and workspaces belong to the caller (the PyTorch caching allocator).
+ *   - `stream` is a hipStream_t; every call is asynchronous on it, nothing synchronises inside.
+ *   - Return value: 0 = ok, < 0 = argument error detected on the host before any launch
+ *     (LSK_EARG, LSK_ESHAPE, LSK_EUNSUPPORTED, LSK_EWORKSPACE), > 0 = hipError_t of the launch.
+ *     lsk_last_error() returns the message of the calling thread's last error.
+ *   - Index arrays are int32 unless stated; token ids and sequence buffers are int64 (torch.long).
+ */
+#ifndef LSK_H_
+#define LSK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LSK_ABI_VERSION 1
+
+#define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
+#define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
+#define LSK_EPI_SILU_MUL 2 /* C = rnd(rnd(silu(rnd(g))) * rnd(u)), [g;u] = A W^T */
+
+#define LSK_ATTN_SPLIT 512 /* KV positions per flash-decoding split (bf16 path) */
+
+const char* lsk_last_error(void);
+int lsk_abi_version(void);
+
+/* RMSNorm: out = w * (x * rsqrt(mean(x^2) + eps)).to(dtype).
+ * Replaces common/model.py:153-156 (rms_norm), used at solutions/packed.py:175,183 and common/model.py:330. */
+int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, int n_rows, int dim, float eps, long ldx,
+                long ldo, void* stream);
+
+/* RoPE of q and k + KV append: qkv [N, (Hq+2Hkv)D] -> q_out [N, Hq, D], k/v into the cache rows
+ * [B, Hkv, S, D] at (rows[t], pos[t]).  cos/sin tables: fp32 [tab_len, D] (device).
+ * Replaces solutions/packed.py:176-181 (split, apply_rope, cache index_put) with
+ * common/model.py:143-150 (apply_rope) and solutions/packed.py:106-107 (cos/sin gather + cast). */
+int lsk_rope_append(int dtype, const void* qkv, void* q_out, void* kcache, void* vcache, const float* cos_tab,
+                    const float* sin_tab, int tab_len, const int32_t* rows, const int32_t* pos, int n_tokens,
+                    int n_heads, int n_kv_heads, int head_dim, int max_batch, int max_seq, void* stream);
+
+/* KV append without RoPE: kcache[rows[t], :, pos[t]] = k[t]; same for v.
+ * Replaces solutions/packed.py:180-181 and common/model.py:343-344. */
+int lsk_kv_append(int dtype, const void* k, const void* v, void* kcache, void* vcache, const int32_t* rows,
+                  const int32_t* pos, int n_tokens, int n_kv_heads, int head_dim, int max_batch, int max_seq,
+                  void* stream);
+
+/* Host-side planner for lsk_ragged_attn (host pointers, no GPU work).
+ * blocks: int32 [nb][4] = {q_start, pos0, T, row}.  Writes work items int32 [n][8] and combine
+ * groups int32 [n][8]; `split` = KV positions per split (LSK_ATTN_SPLIT for bf16; >= the longest
+ * context, e.g. 1<<30, for the unsplit fp32 path).  Mirrors the per-bucket metadata of
+ * solutions/packed.py:109-138 (build_packed) without the dense masks. */
+int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
+                  int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts);
+
+/* Workspace bytes for the split partials of a plan with n_parts partial slots. */
+size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
+
+/* Ragged verify/decode attention: a query at position p of row r attends cache[r, :, 0..p].
+ * q [N, Hq, D], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
+ * Replaces solutions/packed.py:142-166 (_attend: per-bucket gather + masked SDPA + scatter)
+ * and common/model.py:352-364 (the padded path's masked SDPA). */
+int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
+                    const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts, void* out,
+                    int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
+                    size_t ws_bytes, void* stream);
+
+/* GEMM C = epilogue(A W^T), A [M,K] (lda), W [N_w,K] (ldw), C [M,N] (ldc), R residual [M,N] (ldr).
+ * For LSK_EPI_SILU_MUL, W has 2*ffn rows [gate; up] and N == ffn.
+ * Replaces F.linear at solutions/packed.py:175 (wqkv), 182 (wo + residual), 183-185 (w13, silu*mul,
+ * w2 + residual) and common/model.py:330 (lm_head). */
+int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc, const void* R, long ldr,
+             int M, int N, int K, int epilogue, int ffn, void* stream);
+
+/* Tile the bf16 GEMM picks for (M, N) (informational; every tile gives identical results). */
+int lsk_gemm_tile(int M, int N, int* ns_out, int* ms_out);
+
+/* Embedding gather with the engine's id assembly: out[t] = table[id_t],
+ * id_t = (sel && sel[t] >= 0) ? seq_buf[sel[t]] : alt[t]  (int64 ids; out-of-range id -> zero row).
+ * Replaces solutions/engine.py:345-346 (torch.where id assembly) + common/model.py:325-326 (F.embedding). */
+int lsk_embed(const void* table, long vocab, long row_bytes, const int64_t* seq_buf, long seq_len,
+              const int64_t* sel, const int64_t* alt, void* out, int n_tokens, void* stream);
+
+/* Row copy dst[dst_idx[i]] = src[src_idx[i]] (int64 indices, NULL = identity).
+ * Replaces the exit_h staging/gathers of solutions/engine.py:349-350 and 453-455. */
+int lsk_copy_rows(void* dst, const int64_t* dst_idx, long n_dst, const void* src, const int64_t* src_idx, long n_src,
+                  long row_bytes, int n, void* stream);
+
+/* Row-wise argmax (first index on ties) of dtype logits [n_rows, ld]; out[dst_idx ? dst_idx[m] : m] (int64).
+ * Replaces .argmax(-1) at solutions/engine.py:227,255,352,463,478. */
+int lsk_argmax(int dtype, const void* logits, long ld, int n_rows, int vocab, int64_t* out, const int64_t* dst_idx,
+               void* stream);
+
+/* Greedy acceptance of nv verifiers (see the kernel comment); forced = optional per-verifier
+ * acceptance override (-1 = natural).  Replaces solutions/engine.py:461-476 (dr / scatter_reduce amin /
+ * last_tok / seq_buf write); kv_len (optional) receives the pointer rollback of solutions/engine.py:383. */
+int lsk_greedy_accept(const int64_t* Yv, int64_t* seq_buf, int Dm1, const int32_t* slots, const int32_t* starts,
+                      const int32_t* Ts, const int32_t* forced, int nv, int64_t* acc_out, int64_t* y_out,
+                      int64_t* kv_len, void* stream);
+
+/* Pointer rollback: kv_len[slots[j]] += accepted[j] + 1; moves no KV.
+ * Replaces solutions/engine.py:381-384 (pos += a + 1; d = 0) for a device-resident length array. */
+int lsk_kv_rollback(int64_t* kv_len, const int32_t* slots, const int64_t* accepted, int nv, void* stream);
+
+/* ---- native layer-range runner (solutions/packed.py:169-196, packed_layer / packed_layers) ----
+ * A model handle holds host copies of per-layer device pointers (weights [out, in] row-major,
+ * KV caches [B, Hkv, S, D], fp32 RoPE tables [tab_len, D]); it owns no device memory.
+ * Returns a handle > 0, or a negative error code. */
+long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, int n_kv_heads, int head_dim, int ffn, int vocab,
+                      float eps, const void* const* wqkv, const void* const* wo, const void* const* w13,
+                      const void* const* w2, const void* const* attn_norm, const void* const* ffn_norm,
+                      void* const* kcache, void* const* vcache, int max_batch, int max_seq, const float* cos_tab,
+                      const float* sin_tab, int tab_len);
+int lsk_model_destroy(long handle);
+
+/* Workspace bytes lsk_forward_layers needs for n_tokens packed tokens and n_parts attention partial slots. */
+size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts);
+
+/* Layers [start, end) over n_tokens packed tokens: x_out = layers(x_in) (x_in is not modified).
+ * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8] (see lsk_attn_plan).
+ * capture: NULL or a host array of n_layers device pointers; capture[i] != NULL receives layer i's output
+ * (solutions/packed.py:190-195).  Replaces packed_layers (solutions/packed.py:188-196). */
+int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
+                       const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, void* workspace,
+                       size_t ws_bytes, void* const* capture, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LSK_H_ */

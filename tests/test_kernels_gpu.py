@@ -1,0 +1,306 @@
+"""Kernel-level parity of liblsk against the CPU oracle / fp64 references (GPU).
+
+Bars: bit-exact for data movement and index work (KV append, RoPE, embed, row copies, argmax,
+acceptance); tolerance for reductions (GEMM, RMSNorm, attention), written in each test.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle.model import brute_attention, rms_norm as o_rms_norm, rope as o_rope
+
+pytestmark = pytest.mark.gpu
+
+BF16, F32 = torch.bfloat16, torch.float32
+
+
+def _lsk():
+    from thesis_amd import _lsk
+
+    _lsk.load()
+    return _lsk
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ----------------------------------------------------------------------------- GEMM
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 64), (5, 128, 256), (16, 64, 96), (17, 256, 512), (33, 128, 4160),
+                                   (64, 4096, 256), (100, 320, 1024), (288, 512, 2048)])
+def test_gemm_bf16_none_matches_fp32_reference(cuda, M, N, K):
+    lsk = _lsk()
+    g = _gen(M * 7 + N)
+    a = torch.randn(M, K, generator=g).to(BF16)
+    w = torch.randn(N, K, generator=g).to(BF16)
+    ref = a.float() @ w.float().t()                      # exact products, fp32 accumulation
+    got = lsk.gemm(a.to(cuda), w.to(cuda)).cpu().float()
+    # bf16 output rounding (2^-8 relative) + fp32 accumulation-order error
+    tol = 2.0 ** -8 * ref.abs() + 1e-3 * math.sqrt(K)
+    assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max()
+
+
+def test_gemm_bf16_is_batch_invariant(cuda):
+    """Every row's result is bitwise independent of M and of which rows share a tile."""
+    lsk = _lsk()
+    g = _gen(3)
+    K, N = 1024, 384
+    a = torch.randn(200, K, generator=g).to(BF16).to(cuda)
+    w = torch.randn(N, K, generator=g).to(BF16).to(cuda)
+    full = lsk.gemm(a, w)
+    for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104)]:
+        part = lsk.gemm(a[lo:hi].contiguous(), w)
+        assert torch.equal(part, full[lo:hi]), (lo, hi)
+
+
+def test_gemm_bf16_epilogues_match_reference_rounding(cuda):
+    """RESIDUAL: rnd(R + rnd(acc)); SILU_MUL: rnd(rnd(silu(rnd(g))) * rnd(u))  (solutions/packed.py:182-185)."""
+    lsk = _lsk()
+    g = _gen(11)
+    M, K, F_ = 37, 512, 256
+    a = torch.randn(M, K, generator=g).to(BF16)
+    w13 = (torch.randn(2 * F_, K, generator=g) * 0.05).to(BF16)
+    r = torch.randn(M, 2 * F_, generator=g).to(BF16)
+    acc = (a.float() @ w13.float().t())
+    # residual: compare with the same formula on the CPU from the fp32 accumulation
+    got_r = lsk.gemm(a.to(cuda), w13.to(cuda), residual=r.to(cuda), epilogue=lsk.EPI_RESIDUAL).cpu()
+    ref_r = (r.float() + acc.to(BF16).float()).to(BF16)
+    close = (got_r.float() - ref_r.float()).abs() <= 2.0 ** -7 * ref_r.float().abs() + 1e-2
+    assert close.all()
+    got_s = lsk.gemm(a.to(cuda), w13.to(cuda), epilogue=lsk.EPI_SILU_MUL).cpu()
+    gg, uu = acc.to(BF16).chunk(2, dim=-1)
+    ref_s = F.silu(gg) * uu                               # torch bf16 ops: the reference's rounding points
+    assert ((got_s.float() - ref_s.float()).abs() <= 2.0 ** -6 * ref_s.float().abs() + 2e-3).all()
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 8, 16), (7, 64, 64), (33, 100, 130)])
+def test_gemm_f32(cuda, M, N, K):
+    lsk = _lsk()
+    g = _gen(5)
+    a, w = torch.randn(M, K, generator=g), torch.randn(N, K, generator=g)
+    got = lsk.gemm(a.to(cuda), w.to(cuda)).cpu()
+    assert torch.allclose(got, a.double().mm(w.double().t()).float(), rtol=1e-5, atol=1e-5)
+    r = torch.randn(M, N, generator=g)
+    got = lsk.gemm(a.to(cuda), w.to(cuda), residual=r.to(cuda), epilogue=lsk.EPI_RESIDUAL).cpu()
+    assert torch.allclose(got, r + a @ w.t(), rtol=1e-5, atol=1e-5)
+    w13 = torch.randn(2 * N, K, generator=g)
+    got = lsk.gemm(a.to(cuda), w13.to(cuda), epilogue=lsk.EPI_SILU_MUL).cpu()
+    gg, uu = (a @ w13.t()).chunk(2, dim=-1)
+    assert torch.allclose(got, F.silu(gg) * uu, rtol=1e-4, atol=1e-5)
+
+
+# ----------------------------------------------------------------------------- RMSNorm
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+def test_rmsnorm(cuda, dtype):
+    lsk = _lsk()
+    g = _gen(1)
+    x = (torch.randn(19, 4096, generator=g) * 3).to(dtype)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(dtype)
+    got = lsk.rmsnorm(x.to(cuda), w.to(cuda), 1e-5).cpu()
+    ref = o_rms_norm(x, w, 1e-5)
+    if dtype == F32:
+        assert torch.allclose(got, ref, rtol=2e-6, atol=1e-6)
+    else:
+        # the mean's summation order differs; after the bf16 cast almost every element is identical
+        # and the rest differ by one bf16 ulp
+        diff = (got.float() - ref.float()).abs()
+        assert (diff <= 2.0 ** -7 * ref.float().abs() + 1e-6).all()
+        assert (got == ref).float().mean() > 0.98
+
+
+# ----------------------------------------------------------------------------- RoPE + append
+
+@pytest.mark.parametrize("dtype,D", [(BF16, 128), (BF16, 64), (F32, 16)])
+def test_rope_append_is_bit_exact(cuda, dtype, D):
+    """q_out and the appended K are bitwise the oracle's rope(); V is copied bitwise; nothing else in
+    the cache changes (solutions/packed.py:176-181)."""
+    lsk = _lsk()
+    from oracle.model import OracleConfig, rope_tables
+
+    g = _gen(D)
+    Hq, Hkv, B, S, N = 8, 2, 3, 256, 11
+    cfg = OracleConfig(64, 64, 1, Hq, Hkv, D, 64, rope_theta=500000.0)
+    cos, sin = rope_tables(cfg, S)
+    qkv = torch.randn(N, (Hq + 2 * Hkv) * D, generator=g).to(dtype)
+    rows = torch.randint(0, B, (N,), generator=g)
+    pos = torch.randperm(S, generator=g)[:N]             # distinct (row, pos) slots
+    kc = torch.zeros(B, Hkv, S, D, dtype=dtype)
+    vc = torch.zeros_like(kc)
+    kd, vd = kc.to(cuda), vc.to(cuda)
+    q_out = torch.empty(N, Hq, D, dtype=dtype, device=cuda)
+    lsk.rope_append(qkv.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda),
+                    rows.to(torch.int32).to(cuda), pos.to(torch.int32).to(cuda), Hq, Hkv, D)
+    c = cos[pos].to(dtype).unsqueeze(1)
+    s = sin[pos].to(dtype).unsqueeze(1)
+    q_ref = o_rope(qkv[:, :Hq * D].view(N, Hq, D), c, s)
+    k_ref = o_rope(qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D), c, s)
+    v_ref = qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D)
+    assert torch.equal(q_out.cpu(), q_ref)
+    kc[rows, :, pos] = k_ref
+    vc[rows, :, pos] = v_ref
+    assert torch.equal(kd.cpu(), kc)
+    assert torch.equal(vd.cpu(), vc)
+
+
+def test_kv_append_is_bit_exact(cuda):
+    lsk = _lsk()
+    g = _gen(2)
+    B, Hkv, S, D, N = 4, 8, 128, 128, 9
+    k = torch.randn(N, Hkv, D, generator=g).to(BF16)
+    v = torch.randn(N, Hkv, D, generator=g).to(BF16)
+    rows = torch.randint(0, B, (N,), generator=g)
+    pos = torch.randperm(S, generator=g)[:N]
+    kc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
+    vc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
+    kd, vd = kc.to(cuda), vc.to(cuda)
+    lsk.kv_append(k.to(cuda), v.to(cuda), kd, vd, rows.to(torch.int32).to(cuda), pos.to(torch.int32).to(cuda))
+    kc[rows, :, pos] = k
+    vc[rows, :, pos] = v
+    assert torch.equal(kd.cpu(), kc) and torch.equal(vd.cpu(), vc)
+
+
+# ----------------------------------------------------------------------------- attention
+
+def _attn_case(seed, dtype, B, Hq, Hkv, D, S, blocks):
+    """blocks: list of (row, pos0, T); returns q, caches, host block table and reference output."""
+    g = _gen(seed)
+    N = sum(T for _, _, T in blocks)
+    q = torch.randn(N, Hq, D, generator=g).to(dtype)
+    kc = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    vc = torch.randn(B, Hkv, S, D, generator=g).to(dtype)
+    rows, pos, tab, off = [], [], [], 0
+    for (r, p0, T) in blocks:
+        tab.append((off, p0, T, r))
+        rows += [r] * T
+        pos += list(range(p0, p0 + T))
+        off += T
+    ref = brute_attention(q, kc, vc, rows, pos, Hq // Hkv)
+    return q, kc, vc, np.array(tab, dtype=np.int32), ref
+
+
+def _run_attn(lsk, cuda, q, kc, vc, tab, split):
+    Hq, D = q.shape[1], q.shape[2]
+    Hkv = kc.shape[1]
+    works, groups, n_parts = lsk.attn_plan(tab, Hq // Hkv, split)
+    out = torch.empty(q.shape[0], Hq * D, dtype=q.dtype, device=cuda)
+    ws = torch.empty(max(lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=cuda)
+    gdev = torch.from_numpy(groups).to(cuda) if len(groups) else None
+    lsk.ragged_attn(q.to(cuda), kc.to(cuda), vc.to(cuda), torch.from_numpy(tab).to(cuda),
+                    torch.from_numpy(works).to(cuda), len(works), gdev, len(groups), n_parts, out, Hq,
+                    1.0 / math.sqrt(D), ws)
+    return out.cpu()
+
+
+ATTN_CASES = [
+    # (B, Hq, Hkv, D, S, blocks)
+    (3, 32, 8, 128, 1024, [(0, 5, 1), (1, 100, 4), (2, 63, 9)]),
+    (4, 32, 8, 128, 2048, [(1, 700, 1), (3, 1500, 7), (0, 511, 2), (2, 1023, 9)]),  # split boundaries
+    (2, 32, 32, 128, 512, [(0, 10, 3), (1, 300, 5)]),                                 # MHA (7B shape)
+    (3, 32, 8, 64, 1024, [(0, 0, 40), (2, 200, 6), (1, 64, 1)]),                       # D = 64, prefill chunk
+]
+
+
+@pytest.mark.parametrize("case", range(len(ATTN_CASES)))
+def test_ragged_attention_bf16_matches_brute_force(cuda, case):
+    lsk = _lsk()
+    B, Hq, Hkv, D, S, blocks = ATTN_CASES[case]
+    q, kc, vc, tab, ref = _attn_case(case, BF16, B, Hq, Hkv, D, S, blocks)
+    got = _run_attn(lsk, cuda, q, kc, vc, tab, lsk.ATTN_SPLIT).double()
+    # bf16 inputs are exact in the fp64 reference; the kernel rounds P to bf16 and the output to bf16
+    err = (got - ref).abs()
+    assert err.max() < 2e-2, err.max()
+    assert err.mean() < 3e-3, err.mean()
+
+
+def test_ragged_attention_f32_matches_brute_force(cuda):
+    lsk = _lsk()
+    q, kc, vc, tab, ref = _attn_case(9, F32, 3, 4, 2, 16, 256, [(0, 3, 1), (1, 30, 5), (2, 100, 9)])
+    got = _run_attn(lsk, cuda, q, kc, vc, tab, 1 << 30).double()
+    assert (got - ref).abs().max() < 1e-5
+
+
+def test_ragged_attention_bf16_is_batch_invariant(cuda):
+    """A query's output is bitwise the same alone (T = 1) and inside a verify block that crosses a
+    split boundary."""
+    lsk = _lsk()
+    B, Hq, Hkv, D, S = 2, 32, 8, 128, 2048
+    blocks = [(0, 505, 9), (1, 1020, 8)]
+    q, kc, vc, tab, _ = _attn_case(21, BF16, B, Hq, Hkv, D, S, blocks)
+    full = _run_attn(lsk, cuda, q, kc, vc, tab, lsk.ATTN_SPLIT)
+    off = 0
+    for (r, p0, T) in blocks:
+        for t in range(T):
+            one = np.array([(0, p0 + t, 1, r)], dtype=np.int32)
+            got = _run_attn(lsk, cuda, q[off + t:off + t + 1].contiguous(), kc, vc, one, lsk.ATTN_SPLIT)
+            assert torch.equal(got[0], full[off + t]), (r, p0, t)
+        off += T
+
+
+# ----------------------------------------------------------------------------- glue
+
+def test_argmax_first_index_on_ties(cuda):
+    lsk = _lsk()
+    x = torch.zeros(4, 1000, dtype=BF16)
+    x[0, 17] = x[0, 900] = 3.0
+    x[1, :] = -1.0
+    x[2, 999] = 1.0
+    x[3] = torch.randn(1000, generator=_gen(0)).to(BF16)
+    out = torch.empty(4, dtype=torch.long, device=cuda)
+    lsk.argmax(x.to(cuda), out)
+    assert out.cpu().tolist() == x.float().argmax(-1).tolist() == [17, 0, 999, int(x[3].float().argmax())]
+
+
+def test_embed_and_copy_rows(cuda):
+    lsk = _lsk()
+    g = _gen(4)
+    table = torch.randn(50, 64, generator=g).to(BF16)
+    seq = torch.tensor([[5, 6, 7], [8, 9, 10]], dtype=torch.long)
+    sel = torch.tensor([0, -1, 4, 2, -1], dtype=torch.long)
+    alt = torch.tensor([0, 33, 0, 0, 49], dtype=torch.long)
+    out = torch.empty(5, 64, dtype=BF16, device=cuda)
+    lsk.embed(table.to(cuda), alt.to(cuda), out, seq.to(cuda).view(-1), sel.to(cuda))
+    ids = [5, 33, 9, 7, 49]
+    assert torch.equal(out.cpu(), table[ids])
+    dst = torch.zeros(6, 64, dtype=BF16, device=cuda)
+    lsk.copy_rows(dst, torch.tensor([5, 0], device=cuda), out, torch.tensor([1, 3], device=cuda), 2)
+    assert torch.equal(dst.cpu()[5], table[33]) and torch.equal(dst.cpu()[0], table[7])
+    assert (dst.cpu()[1:5] == 0).all()
+
+
+def test_greedy_accept_matches_closed_form(cuda):
+    """acc = min{j : Y_j != draft_{j+1}} <= d; forced: min(draw, d) and drafts[0..a-1] + Y[a]."""
+    lsk = _lsk()
+    rng = np.random.default_rng(0)
+    Dm1, B = 6, 5
+    seq = rng.integers(0, 9, size=(B, Dm1))
+    slots = np.array([3, 0, 4])
+    Ts = np.array([4, 1, 6])
+    starts = np.concatenate([[0], np.cumsum(Ts)[:-1]])
+    Y = rng.integers(0, 9, size=int(Ts.sum()))
+    Y[starts[0]:starts[0] + 2] = seq[3, 1:3]            # first two drafts of slot 3 accepted
+    forced = np.array([-1, -1, 2])
+    dev = lambda a, dt=torch.int32: torch.as_tensor(a, dtype=dt).to(cuda)  # noqa: E731
+    sb = dev(seq.reshape(-1), torch.long)
+    acc = torch.empty(3, dtype=torch.long, device=cuda)
+    yo = torch.empty(len(Y), dtype=torch.long, device=cuda)
+    kvl = dev(np.full(B, 100), torch.long)
+    lsk.greedy_accept(dev(Y, torch.long), sb, Dm1, dev(slots), dev(starts), dev(Ts), dev(forced), 3, acc, yo, kvl)
+    acc_h, yo_h, sb_h = acc.cpu().numpy(), yo.cpu().numpy(), sb.cpu().numpy().reshape(B, Dm1)
+    for j in range(3):
+        i, s, T = slots[j], starts[j], Ts[j]
+        nat = next((jj for jj in range(T - 1) if Y[s + jj] != seq[i, jj + 1]), T - 1)
+        a = min(forced[j], T - 1) if forced[j] >= 0 else nat
+        assert acc_h[j] == a
+        toks = list(seq[i, 1:1 + a]) + [Y[s + a]] if forced[j] >= 0 else list(Y[s:s + a + 1])
+        assert list(yo_h[s:s + a + 1]) == toks
+        assert sb_h[i, 0] == Y[s + a]
+        assert kvl.cpu()[i] == 100 + a + 1
+    assert acc_h[0] == 2

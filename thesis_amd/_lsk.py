@@ -1,0 +1,275 @@
+"""ctypes binding of liblsk.so, the C ABI of the gfx950 kernels (include/lsk.h).
+
+Only device pointers, sizes and the current HIP stream cross the boundary.  Tensors stay owned by
+PyTorch (device memory + streams are plumbing; every FLOP of the packed forward runs in liblsk).
+There is no fallback: a missing or stale library raises at the first call.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from pathlib import Path
+
+import numpy as np
+import torch
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblsk.so"
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
+ATTN_SPLIT = 512          # LSK_ATTN_SPLIT
+ATTN_ROWS = 64            # query rows per attention workgroup
+ABI_VERSION = 1
+
+# name -> (restype, argtypes)
+_P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
+_SIGS = {
+    "lsk_last_error": (ctypes.c_char_p, []),
+    "lsk_abi_version": (_I, []),
+    "lsk_rmsnorm": (_I, [_I, _P, _P, _P, _I, _I, _F, _L, _L, _P]),
+    "lsk_rope_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "lsk_kv_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
+    "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
+    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z, _P]),
+    "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
+    "lsk_gemm_tile": (_I, [_I, _I, _P, _P]),
+    "lsk_embed": (_I, [_P, _L, _L, _P, _L, _P, _P, _P, _I, _P]),
+    "lsk_copy_rows": (_I, [_P, _P, _L, _P, _P, _L, _L, _I, _P]),
+    "lsk_argmax": (_I, [_I, _P, _L, _I, _I, _P, _P, _P]),
+    "lsk_greedy_accept": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
+    "lsk_kv_rollback": (_I, [_P, _P, _P, _I, _P]),
+    "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
+    "lsk_model_destroy": (_I, [_L]),
+    "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
+    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _Z, _P, _P]),
+}
+EXPORTS = tuple(_SIGS)
+
+_lib = None
+
+
+class LskError(RuntimeError):
+    pass
+
+
+def load(path: str | os.PathLike | None = None):
+    """Load liblsk.so (once).  Raises if it is missing: there is no CPU fallback."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = Path(path) if path is not None else LIB_PATH
+    if not p.exists():
+        raise LskError(f"{p} is missing: build it with `python -c 'import __graft_entry__ as g; g.build()'`")
+    lib = ctypes.CDLL(str(p))
+    for name, (res, args) in _SIGS.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.lsk_abi_version() != ABI_VERSION:
+        raise LskError(f"liblsk ABI {lib.lsk_abi_version()} != {ABI_VERSION}; rebuild")
+    if path is None:
+        _lib = lib
+    return lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().lsk_last_error().decode(errors="replace")
+        raise LskError(f"{what} failed ({rc}): {msg}")
+
+
+def _ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return DTYPE_BF16
+    if dtype == torch.float32:
+        return DTYPE_F32
+    raise LskError(f"unsupported dtype {dtype} (bf16 and fp32 only)")
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise LskError(f"liblsk kernels need CUDA (HIP) tensors, got {t.device}")
+
+
+# ----------------------------------------------------------------------------- ops
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(x, w)
+    assert x.dim() == 2 and x.stride(1) == 1 and w.is_contiguous() and w.numel() == x.shape[1]
+    if out is None:
+        out = torch.empty_like(x)
+    _check(load().lsk_rmsnorm(dtype_code(x.dtype), _ptr(x), _ptr(w), _ptr(out), x.shape[0], x.shape[1], float(eps),
+                              x.stride(0), out.stride(0), _stream()), "lsk_rmsnorm")
+    return out
+
+
+def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads, head_dim):
+    _dev(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
+    N = qkv.shape[0]
+    B, Hkv, S, D = kcache.shape
+    assert qkv.is_contiguous() and q_out.is_contiguous() and kcache.is_contiguous() and vcache.is_contiguous()
+    assert cos_tab.dtype == torch.float32 and cos_tab.is_contiguous() and cos_tab.shape[1] == head_dim
+    _check(load().lsk_rope_append(dtype_code(qkv.dtype), _ptr(qkv), _ptr(q_out), _ptr(kcache), _ptr(vcache),
+                                  _ptr(cos_tab), _ptr(sin_tab), cos_tab.shape[0], _ptr(rows_i32), _ptr(pos_i32), N,
+                                  n_heads, n_kv_heads, head_dim, B, S, _stream()), "lsk_rope_append")
+
+
+def kv_append(k, v, kcache, vcache, rows_i32, pos_i32):
+    _dev(k, v, kcache, vcache, rows_i32, pos_i32)
+    B, Hkv, S, D = kcache.shape
+    assert k.is_contiguous() and v.is_contiguous() and k.shape[1:] == (Hkv, D)
+    _check(load().lsk_kv_append(dtype_code(k.dtype), _ptr(k), _ptr(v), _ptr(kcache), _ptr(vcache), _ptr(rows_i32),
+                                _ptr(pos_i32), k.shape[0], Hkv, D, B, S, _stream()), "lsk_kv_append")
+
+
+def attn_plan(blocks: np.ndarray, group: int, split: int):
+    """blocks int32 [nb, 4] = (q_start, pos0, T, row) -> (works [n,8], groups [n,8], n_parts)."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.int32)
+    nb = blocks.shape[0]
+    rows = int(((blocks[:, 2].astype(np.int64) * group + ATTN_ROWS - 1) // ATTN_ROWS).sum()) if nb else 0
+    max_ctx = int((blocks[:, 1].astype(np.int64) + blocks[:, 2]).max()) if nb else 0
+    max_works = max(1, rows * max(1, (max_ctx + split - 1) // split))
+    max_groups = max(1, rows)
+    works = np.zeros((max_works, 8), dtype=np.int32)
+    groups = np.zeros((max_groups, 8), dtype=np.int32)
+    nw, ng, npart = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
+    _check(load().lsk_attn_plan(blocks.ctypes.data, nb, group, split, works.ctypes.data, max_works,
+                                groups.ctypes.data, max_groups, ctypes.byref(nw), ctypes.byref(ng),
+                                ctypes.byref(npart)), "lsk_attn_plan")
+    return works[:nw.value], groups[:ng.value], npart.value
+
+
+def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
+    return int(load().lsk_attn_workspace_bytes(n_parts, n_kv_heads, head_dim))
+
+
+def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
+                scale, workspace=None):
+    _dev(q, kcache, vcache, blocks_dev, works_dev, out)
+    B, Hkv, S, D = kcache.shape
+    ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+    _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
+                                  _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(out), n_heads,
+                                  Hkv, D, S, float(scale), _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
+
+
+def gemm(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+         epilogue: int = EPI_NONE) -> torch.Tensor:
+    _dev(a, w, out, residual)
+    assert a.dim() == 2 and w.dim() == 2 and a.stride(1) == 1 and w.stride(1) == 1
+    M, K = a.shape
+    if epilogue == EPI_SILU_MUL:
+        N = w.shape[0] // 2
+        ffn = N
+    else:
+        N = w.shape[0]
+        ffn = 0
+    if out is None:
+        out = torch.empty(M, N, dtype=a.dtype, device=a.device)
+    ldr = residual.stride(0) if residual is not None else 0
+    _check(load().lsk_gemm(dtype_code(a.dtype), _ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(out), out.stride(0),
+                           _ptr(residual), ldr, M, N, K, epilogue, ffn, _stream()), "lsk_gemm")
+    return out
+
+
+def embed(table: torch.Tensor, alt_ids: torch.Tensor, out: torch.Tensor, seq_buf: torch.Tensor | None = None,
+          sel: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(table, alt_ids, out, seq_buf, sel)
+    n = alt_ids.numel()
+    row_bytes = table.shape[1] * table.element_size()
+    _check(load().lsk_embed(_ptr(table), table.shape[0], row_bytes, _ptr(seq_buf),
+                            seq_buf.numel() if seq_buf is not None else 0, _ptr(sel), _ptr(alt_ids), _ptr(out), n,
+                            _stream()), "lsk_embed")
+    return out
+
+
+def copy_rows(dst: torch.Tensor, dst_idx, src: torch.Tensor, src_idx, n: int) -> None:
+    _dev(dst, src, dst_idx, src_idx)
+    row_bytes = dst[0].numel() * dst.element_size()
+    assert src[0].numel() * src.element_size() == row_bytes
+    _check(load().lsk_copy_rows(_ptr(dst), _ptr(dst_idx), dst.shape[0], _ptr(src), _ptr(src_idx), src.shape[0],
+                                row_bytes, n, _stream()), "lsk_copy_rows")
+
+
+def argmax(logits: torch.Tensor, out: torch.Tensor, dst_idx: torch.Tensor | None = None, n_rows: int | None = None):
+    _dev(logits, out, dst_idx)
+    n = logits.shape[0] if n_rows is None else n_rows
+    _check(load().lsk_argmax(dtype_code(logits.dtype), _ptr(logits), logits.stride(0), n, logits.shape[1], _ptr(out),
+                             _ptr(dst_idx), _stream()), "lsk_argmax")
+    return out
+
+
+def greedy_accept(Yv, seq_buf, Dm1, slots, starts, Ts, forced, nv, acc_out, y_out, kv_len=None):
+    _dev(Yv, seq_buf, slots, starts, Ts, forced, acc_out, y_out, kv_len)
+    _check(load().lsk_greedy_accept(_ptr(Yv), _ptr(seq_buf), Dm1, _ptr(slots), _ptr(starts), _ptr(Ts), _ptr(forced),
+                                    nv, _ptr(acc_out), _ptr(y_out), _ptr(kv_len), _stream()), "lsk_greedy_accept")
+
+
+def kv_rollback(kv_len, slots, accepted, nv):
+    _dev(kv_len, slots, accepted)
+    _check(load().lsk_kv_rollback(_ptr(kv_len), _ptr(slots), _ptr(accepted), nv, _stream()), "lsk_kv_rollback")
+
+
+# ----------------------------------------------------------------------------- layer-range runner
+
+def _ptr_array(ptrs):
+    arr = (ctypes.c_void_p * len(ptrs))()
+    for i, p in enumerate(ptrs):
+        arr[i] = p
+    return arr
+
+
+class NativeModel:
+    """Handle of the native layer-range runner for one (weights, KV cache, RoPE table) set."""
+
+    def __init__(self, dtype, n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, eps, layers, kcache, vcache,
+                 cos_tab, sin_tab):
+        lib = load()
+        _dev(cos_tab, sin_tab)
+        B, Hkv, S, D = kcache[0].shape
+        self._keep = (layers, kcache, vcache, cos_tab, sin_tab)
+        h = lib.lsk_model_create(
+            dtype_code(dtype), n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, float(eps),
+            _ptr_array([lw.wqkv.data_ptr() for lw in layers]), _ptr_array([lw.wo.data_ptr() for lw in layers]),
+            _ptr_array([lw.w13.data_ptr() for lw in layers]), _ptr_array([lw.w2.data_ptr() for lw in layers]),
+            _ptr_array([lw.attn_norm.data_ptr() for lw in layers]),
+            _ptr_array([lw.ffn_norm.data_ptr() for lw in layers]),
+            _ptr_array([t.data_ptr() for t in kcache]), _ptr_array([t.data_ptr() for t in vcache]),
+            B, S, cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0])
+        if h <= 0:
+            _check(int(h), "lsk_model_create")
+        self.handle = h
+        self.n_layers = n_layers
+
+    def workspace_bytes(self, n_tokens: int, n_parts: int) -> int:
+        return int(load().lsk_segment_workspace_bytes(self.handle, n_tokens, n_parts))
+
+    def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, workspace,
+                       capture_ptrs=None):
+        _dev(x_in, x_out, meta_dev, workspace)
+        cap = _ptr_array(capture_ptrs) if capture_ptrs is not None else None
+        ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
+        _check(load().lsk_forward_layers(self.handle, _ptr(x_in), _ptr(x_out), n_tokens, start, end, _ptr(meta_dev),
+                                         nb, n_works, n_groups, n_parts, _ptr(workspace), ws_bytes, cap, _stream()),
+               "lsk_forward_layers")
+
+    def __del__(self):
+        try:
+            if getattr(self, "handle", 0) > 0 and _lib is not None:
+                _lib.lsk_model_destroy(self.handle)
+        except Exception:
+            pass

@@ -1,0 +1,42 @@
+"""Build liblsk.so (gfx950) in-tree: thesis_amd/_lib/liblsk.so.
+
+    python -m thesis_amd.build
+"""
+
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+SOURCES = ["lsk_elementwise.hip", "lsk_attention.hip", "lsk_gemm.hip", "lsk_runtime.hip"]
+OUT = ROOT / "thesis_amd" / "_lib" / "liblsk.so"
+
+FLAGS = [
+    "--offload-arch=gfx950", "-O3", "-std=c++17", "-shared", "-fPIC",
+    # elementwise kernels reproduce the reference's rounding points: one rounding per operation
+    "-ffp-contract=off",
+    # no packed-fp32 instructions anywhere
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+
+def build(verbose: bool = False) -> Path:
+    hipcc = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+    OUT.parent.mkdir(parents=True, exist_ok=True)
+    tmp = OUT.with_suffix(".so.tmp")
+    cmd = [hipcc, *FLAGS, *[str(ROOT / "csrc" / s) for s in SOURCES], "-o", str(tmp)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    err = "\n".join(l for l in res.stderr.splitlines() if "packed-fp32-ops" not in l)
+    if res.returncode != 0:
+        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{err}")
+    if verbose and err.strip():
+        print(err, file=sys.stderr)
+    os.replace(tmp, OUT)
+    return OUT
+
+
+if __name__ == "__main__":
+    print(build(verbose=True))
