@@ -192,6 +192,8 @@ class LayerSkipLlama:
     def __init__(self, cfg: ModelConfig, embed: Tensor, layers: list, norm: Tensor, lm_head: Tensor, device, dtype,
                  max_seq: int):
         self.device = torch.device(device)
+        if self.device.type == "cuda" and self.device.index is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
         if self.device.type != "cuda":
             raise _lsk.LskError("LayerSkipLlama runs on the GPU only (liblsk kernels); the CPU oracle lives in "
                                 "oracle/ for tests")

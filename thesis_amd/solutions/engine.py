@@ -1,0 +1,611 @@
+"""EESD engine: batched early-exit self-speculation with packed shallow / deep steps on MI355X
+(solutions/engine.py surface: EngineConfig, Request, Rec, EESDEngine.assign / step / run / run_poisson).
+
+Step semantics are the reference's (solutions/engine.py:1-27, 269-489):
+  shallow step  every decoding slot runs its current input token (last committed token if d = 0, else
+                its newest draft) at position pos + d through layers [0, k) and the shared exit head
+                -> one draft (seq_buf[i, d + 1]); its layer-k hidden state is kept in exit_h[i, d].
+  deep step     the verifying slots (scheduler's V) run their newest draft through [0, k) in the same
+                shallow segment, then all d + 1 tokens (inputs exit_h[i, 0..d]) at pos..pos + d through
+                [k, L) + head; greedy acceptance; the other slots draft in the same step.
+  rollback      pointer only: pos += acc + 1, d = 0; rejected drafts' KV stays beyond pos, is never read
+                (queries read positions <= their own) and is overwritten next round.
+Device glue (id assembly + embedding, exit_h staging, draft head + argmax scatter into seq_buf, verify
+gathers, greedy acceptance) runs in liblsk; the host reads the device once per deep step (accepted
+counts + verified tokens) and never in a shallow step.
+
+Harness hook with no reference counterpart: `forced_accept_p` replaces each verifier's acceptance by
+a seeded draw min(Geometric(p) - 1, d) and commits drafts[0..a-1] + Yv[a] (the tokens whose KV the deep
+segment wrote), as the measured configurations prescribe.
+Not built yet (raise NotImplementedError): exit="m2" (probe steps) and prefill="m3" (piggyback chunks).
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import asdict, dataclass, field
+from typing import Callable, Optional
+
+import numpy as np
+import torch
+
+from .. import _lsk
+from ..common.timing import Interval
+from .packed import Block, build_packed, packed_layers, upload
+from .schedulers import make_scheduler
+
+FREE, PREFILL, DECODE = 0, 1, 2
+
+
+@dataclass
+class EngineConfig:
+    mode: str = "spec"              # spec | ar
+    sched: str = "fixed"            # fixed | aspire | m1 | fsm-sync | aspire-fsm
+    gamma: int = 4
+    k: int = 3
+    exit: str = "fixed"             # fixed (m2: not built)
+    prefill: str = "separate"       # separate (m3: not built)
+    d_max: int = 16
+    sla_steps: int = 32
+    initial_draft: int = 3
+    min_draft: int = 1
+    omega: float = 0.8
+    alpha0: float = 0.9
+    probe_every: int = 20
+    k_cands: tuple = (2, 3, 4, 5, 6, 7, 8)
+    switch_margin: float = 0.05
+    max_wait: int = 3
+    knee_safety: float = 0.9
+    prefill_chunk: int = 512
+    bucketing: str = "exact"
+    m3_chunk_cap: Optional[int] = None
+    m2_force: Optional[str] = None
+    forced_accept_p: Optional[float] = None
+    forced_seed: int = 0
+
+    def label(self) -> str:
+        if self.mode == "ar":
+            return "ar"
+        s = f"{self.sched}" + (f"-g{self.gamma}" if self.sched == "fixed" else "")
+        return f"{s}-{'k' + str(self.k) if self.exit == 'fixed' else 'm2'}-{self.prefill}"
+
+
+@dataclass
+class Request:
+    pid: str
+    prompt: list
+    out: list = field(default_factory=list)
+    finish: Optional[str] = None
+    rec_assign: int = 0
+    rec_first: int = -1
+    rec_finish: int = -1
+    wall_arrival: float = 0.0
+    wall_first: float = 0.0
+    measured: bool = False
+    pf_sh: int = 0
+    pf_dp: int = 0
+    piggybacked: int = 0
+    key: int = -1                   # assignment counter (forced-acceptance stream)
+
+
+@dataclass
+class Rec:
+    kind: str
+    iv: Interval
+    measured: bool
+    n_sh: int = 0
+    n_dp: int = 0
+    n_chunk: int = 0
+    plan_ms: float = 0.0
+    k: int = 0
+    _ms: Optional[float] = None
+
+    @property
+    def ms(self) -> float:
+        if self._ms is None:
+            self._ms = self.iv.ms
+        return self._ms
+
+
+class ForcedAcceptance:
+    """a = Geometric(p) - 1 per verification round, from default_rng([seed, key]) of the request."""
+
+    def __init__(self, p: float, seed: int = 0):
+        self.p, self.seed = p, seed
+        self.streams: dict = {}
+
+    def draw(self, key: int) -> int:
+        rng = self.streams.get(key)
+        if rng is None:
+            rng = self.streams[key] = np.random.default_rng([self.seed, key])
+        return int(rng.geometric(self.p)) - 1
+
+
+class EESDEngine:
+    def __init__(self, model, B: int, max_prompt: int, max_new: int, eos_ids, cfg: EngineConfig, cost_model,
+                 stop_for: Optional[Callable] = None, ref: Optional[dict] = None):
+        if cfg.mode == "ar" and cfg.prefill != "separate":
+            raise ValueError("AR mode supports --prefill separate only")
+        if cfg.exit != "fixed":
+            raise NotImplementedError("exit='m2' (probe steps) is not built in this engine yet")
+        if cfg.prefill != "separate":
+            raise NotImplementedError("prefill='m3' (piggyback chunks) is not built in this engine yet")
+        self.m, self.dev, self.B, self.cfg, self.cm = model, model.device, B, cfg, cost_model
+        self.max_new, self.eos = max_new, set(eos_ids)
+        self.stop_for = stop_for or (lambda pid: None)
+        self.k = cfg.k
+        self.L = model.n_layers
+        if not 1 <= self.k < self.L:
+            raise ValueError("exit layer must be in [1, n_layers)")
+        Dm = cfg.d_max
+        self.Dm1 = Dm + 1
+        model.allocate_cache(B, max_prompt + max_new + Dm + 40)
+        self.seq_buf = torch.zeros(B, self.Dm1, dtype=torch.long, device=self.dev)
+        self.exit_h = torch.zeros(B, self.Dm1, model.cfg.dim, dtype=model.dtype, device=self.dev)
+        self.state = np.zeros(B, dtype=np.int64)
+        self.pos = np.zeros(B, dtype=np.int64)
+        self.d = np.zeros(B, dtype=np.int64)
+        self.gen = np.zeros(B, dtype=np.int64)
+        self.req: list = [None] * B
+        self.pending: list = [[] for _ in range(B)]
+        self.steps_since_deep = 0
+        self.records: list = []
+        self.sched = make_scheduler(cfg.sched, B, cost_model, self.k, gamma=cfg.gamma, d_max=Dm,
+                                    sla_steps=cfg.sla_steps, initial_draft=cfg.initial_draft, omega=cfg.omega,
+                                    alpha0=cfg.alpha0, min_draft=cfg.min_draft) if cfg.mode == "spec" else None
+        self.exitc = None
+        self.m3 = None
+        self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
+        self._keys = 0
+        self.measuring = False
+        self.stats = {"steps": 0, "deep_steps": 0, "probe_steps": 0, "deep_tokens": 0, "verifiers": 0, "drafted": 0,
+                      "accepted": 0, "committed": 0, "plan_ms": 0.0, "plan_calls": 0, "prefill_tokens": 0,
+                      "piggyback_tokens": 0, "separate_prefills": 0, "m3_fallbacks": 0, "dropped_drafts": 0,
+                      "kv_read_pos": 0, "kv_gathered_pos": 0}
+        self.round_len = cfg.gamma
+        self.kv_bytes_per_pos = 2 * model.cfg.n_kv_heads * model.cfg.head_dim * model.dtype.itemsize
+        self.fallback_reasons: dict = {}
+
+    # ------------------------------------------------------------------ helpers
+    def _rec(self, kind, iv, **kw) -> Rec:
+        r = Rec(kind, iv, self.measuring, k=self.k, **kw)
+        self.records.append(r)
+        return r
+
+    def _commit(self, slot: int, toks) -> int:
+        r = self.req[slot]
+        n = 0
+        for t in toks:
+            if r.finish is not None:
+                break
+            r.out.append(int(t))
+            n += 1
+            if int(t) in self.eos:
+                r.finish = "eos"
+            elif len(r.out) >= self.max_new:
+                r.finish = "length"
+        stop = self.stop_for(r.pid)
+        if n and stop and r.finish is None:
+            cut = stop(r.out, n)
+            if cut is not None:
+                n -= len(r.out) - cut
+                del r.out[cut:]
+                r.finish = "stop"
+        self.gen[slot] = len(r.out)
+        return n
+
+    def _first_token(self, slot: int, y0: int) -> int:
+        r = self.req[slot]
+        r.rec_first = len(self.records) - 1
+        r.wall_first = time.perf_counter()
+        self.state[slot] = DECODE
+        self.pos[slot] = len(r.prompt)
+        self.d[slot] = 0
+        if self.sched is not None:
+            self.sched.reset(slot)
+        return self._commit(slot, [y0])
+
+    def _flat(self):
+        return self.seq_buf.view(-1), self.exit_h.view(-1, self.exit_h.shape[-1])
+
+    # ------------------------------------------------------------------ assignment / prefill
+    def assign(self, slot: int, req: Request) -> int:
+        req.rec_assign = len(self.records)
+        req.measured = self.measuring
+        if req.key < 0:
+            req.key = self._keys
+        self._keys += 1
+        self.req[slot] = req
+        self.pending[slot] = []
+        self.d[slot] = 0
+        return self._prefill_separate(slot)
+
+    @torch.inference_mode()
+    def _prefill_separate(self, slot: int) -> int:
+        m, r = self.m, self.req[slot]
+        n = len(r.prompt)
+        if n < 1:
+            raise ValueError("empty prompt")
+        iv = Interval(self.dev).start()
+        h = None
+        for s in range(0, n, self.cfg.prefill_chunk):
+            c = min(self.cfg.prefill_chunk, n - s)
+            pb = build_packed(m, [Block(slot, s, c)], self.cfg.bucketing)
+            self._kv(pb, self.L)
+            x = m.embed(upload(r.prompt[s:s + c], self.dev))
+            h = packed_layers(m, x, pb, 0, self.L)
+        sb, _ = self._flat()
+        y0 = m.head_argmax(h[-1:])
+        _lsk.copy_rows(sb.view(-1, 1), upload([slot * self.Dm1], self.dev), y0.view(-1, 1), None, 1)
+        iv.stop()
+        self._rec("prefill", iv, n_chunk=n)
+        self.stats["separate_prefills"] += 1
+        if self.measuring:
+            self.stats["prefill_tokens"] += n
+        return self._first_token(slot, int(y0.item()))
+
+    # ------------------------------------------------------------------ one step
+    @torch.inference_mode()
+    def step(self) -> tuple:
+        """Run one step; returns (committed tokens, slots that finished)."""
+        if self.cfg.mode == "ar":
+            return self._ar_step()
+        return self._spec_step()
+
+    def _ar_step(self):
+        m = self.m
+        dec = np.flatnonzero(self.state == DECODE)
+        if len(dec) == 0:
+            return 0, []
+        pb = build_packed(m, [Block(int(i), int(self.pos[i]), 1) for i in dec], self.cfg.bucketing)
+        self._kv(pb, self.L)
+        slots = np.array([b.row for b in pb.blocks], dtype=np.int64)
+        idx = upload(slots * self.Dm1, self.dev)
+        sb, _ = self._flat()
+        iv = Interval(self.dev).start()
+        x = m.buffer("x_in", (len(slots), m.cfg.dim), m.dtype)
+        _lsk.embed(m.embed_w, idx, x, sb, idx)
+        h = packed_layers(m, x, pb, 0, self.L)
+        y = m.head_argmax(h)
+        _lsk.copy_rows(sb.view(-1, 1), idx, y.view(-1, 1), None, len(slots))
+        iv.stop()
+        self._rec("ar", iv, n_sh=len(slots), n_dp=len(slots))
+        y_h = y.tolist()
+        committed, done = 0, []
+        for s, t in zip(slots.tolist(), y_h):
+            self.pos[s] += 1
+            committed += self._commit(s, [t])
+            if self.req[s].finish:
+                done.append(s)
+        self._account(committed, deep=True, n_deep=len(slots), verifiers=len(slots))
+        return committed, done
+
+    def _spec_step(self):
+        m, cfg, k = self.m, self.cfg, self.k
+        Dm1 = self.Dm1
+        t0 = time.perf_counter()
+        dec = self.state == DECODE
+        d = self.d.copy()
+        ctx = np.where(dec, self.pos + d, 0)
+        V = self.sched.decide(d, ctx, dec, self.steps_since_deep) if dec.any() else np.zeros(self.B, dtype=bool)
+        V = (V | (dec & (d >= cfg.d_max))) & dec & (d >= 1)
+        deep = bool(V.any())
+        Dr = dec & ~V
+        plan_ms = 1000 * (time.perf_counter() - t0)
+
+        dslots = np.flatnonzero(dec)
+        if len(dslots) == 0:
+            return 0, []
+        blocks = [Block(int(i), int(self.pos[i] + d[i]), 1, ("sh", int(i))) for i in dslots]
+        pb = build_packed(m, blocks, cfg.bucketing)
+        self._kv(pb, k)
+        N = pb.n_tokens
+        sl = np.fromiter((b.tag[1] for b in pb.blocks), dtype=np.int64, count=N)   # T = 1: token j <-> block j
+        sel = sl * Dm1 + d[sl]
+        drf_src = np.flatnonzero(Dr[sl])
+        drf_dst = sel[drf_src] + 1
+        nd = len(drf_src)
+        glue = upload(np.concatenate([sel, drf_src, drf_dst]), self.dev)
+        sel_t, drf_src_t, drf_dst_t = glue[:N], glue[N:N + nd], glue[N + nd:]
+        sb, exh = self._flat()
+        iv = Interval(self.dev).start()
+        x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+        _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
+        h = packed_layers(m, x, pb, 0, k)
+        _lsk.copy_rows(exh, sel_t, h, None, N)                                   # exit_h[i, d_i] = h
+        if nd:
+            hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
+            _lsk.copy_rows(hx, None, h, drf_src_t, nd)
+            m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                         # seq_buf[i, d_i + 1] = draft
+        readback = None
+        n_v_tok = 0
+        if deep:
+            readback, n_v_tok, vinfo = self._deep(V, d)
+        iv.stop()
+        self._rec("deep" if deep else "shallow", iv, n_sh=N, n_dp=n_v_tok, plan_ms=plan_ms)
+        self.d[Dr] += 1
+        if not deep:
+            self.steps_since_deep += 1
+            self._account(0, deep=False, plan_ms=plan_ms)
+            return 0, []
+        rb = readback.tolist()
+        vslots, vstarts, vT = vinfo
+        nv = len(vslots)
+        acc = np.array(rb[:nv], dtype=np.int64)
+        Y = rb[nv:nv + n_v_tok]
+        accepted = np.zeros(self.B, dtype=np.int64)
+        committed, done = 0, []
+        for j, i in enumerate(vslots):
+            a = int(acc[j])
+            accepted[i] = a
+            toks = Y[vstarts[j]:vstarts[j] + a + 1]
+            self.pos[i] += a + 1
+            self.d[i] = 0
+            committed += self._commit(i, toks)
+            if self.measuring and self.req[i].finish is None:
+                self.stats["drafted"] += int(d[i])
+                self.stats["accepted"] += a
+            if self.req[i].finish:
+                done.append(i)
+        self.sched.observe(V, accepted, d)
+        self.round_len = self.steps_since_deep
+        self.steps_since_deep = 0
+        self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms)
+        return committed, done
+
+    def _deep(self, V, d):
+        """Deep segment (inside the step's interval).  Returns the int64 readback
+        [accepted per verifier | committed/verified tokens], the verify token count and verifier info."""
+        m, k, L, Dm1 = self.m, self.k, self.L, self.Dm1
+        vb = [Block(int(i), int(self.pos[i]), int(d[i]) + 1, ("v", int(i))) for i in np.flatnonzero(V)]
+        pb = build_packed(m, vb, self.cfg.bucketing)
+        self._kv(pb, L - k)
+        nv, n = len(pb.blocks), pb.n_tokens
+        vslots = [b.tag[1] for b in pb.blocks]
+        vT = [b.T for b in pb.blocks]
+        vstarts = [int(o) for o in pb.offsets[:-1]]
+        slots_a = np.asarray(vslots, dtype=np.int64)
+        T_a = np.asarray(vT, dtype=np.int64)
+        src = np.repeat(slots_a * Dm1, T_a) + (np.arange(n) - np.repeat(pb.offsets[:-1], T_a))
+        if self.forced is not None:
+            forced = np.array([self.forced.draw(self.req[i].key) for i in vslots], dtype=np.int64)
+        else:
+            forced = np.full(nv, -1, dtype=np.int64)
+        src_t = upload(src, self.dev)
+        info = upload(np.concatenate([slots_a, np.asarray(vstarts, dtype=np.int64), T_a, forced]), self.dev,
+                      dtype=torch.int32)
+        slots_t, starts_t, T_t, forced_t = info[:nv], info[nv:2 * nv], info[2 * nv:3 * nv], info[3 * nv:4 * nv]
+        sb, exh = self._flat()
+        x = m.buffer("x_deep", (n, m.cfg.dim), m.dtype)
+        _lsk.copy_rows(x, None, exh, src_t, n)                                    # x = exit_h[i, 0..d_i]
+        hd = packed_layers(m, x, pb, k, L)
+        Yv = m.head_argmax(hd)
+        rb = torch.empty(nv + n, dtype=torch.long, device=self.dev)
+        _lsk.greedy_accept(Yv, sb, Dm1, slots_t, starts_t, T_t, forced_t, nv, rb[:nv], rb[nv:])
+        return rb.cpu(), n, (vslots, vstarts, vT)
+
+    def _kv(self, pb, n_layers: int) -> None:
+        if self.measuring:
+            self.stats["kv_read_pos"] += pb.kv_read_padded * n_layers
+            self.stats["kv_gathered_pos"] += pb.kv_gathered * n_layers
+
+    def _account(self, committed, deep, n_deep=0, verifiers=0, plan_ms=0.0, probe=False):
+        if not self.measuring:
+            return
+        st = self.stats
+        st["steps"] += 1
+        st["committed"] += committed
+        st["plan_ms"] += plan_ms
+        st["plan_calls"] += 1
+        if deep:
+            st["deep_steps"] += 1
+            st["deep_tokens"] += n_deep
+            st["verifiers"] += verifiers
+            st["probe_steps"] += int(probe)
+
+    # ------------------------------------------------------------------ drivers
+    def run(self, prompts: list, mode: str = "cyclic", warmup_samples: int = 8, warmup_per_slot: float = 1.0,
+            min_eval: int = 16, min_eval_per_slot: float = 2.0, max_eval: int = 256, converge_threshold: float = 0.01,
+            converge_window: int = 4, keep_outputs: bool = False, max_steps: Optional[int] = None) -> dict:
+        """ASPIRE cyclic replay or a static pass over the prompts (solutions/engine.py:544-623)."""
+        B, n_pool = self.B, len(prompts)
+        warmup_n = 0 if mode == "static" else max(warmup_samples, math.ceil(warmup_per_slot * B))
+        min_eval_n = max(min_eval, math.ceil(min_eval_per_slot * B))
+        max_eval_n = max(max_eval, min_eval_n)
+        self.measuring = warmup_n == 0
+        t_wall0 = self._wall_now() if self.measuring else None
+        cursor, total_done, evaluated, stable, anchor, stop_reason = 0, 0, 0, 0, None, None
+        completions, rec_measure_start, tok_measured = [], 0, 0
+
+        def make(p):
+            return Request(p.pid, list(p.tokens))
+
+        for slot in range(B):
+            if mode == "static" and cursor >= n_pool:
+                break
+            self.assign(slot, make(prompts[cursor % n_pool]))
+            cursor += 1
+        pre_done = [i for i in range(B) if self.req[i] is not None and self.req[i].finish]
+        steps = 0
+        while True:
+            if not pre_done and not ((self.state == DECODE) | (self.state == PREFILL)).any():
+                stop_reason = "pool_exhausted"
+                break
+            if pre_done:
+                committed, done = 0, pre_done
+                pre_done = []
+            else:
+                committed, done = self.step()
+                steps += 1
+            if self.measuring:
+                tok_measured += committed
+            queue = list(done)
+            while queue:
+                slot = queue.pop(0)
+                r = self.req[slot]
+                if r is None:
+                    continue
+                r.rec_finish = len(self.records) - 1
+                completions.append(self._completion(r, keep_outputs))
+                total_done += 1
+                self.state[slot] = FREE
+                self.req[slot] = None
+                if not self.measuring:
+                    if total_done >= warmup_n:
+                        self.measuring = True
+                        rec_measure_start = len(self.records)
+                        t_wall0 = self._wall_now()
+                elif mode == "cyclic":
+                    evaluated += 1
+                    if evaluated >= min_eval_n:
+                        thr = self._throughput(rec_measure_start, tok_measured)
+                        if anchor is None:
+                            anchor = thr
+                        elif abs(thr - anchor) / max(anchor, 1e-9) < converge_threshold:
+                            stable += 1
+                        else:
+                            stable, anchor = 0, thr
+                        if stable >= converge_window:
+                            stop_reason = "converged"
+                    if stop_reason is None and evaluated >= max_eval_n:
+                        stop_reason = "max_eval_samples"
+                if stop_reason is None and (mode == "cyclic" or cursor < n_pool):
+                    self.assign(slot, make(prompts[cursor % n_pool]))
+                    cursor += 1
+                    if self.req[slot].finish:
+                        queue.append(slot)
+            if stop_reason is not None:
+                break
+            if max_steps is not None and steps >= max_steps:
+                stop_reason = "max_steps"
+                break
+        if self.dev.type == "cuda":
+            torch.cuda.synchronize(self.dev)
+        wall_s = time.perf_counter() - t_wall0 if t_wall0 is not None else None
+        return self._result(completions, rec_measure_start, tok_measured, stop_reason, wall_s)
+
+    def run_poisson(self, prompts: list, rate_per_s: float, n_requests: int, warm_requests: int = 8, seed: int = 0,
+                    keep_outputs: bool = False) -> dict:
+        """Open loop: Poisson arrivals in wall-clock time, FIFO into free slots (solutions/engine.py:625-673)."""
+        rng = np.random.default_rng(seed)
+        queue, completions, cursor = [], [], 0
+        t0 = time.perf_counter()
+        next_arr = t0 + rng.exponential(1 / rate_per_s)
+        rec_measure_start, tok_measured = 0, 0
+        self.measuring = warm_requests == 0
+        total_done = 0
+        t_meas = t0
+        while total_done < n_requests + warm_requests:
+            now = time.perf_counter()
+            while next_arr <= now:
+                p = prompts[cursor % len(prompts)]
+                cursor += 1
+                queue.append(Request(p.pid, list(p.tokens), wall_arrival=next_arr))
+                next_arr += rng.exponential(1 / rate_per_s)
+            instant = []
+            for slot in np.flatnonzero(self.state == FREE):
+                if not queue:
+                    break
+                self.assign(int(slot), queue.pop(0))
+                if self.req[int(slot)].finish:
+                    instant.append(int(slot))
+            if not instant and not ((self.state == DECODE) | (self.state == PREFILL)).any():
+                time.sleep(max(0.0, min(next_arr - time.perf_counter(), 0.01)))
+                continue
+            committed, done = (0, instant) if instant else self.step()
+            if self.measuring:
+                tok_measured += committed
+            for slot in done:
+                r = self.req[slot]
+                r.rec_finish = len(self.records) - 1
+                completions.append(self._completion(r, keep_outputs))
+                total_done += 1
+                self.state[slot] = FREE
+                self.req[slot] = None
+                if not self.measuring and total_done >= warm_requests:
+                    self.measuring = True
+                    rec_measure_start = len(self.records)
+                    t_meas = self._wall_now()
+        if self.dev.type == "cuda":
+            torch.cuda.synchronize(self.dev)
+        res = self._result(completions, rec_measure_start, tok_measured, "n_requests", time.perf_counter() - t_meas)
+        res["metrics"]["poisson_rate_per_s"] = rate_per_s
+        res["metrics"]["queue_left"] = len(queue)
+        return res
+
+    # ------------------------------------------------------------------ results
+    def _throughput(self, start: int, tokens: int) -> float:
+        ms = sum(r.ms for r in self.records[start:] if r.kind != "prefill")
+        return tokens / (ms / 1000) if ms > 0 else 0.0
+
+    def _completion(self, r: Request, keep: bool) -> dict:
+        c = {"pid": r.pid, "prompt_len": len(r.prompt), "generated": len(r.out), "finish_reason": r.finish,
+             "measured": r.measured, "rec_assign": r.rec_assign, "rec_first": r.rec_first, "rec_finish": r.rec_finish,
+             "piggybacked": r.piggybacked, "wall_ttft_s": (r.wall_first - r.wall_arrival) if r.wall_arrival else None}
+        if keep:
+            c["tokens"] = list(r.out)
+        return c
+
+    def _wall_now(self) -> float:
+        if self.dev.type == "cuda":
+            torch.cuda.synchronize(self.dev)
+        return time.perf_counter()
+
+    def _result(self, completions, start, tokens, stop_reason, wall_s=None) -> dict:
+        """Metrics with the reference's names and definitions (solutions/engine.py:694-753)."""
+        recs = self.records
+        ms = np.array([r.ms for r in recs]) if recs else np.zeros(0)
+        cum = np.concatenate([[0.0], np.cumsum(ms)])
+        meas = np.array([r.measured for r in recs], dtype=bool)
+        kinds = np.array([r.kind for r in recs])
+        decode_ms = float(ms[meas & (kinds != "prefill")].sum()) if len(ms) else 0.0
+        prefill_ms = float(ms[meas & (kinds == "prefill")].sum()) if len(ms) else 0.0
+        ttft, tpot = [], []
+        for c in completions:
+            if not c["measured"] or c["rec_first"] < 0:
+                continue
+            ttft.append(cum[c["rec_first"] + 1] - cum[c["rec_assign"]])
+            if c["generated"] > 1 and c["rec_finish"] > c["rec_first"]:
+                seg = slice(c["rec_first"] + 1, c["rec_finish"] + 1)
+                tpot.append(ms[seg][kinds[seg] != "prefill"].sum() / (c["generated"] - 1))
+        st = dict(self.stats)
+        nsteps = max(st["steps"], 1)
+        piggy_ms = float(sum(r.ms for r in recs if r.measured and r.n_chunk and r.kind != "prefill"))
+        tot = decode_ms + prefill_ms
+        metrics = {
+            "config": self.cfg.label(), "B": self.B, "stop_reason": stop_reason,
+            "measured_tokens": tokens, "decode_ms": decode_ms, "prefill_ms": prefill_ms,
+            "throughput_tok_s": tokens / (decode_ms / 1000) if decode_ms else None,
+            "e2e_throughput_tok_s": tokens / (tot / 1000) if tot else None,
+            "wall_s": wall_s,
+            "wall_throughput_tok_s": tokens / wall_s if wall_s else None,
+            "host_overhead_share": (1 - tot / (1000 * wall_s)) if wall_s else None,
+            "prefill_time_share": prefill_ms / tot if tot else None,
+            "prefill_tokens_separate": st["prefill_tokens"], "prefill_tokens_piggyback": st["piggyback_tokens"],
+            "piggyback_share_of_prefill_tokens": st["piggyback_tokens"] / max(st["piggyback_tokens"]
+                                                                              + st["prefill_tokens"], 1),
+            "steps_with_piggyback_ms": piggy_ms,
+            "deep_steps_per_token": st["deep_steps"] / max(st["committed"], 1),
+            "deep_exec_fraction": st["deep_steps"] / nsteps,
+            "tokens_per_deep_step": st["deep_tokens"] / max(st["deep_steps"], 1),
+            "verifiers_per_deep_step": st["verifiers"] / max(st["deep_steps"], 1),
+            "acceptance_rate": st["accepted"] / max(st["drafted"], 1),
+            "plan_ms_per_step": st["plan_ms"] / max(st["plan_calls"], 1),
+            "ttft_ms_mean": float(np.mean(ttft)) if ttft else None,
+            "ttft_ms_p99": float(np.percentile(ttft, 99)) if ttft else None,
+            "tpot_ms_mean": float(np.mean(tpot)) if tpot else None,
+            "tpot_ms_p99": float(np.percentile(tpot, 99)) if tpot else None,
+            "k_final": self.k, "k_timeline": [(0, self.k)], "k_alpha": None,
+            "probe_steps": st["probe_steps"], "dropped_drafts_at_switch": st["dropped_drafts"],
+            "m3_fallbacks": st["m3_fallbacks"], "m3_fallback_reasons": dict(self.fallback_reasons),
+            "oracle_coverage": None,
+            "gamma_final": getattr(self.sched, "gamma", None) if self.sched is not None else None,
+            "kv_gather_share": st["kv_gathered_pos"] / max(st["kv_read_pos"], 1),
+            "kv_read_bytes": st["kv_read_pos"] * self.kv_bytes_per_pos,
+            "kv_gathered_bytes": st["kv_gathered_pos"] * self.kv_bytes_per_pos,
+            "separate_prefills": st["separate_prefills"],
+            "evaluated_completions": sum(1 for c in completions if c["measured"]),
+            "steps": st["steps"], "deep_steps": st["deep_steps"],
+        }
+        return {"metrics": metrics, "engine_config": asdict(self.cfg), "completions": completions}
