@@ -1,0 +1,333 @@
+"""Benchmark: packed self-speculative decoding of the Llama3-8B shape at B=32 on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W]
+
+Workload (one "step" = one EESD engine step over the 32-request batch: a packed shallow segment
+through layers [0, 8) + draft head, plus, when the scheduler verifies, a packed deep segment through
+[8, 32) + head + greedy acceptance):
+  Llama3-8B shape (32 layers, hidden 4096, 32 q / 8 kv heads, head_dim 128, FFN 14336, vocab 128256),
+  bf16 random init (seeded, generated on the GPU); B = 32 requests, prompt ids uniform over the vocab,
+  prompt lengths uniform in [128, 1024], up to 256 new tokens; exit layer 8; per-request draft length
+  chosen in [2, 8] by the latency-aware (aspire) policy; acceptance forced by a seeded geometric draw
+  (p = 0.3).  Prompts are prefilled before the timed region; weights, KV cache and metadata are in HBM.
+value = committed (generated) tokens over the K timed steps / wall time of those steps.
+
+Also measured: per-kernel-class HIP-event timing of a separate profiling pass (algorithmic bytes and
+flops per launch -> roofline fraction), the isolated verify-attention microbenchmark (256 requests,
+GQA 32/8, head_dim 128, lognormal contexts, 1-9 query rows each, KV append + rollback), and the CPU
+oracle replaying a bounded sample of the same steps on the host cores (cpu_baseline).
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = "generated tokens/s at 1 GPU (8B-shape, B=32); verify-attn HBM GB/s % of peak"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+# ----------------------------------------------------------------------------- main workload
+
+def build_engine(seed: int, max_new: int, B: int):
+    from thesis_amd.common.data import synthetic_prompts
+    from thesis_amd.common.model import PRESETS, LayerSkipLlama
+    from thesis_amd.solutions.cost_model import mi355x_cost_model
+    from thesis_amd.solutions.engine import EESDEngine, EngineConfig, Request
+
+    cfg = PRESETS["llama3-8b"]
+    model = LayerSkipLlama.random(cfg, seed=seed, dtype=torch.bfloat16, max_seq=2048)
+    prompts = synthetic_prompts(B, cfg.vocab_size, 128, 1024, seed=seed + 1)
+    ecfg = EngineConfig(sched="aspire", k=8, d_max=8, min_draft=2, initial_draft=3, forced_accept_p=0.3,
+                        forced_seed=seed)
+    eng = EESDEngine(model, B, 1024, max_new, (), ecfg, mi355x_cost_model(cfg))
+    for i, p in enumerate(prompts):
+        eng.assign(i, Request(p.pid, list(p.tokens)))
+    return cfg, model, eng, prompts
+
+
+def engine_step(eng) -> int:
+    """One step; finished requests leave the batch (no refill inside the measurement)."""
+    from thesis_amd.solutions.engine import FREE
+
+    committed, done = eng.step()
+    for s in done:
+        eng.state[s] = FREE
+        eng.req[s] = None
+    return committed
+
+
+def run_main(args):
+    from thesis_amd import _lsk
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    t0 = time.time()
+    cfg, model, eng, prompts = build_engine(args.seed, args.max_new, args.batch)
+    torch.cuda.synchronize()
+    log(f"[bench] model + prefill of {len(prompts)} prompts: {time.time() - t0:.1f}s")
+    eng.measuring = True
+    for _ in range(args.warmup):
+        engine_step(eng)
+    eng.trace = []
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    committed = 0
+    for _ in range(args.steps):
+        committed += engine_step(eng)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t1
+    trace = eng.trace
+    eng.trace = None
+    n_deep = sum(1 for s in trace if s["dp"])
+    log(f"[bench] {args.steps} steps ({n_deep} deep) in {elapsed * 1e3:.1f} ms: {committed} tokens "
+        f"-> {committed / elapsed:.1f} tok/s")
+
+    # ---- profiling pass: per-class kernel time with HIP events (separate from the timed steps)
+    prof = {}
+    if args.profile_steps > 0:
+        _lsk.Profiler.enable(True)
+        for _ in range(args.profile_steps):
+            if not (eng.state == 2).any():
+                break
+            engine_step(eng)
+        prof = _lsk.Profiler.collect()
+        _lsk.Profiler.enable(False)
+    return cfg, model, eng, committed, elapsed, trace, prof
+
+
+def summarize_kernels(prof: dict) -> dict:
+    out = {}
+    for name, p in prof.items():
+        ms = p["ms"]
+        gbs = p["bytes"] / (ms * 1e-3) / 1e9 if ms > 0 else 0.0
+        tfs = p["flops"] / (ms * 1e-3) / 1e12 if ms > 0 else 0.0
+        out[name] = {"launches": p["launches"], "total_ms": round(ms, 3),
+                     "avg_us": round(1e3 * ms / max(p["launches"], 1), 2),
+                     "bytes_per_launch": p["bytes"] / max(p["launches"], 1),
+                     "achieved_GBs": round(gbs, 1), "hbm_frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "achieved_TFLOPs": round(tfs, 2), "mfma_frac": round(tfs / BF16_PEAK_TFLOPS, 4)}
+    return out
+
+
+# ----------------------------------------------------------------------------- attention microbenchmark
+
+def attention_case(seed: int = 0, n_req: int = 256, median: float = 1500.0, sigma: float = 0.5):
+    """Verify-attention microbenchmark inputs: contexts lognormal(median, sigma) clipped to [64, 8192],
+    1..9 query rows per request, accepted = min(Geometric(0.35) - 1, T - 1)."""
+    rng = np.random.default_rng(seed)
+    ctx = np.clip(np.round(np.exp(np.log(median) + sigma * rng.standard_normal(n_req))), 64, 8192).astype(np.int64)
+    T = rng.integers(1, 10, size=n_req)
+    acc = np.minimum(rng.geometric(0.35, size=n_req) - 1, T - 1)
+    return ctx, T, acc
+
+
+def run_attention_bench(args):
+    from thesis_amd import _lsk
+
+    dev = torch.device("cuda:0")
+    Hq, Hkv, D = 32, 8, 128
+    ctx, T, acc = attention_case(args.seed)
+    B = len(ctx)
+    S = int(math.ceil((ctx + T).max() / 64) * 64)
+    N = int(T.sum())
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    kc = torch.empty(B, Hkv, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    vc = torch.empty_like(kc).normal_(generator=g)
+    q = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    k_new = torch.empty(N, Hkv, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    v_new = torch.empty_like(k_new).normal_(generator=g)
+    offs = np.concatenate([[0], np.cumsum(T)[:-1]])
+    blocks = np.stack([offs, ctx, T, np.arange(B)], axis=1).astype(np.int32)
+    works, groups, n_parts = _lsk.attn_plan(blocks, Hq // Hkv, _lsk.ATTN_SPLIT)
+    blk_d = torch.from_numpy(blocks).to(dev)
+    wk_d = torch.from_numpy(works).to(dev)
+    gr_d = torch.from_numpy(groups).to(dev) if len(groups) else None
+    ws = torch.empty(max(_lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=dev)
+    out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+    rows = torch.from_numpy(np.repeat(np.arange(B), T).astype(np.int32)).to(dev)
+    pos = torch.from_numpy((np.repeat(ctx, T) + (np.arange(N) - np.repeat(offs, T))).astype(np.int32)).to(dev)
+    slots = torch.arange(B, dtype=torch.int32, device=dev)
+    acc_d = torch.from_numpy(acc).to(dev)
+    kv_len = torch.from_numpy(ctx.copy()).to(dev)
+
+    def attn():
+        _lsk.ragged_attn(q, kc, vc, blk_d, wk_d, len(works), gr_d, len(groups), n_parts, out, Hq,
+                         1.0 / math.sqrt(D), ws)
+
+    def timed(fn, iters):
+        for _ in range(5):
+            fn()
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(iters)]
+        for e0, e1 in ev:
+            e0.record()
+            fn()
+            e1.record()
+        torch.cuda.synchronize()
+        return float(np.mean([e0.elapsed_time(e1) for e0, e1 in ev]))
+
+    t_attn = timed(attn, args.attn_iters)
+    t_append = timed(lambda: _lsk.kv_append(k_new, v_new, kc, vc, rows, pos), args.attn_iters)
+    t_rb = timed(lambda: _lsk.kv_rollback(kv_len, slots, acc_d, B), args.attn_iters)
+    kv_bytes = float((ctx + T).sum()) * Hkv * D * 2 * 2
+    qo_bytes = float(N) * Hq * D * 2 * 2
+    attn_bytes = kv_bytes + qo_bytes
+    attn_flops = 4.0 * Hq * D * float((T * ctx + T * (T + 1) // 2).sum())
+    app_bytes = 2.0 * 2 * N * Hkv * D * 2
+    res = {
+        "workload": "verify attention: 256 requests, GQA 32/8, head_dim 128, bf16 KV, lognormal contexts "
+                    "(median 1500, sigma 0.5, clip [64, 8192]), 1-9 query rows each",
+        "contexts": {"sum": int(ctx.sum()), "median": float(np.median(ctx)), "max": int(ctx.max())},
+        "query_rows": N, "work_items": int(len(works)), "split_positions": _lsk.ATTN_SPLIT,
+        "attn_us": round(1e3 * t_attn, 2), "attn_bytes": attn_bytes,
+        "attn_GBs": round(attn_bytes / (t_attn * 1e-3) / 1e9, 1),
+        "attn_hbm_frac": round(attn_bytes / (t_attn * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "attn_TFLOPs": round(attn_flops / (t_attn * 1e-3) / 1e12, 2),
+        "kv_append_us": round(1e3 * t_append, 2), "kv_append_GBs": round(app_bytes / (t_append * 1e-3) / 1e9, 1),
+        "rollback_us": round(1e3 * t_rb, 2), "rollback_bytes": int(B * 8),
+    }
+    # size-independent property at full size: a sample of requests against the fp64 brute force
+    if args.check_attn:
+        from oracle.model import brute_attention
+
+        got = out.float().cpu()
+        kh, vh, qh = kc.cpu(), vc.cpu(), q.cpu()
+        worst = 0.0
+        for r in (0, B // 2, B - 1):
+            sl = slice(int(offs[r]), int(offs[r] + T[r]))
+            ref = brute_attention(qh[sl], kh, vh, [r] * int(T[r]), list(range(ctx[r], ctx[r] + T[r])), Hq // Hkv)
+            worst = max(worst, float((got[sl].double() - ref).abs().max()))
+        res["check_max_abs_err_vs_fp64"] = worst
+    del kc, vc
+    torch.cuda.empty_cache()
+    return res
+
+
+# ----------------------------------------------------------------------------- CPU baseline
+
+def run_cpu_baseline(args, trace: list, k: int):
+    """The CPU oracle replays the GPU run's first timed steps (same segment shapes, bf16) on the host
+    cores until ~args.cpu_seconds have elapsed; tokens/s = tokens those steps committed / CPU time."""
+    from oracle.model import OBlock, OracleConfig, OracleLlama, build_packed, packed_layers
+    from thesis_amd.common.model import PRESETS
+
+    c = PRESETS["llama3-8b"]
+    ocfg = OracleConfig(c.vocab_size, c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate_size,
+                        c.norm_eps, c.rope_theta, c.max_position_embeddings)
+    threads = torch.get_num_threads()
+    t0 = time.time()
+    m = OracleLlama.synthetic(ocfg, dtype=torch.bfloat16, seed=args.seed, max_seq=2048)
+    m.allocate_cache(args.batch, 1024 + args.max_new + 8 + 40)
+    log(f"[bench] CPU oracle model ready in {time.time() - t0:.1f}s ({threads} threads)")
+    g = torch.Generator().manual_seed(0)
+    spent, tokens, steps, n_deep = 0.0, 0, 0, 0
+    with torch.inference_mode():
+        for st in trace:
+            ts = time.perf_counter()
+            pb = build_packed(m, [OBlock(*b) for b in st["sh"]])
+            x = m.embed(torch.randint(0, ocfg.vocab_size, (pb.n_tokens,), generator=g))
+            h = packed_layers(m, x, pb, 0, k)
+            if st["n_draft"]:
+                m.head(h[:st["n_draft"]]).argmax(-1)
+            if st["dp"]:
+                pbd = build_packed(m, [OBlock(*b) for b in st["dp"]])
+                xd = (torch.randn(pbd.n_tokens, ocfg.dim, generator=g) * 0.1).to(torch.bfloat16)
+                hd = packed_layers(m, xd, pbd, k, ocfg.n_layers)
+                m.head(hd).argmax(-1)
+                n_deep += 1
+            spent += time.perf_counter() - ts
+            tokens += st["committed"]
+            steps += 1
+            if spent >= args.cpu_seconds and tokens > 0:
+                break
+    del m
+    return {"value": round(tokens / spent, 2) if spent > 0 else None, "unit": "tokens/s", "cores": threads,
+            "kind": "port",
+            "sample": f"CPU oracle (torch-CPU restatement, bf16) replaying the first {steps} timed engine steps "
+                      f"({n_deep} deep) of this run with the same packed segment shapes; {tokens} committed "
+                      f"tokens in {spent:.1f}s"}
+
+
+# ----------------------------------------------------------------------------- main
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=300)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--max-new", type=int, default=256)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--profile-steps", type=int, default=40)
+    ap.add_argument("--attn-iters", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-attn", action="store_true")
+    ap.add_argument("--check-attn", action="store_true")
+    ap.add_argument("--out", type=str, default=None, help="also write the JSON line to this file")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only: this build has no multi-GPU path (requested --gpus {args.gpus}); "
+              "the packed forward shards by request, see DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a HIP device", file=sys.stderr)
+        sys.exit(2)
+
+    cfg, model, eng, committed, elapsed, trace, prof = run_main(args)
+    kernels = summarize_kernels(prof)
+    del model, eng
+    torch.cuda.empty_cache()
+    attn = None if args.no_attn else run_attention_bench(args)
+
+    # dominant kernel class of the decode step (largest total time in the profiling pass)
+    roofline = None
+    if kernels:
+        dom = max(kernels, key=lambda n: kernels[n]["total_ms"])
+        kd = kernels[dom]
+        bound = "hbm" if kd["hbm_frac"] >= kd["mfma_frac"] else "mfma"
+        ach = kd["achieved_GBs"] if bound == "hbm" else kd["achieved_TFLOPs"]
+        peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
+        roofline = {"kernel": dom, "bound": bound, "achieved": ach, "peak": peak,
+                    "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(ach / peak, 4),
+                    "traffic": None, "avg_launch_us": kd["avg_us"], "bytes_per_launch": kd["bytes_per_launch"]}
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
+
+    line = {
+        "metric": METRIC, "value": round(committed / elapsed, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(1e3 * elapsed / args.steps, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "llama3-8b-shape packed self-speculative decode (EESD)", "B": args.batch,
+                   "prompt_len": [128, 1024], "max_new": args.max_new, "exit_layer": 8, "draft_len": [2, 8],
+                   "scheduler": "aspire (latency-aware)", "acceptance": "forced geometric p=0.3",
+                   "weights": "random init bf16", "parallelism": "single GPU"},
+        "roofline": roofline, "cpu_baseline": cpu, "verify_attn": attn, "kernels": kernels,
+        "steps_detail": {"committed_tokens": committed, "deep_steps": sum(1 for s in trace if s["dp"]),
+                         "mean_shallow_rows": float(np.mean([len(s["sh"]) for s in trace])) if trace else None,
+                         "mean_deep_rows": float(np.mean([sum(b[2] for b in s["dp"]) for s in trace if s["dp"]]))
+                         if any(s["dp"] for s in trace) else None},
+    }
+    txt = json.dumps(line)
+    print(txt, flush=True)
+    if args.out:
+        Path(args.out).write_text(txt + "\n")
+
+
+if __name__ == "__main__":
+    main()

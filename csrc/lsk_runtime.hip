@@ -42,6 +42,28 @@ Model* get(long h) {
 
 size_t elem_size(int dtype) { return dtype == LSK_DTYPE_BF16 ? 2 : 4; }
 
+// ---- optional per-launch profiling: a pair of HIP events around each launch, tagged with its kernel
+// class and ALGORITHMIC bytes / flops (the figures a roofline is computed from), summed at collect time.
+struct ProfRec {
+  int cls;
+  double bytes, flops;
+  hipEvent_t e0, e1;
+};
+std::vector<ProfRec> g_prof;
+std::vector<hipEvent_t> g_event_pool;
+bool g_prof_on = false;
+
+hipEvent_t pool_event() {
+  if (!g_event_pool.empty()) {
+    hipEvent_t e = g_event_pool.back();
+    g_event_pool.pop_back();
+    return e;
+  }
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return nullptr;
+  return e;
+}
+
 struct Layout {
   size_t xn, qkv, q, attn, h, part, total;
 };
@@ -67,6 +89,45 @@ Layout layout(const Model& m, int N, int n_parts) {
 }
 
 }  // namespace
+
+extern "C" int lsk_prof_enable(int on) {
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_prof_on = on != 0;
+  return 0;
+}
+
+extern "C" int lsk_prof_start(int cls, double bytes, double flops, void* stream) {
+  if (!g_prof_on) return 0;
+  ProfRec r{cls, bytes, flops, pool_event(), pool_event()};
+  LSK_REQUIRE(r.e0 && r.e1, LSK_EARG, "lsk_prof_start: event creation failed");
+  (void)hipEventRecord(r.e0, (hipStream_t)stream);
+  g_prof.push_back(r);
+  return 0;
+}
+
+extern "C" int lsk_prof_stop(void* stream) {
+  if (!g_prof_on || g_prof.empty()) return 0;
+  (void)hipEventRecord(g_prof.back().e1, (hipStream_t)stream);
+  return 0;
+}
+
+// Sums per class c < n_classes: ms[c], bytes[c], flops[c], count[c]; synchronises; clears the records.
+extern "C" int lsk_prof_collect(int n_classes, double* ms, double* bytes, double* flops, long* count) {
+  for (int c = 0; c < n_classes; ++c) { ms[c] = bytes[c] = flops[c] = 0.0; count[c] = 0; }
+  for (auto& r : g_prof) {
+    hipError_t e = hipEventSynchronize(r.e1);
+    if (e != hipSuccess) { lsk_set_error("lsk_prof_collect: %s", hipGetErrorString(e)); return (int)e; }
+    float t = 0.f;
+    (void)hipEventElapsedTime(&t, r.e0, r.e1);
+    if (r.cls >= 0 && r.cls < n_classes) {
+      ms[r.cls] += t; bytes[r.cls] += r.bytes; flops[r.cls] += r.flops; count[r.cls] += 1;
+    }
+    g_event_pool.push_back(r.e0);
+    g_event_pool.push_back(r.e1);
+  }
+  g_prof.clear();
+  return 0;
+}
 
 extern "C" long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, int n_kv_heads, int head_dim, int ffn,
                                  int vocab, float eps, const void* const* wqkv, const void* const* wo,
@@ -113,7 +174,8 @@ extern "C" size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_p
 // layer i (the hidden state entering exit layer i + 1; solutions/packed.py:190-195).
 extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
                                   const int32_t* meta, int nb, int n_works, int n_groups, int n_parts,
-                                  void* workspace, size_t ws_bytes, void* const* capture, void* stream) {
+                                  void* workspace, size_t ws_bytes, void* const* capture, double attn_bytes,
+                                  double attn_flops, void* stream) {
   Model* m = get(handle);
   LSK_REQUIRE(m != nullptr, LSK_EARG, "lsk_forward_layers: bad handle %ld", handle);
   LSK_REQUIRE(0 <= start && start <= end && end <= m->n_layers, LSK_ESHAPE, "lsk_forward_layers: bad range [%d, %d)",
@@ -148,23 +210,42 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
   const int qd = m->n_heads * m->head_dim, kvd = m->n_kv_heads * m->head_dim;
   const float scale = (float)(1.0 / sqrt((double)m->head_dim));
   int rc;
+  const double es_d = (double)es, Nd = N, dimd = m->dim, qkvd = qd + 2 * kvd, ffd = m->ffn;
+  const double norm_bytes = es_d * (2.0 * Nd * dimd + dimd);
+  auto gemm_bytes = [&](double M_, double Nw, double K_, double Nout, bool res) {
+    return es_d * (K_ * Nw + M_ * K_ + M_ * Nout * (res ? 2.0 : 1.0));
+  };
+#define LSK_PROF(cls, b, f, call)                                \
+  do {                                                           \
+    lsk_prof_start((cls), (b), (f), stream);                     \
+    if ((rc = (call))) return rc;                                \
+    lsk_prof_stop(stream);                                       \
+  } while (0)
   for (int i = start; i < end; ++i) {
     const void* xi = (i == start) ? x_in : x_out;
-    if ((rc = lsk_rmsnorm(m->dtype, xi, m->attn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream))) return rc;
-    if ((rc = lsk_gemm(m->dtype, xn, m->dim, m->wqkv[i], m->dim, qkv, qd + 2 * kvd, nullptr, 0, N, qd + 2 * kvd,
-                       m->dim, LSK_EPI_NONE, 0, stream))) return rc;
-    if ((rc = lsk_rope_append(m->dtype, qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab, m->tab_len, rows, pos, N,
-                              m->n_heads, m->n_kv_heads, m->head_dim, m->max_batch, m->max_seq, stream))) return rc;
-    if ((rc = lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts,
-                              attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes,
-                              stream))) return rc;
-    if ((rc = lsk_gemm(m->dtype, attn, qd, m->wo[i], qd, x_out, m->dim, xi, m->dim, N, m->dim, qd, LSK_EPI_RESIDUAL, 0,
-                       stream))) return rc;
-    if ((rc = lsk_rmsnorm(m->dtype, x_out, m->ffn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream))) return rc;
-    if ((rc = lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
-                       LSK_EPI_SILU_MUL, m->ffn, stream))) return rc;
-    if ((rc = lsk_gemm(m->dtype, h, m->ffn, m->w2[i], m->ffn, x_out, m->dim, x_out, m->dim, N, m->dim, m->ffn,
-                       LSK_EPI_RESIDUAL, 0, stream))) return rc;
+    LSK_PROF(LSK_PROF_NORM, norm_bytes, 4.0 * Nd * dimd,
+             lsk_rmsnorm(m->dtype, xi, m->attn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream));
+    LSK_PROF(LSK_PROF_GEMM_QKV, gemm_bytes(Nd, qkvd, dimd, qkvd, false), 2.0 * Nd * dimd * qkvd,
+             lsk_gemm(m->dtype, xn, m->dim, m->wqkv[i], m->dim, qkv, qd + 2 * kvd, nullptr, 0, N, qd + 2 * kvd, m->dim,
+                      LSK_EPI_NONE, 0, stream));
+    LSK_PROF(LSK_PROF_ROPE, es_d * 2.0 * Nd * qkvd, 6.0 * Nd * (qd + kvd),
+             lsk_rope_append(m->dtype, qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab, m->tab_len, rows, pos, N,
+                             m->n_heads, m->n_kv_heads, m->head_dim, m->max_batch, m->max_seq, stream));
+    LSK_PROF(LSK_PROF_ATTN, attn_bytes, attn_flops,
+             lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts, attn,
+                             m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes, stream));
+    LSK_PROF(LSK_PROF_GEMM_O, gemm_bytes(Nd, dimd, qd, dimd, true), 2.0 * Nd * qd * dimd,
+             lsk_gemm(m->dtype, attn, qd, m->wo[i], qd, x_out, m->dim, xi, m->dim, N, m->dim, qd, LSK_EPI_RESIDUAL, 0,
+                      stream));
+    LSK_PROF(LSK_PROF_NORM, norm_bytes, 4.0 * Nd * dimd,
+             lsk_rmsnorm(m->dtype, x_out, m->ffn_norm[i], xn, N, m->dim, m->eps, m->dim, m->dim, stream));
+    LSK_PROF(LSK_PROF_GEMM_W13, gemm_bytes(Nd, 2.0 * ffd, dimd, ffd, false), 4.0 * Nd * dimd * ffd,
+             lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
+                      LSK_EPI_SILU_MUL, m->ffn, stream));
+    LSK_PROF(LSK_PROF_GEMM_W2, gemm_bytes(Nd, dimd, ffd, dimd, true), 2.0 * Nd * ffd * dimd,
+             lsk_gemm(m->dtype, h, m->ffn, m->w2[i], m->ffn, x_out, m->dim, x_out, m->dim, N, m->dim, m->ffn,
+                      LSK_EPI_RESIDUAL, 0, stream));
+#undef LSK_PROF
     if (capture && capture[i]) {
       hipError_t e = hipMemcpyAsync(capture[i], x_out, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
       if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }

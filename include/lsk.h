@@ -130,7 +130,28 @@ size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts);
  * (solutions/packed.py:190-195).  Replaces packed_layers (solutions/packed.py:188-196). */
 int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
                        const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, void* workspace,
-                       size_t ws_bytes, void* const* capture, void* stream);
+                       size_t ws_bytes, void* const* capture, double attn_bytes, double attn_flops, void* stream);
+
+/* ---- optional per-launch profiling (no reference counterpart: measurement support) ----
+ * When enabled, the layer runner (and callers using lsk_prof_start/stop around their own launches)
+ * bracket each launch with HIP events on its stream, tagged with a class and the launch's algorithmic
+ * bytes / flops.  lsk_prof_collect synchronises and returns per-class sums.  attn_bytes / attn_flops of
+ * lsk_forward_layers are the per-layer algorithmic figures of the attention launch (profiling only). */
+#define LSK_PROF_NORM 0
+#define LSK_PROF_GEMM_QKV 1
+#define LSK_PROF_ROPE 2
+#define LSK_PROF_ATTN 3
+#define LSK_PROF_GEMM_O 4
+#define LSK_PROF_GEMM_W13 5
+#define LSK_PROF_GEMM_W2 6
+#define LSK_PROF_GEMM_HEAD 7
+#define LSK_PROF_ARGMAX 8
+#define LSK_PROF_GLUE 9
+#define LSK_PROF_CLASSES 10
+int lsk_prof_enable(int on);
+int lsk_prof_start(int cls, double bytes, double flops, void* stream);
+int lsk_prof_stop(void* stream);
+int lsk_prof_collect(int n_classes, double* ms, double* bytes, double* flops, long* count);
 
 #ifdef __cplusplus
 }

@@ -199,6 +199,41 @@ class OracleLlama:
         self.rope_cos, self.rope_sin = rope_tables(cfg, max_seq)
         self.cache: Optional[OracleCache] = None
 
+    @classmethod
+    def synthetic(cls, cfg: OracleConfig, dtype=torch.bfloat16, seed: int = 0, std: float = 0.02,
+                  max_seq: int = 2048, pool_elems: int = 1 << 26) -> "OracleLlama":
+        """Full-size model for CPU timing: every weight matrix is its own allocation, filled from one
+        seeded N(0, std) pool at random offsets (drawing 8e9 fresh normals on the CPU would take minutes;
+        the cost of the forward does not depend on the values)."""
+        g = torch.Generator().manual_seed(seed)
+        pool = (torch.randn(pool_elems, generator=g) * std).to(dtype)
+        offs = iter(torch.randint(0, pool_elems, (1 << 16,), generator=g).tolist())
+
+        def fill(r, c):
+            t = torch.empty(r * c, dtype=dtype)
+            pos, o = 0, next(offs)
+            while pos < t.numel():
+                n = min(t.numel() - pos, pool_elems - o)
+                t[pos:pos + n] = pool[o:o + n]
+                pos, o = pos + n, 0
+            return t.view(r, c)
+
+        self = cls.__new__(cls)
+        self.cfg, self.dtype, self.device = cfg, dtype, torch.device("cpu")
+        self.group = cfg.n_heads // cfg.n_kv_heads
+        self.q_size = cfg.n_heads * cfg.head_dim
+        self.kv_size = cfg.n_kv_heads * cfg.head_dim
+        ones = torch.ones(cfg.dim, dtype=dtype)
+        self.layers = [OracleLayer(fill(self.q_size + 2 * self.kv_size, cfg.dim), fill(cfg.dim, self.q_size),
+                                   fill(2 * cfg.intermediate_size, cfg.dim), fill(cfg.dim, cfg.intermediate_size),
+                                   ones, ones) for _ in range(cfg.n_layers)]
+        self.embed_w = fill(cfg.vocab_size, cfg.dim)
+        self.norm_w = ones
+        self.lm_head_w = self.embed_w if cfg.tie_word_embeddings else fill(cfg.vocab_size, cfg.dim)
+        self.rope_cos, self.rope_sin = rope_tables(cfg, max_seq)
+        self.cache = None
+        return self
+
     @property
     def n_layers(self) -> int:
         return self.cfg.n_layers

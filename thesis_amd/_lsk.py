@@ -44,8 +44,15 @@ _SIGS = {
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
     "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
-    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _Z, _P, _P]),
+    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _Z, _P, ctypes.c_double,
+                                ctypes.c_double, _P]),
+    "lsk_prof_enable": (_I, [_I]),
+    "lsk_prof_start": (_I, [_I, ctypes.c_double, ctypes.c_double, _P]),
+    "lsk_prof_stop": (_I, [_P]),
+    "lsk_prof_collect": (_I, [_I, _P, _P, _P, _P]),
 }
+PROF_CLASSES = ("rmsnorm", "gemm_qkv", "rope_append", "attention", "gemm_o", "gemm_w13", "gemm_w2", "gemm_lm_head",
+                "argmax", "glue")
 EXPORTS = tuple(_SIGS)
 
 _lib = None
@@ -259,12 +266,13 @@ class NativeModel:
         return int(load().lsk_segment_workspace_bytes(self.handle, n_tokens, n_parts))
 
     def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, workspace,
-                       capture_ptrs=None):
+                       capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
         _dev(x_in, x_out, meta_dev, workspace)
         cap = _ptr_array(capture_ptrs) if capture_ptrs is not None else None
         ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
         _check(load().lsk_forward_layers(self.handle, _ptr(x_in), _ptr(x_out), n_tokens, start, end, _ptr(meta_dev),
-                                         nb, n_works, n_groups, n_parts, _ptr(workspace), ws_bytes, cap, _stream()),
+                                         nb, n_works, n_groups, n_parts, _ptr(workspace), ws_bytes, cap,
+                                         float(attn_bytes), float(attn_flops), _stream()),
                "lsk_forward_layers")
 
     def __del__(self):
@@ -273,3 +281,35 @@ class NativeModel:
                 _lib.lsk_model_destroy(self.handle)
         except Exception:
             pass
+
+
+# ----------------------------------------------------------------------------- profiling
+
+class Profiler:
+    """Per-class HIP-event timing of liblsk launches (algorithmic bytes / flops per launch)."""
+
+    enabled = False
+
+    @classmethod
+    def enable(cls, on: bool = True) -> None:
+        load().lsk_prof_enable(1 if on else 0)
+        cls.enabled = on
+
+    @staticmethod
+    def start(cls_idx: int, nbytes: float, flops: float) -> None:
+        if Profiler.enabled:
+            load().lsk_prof_start(cls_idx, float(nbytes), float(flops), _stream())
+
+    @staticmethod
+    def stop() -> None:
+        if Profiler.enabled:
+            load().lsk_prof_stop(_stream())
+
+    @staticmethod
+    def collect() -> dict:
+        n = len(PROF_CLASSES)
+        ms, by, fl, ct = (np.zeros(n), np.zeros(n), np.zeros(n), np.zeros(n, dtype=np.int64))
+        _check(load().lsk_prof_collect(n, ms.ctypes.data, by.ctypes.data, fl.ctypes.data, ct.ctypes.data),
+               "lsk_prof_collect")
+        return {PROF_CLASSES[i]: {"ms": float(ms[i]), "bytes": float(by[i]), "flops": float(fl[i]),
+                                  "launches": int(ct[i])} for i in range(n) if ct[i]}

@@ -333,11 +333,19 @@ class LayerSkipLlama:
             out = torch.empty(n, dtype=torch.long, device=self.device)
         if n == 0:
             return out
-        xn = self.buffer("head_xn", (n, self.cfg.dim), self.dtype)
+        es, dim, V = self.dtype.itemsize, self.cfg.dim, self.cfg.vocab_size
+        xn = self.buffer("head_xn", (n, dim), self.dtype)
+        P = _lsk.Profiler
+        P.start(0, es * (2.0 * n * dim + dim), 4.0 * n * dim)
         _lsk.rmsnorm(x, self.norm_w, self.cfg.norm_eps, out=xn)
-        logits = self.buffer("head_logits", (n, self.cfg.vocab_size), self.dtype)
+        P.stop()
+        logits = self.buffer("head_logits", (n, V), self.dtype)
+        P.start(7, es * (float(V) * dim + n * dim + n * V), 2.0 * n * dim * V)
         _lsk.gemm(xn, self.lm_head_w, out=logits)
+        P.stop()
+        P.start(8, es * float(n) * V, float(n) * V)
         _lsk.argmax(logits, out, dst_idx)
+        P.stop()
         return out
 
     # ---------------------------------------------------------------- padded path (DecodeEngine)

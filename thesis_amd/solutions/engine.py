@@ -166,6 +166,7 @@ class EESDEngine:
         self.round_len = cfg.gamma
         self.kv_bytes_per_pos = 2 * model.cfg.n_kv_heads * model.cfg.head_dim * model.dtype.itemsize
         self.fallback_reasons: dict = {}
+        self.trace: Optional[list] = None     # set to [] to log every step's segment shapes
 
     # ------------------------------------------------------------------ helpers
     def _rec(self, kind, iv, **kw) -> Rec:
@@ -325,6 +326,10 @@ class EESDEngine:
         iv.stop()
         self._rec("deep" if deep else "shallow", iv, n_sh=N, n_dp=n_v_tok, plan_ms=plan_ms)
         self.d[Dr] += 1
+        if self.trace is not None:
+            self.trace.append({"sh": [(b.row, b.pos0, b.T) for b in pb.blocks], "n_draft": nd,
+                               "dp": [(int(i), int(self.pos[i]), int(d[i]) + 1) for i in np.flatnonzero(V)],
+                               "committed": 0})
         if not deep:
             self.steps_since_deep += 1
             self._account(0, deep=False, plan_ms=plan_ms)
@@ -349,6 +354,8 @@ class EESDEngine:
             if self.req[i].finish:
                 done.append(i)
         self.sched.observe(V, accepted, d)
+        if self.trace is not None:
+            self.trace[-1]["committed"] = committed
         self.round_len = self.steps_since_deep
         self.steps_since_deep = 0
         self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms)

@@ -80,6 +80,8 @@ class PackedBatch:
     n_works: int = 0
     n_groups: int = 0
     n_parts: int = 0
+    attn_bytes: float = 0.0
+    attn_flops: float = 0.0
     _model: object = None
 
     def block_slice(self, i: int) -> slice:
@@ -136,6 +138,12 @@ def pack_blocks(model, ordered: list, groups: Optional[list] = None, bucketing: 
                            grps.ravel()]).astype(np.int32)
     pb = PackedBatch(list(ordered), offsets, pos_h, rows_h, n_tokens=N, nb=nb, n_works=len(works),
                      n_groups=len(grps), n_parts=n_parts, _model=model)
+    # algorithmic work of one attention launch (per layer): K+V of every attended position read once per
+    # (block, KV head), Q read and O written once; flops = 4 Hq D per (query, attended position)
+    c = model.cfg
+    es = model.dtype.itemsize
+    pb.attn_bytes = float((pos0 + Ts).sum()) * c.n_kv_heads * c.head_dim * 2 * es + N * c.n_heads * c.head_dim * 2 * es
+    pb.attn_flops = 4.0 * c.n_heads * c.head_dim * float((Ts * pos0 + Ts * (Ts + 1) // 2).sum())
     pb.meta = upload(meta, model.device, dtype=torch.int32) if N else None
     # ---- reference bucket bookkeeping (solutions/packed.py:109-138), host only
     if groups is None:
@@ -207,7 +215,7 @@ def packed_layers(model, x: torch.Tensor, pb: PackedBatch, start: int, end: int,
                     cap_ptrs[k - 1] = t.data_ptr()
     ws = model.workspace(model.native.workspace_bytes(N, pb.n_parts))
     model.native.forward_layers(x, out, N, start, end, pb.meta, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, ws,
-                                cap_ptrs)
+                                cap_ptrs, pb.attn_bytes, pb.attn_flops)
     return out
 
 
