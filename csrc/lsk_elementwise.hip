@@ -43,56 +43,139 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
-// ----------------------------------------------------------------------------- RMSNorm
-// out = w * (x * rsqrt(mean(x^2) + eps)).to(dtype)        (common/model.py:153-156)
-// One 256-thread workgroup per row.  The sum of squares is accumulated per thread over a
-// fixed stride, reduced per wave by an xor tree and across the four waves in index order,
-// so a row's result never depends on the other rows of the call.
+// ----------------------------------------------------------------------------- RMSNorm (+ residual add)
+// x_new = rnd(x + rnd(sum_s P[s]))   (x + F.linear(...) with the GEMM's K-slice partials, s in order;
+//                                     KS = 0: x_new = x)
+// out   = w * (x_new * rsqrt(mean(x_new^2) + eps)).to(dtype)      (common/model.py:153-156)
+// One 256-thread workgroup per row, 8 consecutive elements per thread per pass (16-byte loads).  The sum
+// of squares is accumulated per thread in element order, reduced per wave by an xor tree and across the
+// four waves in index order, so a row's result never depends on the other rows of the call.
 template <typename T>
-__global__ __launch_bounds__(256) void rmsnorm_kernel(const T* __restrict__ x, const T* __restrict__ w,
-                                                      T* __restrict__ out, int dim, float eps, long ldx,
-                                                      long ldo) {
-  const int row = blockIdx.x;
-  const T* xr = x + (long)row * ldx;
-  T* orow = out + (long)row * ldo;
-  float ss = 0.f;
-  for (int j = threadIdx.x; j < dim; j += 256) {
-    float v = Elem<T>::ld(xr + j);
-    ss += v * v;
+struct Vec8;
+template <>
+struct Vec8<uint16_t> {
+  static __device__ __forceinline__ void ld(const uint16_t* p, float* v) {
+    const uint4 u = *(const uint4*)p;
+    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(w[i] << 16);
+      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+    }
   }
+  static __device__ __forceinline__ void st(uint16_t* p, const float* v) {
+    uint4 u;
+    u.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+    u.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+    u.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
+    u.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
+    *(uint4*)p = u;
+  }
+};
+template <>
+struct Vec8<float> {
+  static __device__ __forceinline__ void ld(const float* p, float* v) {
+    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  static __device__ __forceinline__ void st(float* p, const float* v) {
+    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
+    *(float4*)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  }
+};
+
+#define NORM_MAX_PASSES 4  // dim <= 4 * 256 * 8 = 8192
+
+template <typename T>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ x, long ldx, const float* __restrict__ P,
+                                                          int KS, long pstride, const T* __restrict__ w,
+                                                          T* __restrict__ x_out, long ldxo, T* __restrict__ out,
+                                                          long ldo, int dim, float eps) {
+  const int row = blockIdx.x;
+  const int tid = threadIdx.x;
+  float v[NORM_MAX_PASSES][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int p = 0; p < NORM_MAX_PASSES; ++p) {
+    const int j = (p * 256 + tid) * 8;
+    if (j < dim) {
+      Vec8<T>::ld(x + (long)row * ldx + j, v[p]);
+      if (KS > 0) {
+        float acc[8];
+        const float* pr = P + (long)row * dim + j;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = pr[i];
+        for (int s2 = 1; s2 < KS; ++s2)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pr[s2 * pstride + i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[p][i] = Elem<T>::round(v[p][i] + Elem<T>::round(acc[i]));
+        if (x_out != nullptr) Vec8<T>::st(x_out + (long)row * ldxo + j, v[p]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ss += v[p][i] * v[p][i];
+    }
+  }
+  if (out == nullptr) return;
   ss = wave_sum(ss);
   __shared__ float red[4];
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) red[wave] = ss;
+  const int wave = tid >> 6;
+  if ((tid & 63) == 0) red[wave] = ss;
   __syncthreads();
   const float tot = ((red[0] + red[1]) + red[2]) + red[3];
   const float mean = tot / (float)dim;
   const float r = 1.0f / sqrtf(mean + eps);
-  for (int j = threadIdx.x; j < dim; j += 256) {
-    float n = Elem<T>::round(Elem<T>::ld(xr + j) * r);
-    Elem<T>::st(orow + j, Elem<T>::ld(w + j) * n);
+#pragma unroll
+  for (int p = 0; p < NORM_MAX_PASSES; ++p) {
+    const int j = (p * 256 + tid) * 8;
+    if (j < dim) {
+      float wv[8], o[8];
+      Vec8<T>::ld(w + j, wv);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = wv[i] * Elem<T>::round(v[p][i] * r);
+      Vec8<T>::st(out + (long)row * ldo + j, o);
+    }
   }
+}
+
+template <typename T>
+static void launch_add_rmsnorm(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
+                               void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim, float eps,
+                               hipStream_t s) {
+  add_rmsnorm_kernel<T><<<n_rows, 256, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w, (T*)x_out, ldxo,
+                                               (T*)out, ldo, dim, eps);
+}
+
+extern "C" int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w,
+                               float eps, void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim,
+                               void* stream) {
+  LSK_REQUIRE(x != nullptr && (ks == 0 || partials != nullptr) && (out == nullptr || w != nullptr), LSK_EARG,
+              "lsk_add_rmsnorm: null pointer");
+  LSK_REQUIRE(n_rows >= 0 && dim > 0 && dim % 8 == 0 && dim <= NORM_MAX_PASSES * 256 * 8 && ldx >= dim && ks >= 0 &&
+                  ldx % 8 == 0 && (out == nullptr || (ldo >= dim && ldo % 8 == 0)) &&
+                  (x_out == nullptr || (ldxo >= dim && ldxo % 8 == 0)),
+              LSK_ESHAPE, "lsk_add_rmsnorm: bad shape n_rows=%d dim=%d", n_rows, dim);
+  if (n_rows == 0) return 0;
+  const long pstride = (long)n_rows * dim;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == LSK_DTYPE_BF16)
+    launch_add_rmsnorm<uint16_t>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, n_rows, dim, eps, s);
+  else if (dtype == LSK_DTYPE_F32)
+    launch_add_rmsnorm<float>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, n_rows, dim, eps, s);
+  else
+    LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_add_rmsnorm: dtype %d", dtype);
+  return lsk_check_launch("lsk_add_rmsnorm");
 }
 
 extern "C" int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, int n_rows, int dim, float eps,
                            long ldx, long ldo, void* stream) {
   LSK_REQUIRE(x && w && out, LSK_EARG, "lsk_rmsnorm: null pointer");
-  LSK_REQUIRE(n_rows >= 0 && dim > 0 && ldx >= dim && ldo >= dim, LSK_ESHAPE,
-              "lsk_rmsnorm: bad shape n_rows=%d dim=%d ldx=%ld ldo=%ld", n_rows, dim, ldx, ldo);
-  if (n_rows == 0) return 0;
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == LSK_DTYPE_BF16)
-    rmsnorm_kernel<uint16_t><<<n_rows, 256, 0, s>>>((const uint16_t*)x, (const uint16_t*)w, (uint16_t*)out, dim,
-                                                    eps, ldx, ldo);
-  else if (dtype == LSK_DTYPE_F32)
-    rmsnorm_kernel<float><<<n_rows, 256, 0, s>>>((const float*)x, (const float*)w, (float*)out, dim, eps, ldx, ldo);
-  else
-    LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_rmsnorm: dtype %d", dtype);
-  return lsk_check_launch("lsk_rmsnorm");
+  return lsk_add_rmsnorm(dtype, x, ldx, nullptr, 0, w, eps, nullptr, 0, out, ldo, n_rows, dim, stream);
 }
 
 // ----------------------------------------------------------------------------- RoPE + KV append
-// qkv [N, (Hq + 2 Hkv) D] = [q | k | v] per token (solutions/packed.py:175-176).
+// qkv [N, (Hq + 2 Hkv) D] = [q | k | v] per token (solutions/packed.py:175-176); from_p: the values are
+// rnd(sum_s P[s][t][:]) (the QKV GEMM's K-slice partials, s in order) instead of a materialised qkv.
 // q heads:  q_out[t, h]                       = rope(q)   (common/model.py:148-150)
 // k heads:  kcache[row_t, h, pos_t]           = rope(k)   (solutions/packed.py:180)
 // v heads:  vcache[row_t, h, pos_t]           = v         (solutions/packed.py:181)
@@ -100,73 +183,100 @@ extern "C" int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, i
 // rope(x)[j + D/2] = x[j+D/2] * c[j+D/2] + x[j] * s[j+D/2]
 // with c, s = the fp32 tables at pos_t stored to the model dtype first (solutions/packed.py:106-107)
 // and one dtype rounding after each multiply and after the add.
+// Grid: (token, head); a thread owns one rotation pair (j, j + D/2) or, for v heads, two elements.
 template <typename T>
-__global__ __launch_bounds__(256) void rope_append_kernel(const T* __restrict__ qkv, T* __restrict__ q_out,
-                                                          T* __restrict__ kc, T* __restrict__ vc,
-                                                          const float* __restrict__ cos_tab,
-                                                          const float* __restrict__ sin_tab,
-                                                          const int32_t* __restrict__ rows,
-                                                          const int32_t* __restrict__ pos, int Hq, int Hkv, int D,
-                                                          int max_batch, int max_seq, int tab_len) {
-  const int t = blockIdx.x;
+__device__ __forceinline__ float qkv_val(const T* qkv, const float* P, int KS, long pstride, long idx) {
+  if (P == nullptr) return Elem<T>::ld(qkv + idx);
+  float a = P[idx];
+  for (int s = 1; s < KS; ++s) a = a + P[s * pstride + idx];
+  return Elem<T>::round(a);
+}
+
+template <typename T>
+__global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __restrict__ P, int KS, long pstride,
+                                   T* __restrict__ q_out, T* __restrict__ kc, T* __restrict__ vc,
+                                   const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
+                                   const int32_t* __restrict__ rows, const int32_t* __restrict__ pos, int Hq, int Hkv,
+                                   int D, int max_batch, int max_seq, int tab_len) {
+  const int t = blockIdx.x, h = blockIdx.y;
   const int row = rows[t], p = pos[t];
   if (row < 0 || row >= max_batch || p < 0 || p >= max_seq || p >= tab_len) return;  // host validates too
   const int half = D >> 1;
-  const int width = (Hq + 2 * Hkv) * D;
-  const T* src = qkv + (long)t * width;
-  const float* ct = cos_tab + (long)p * D;
-  const float* st = sin_tab + (long)p * D;
-  // rotated heads: Hq + Hkv heads x half pairs
-  const int n_pairs = (Hq + Hkv) * half;
-  for (int e = threadIdx.x; e < n_pairs; e += blockDim.x) {
-    const int h = e / half, j = e - h * half;
-    const T* xh = src + h * D;
-    const float x1 = Elem<T>::ld(xh + j), x2 = Elem<T>::ld(xh + j + half);
-    const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
-    const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
-    const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
-    const float a2 = Elem<T>::round(x2 * c2), b2 = Elem<T>::round(x1 * s2);
-    const float o1 = a1 + b1, o2 = a2 + b2;
-    T* dst;
-    if (h < Hq) {
-      dst = q_out + ((long)t * Hq + h) * D;
+  const long width = (long)(Hq + 2 * Hkv) * D;
+  const long base = (long)t * width + (long)h * D;
+  for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    if (h < Hq + Hkv) {
+      const float* ct = cos_tab + (long)p * D;
+      const float* st = sin_tab + (long)p * D;
+      const float x1 = qkv_val(qkv, P, KS, pstride, base + j);
+      const float x2 = qkv_val(qkv, P, KS, pstride, base + j + half);
+      const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
+      const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
+      const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
+      const float a2 = Elem<T>::round(x2 * c2), b2 = Elem<T>::round(x1 * s2);
+      const float o1 = a1 + b1, o2 = a2 + b2;
+      T* dst = (h < Hq) ? q_out + ((long)t * Hq + h) * D
+                        : kc + (((long)row * Hkv + (h - Hq)) * max_seq + p) * D;
+      Elem<T>::st(dst + j, o1);
+      Elem<T>::st(dst + j + half, o2);
     } else {
-      const int hk = h - Hq;
-      dst = kc + (((long)row * Hkv + hk) * max_seq + p) * D;
+      T* dst = vc + (((long)row * Hkv + (h - Hq - Hkv)) * max_seq + p) * D;
+      Elem<T>::st(dst + j, qkv_val(qkv, P, KS, pstride, base + j));
+      Elem<T>::st(dst + j + half, qkv_val(qkv, P, KS, pstride, base + j + half));
     }
-    Elem<T>::st(dst + j, o1);
-    Elem<T>::st(dst + j + half, o2);
   }
-  // v heads: plain copy into the cache
-  const T* vsrc = src + (Hq + Hkv) * D;
-  for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) {
-    const int hk = e / D, d = e - hk * D;
-    vc[(((long)row * Hkv + hk) * max_seq + p) * D + d] = vsrc[e];
-  }
+}
+
+template <typename T>
+static void launch_rope(const void* qkv, const float* P, int KS, long pstride, void* q_out, void* kc, void* vc,
+                        const float* ct, const float* st, const int32_t* rows, const int32_t* pos, int N, int Hq,
+                        int Hkv, int D, int B, int S, int tab_len, hipStream_t s) {
+  dim3 grid(N, Hq + 2 * Hkv);
+  const int threads = (D / 2 + 63) / 64 * 64;
+  rope_append_kernel<T><<<grid, threads, 0, s>>>((const T*)qkv, P, KS, pstride, (T*)q_out, (T*)kc, (T*)vc, ct, st,
+                                                  rows, pos, Hq, Hkv, D, B, S, tab_len);
+}
+
+static int rope_common(int dtype, const void* qkv, const float* P, int KS, void* q_out, void* kcache, void* vcache,
+                       const float* cos_tab, const float* sin_tab, int tab_len, const int32_t* rows,
+                       const int32_t* pos, int n_tokens, int n_heads, int n_kv_heads, int head_dim, int max_batch,
+                       int max_seq, void* stream) {
+  LSK_REQUIRE((qkv || P) && q_out && kcache && vcache && cos_tab && sin_tab && rows && pos, LSK_EARG,
+              "lsk_rope_append: null pointer");
+  LSK_REQUIRE(n_tokens >= 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && (head_dim % 2) == 0 &&
+                  head_dim <= 512 && n_heads % n_kv_heads == 0 && max_batch > 0 && max_seq > 0 && tab_len > 0 &&
+                  KS >= 1,
+              LSK_ESHAPE, "lsk_rope_append: bad shape");
+  if (n_tokens == 0) return 0;
+  const long pstride = (long)n_tokens * (n_heads + 2 * n_kv_heads) * head_dim;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == LSK_DTYPE_BF16)
+    launch_rope<uint16_t>(qkv, P, KS, pstride, q_out, kcache, vcache, cos_tab, sin_tab, rows, pos, n_tokens, n_heads,
+                          n_kv_heads, head_dim, max_batch, max_seq, tab_len, s);
+  else if (dtype == LSK_DTYPE_F32)
+    launch_rope<float>(qkv, P, KS, pstride, q_out, kcache, vcache, cos_tab, sin_tab, rows, pos, n_tokens, n_heads,
+                       n_kv_heads, head_dim, max_batch, max_seq, tab_len, s);
+  else
+    LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_rope_append: dtype %d", dtype);
+  return lsk_check_launch("lsk_rope_append");
 }
 
 extern "C" int lsk_rope_append(int dtype, const void* qkv, void* q_out, void* kcache, void* vcache,
                                const float* cos_tab, const float* sin_tab, int tab_len, const int32_t* rows,
                                const int32_t* pos, int n_tokens, int n_heads, int n_kv_heads, int head_dim,
                                int max_batch, int max_seq, void* stream) {
-  LSK_REQUIRE(qkv && q_out && kcache && vcache && cos_tab && sin_tab && rows && pos, LSK_EARG,
-              "lsk_rope_append: null pointer");
-  LSK_REQUIRE(n_tokens >= 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && (head_dim % 2) == 0 &&
-                  n_heads % n_kv_heads == 0 && max_batch > 0 && max_seq > 0 && tab_len > 0,
-              LSK_ESHAPE, "lsk_rope_append: bad shape");
-  if (n_tokens == 0) return 0;
-  hipStream_t s = (hipStream_t)stream;
-  if (dtype == LSK_DTYPE_BF16)
-    rope_append_kernel<uint16_t><<<n_tokens, 256, 0, s>>>(
-        (const uint16_t*)qkv, (uint16_t*)q_out, (uint16_t*)kcache, (uint16_t*)vcache, cos_tab, sin_tab, rows, pos,
-        n_heads, n_kv_heads, head_dim, max_batch, max_seq, tab_len);
-  else if (dtype == LSK_DTYPE_F32)
-    rope_append_kernel<float><<<n_tokens, 256, 0, s>>>((const float*)qkv, (float*)q_out, (float*)kcache,
-                                                       (float*)vcache, cos_tab, sin_tab, rows, pos, n_heads,
-                                                       n_kv_heads, head_dim, max_batch, max_seq, tab_len);
-  else
-    LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_rope_append: dtype %d", dtype);
-  return lsk_check_launch("lsk_rope_append");
+  LSK_REQUIRE(qkv != nullptr, LSK_EARG, "lsk_rope_append: null qkv");
+  return rope_common(dtype, qkv, nullptr, 1, q_out, kcache, vcache, cos_tab, sin_tab, tab_len, rows, pos, n_tokens,
+                     n_heads, n_kv_heads, head_dim, max_batch, max_seq, stream);
+}
+
+extern "C" int lsk_rope_append_partial(int dtype, const float* partials, int ks, void* q_out, void* kcache,
+                                       void* vcache, const float* cos_tab, const float* sin_tab, int tab_len,
+                                       const int32_t* rows, const int32_t* pos, int n_tokens, int n_heads,
+                                       int n_kv_heads, int head_dim, int max_batch, int max_seq, void* stream) {
+  LSK_REQUIRE(partials != nullptr, LSK_EARG, "lsk_rope_append_partial: null partials");
+  return rope_common(dtype, nullptr, partials, ks, q_out, kcache, vcache, cos_tab, sin_tab, tab_len, rows, pos,
+                     n_tokens, n_heads, n_kv_heads, head_dim, max_batch, max_seq, stream);
 }
 
 // Plain KV append (no RoPE): kcache[row_t, h, pos_t] = k[t, h]; vcache likewise.

@@ -1,23 +1,33 @@
 // Projection / LM-head GEMMs over the packed token rows (solutions/packed.py:175,182,183-185;
 // common/model.py:330):  C[m][n] = epilogue( sum_k A[m][k] * W[n][k] )   (F.linear, W = [out, in]).
 //
-// bf16 path (gfx950 MFMA v_mfma_f32_16x16x32_bf16, fp32 accumulation).  Both operands are
-// K-contiguous, so every lane fetches its MFMA fragment with one 16-byte load straight from HBM/L2
-// (no LDS staging: at decode sizes the weights are streamed exactly once and the activation rows
-// are L2-resident).  A workgroup = 4 waves computes a (16*NS features) x (16*MS tokens) tile; the
-// waves split K into 128-element chunks (wave w takes chunks w, w+4, ...) and their partial sums
-// are added in wave order through LDS.  The reduction order of every output element is therefore
-// fixed by K alone: it does not depend on M, on the tile shape, or on which rows share a tile, so a
-// token's logits are bitwise identical whether it is decoded alone or inside a packed verify batch.
+// bf16 path (gfx950 MFMA v_mfma_f32_16x16x32_bf16, fp32 accumulation).  Decode GEMMs are skinny
+// (M = 1..~300 tokens against 6k-128k weight rows), so the kernel is a weight stream: both operands
+// are K-contiguous and every lane fetches its MFMA fragment with one 16-byte load (no LDS staging);
+// a workgroup of 4 waves owns a (16*NS weight rows) x (16*MS tokens) tile, the waves split K into
+// 128-element chunks (wave w takes chunks w, w+4, ... of its K slice, with the next chunk prefetched
+// into registers) and their partial sums are added in wave order through LDS.  Wide tiles (NS = 4)
+// cut the re-reads of the token rows; weight matrices with few rows (qkv, o, w2 of the 8B shape)
+// use NS = 2 and a fixed split of K into KS slices whose fp32 partial sums the NEXT kernel reduces
+// in slice order (RoPE + append, add + RMSNorm), because a cross-workgroup reduction inside the GEMM
+// needs device-scope fences that cost more than the split saves on MI355X.
+//
+// Batch invariance: (NS, KS) are chosen from the weight shape (N, K) only (lsk_gemm_plan) and the
+// reduction order of every output element is fixed by (K, KS): chunks in order within a wave, waves in
+// order, slices in order.  It does not depend on M or on which rows share a tile, so a token's result
+// is bitwise the same whether it is decoded alone or inside a packed verify batch.
 //
 // Epilogues (the reference's dtype rounding points):
 //   NONE      C = rnd(acc)
 //   RESIDUAL  C = rnd(R + rnd(acc))                       x + F.linear(...)
 //   SILU_MUL  C = rnd(rnd(silu(rnd(g))) * rnd(u))         g, u = rows n and ffn + n of W (w13)
+//   PARTIAL   P[s][m][n] = acc over K slice s (fp32), reduced later in slice order
+//   ARGMAX    per (token, 16*NS-row tile): max of rnd(acc) and its first index (LM head + greedy pick)
 #include "lsk_common.h"
 #include "../include/lsk.h"
 
-#define KCHUNK 128
+#define EPI_PARTIAL 3
+#define EPI_ARGMAX 4
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
@@ -25,8 +35,10 @@ template <int NS, int MS, int EPI>
 __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
                                                         const uint16_t* __restrict__ W, long ldw,
                                                         uint16_t* __restrict__ C, long ldc,
-                                                        const uint16_t* __restrict__ R, long ldr, int M, int N,
-                                                        int K, int ffn) {
+                                                        const uint16_t* __restrict__ R, long ldr,
+                                                        float* __restrict__ P, float* __restrict__ amax_v,
+                                                        int* __restrict__ amax_i, int M, int N, int K, int ffn,
+                                                        int kslice) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
@@ -35,100 +47,200 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
   const int l16 = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16 * NS;
   const int m0 = blockIdx.y * 16 * MS;
+  const int s = blockIdx.z;
+  const int k0 = s * kslice;
+  const int k1 = min(K, k0 + kslice);
 
   const uint16_t* wrow[NT];
 #pragma unroll
-  for (int s = 0; s < NT; ++s) {
-    int n = (s < NS) ? (n0 + 16 * s + l16) : (ffn + n0 + 16 * (s - NS) + l16);
-    const int nmax = (EPI == LSK_EPI_SILU_MUL) ? (s < NS ? ffn - 1 : 2 * ffn - 1) : N - 1;
-    n = n < nmax ? n : nmax;  // clamp: padded features load a valid row, results discarded
-    wrow[s] = W + (long)n * ldw + 8 * lg;
+  for (int t = 0; t < NT; ++t) {
+    int n = (t < NS) ? (n0 + 16 * t + l16) : (ffn + n0 + 16 * (t - NS) + l16);
+    const int nmax = (EPI == LSK_EPI_SILU_MUL) ? (t < NS ? ffn - 1 : 2 * ffn - 1) : N - 1;
+    n = n < nmax ? n : nmax;  // clamp: padded rows load a valid row, results discarded
+    wrow[t] = W + (long)n * ldw + k0 + 8 * lg;
   }
   const uint16_t* arow[MS];
 #pragma unroll
   for (int t = 0; t < MS; ++t) {
     int m = m0 + 16 * t + l16;
     m = m < M - 1 ? m : M - 1;
-    arow[t] = A + (long)m * lda + 8 * lg;
+    arow[t] = A + (long)m * lda + k0 + 8 * lg;
   }
 
   lsk_f32x4 acc[NT][MS];
 #pragma unroll
-  for (int s = 0; s < NT; ++s)
+  for (int a = 0; a < NT; ++a)
 #pragma unroll
-    for (int t = 0; t < MS; ++t) acc[s][t] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int t = 0; t < MS; ++t) acc[a][t] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 
-  const int nk32 = K / 32;
-  for (int c = wave; c * 4 < nk32; c += 4) {
-    const int kk0 = c * 4;
-    if (kk0 + 4 <= nk32) {
-      lsk_bf16x8 wf[4][NT], af[4][MS];
+  const int nk32 = (k1 - k0) / 32;
+  const int nfull = nk32 / 4;  // full 128-element chunks of the slice
+  lsk_bf16x8 wf[2][4][NT], af[2][4][MS];
+  auto load = [&](int buf, int c) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const int k = (kk0 + ks) * 32;
+    for (int ks = 0; ks < 4; ++ks) {
+      const int k = c * 128 + ks * 32;
 #pragma unroll
-        for (int s = 0; s < NT; ++s) wf[ks][s] = *(const lsk_bf16x8*)(wrow[s] + k);
+      for (int a = 0; a < NT; ++a) wf[buf][ks][a] = *(const lsk_bf16x8*)(wrow[a] + k);
 #pragma unroll
-        for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
-      }
+      for (int t = 0; t < MS; ++t) af[buf][ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
+    }
+  };
+  auto comp = [&](int buf) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-        for (int s = 0; s < NT; ++s)
+      for (int a = 0; a < NT; ++a)
 #pragma unroll
-          for (int t = 0; t < MS; ++t)
-            acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ks][s], af[ks][t], acc[s][t], 0, 0, 0);
-    } else {
-      for (int kk = kk0; kk < nk32; ++kk) {
-        const int k = kk * 32;
-        lsk_bf16x8 wf[NT], af[MS];
+        for (int t = 0; t < MS; ++t)
+          acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][ks][a], af[buf][ks][t], acc[a][t], 0, 0, 0);
+  };
+  // full chunks c = wave, wave + 4, ... with the next chunk in flight while computing the current one
+  {
+    int c = wave;
+    if (c < nfull) load(0, c);
+    for (; c < nfull; c += 8) {
+      if (c + 4 < nfull) load(1, c + 4);
+      comp(0);
+      if (c + 4 >= nfull) break;
+      if (c + 8 < nfull) load(0, c + 8);
+      comp(1);
+    }
+  }
+  // tail chunk (slice length % 128 != 0): owned by wave nfull % 4, k-steps in order
+  if (wave == (nfull & 3)) {
+    for (int kk = nfull * 4; kk < nk32; ++kk) {
+      const int k = kk * 32;
+      lsk_bf16x8 w1[NT], a1[MS];
 #pragma unroll
-        for (int s = 0; s < NT; ++s) wf[s] = *(const lsk_bf16x8*)(wrow[s] + k);
+      for (int a = 0; a < NT; ++a) w1[a] = *(const lsk_bf16x8*)(wrow[a] + k);
 #pragma unroll
-        for (int t = 0; t < MS; ++t) af[t] = *(const lsk_bf16x8*)(arow[t] + k);
+      for (int t = 0; t < MS; ++t) a1[t] = *(const lsk_bf16x8*)(arow[t] + k);
 #pragma unroll
-        for (int s = 0; s < NT; ++s)
+      for (int a = 0; a < NT; ++a)
 #pragma unroll
-          for (int t = 0; t < MS; ++t)
-            acc[s][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[s], af[t], acc[s][t], 0, 0, 0);
-      }
+        for (int t = 0; t < MS; ++t)
+          acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(w1[a], a1[t], acc[a][t], 0, 0, 0);
     }
   }
 
-  // partial sums -> LDS, element ((s*MS + t)*64 + lane)*4 + i  <->  feature 16s + 4lg + i, token 16t + l16
+  // partial sums -> LDS, element ((a*MS + t)*64 + lane)*4 + i  <->  row 16a + 4lg + i, token 16t + l16
   float* my = red + wave * E;
 #pragma unroll
-  for (int s = 0; s < NT; ++s)
+  for (int a = 0; a < NT; ++a)
 #pragma unroll
     for (int t = 0; t < MS; ++t)
-      *(float4*)(my + ((s * MS + t) * 64 + lane) * 4) = make_float4(acc[s][t][0], acc[s][t][1], acc[s][t][2], acc[s][t][3]);
+      *(float4*)(my + ((a * MS + t) * 64 + lane) * 4) = make_float4(acc[a][t][0], acc[a][t][1], acc[a][t][2], acc[a][t][3]);
   __syncthreads();
 
   constexpr int TN = 16 * NS, TM = 16 * MS;
-  for (int o = tid; o < TN * TM; o += 256) {
-    const int ml = o / TN, nl = o - ml * TN;
-    const int m = m0 + ml, n = n0 + nl;
-    if (m >= M || n >= N) continue;
-    const int t = ml >> 4, ll = ml & 15;
-    const int s = nl >> 4, w16 = nl & 15;
-    const int ln = (w16 >> 2) * 16 + ll, i = w16 & 3;
-    const int e = ((s * MS + t) * 64 + ln) * 4 + i;
-    const float v = ((red[e] + red[E + e]) + red[2 * E + e]) + red[3 * E + e];
-    float outv;
-    if constexpr (EPI == LSK_EPI_SILU_MUL) {
-      const int eu = (((s + NS) * MS + t) * 64 + ln) * 4 + i;
-      const float u = ((red[eu] + red[E + eu]) + red[2 * E + eu]) + red[3 * E + eu];
-      outv = rbf(silu_f(rbf(v))) * rbf(u);
-    } else if constexpr (EPI == LSK_EPI_RESIDUAL) {
-      outv = bf2f(R[(long)m * ldr + n]) + rbf(v);
-    } else {
-      outv = v;
+  auto reduced = [&](int a, int ml, int w16) {
+    const int e = ((a * MS + (ml >> 4)) * 64 + (w16 >> 2) * 16 + (ml & 15)) * 4 + (w16 & 3);
+    return ((red[e] + red[E + e]) + red[2 * E + e]) + red[3 * E + e];
+  };
+  if constexpr (EPI == EPI_ARGMAX) {
+    // reduced, bf16-rounded logits back into wave 0's region, then one thread per token scans the tile
+    float vals[TN * TM / 256];
+#pragma unroll
+    for (int j = 0; j < TN * TM / 256; ++j) {
+      const int o = tid + 256 * j;
+      const int ml = o / TN, nl = o - ml * TN;
+      vals[j] = rbf(reduced(nl >> 4, ml, nl & 15));
+      const int m = m0 + ml, n = n0 + nl;
+      if (C != nullptr && m < M && n < N) C[(long)m * ldc + n] = f2bf(vals[j]);
     }
-    C[(long)m * ldc + n] = f2bf(outv);
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < TN * TM / 256; ++j) red[tid + 256 * j] = vals[j];
+    __syncthreads();
+    if (tid < TM) {
+      const int m = m0 + tid;
+      if (m < M) {
+        float best = -INFINITY;
+        int bi = -1;
+        for (int nl = 0; nl < TN; ++nl) {
+          const int n = n0 + nl;
+          if (n >= N) break;
+          const float v = red[tid * TN + nl];
+          if (bi < 0 || v > best) {
+            best = v;
+            bi = n;
+          }
+        }
+        amax_v[(long)m * gridDim.x + blockIdx.x] = best;
+        amax_i[(long)m * gridDim.x + blockIdx.x] = bi;
+      }
+    }
+    return;
+  } else {
+    for (int o = tid; o < TN * TM; o += 256) {
+      const int ml = o / TN, nl = o - ml * TN;
+      const int m = m0 + ml, n = n0 + nl;
+      if (m >= M || n >= N) continue;
+      const float v = reduced(nl >> 4, ml, nl & 15);
+      if constexpr (EPI == EPI_PARTIAL) {
+        P[((long)s * M + m) * N + n] = v;
+      } else {
+        float outv;
+        if constexpr (EPI == LSK_EPI_SILU_MUL) {
+          const float u = reduced((nl >> 4) + NS, ml, nl & 15);
+          outv = rbf(silu_f(rbf(v))) * rbf(u);
+        } else if constexpr (EPI == LSK_EPI_RESIDUAL) {
+          outv = bf2f(R[(long)m * ldr + n]) + rbf(v);
+        } else {
+          outv = v;
+        }
+        C[(long)m * ldc + n] = f2bf(outv);
+      }
+    }
   }
 }
 
-// fp32 path (parity runs): one wave per output feature, 16 token rows per workgroup row-block.
+// Final greedy pick over the per-tile maxima: larger value wins, ties keep the smaller index
+// (torch.argmax semantics over the bf16 logits).  out[dst ? dst[m] : m] = index.
+__global__ __launch_bounds__(256) void argmax_tiles_kernel(const float* __restrict__ v, const int* __restrict__ idx,
+                                                           int ntiles, int64_t* __restrict__ out,
+                                                           const int64_t* __restrict__ dst) {
+  const int m = blockIdx.x;
+  float best = -INFINITY;
+  int bi = -1;
+  for (int j = threadIdx.x; j < ntiles; j += 256) {
+    const float x = v[(long)m * ntiles + j];
+    const int xi = idx[(long)m * ntiles + j];
+    if (bi < 0 || x > best || (x == best && xi < bi)) {
+      best = x;
+      bi = xi;
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const float ov = __shfl_xor(best, o, 64);
+    const int oi = __shfl_xor(bi, o, 64);
+    if (bi < 0 || (oi >= 0 && (ov > best || (ov == best && oi < bi)))) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  __shared__ float sv[4];
+  __shared__ int si[4];
+  if ((threadIdx.x & 63) == 0) {
+    sv[threadIdx.x >> 6] = best;
+    si[threadIdx.x >> 6] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float b = sv[0];
+    int i = si[0];
+    for (int w = 1; w < 4; ++w)
+      if (i < 0 || (si[w] >= 0 && (sv[w] > b || (sv[w] == b && si[w] < i)))) {
+        b = sv[w];
+        i = si[w];
+      }
+    out[dst ? dst[m] : m] = (int64_t)i;
+  }
+}
+
+// fp32 path (parity runs): one wave per output row of W, 16 token rows per workgroup row-block.
 // Lane l sums k = l, l + 64, ... in order, then a fixed xor tree over the 64 lanes.
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__ A, long lda,
@@ -182,29 +294,64 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
   }
 }
 
-template <int NS, int MS>
-static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, long ldw,
-                        uint16_t* C, long ldc, const uint16_t* R, long ldr, int M, int N, int K, int ffn) {
-  if (epi == LSK_EPI_RESIDUAL)
-    gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, ffn);
-  else if (epi == LSK_EPI_SILU_MUL) {
-    if constexpr (NS <= 2)
-      gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, ffn);
-  } else
-    gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, M, N, K, ffn);
+// ----------------------------------------------------------------------------- host side
+
+// Canonical tiling of a weight shape (N rows x K): NS = 4 when that still yields >= 256 row tiles,
+// else NS = 2 with KS = the smallest power of two giving >= 512 workgroups (K/KS a multiple of 128).
+// Depends on (N, K) only, never on M.
+extern "C" int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out) {
+  LSK_REQUIRE(ns_out && ks_out && N > 0 && K > 0, LSK_EARG, "lsk_gemm_plan: bad arguments");
+  int ns, ks = 1;
+  if (N % 64 == 0 && N / 64 >= 256) {
+    ns = 4;
+  } else if (N % 32 == 0) {
+    ns = 2;
+    while (N / 32 * ks < 512 && K % (2 * ks) == 0 && (K / (2 * ks)) % 128 == 0) ks *= 2;
+  } else {
+    ns = 1;
+  }
+  *ns_out = ns;
+  *ks_out = ks;
+  return 0;
 }
 
-// Tile choice: MS from M, then the widest NS that still gives >= 1024 workgroups (bandwidth needs
-// many waves in flight).  Every choice shares the same K order, so the choice never changes results.
-extern "C" int lsk_gemm_tile(int M, int N, int* ns_out, int* ms_out) {
-  const int ms = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
-  const int mt = (M + 16 * ms - 1) / (16 * ms);
-  int ns = 1;
-  if (N % 64 == 0 && (long)(N / 64) * mt >= 1024) ns = 4;
-  else if (N % 32 == 0 && (long)(N / 32) * mt >= 1024) ns = 2;
-  *ns_out = ns;
-  *ms_out = ms;
-  return 0;
+static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
+
+template <int NS, int MS>
+static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, long ldw,
+                        uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
+                        int N, int K, int ffn, int kslice) {
+  if (epi == LSK_EPI_RESIDUAL)
+    gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
+                                                                    ffn, kslice);
+  else if (epi == LSK_EPI_SILU_MUL) {
+    if constexpr (NS <= 2)
+      gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
+                                                                      K, ffn, kslice);
+  } else if (epi == EPI_PARTIAL)
+    gemm_bf16_kernel<NS, MS, EPI_PARTIAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
+                                                               kslice);
+  else if (epi == EPI_ARGMAX)
+    gemm_bf16_kernel<NS, MS, EPI_ARGMAX><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
+                                                              kslice);
+  else
+    gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
+                                                                ffn, kslice);
+}
+
+static void dispatch_bf16(int ns, int ms, int epi, dim3 grid, hipStream_t s, const void* A, long lda, const void* W,
+                          long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av, int* ai, int M,
+                          int N, int K, int ffn, int kslice) {
+  const uint16_t* a = (const uint16_t*)A;
+  const uint16_t* w = (const uint16_t*)W;
+  uint16_t* c = (uint16_t*)C;
+  const uint16_t* r = (const uint16_t*)R;
+#define LSK_GEMM_CASE(NS_, MS_) \
+  if (ns == NS_ && ms == MS_) launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice);
+  LSK_GEMM_CASE(1, 1) LSK_GEMM_CASE(1, 2) LSK_GEMM_CASE(1, 4)
+  LSK_GEMM_CASE(2, 1) LSK_GEMM_CASE(2, 2) LSK_GEMM_CASE(2, 4)
+  LSK_GEMM_CASE(4, 1) LSK_GEMM_CASE(4, 2) LSK_GEMM_CASE(4, 4)
+#undef LSK_GEMM_CASE
 }
 
 extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc,
@@ -222,20 +369,14 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
     LSK_REQUIRE(K % 32 == 0 && lda % 8 == 0 && ldw % 8 == 0, LSK_ESHAPE,
                 "lsk_gemm: bf16 needs K %% 32 == 0 and 16-byte aligned rows (K=%d)", K);
     LSK_REQUIRE(N % 16 == 0, LSK_ESHAPE, "lsk_gemm: bf16 needs N %% 16 == 0 (N=%d)", N);
-    int ns, ms;
-    lsk_gemm_tile(M, N, &ns, &ms);
-    if (epilogue == LSK_EPI_SILU_MUL && ns == 4) ns = 2;  // keeps the LDS reduction buffer <= 64 KiB
-    dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms));
-    const uint16_t* a = (const uint16_t*)A;
-    const uint16_t* w = (const uint16_t*)W;
-    uint16_t* c = (uint16_t*)C;
-    const uint16_t* r = (const uint16_t*)R;
-#define LSK_GEMM_CASE(NS_, MS_) \
-  if (ns == NS_ && ms == MS_) launch_bf16<NS_, MS_>(epilogue, grid, s, a, lda, w, ldw, c, ldc, r, ldr, M, N, K, ffn);
-    LSK_GEMM_CASE(1, 1) LSK_GEMM_CASE(1, 2) LSK_GEMM_CASE(1, 4)
-    LSK_GEMM_CASE(2, 1) LSK_GEMM_CASE(2, 2) LSK_GEMM_CASE(2, 4)
-    LSK_GEMM_CASE(4, 1) LSK_GEMM_CASE(4, 2) LSK_GEMM_CASE(4, 4)
-#undef LSK_GEMM_CASE
+    // whole-K workgroups; the tile follows the plan of the weight shape (W rows = 2N for silu-mul)
+    int ns, ks;
+    lsk_gemm_plan(epilogue == LSK_EPI_SILU_MUL ? 2 * N : N, K, &ns, &ks);
+    if (epilogue == LSK_EPI_SILU_MUL) ns = ns >= 4 ? 2 : (ns == 2 ? 1 : 1);  // 2*NS rows per tile = the plan's width
+    while (N % (16 * ns) != 0) ns >>= 1;
+    const int ms = ms_for(M);
+    dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), 1);
+    dispatch_bf16(ns, ms, epilogue, grid, s, A, lda, W, ldw, C, ldc, R, ldr, nullptr, nullptr, nullptr, M, N, K, ffn, K);
     return lsk_check_launch("lsk_gemm(bf16)");
   }
   if (dtype == LSK_DTYPE_F32) {
@@ -254,4 +395,52 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
   }
   LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_gemm: dtype %d", dtype);
   return LSK_EUNSUPPORTED;
+}
+
+extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P, int M, int N, int K, int ks,
+                                void* stream) {
+  LSK_REQUIRE(A && W && P, LSK_EARG, "lsk_gemm_partial: null pointer");
+  LSK_REQUIRE(M >= 0 && N > 0 && K > 0 && lda >= K && ldw >= K && ks >= 1 && K % ks == 0 && (K / ks) % 32 == 0 &&
+                  N % 16 == 0 && lda % 8 == 0 && ldw % 8 == 0,
+              LSK_ESHAPE, "lsk_gemm_partial: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
+  if (M == 0) return 0;
+  int ns, kp;
+  lsk_gemm_plan(N, K, &ns, &kp);
+  while (N % (16 * ns) != 0) ns >>= 1;
+  const int ms = ms_for(M);
+  dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks);
+  dispatch_bf16(ns, ms, EPI_PARTIAL, grid, (hipStream_t)stream, A, lda, W, ldw, nullptr, 0, nullptr, 0, P, nullptr,
+                nullptr, M, N, K, 0, K / ks);
+  return lsk_check_launch("lsk_gemm_partial");
+}
+
+extern "C" size_t lsk_head_workspace_bytes(int M, int N) {
+  const size_t nt = (size_t)(N + 63) / 64;
+  return lsk_align_up((size_t)M * nt * 4, 256) * 2;
+}
+
+extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W, long ldw, int M, int N, int K,
+                               void* logits, long ldl, int64_t* out, const int64_t* dst_idx, void* workspace,
+                               size_t ws_bytes, void* stream) {
+  LSK_REQUIRE(A && W && out, LSK_EARG, "lsk_head_argmax: null pointer");
+  LSK_REQUIRE(M >= 0 && N > 0 && K > 0 && lda >= K && ldw >= K && (logits == nullptr || ldl >= N), LSK_ESHAPE,
+              "lsk_head_argmax: bad shape");
+  if (M == 0) return 0;
+  hipStream_t s = (hipStream_t)stream;
+  LSK_REQUIRE(dtype == LSK_DTYPE_BF16, LSK_EUNSUPPORTED, "lsk_head_argmax: bf16 only (fp32 uses lsk_gemm + lsk_argmax)");
+  LSK_REQUIRE(K % 32 == 0 && N % 64 == 0 && lda % 8 == 0 && ldw % 8 == 0, LSK_ESHAPE,
+              "lsk_head_argmax: needs K %% 32 == 0 and N %% 64 == 0 (N=%d K=%d)", N, K);
+  const int nt = N / 64;
+  const size_t half = lsk_align_up((size_t)M * nt * 4, 256);
+  LSK_REQUIRE(workspace != nullptr && ws_bytes >= 2 * half, LSK_EWORKSPACE, "lsk_head_argmax: workspace %zu < %zu",
+              ws_bytes, 2 * half);
+  float* av = (float*)workspace;
+  int* ai = (int*)((char*)workspace + half);
+  const int ms = ms_for(M);
+  dim3 grid(nt, (M + 16 * ms - 1) / (16 * ms), 1);
+  dispatch_bf16(4, ms, EPI_ARGMAX, grid, s, A, lda, W, ldw, logits, ldl, nullptr, 0, nullptr, av, ai, M, N, K, 0, K);
+  int rc = lsk_check_launch("lsk_head_argmax(gemm)");
+  if (rc) return rc;
+  argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
+  return lsk_check_launch("lsk_head_argmax(pick)");
 }

@@ -22,6 +22,7 @@ namespace {
 
 struct Model {
   int dtype, n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab;
+  int ks_qkv, ks_o, ks_w2;  // canonical K splits of the bf16 projections (lsk_gemm_plan)
   float eps;
   std::vector<const void*> wqkv, wo, w13, w2, attn_norm, ffn_norm;
   std::vector<void*> kc, vc;
@@ -65,7 +66,7 @@ hipEvent_t pool_event() {
 }
 
 struct Layout {
-  size_t xn, qkv, q, attn, h, part, total;
+  size_t xn, qkv, q, attn, h, part, gpart, total;
 };
 
 Layout layout(const Model& m, int N, int n_parts) {
@@ -84,6 +85,12 @@ Layout layout(const Model& m, int N, int n_parts) {
   L.attn = take((size_t)N * qd * es);
   L.h = take((size_t)N * m.ffn * es);
   L.part = take(n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, m.n_kv_heads, m.head_dim) : 0);
+  size_t gp = 0;
+  if (m.dtype == LSK_DTYPE_BF16) {
+    const size_t a = (size_t)m.ks_qkv * (qd + 2 * kvd), b = (size_t)m.ks_o * m.dim, c = (size_t)m.ks_w2 * m.dim;
+    gp = (size_t)N * sizeof(float) * (a > b ? (a > c ? a : c) : (b > c ? b : c));
+  }
+  L.gpart = take(gp);
   L.total = off;
   return L;
 }
@@ -149,6 +156,14 @@ extern "C" long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, 
   m->kc.assign(kcache, kcache + n_layers); m->vc.assign(vcache, vcache + n_layers);
   m->max_batch = max_batch; m->max_seq = max_seq;
   m->cos_tab = cos_tab; m->sin_tab = sin_tab; m->tab_len = tab_len;
+  int ns;
+  m->ks_qkv = m->ks_o = m->ks_w2 = 1;
+  if (dtype == LSK_DTYPE_BF16) {
+    const int qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
+    lsk_gemm_plan(qd + 2 * kvd, dim, &ns, &m->ks_qkv);
+    lsk_gemm_plan(dim, qd, &ns, &m->ks_o);
+    lsk_gemm_plan(dim, ffn, &ns, &m->ks_w2);
+  }
   std::lock_guard<std::mutex> lk(g_mu);
   g_models.push_back(m);
   return (long)g_models.size();
@@ -211,6 +226,65 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
   const float scale = (float)(1.0 / sqrt((double)m->head_dim));
   int rc;
   const double es_d = (double)es, Nd = N, dimd = m->dim, qkvd = qd + 2 * kvd, ffd = m->ffn;
+  if (m->dtype == LSK_DTYPE_BF16) {
+    // bf16 flow: the small-N projections (qkv, o, w2) leave fp32 K-slice partials in P that the next
+    // kernel reduces in slice order (RoPE + append; add + RMSNorm, which also materialises the residual
+    // stream x).  Same rounding points as the unfused sequence.
+    float* P = (float*)(ws + L.gpart);
+    const double norm_bytes_b = es_d * (2.0 * Nd * dimd + dimd);
+    auto pbytes = [&](int ks, double width) { return 4.0 * ks * Nd * width; };
+#define LSK_PROF2(cls, b, f, call)                               \
+  do {                                                           \
+    lsk_prof_start((cls), (b), (f), stream);                     \
+    if ((rc = (call))) return rc;                                \
+    lsk_prof_stop(stream);                                       \
+  } while (0)
+    for (int i = start; i < end; ++i) {
+      if (i == start) {
+        LSK_PROF2(LSK_PROF_NORM, norm_bytes_b, 4.0 * Nd * dimd,
+                  lsk_add_rmsnorm(m->dtype, x_in, m->dim, nullptr, 0, m->attn_norm[i], m->eps, nullptr, 0, xn, m->dim,
+                                  N, m->dim, stream));
+      } else {
+        LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_w2, dimd), 4.0 * Nd * dimd,
+                  lsk_add_rmsnorm(m->dtype, x_out, m->dim, P, m->ks_w2, m->attn_norm[i], m->eps, x_out, m->dim, xn,
+                                  m->dim, N, m->dim, stream));
+        if (capture && capture[i - 1]) {
+          hipError_t e = hipMemcpyAsync(capture[i - 1], x_out, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
+          if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }
+        }
+      }
+      LSK_PROF2(LSK_PROF_GEMM_QKV, es_d * (qkvd * dimd + Nd * dimd) + pbytes(m->ks_qkv, qkvd), 2.0 * Nd * dimd * qkvd,
+                lsk_gemm_partial(xn, m->dim, m->wqkv[i], m->dim, P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream));
+      LSK_PROF2(LSK_PROF_ROPE, pbytes(m->ks_qkv, qkvd) + es_d * Nd * qkvd, 6.0 * Nd * (qd + kvd),
+                lsk_rope_append_partial(m->dtype, P, m->ks_qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab,
+                                        m->tab_len, rows, pos, N, m->n_heads, m->n_kv_heads, m->head_dim,
+                                        m->max_batch, m->max_seq, stream));
+      LSK_PROF2(LSK_PROF_ATTN, attn_bytes, attn_flops,
+                lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts,
+                                attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes,
+                                stream));
+      LSK_PROF2(LSK_PROF_GEMM_O, es_d * (dimd * qd + Nd * qd) + pbytes(m->ks_o, dimd), 2.0 * Nd * qd * dimd,
+                lsk_gemm_partial(attn, qd, m->wo[i], qd, P, N, m->dim, qd, m->ks_o, stream));
+      const void* xi = (i == start) ? x_in : x_out;
+      LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_o, dimd), 4.0 * Nd * dimd,
+                lsk_add_rmsnorm(m->dtype, xi, m->dim, P, m->ks_o, m->ffn_norm[i], m->eps, x_out, m->dim, xn, m->dim,
+                                N, m->dim, stream));
+      LSK_PROF2(LSK_PROF_GEMM_W13, es_d * (2.0 * ffd * dimd + Nd * dimd + Nd * ffd), 4.0 * Nd * dimd * ffd,
+                lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
+                         LSK_EPI_SILU_MUL, m->ffn, stream));
+      LSK_PROF2(LSK_PROF_GEMM_W2, es_d * (dimd * ffd + Nd * ffd) + pbytes(m->ks_w2, dimd), 2.0 * Nd * ffd * dimd,
+                lsk_gemm_partial(h, m->ffn, m->w2[i], m->ffn, P, N, m->dim, m->ffn, m->ks_w2, stream));
+    }
+    LSK_PROF2(LSK_PROF_NORM, 2.0 * es_d * Nd * dimd + pbytes(m->ks_w2, dimd), Nd * dimd,
+              lsk_add_rmsnorm(m->dtype, x_out, m->dim, P, m->ks_w2, nullptr, m->eps, x_out, m->dim, nullptr, 0, N,
+                              m->dim, stream));
+    if (capture && capture[end - 1]) {
+      hipError_t e = hipMemcpyAsync(capture[end - 1], x_out, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }
+    }
+#undef LSK_PROF2
+    return 0;
+  }
   const double norm_bytes = es_d * (2.0 * Nd * dimd + dimd);
   auto gemm_bytes = [&](double M_, double Nw, double K_, double Nout, bool res) {
     return es_d * (K_ * Nw + M_ * K_ + M_ * Nout * (res ? 2.0 : 1.0));

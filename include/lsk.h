@@ -80,8 +80,34 @@ int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vc
 int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc, const void* R, long ldr,
              int M, int N, int K, int epilogue, int ffn, void* stream);
 
-/* Tile the bf16 GEMM picks for (M, N) (informational; every tile gives identical results). */
-int lsk_gemm_tile(int M, int N, int* ns_out, int* ms_out);
+/* Canonical bf16 tiling of a weight shape (N rows x K): 16*ns weight rows per workgroup and ks K slices.
+ * Chosen from (N, K) only, so the per-element reduction order never depends on the token count M. */
+int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out);
+
+/* bf16 GEMM into fp32 K-slice partials: P[s][m][n] = sum over k in slice s of A[m][k] W[n][k], s < ks
+ * (ks must equal lsk_gemm_plan's for this shape to keep the canonical reduction order; the consumer adds
+ * the slices in order).  Replaces F.linear at solutions/packed.py:175 (wqkv), 182 (wo), 185 (w2). */
+int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P, int M, int N, int K, int ks,
+                     void* stream);
+
+/* LM head + greedy pick: out[dst_idx ? dst_idx[m] : m] = argmax_n rnd(A[m] . W[n]) (first index on ties),
+ * optionally also storing the bf16 logits [M, ldl].  workspace >= lsk_head_workspace_bytes(M, N).
+ * Replaces F.linear(.., lm_head) + .argmax(-1) (common/model.py:330, solutions/engine.py:255,352,463). */
+size_t lsk_head_workspace_bytes(int M, int N);
+int lsk_head_argmax(int dtype, const void* A, long lda, const void* W, long ldw, int M, int N, int K, void* logits,
+                    long ldl, int64_t* out, const int64_t* dst_idx, void* workspace, size_t ws_bytes, void* stream);
+
+/* Residual add + RMSNorm: x_new = rnd(x + rnd(sum_{s<ks} P[s])) (ks = 0: x_new = x), stored to x_out when
+ * non-NULL; out = rmsnorm(x_new, w) when out != NULL.  P: fp32 [ks][n_rows][dim].
+ * Replaces `x + F.linear(...)` + rms_norm at solutions/packed.py:182-183, 185 + 175. */
+int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w, float eps,
+                    void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim, void* stream);
+
+/* lsk_rope_append reading qkv as rnd(sum_{s<ks} P[s]) from fp32 partials [ks][N][(Hq+2Hkv)D]. */
+int lsk_rope_append_partial(int dtype, const float* partials, int ks, void* q_out, void* kcache, void* vcache,
+                            const float* cos_tab, const float* sin_tab, int tab_len, const int32_t* rows,
+                            const int32_t* pos, int n_tokens, int n_heads, int n_kv_heads, int head_dim,
+                            int max_batch, int max_seq, void* stream);
 
 /* Embedding gather with the engine's id assembly: out[t] = table[id_t],
  * id_t = (sel && sel[t] >= 0) ? seq_buf[sel[t]] : alt[t]  (int64 ids; out-of-range id -> zero row).

@@ -304,3 +304,93 @@ def test_greedy_accept_matches_closed_form(cuda):
         assert sb_h[i, 0] == Y[s + a]
         assert kvl.cpu()[i] == 100 + a + 1
     assert acc_h[0] == 2
+
+
+# ----------------------------------------------------------------------------- split-K partials + fused consumers
+
+@pytest.mark.parametrize("M,N,K", [(32, 4096, 4096), (7, 512, 256), (100, 6144, 4096)])
+def test_gemm_partial_slices(cuda, M, N, K):
+    """Slice partials add up (in slice order) to the fp32 product; rows are bitwise batch invariant."""
+    lsk = _lsk()
+    ns, ks = lsk.gemm_plan(N, K)
+    g = _gen(M + N)
+    a = torch.randn(M, K, generator=g).to(BF16)
+    w = torch.randn(N, K, generator=g).to(BF16)
+    P = lsk.gemm_partial(a.to(cuda), w.to(cuda), ks).cpu()
+    assert P.shape == (ks, M, N)
+    ref = a.float() @ w.float().t()
+    tot = P[0].clone()
+    for s in range(1, ks):
+        tot = tot + P[s]
+    assert torch.allclose(tot, ref, rtol=1e-4, atol=1e-3 * math.sqrt(K))
+    sub = lsk.gemm_partial(a[3:5].contiguous().to(cuda), w.to(cuda), ks).cpu()
+    assert torch.equal(sub, P[:, 3:5])
+
+
+def test_add_rmsnorm_rounding_points(cuda):
+    """x_new = rnd(x + rnd(sum_s P[s])) bitwise; the norm of x_new as the plain kernel computes it."""
+    lsk = _lsk()
+    g = _gen(8)
+    n, dim, ks = 13, 4096, 4
+    x = torch.randn(n, dim, generator=g).to(BF16)
+    P = torch.randn(ks, n, dim, generator=g)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(BF16)
+    xd, xo, xn = x.to(cuda), torch.empty(n, dim, dtype=BF16, device=cuda), torch.empty(n, dim, dtype=BF16, device=cuda)
+    lsk.add_rmsnorm(xd, P.to(cuda), w.to(cuda), 1e-5, x_out=xo, out=xn)
+    acc = P[0].clone()
+    for s in range(1, ks):
+        acc = acc + P[s]
+    x_new = (x.float() + acc.to(BF16).float()).to(BF16)
+    assert torch.equal(xo.cpu(), x_new)
+    plain = lsk.rmsnorm(xo, w.to(cuda), 1e-5).cpu()
+    assert torch.equal(xn.cpu(), plain)
+    ref = o_rms_norm(x_new, w, 1e-5)
+    assert ((xn.cpu().float() - ref.float()).abs() <= 2.0 ** -7 * ref.float().abs() + 1e-6).all()
+
+
+def test_rope_append_partial_is_bit_exact(cuda):
+    lsk = _lsk()
+    from oracle.model import OracleConfig, rope_tables
+
+    g = _gen(31)
+    Hq, Hkv, D, B, S, N, ks = 8, 2, 128, 2, 128, 5, 2
+    cfg = OracleConfig(64, 64, 1, Hq, Hkv, D, 64, rope_theta=500000.0)
+    cos, sin = rope_tables(cfg, S)
+    P = torch.randn(ks, N, (Hq + 2 * Hkv) * D, generator=g)
+    qkv = (P[0] + P[1]).to(BF16)
+    rows = torch.tensor([0, 1, 1, 0, 1])
+    pos = torch.tensor([3, 9, 10, 4, 11])
+    kd = torch.zeros(B, Hkv, S, D, dtype=BF16, device=cuda)
+    vd = torch.zeros_like(kd)
+    q_out = torch.empty(N, Hq, D, dtype=BF16, device=cuda)
+    lsk.rope_append_partial(P.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda), rows.to(torch.int32).to(cuda),
+                            pos.to(torch.int32).to(cuda), Hq, Hkv, D)
+    c, s = cos[pos].to(BF16).unsqueeze(1), sin[pos].to(BF16).unsqueeze(1)
+    assert torch.equal(q_out.cpu(), o_rope(qkv[:, :Hq * D].view(N, Hq, D), c, s))
+    kref = o_rope(qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D), c, s)
+    assert torch.equal(kd.cpu()[rows, :, pos], kref)
+    assert torch.equal(vd.cpu()[rows, :, pos], qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D))
+
+
+def test_head_argmax_matches_logits_argmax(cuda):
+    """Fused head + pick == argmax over the materialised bf16 logits (first index on ties)."""
+    lsk = _lsk()
+    g = _gen(12)
+    M, V, K = 37, 4096 + 64, 512
+    a = torch.randn(M, K, generator=g).to(BF16).to(cuda)
+    w = torch.randn(V, K, generator=g).to(BF16)
+    w[3000] = w[100]                      # duplicate rows -> exact ties, the first index must win
+    w[4100] = w[100]
+    wd = w.to(cuda)
+    logits = lsk.gemm(a, wd)
+    ref = logits.float().argmax(-1)
+    out = torch.empty(M, dtype=torch.long, device=cuda)
+    lo2 = torch.empty(M, V, dtype=BF16, device=cuda)
+    lsk.head_argmax(a, wd, out, logits=lo2)
+    assert torch.equal(out, ref)
+    assert torch.equal(lo2, logits)
+    # scatter into a destination index map
+    dst = torch.arange(M, device=cuda) * 2
+    big = torch.full((2 * M,), -1, dtype=torch.long, device=cuda)
+    lsk.head_argmax(a, wd, big, dst_idx=dst)
+    assert torch.equal(big[::2], ref) and (big[1::2] == -1).all()

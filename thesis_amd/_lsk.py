@@ -35,7 +35,12 @@ _SIGS = {
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
     "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
-    "lsk_gemm_tile": (_I, [_I, _I, _P, _P]),
+    "lsk_gemm_plan": (_I, [_I, _I, _P, _P]),
+    "lsk_gemm_partial": (_I, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _P]),
+    "lsk_head_workspace_bytes": (_Z, [_I, _I]),
+    "lsk_head_argmax": (_I, [_I, _P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _P, _P, _Z, _P]),
+    "lsk_add_rmsnorm": (_I, [_I, _P, _L, _P, _I, _P, _F, _P, _L, _P, _L, _I, _I, _P]),
+    "lsk_rope_append_partial": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lsk_embed": (_I, [_P, _L, _L, _P, _L, _P, _P, _P, _I, _P]),
     "lsk_copy_rows": (_I, [_P, _P, _L, _P, _P, _L, _L, _I, _P]),
     "lsk_argmax": (_I, [_I, _P, _L, _I, _I, _P, _P, _P]),
@@ -313,3 +318,57 @@ class Profiler:
                "lsk_prof_collect")
         return {PROF_CLASSES[i]: {"ms": float(ms[i]), "bytes": float(by[i]), "flops": float(fl[i]),
                                   "launches": int(ct[i])} for i in range(n) if ct[i]}
+
+
+def gemm_plan(N: int, K: int) -> tuple:
+    ns, ks = ctypes.c_int(0), ctypes.c_int(0)
+    _check(load().lsk_gemm_plan(N, K, ctypes.byref(ns), ctypes.byref(ks)), "lsk_gemm_plan")
+    return ns.value, ks.value
+
+
+def gemm_partial(a: torch.Tensor, w: torch.Tensor, ks: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """fp32 K-slice partials [ks, M, N] of a @ w.T (bf16)."""
+    _dev(a, w, out)
+    M, K = a.shape
+    N = w.shape[0]
+    if out is None:
+        out = torch.empty(ks, M, N, dtype=torch.float32, device=a.device)
+    _check(load().lsk_gemm_partial(_ptr(a), a.stride(0), _ptr(w), w.stride(0), _ptr(out), M, N, K, ks, _stream()),
+           "lsk_gemm_partial")
+    return out
+
+
+def head_argmax(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, dst_idx: torch.Tensor | None = None,
+                logits: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    _dev(a, w, out, dst_idx, logits, workspace)
+    M, K = a.shape
+    N = w.shape[0]
+    need = int(load().lsk_head_workspace_bytes(M, N))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=a.device)
+    _check(load().lsk_head_argmax(dtype_code(a.dtype), _ptr(a), a.stride(0), _ptr(w), w.stride(0), M, N, K,
+                                  _ptr(logits), logits.stride(0) if logits is not None else 0, _ptr(out),
+                                  _ptr(dst_idx), _ptr(workspace), workspace.numel() * workspace.element_size(),
+                                  _stream()), "lsk_head_argmax")
+    return out
+
+
+def add_rmsnorm(x: torch.Tensor, partials: torch.Tensor | None, w: torch.Tensor | None, eps: float,
+                x_out: torch.Tensor | None = None, out: torch.Tensor | None = None) -> None:
+    _dev(x, partials, w, x_out, out)
+    n, dim = x.shape
+    ks = partials.shape[0] if partials is not None else 0
+    _check(load().lsk_add_rmsnorm(dtype_code(x.dtype), _ptr(x), x.stride(0), _ptr(partials), ks, _ptr(w), float(eps),
+                                  _ptr(x_out), x_out.stride(0) if x_out is not None else 0, _ptr(out),
+                                  out.stride(0) if out is not None else 0, n, dim, _stream()), "lsk_add_rmsnorm")
+
+
+def rope_append_partial(partials, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads,
+                        head_dim):
+    _dev(partials, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
+    ks, N, _ = partials.shape
+    B, Hkv, S, D = kcache.shape
+    _check(load().lsk_rope_append_partial(dtype_code(q_out.dtype), _ptr(partials), ks, _ptr(q_out), _ptr(kcache),
+                                          _ptr(vcache), _ptr(cos_tab), _ptr(sin_tab), cos_tab.shape[0],
+                                          _ptr(rows_i32), _ptr(pos_i32), N, n_heads, n_kv_heads, head_dim, B, S,
+                                          _stream()), "lsk_rope_append_partial")

@@ -339,6 +339,13 @@ class LayerSkipLlama:
         P.start(0, es * (2.0 * n * dim + dim), 4.0 * n * dim)
         _lsk.rmsnorm(x, self.norm_w, self.cfg.norm_eps, out=xn)
         P.stop()
+        if self.dtype == torch.bfloat16:
+            # fused LM head + per-tile argmax, then the pick over tiles (no logits materialised)
+            ws = self.buffer("head_ws", (int(_lsk.load().lsk_head_workspace_bytes(n, V)),), torch.uint8)
+            P.start(7, es * (float(V) * dim + n * dim), 2.0 * n * dim * V)
+            _lsk.head_argmax(xn, self.lm_head_w, out, dst_idx, workspace=ws)
+            P.stop()
+            return out
         logits = self.buffer("head_logits", (n, V), self.dtype)
         P.start(7, es * (float(V) * dim + n * dim + n * V), 2.0 * n * dim * V)
         _lsk.gemm(xn, self.lm_head_w, out=logits)
