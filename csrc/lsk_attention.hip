@@ -6,48 +6,47 @@
 //
 // Layouts
 //   q      [N, Hq, D]            (packed token axis; RoPE applied)
-//   cache  [B, Hkv, S, D]        (per layer; KVCache of common/model.py:171-183)
+//   K      [B, Hkv, S, D]        (per layer; the KVCache layout of common/model.py:171-183)
+//   V      [B, Hkv, D, S]        (stored transposed: position-contiguous rows per (head, d))
 //   out    [N, Hq * D]
 //   blocks int32 [nb][4] = {q_start, pos0, T, row}
 //   works  int32 [n_work][8] = {blk, row0, nrows, kv_lo, kv_hi, part, 0, 0}
 //   groups int32 [n_group][8] = {blk, row0, nrows, part_first, n_split, 0, 0, 0}
 // The G query heads of a KV head are folded into query rows: row = t * G + g (t = token of the
-// block, g = head within the group), so one workgroup reads each KV tile once for all G*T rows.
-//
-// bf16 path (MFMA, gfx950): a workgroup = 4 waves, one 16-row query tile per wave, the 64-position
-// K/V tiles are staged once in LDS for the four waves.  Scores are computed transposed,
-// S^T[pos][q] = K Q^T with v_mfma_f32_16x16x32_bf16, so every lane owns one query column: the
-// online softmax state (running max, row sum) is lane-local and only needs xor shuffles across the
-// four 16-lane groups.  O^T[d][q] = V^T P^T with v_mfma_f32_16x16x16_bf16 takes P^T straight from
-// the score registers (same lane layout), V^T fragments are read from LDS.
+// block, g = head within the group); a workgroup serves 16 rows, so one KV read serves G*T <= 16 rows.
 //
 // Long contexts are split into fixed, position-aligned chunks of LSK_ATTN_SPLIT positions
-// (flash-decoding).  Because split boundaries, tile boundaries and the combine order depend only on
-// absolute positions, the result for a query never depends on which other tokens share its block
-// or batch (batch invariance: a T = 1 decode query and the same query inside a T = 9 verify block
-// give bitwise identical outputs).
+// (flash-decoding).  Split boundaries, tile boundaries, the wave that owns a tile and both merge
+// orders depend only on absolute positions, so the result for a query never depends on which other
+// tokens share its block or batch (batch invariance: a T = 1 decode query and the same query inside a
+// T = 9 verify block give bitwise identical outputs).
 #include "lsk_common.h"
 #include "../include/lsk.h"
 
 #define ATTN_TILE 64
-#define ATTN_ROWS 64  // query rows per workgroup (4 waves x 16)
+#define ATTN_ROWS 16  // query rows per workgroup (one MFMA column tile)
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// bf16 path.  Cache layouts: K [B, Hkv, S, D], V transposed [B, Hkv, D, S] (V^T), so both MFMA operands
+// come straight from HBM as 16-byte vectors:
+//   S^T[pos][q] = K Q^T        v_mfma_f32_16x16x32_bf16, A = K rows (16 positions x 32 d), B = Q^T
+//   O^T[d][q]  += V^T P^T      v_mfma_f32_16x16x32_bf16, A = V^T (16 d x 32 positions), B = P^T
+// Each lane owns one query column (l16), so the running max / row sum are lane-local up to xor shuffles
+// over the four 16-lane groups.  A 32-position step uses two S^T sub-tiles whose MFMA rows are mapped to
+// positions so that lane group g holds positions 8g .. 8g+7 of the step: exactly the 8 consecutive
+// positions its P^T fragment and its 16-byte V^T load need.
+// The 4 waves of a workgroup take the 64-position tiles of the work item's KV range round robin
+// (tile index within the split mod 4) and are merged in wave order through LDS.
 template <int D>
 __global__ __launch_bounds__(256) void attn_bf16_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
     const int32_t* __restrict__ blocks, const int32_t* __restrict__ works, uint16_t* __restrict__ out,
     float* __restrict__ o_part, float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
-  constexpr int KSTEPS = D / 32;   // 16x16x32 k-steps over the head dim
-  constexpr int CT = D / 16;       // 16-wide d tiles of O^T
-  constexpr int LDS_STRIDE = D + 8;  // bf16 elements per staged row (16 B pad against bank conflicts)
-  constexpr int CHUNKS = ATTN_TILE * D / 8;  // 16-byte chunks per K (or V) tile
-  constexpr int PER_THREAD = CHUNKS / 256;
-  static_assert(CHUNKS % 256 == 0, "tile must split evenly over 256 threads");
-
-  __shared__ __attribute__((aligned(16))) uint16_t sK[ATTN_TILE * LDS_STRIDE];
-  __shared__ __attribute__((aligned(16))) uint16_t sV[ATTN_TILE * LDS_STRIDE];
+  constexpr int KSTEPS = D / 32;
+  constexpr int CT = D / 16;
+  __shared__ float s_ml[4][2][ATTN_ROWS];
+  __shared__ __attribute__((aligned(16))) float s_o[4][ATTN_ROWS][D + 4];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63;
@@ -60,107 +59,76 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
   const int32_t* bm = blocks + (long)blk * 4;
   const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
 
-  // ---- this lane's query column
-  const int rloc = wave * 16 + l16;  // row within the group
-  const bool qvalid = rloc < nrows;
-  const int r = row0 + (qvalid ? rloc : 0);
+  const bool qvalid = l16 < nrows;
+  const int r = row0 + (qvalid ? l16 : 0);
   const int t = r / G, g = r - t * G;
   const int qpos = pos0 + t;
   const int hq = kvh * G + g;
-  const bool wave_active = wave * 16 < nrows;
 
   lsk_bf16x8 qf[KSTEPS];
   {
     const uint16_t* qrow = q + ((long)(q_start + t) * Hq + hq) * D;
 #pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) {
-      if (qvalid) {
-        qf[j] = *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg);
-      } else {
-        qf[j] = (lsk_bf16x8){};
-      }
-    }
+    for (int j = 0; j < KSTEPS; ++j) qf[j] = qvalid ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
   }
-
   lsk_f32x4 oacc[CT];
 #pragma unroll
   for (int c = 0; c < CT; ++c) oacc[c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
-  const long head_base = ((long)crow * Hkv + kvh) * (long)S * D;
-  const uint16_t* kbase = kc + head_base;
-  const uint16_t* vbase = vc + head_base;
+  const long head = (long)crow * Hkv + kvh;
+  const uint16_t* kbase = kc + head * (long)S * D;
+  const uint16_t* vbase = vt + head * (long)D * S;
+  // MFMA row l16 of S^T sub-tile a <-> position 8 * (l16 / 4) + 4 * a + l16 % 4 of the 32-position step
+  const int krow0 = 8 * (l16 >> 2) + (l16 & 3);
 
-  uint4 kreg[PER_THREAD], vreg[PER_THREAD];
-  auto load_tile = [&](int tb) {
+  for (int tb = kv_lo + ATTN_TILE * wave; tb < kv_hi; tb += 4 * ATTN_TILE) {
 #pragma unroll
-    for (int u = 0; u < PER_THREAD; ++u) {
-      const int c = tid + 256 * u;
-      const int p = c / (D / 8), d8 = c - p * (D / 8);
-      if (tb + p < kv_hi) {
-        const long off = (long)(tb + p) * D + d8 * 8;
-        kreg[u] = *(const uint4*)(kbase + off);
-        vreg[u] = *(const uint4*)(vbase + off);
-      } else {
-        kreg[u] = make_uint4(0, 0, 0, 0);
-        vreg[u] = make_uint4(0, 0, 0, 0);
+    for (int h = 0; h < 2; ++h) {
+      const int sb = tb + 32 * h;  // 32-position step
+      if (sb >= kv_hi) break;
+      lsk_bf16x8 kf[2][KSTEPS];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const uint16_t* krow = kbase + (long)(sb + krow0 + 4 * a) * D + 8 * lg;
+#pragma unroll
+        for (int j = 0; j < KSTEPS; ++j) kf[a][j] = *(const lsk_bf16x8*)(krow + 32 * j);
       }
-    }
-  };
-
-  load_tile(kv_lo);
-  for (int tb = kv_lo; tb < kv_hi; tb += ATTN_TILE) {
-    __syncthreads();  // previous tile fully consumed
+      lsk_bf16x8 vf[CT];
 #pragma unroll
-    for (int u = 0; u < PER_THREAD; ++u) {
-      const int c = tid + 256 * u;
-      const int p = c / (D / 8), d8 = c - p * (D / 8);
-      *(uint4*)(sK + p * LDS_STRIDE + d8 * 8) = kreg[u];
-      *(uint4*)(sV + p * LDS_STRIDE + d8 * 8) = vreg[u];
-    }
-    __syncthreads();
-    if (tb + ATTN_TILE < kv_hi) load_tile(tb + ATTN_TILE);  // in flight during the compute below
-
-    if (wave_active) {
-      // ---- S^T tile: 4 sub-tiles of 16 positions x 16 queries
-      lsk_f32x4 sacc[4];
+      for (int c = 0; c < CT; ++c) vf[c] = *(const lsk_bf16x8*)(vbase + (long)(16 * c + l16) * S + sb + 8 * lg);
+      lsk_f32x4 sacc[2];
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        sacc[p] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
-        const uint16_t* krow = sK + (16 * p + l16) * LDS_STRIDE + 8 * lg;
+      for (int a = 0; a < 2; ++a) {
+        sacc[a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < KSTEPS; ++j) {
-          const lsk_bf16x8 kf = *(const lsk_bf16x8*)(krow + 32 * j);
-          sacc[p] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qf[j], sacc[p], 0, 0, 0);
-        }
+        for (int j = 0; j < KSTEPS; ++j)
+          sacc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[j], sacc[a], 0, 0, 0);
       }
-      // ---- online softmax (log2 domain), lane-local per query column
-      float sv[4][4];
+      // sacc[a][i] <-> position sb + 8 lg + 4 a + i, query l16
+      float sv[8];
       float mt = -INFINITY;
 #pragma unroll
-      for (int p = 0; p < 4; ++p)
+      for (int a = 0; a < 2; ++a)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int kp = tb + 16 * p + 4 * lg + i;
+          const int kp = sb + 8 * lg + 4 * a + i;
           const bool ok = qvalid && kp < kv_hi && kp <= qpos;
-          const float s = ok ? sacc[p][i] * scale_log2 : -INFINITY;
-          sv[p][i] = s;
-          mt = fmaxf(mt, s);
+          const float sc = ok ? sacc[a][i] * scale_log2 : -INFINITY;
+          sv[4 * a + i] = sc;
+          mt = fmaxf(mt, sc);
         }
       mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
       mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
       const float m_new = fmaxf(m_run, mt);
       const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
       float rs = 0.f;
-      lsk_s16x4 pb[4];
+      lsk_bf16x8 pb;
 #pragma unroll
-      for (int p = 0; p < 4; ++p) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float e = (sv[p][i] == -INFINITY) ? 0.f : fast_exp2(sv[p][i] - m_new);
-          rs += e;
-          pb[p][i] = (short)f2bf(e);
-        }
+      for (int e = 0; e < 8; ++e) {
+        const float pe = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
+        rs += pe;
+        pb[e] = __builtin_bit_cast(__bf16, f2bf(pe));
       }
       rs += __shfl_xor(rs, 16, 64);
       rs += __shfl_xor(rs, 32, 64);
@@ -172,44 +140,44 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
         oacc[c][1] *= alpha;
         oacc[c][2] *= alpha;
         oacc[c][3] *= alpha;
-      }
-      // ---- O^T += V^T P^T
-#pragma unroll
-      for (int p = 0; p < 4; ++p) {
-        const uint16_t* vcol = sV + (16 * p + 4 * lg) * LDS_STRIDE + l16;
-#pragma unroll
-        for (int c = 0; c < CT; ++c) {
-          lsk_s16x4 va;
-          va[0] = (short)vcol[0 * LDS_STRIDE + 16 * c];
-          va[1] = (short)vcol[1 * LDS_STRIDE + 16 * c];
-          va[2] = (short)vcol[2 * LDS_STRIDE + 16 * c];
-          va[3] = (short)vcol[3 * LDS_STRIDE + 16 * c];
-          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb[p], oacc[c], 0, 0, 0);
-        }
+        oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[c], pb, oacc[c], 0, 0, 0);
       }
     }
   }
-
-  if (!wave_active || !qvalid) return;
-  if (part < 0) {
-    uint16_t* orow = out + (long)(q_start + t) * Hq * D + (long)hq * D;
+  // ---- merge the four waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
+  if (lg == 0) {
+    s_ml[wave][0][l16] = m_run;
+    s_ml[wave][1][l16] = l_run;
+  }
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      ushort4 o;
-      o.x = f2bf(oacc[c][0] / l_run);
-      o.y = f2bf(oacc[c][1] / l_run);
-      o.z = f2bf(oacc[c][2] / l_run);
-      o.w = f2bf(oacc[c][3] / l_run);
-      *(ushort4*)(orow + 16 * c + 4 * lg) = o;
+  for (int c = 0; c < CT; ++c)
+    *(float4*)(&s_o[wave][l16][16 * c + 4 * lg]) = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+  __syncthreads();
+  for (int e = tid; e < ATTN_ROWS * D; e += 256) {
+    const int qr = e / D, d = e - qr * D;
+    if (qr >= nrows) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][0][qr]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float mw = s_ml[w][0][qr];
+      const float ew = (mw == -INFINITY) ? 0.f : ((mw == M) ? 1.f : fast_exp2(mw - M));
+      L = L + ew * s_ml[w][1][qr];
+      O = O + ew * s_o[w][qr][d];
     }
-  } else {
-    const long slot = ((long)part * Hkv + kvh) * ATTN_ROWS + rloc;
-    float* op = o_part + slot * D;
-#pragma unroll
-    for (int c = 0; c < CT; ++c) *(float4*)(op + 16 * c + 4 * lg) = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
-    if (lg == 0) {
-      ml_part[slot * 2 + 0] = m_run;
-      ml_part[slot * 2 + 1] = l_run;
+    const int rr = row0 + qr;
+    const int tt = rr / G, gg = rr - tt * G;
+    if (part < 0) {
+      out[(long)(q_start + tt) * Hq * D + (long)(kvh * G + gg) * D + d] = f2bf(O / L);
+    } else {
+      const long slot = ((long)part * Hkv + kvh) * ATTN_ROWS + qr;
+      o_part[slot * D + d] = O;
+      if (d == 0) {
+        ml_part[slot * 2 + 0] = M;
+        ml_part[slot * 2 + 1] = L;
+      }
     }
   }
 }
@@ -248,7 +216,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
 }
 
 // ----------------------------------------------------------------------------- fp32 path
-// Straightforward per-query kernel for fp32 models (parity runs): one wave per query row, the
+// Straightforward per-query kernel for fp32 models (parity runs; V cache transposed as in the bf16
+// path): one wave per query row, the
 // row's positions 0..qpos in 64-position chunks (lane = position), online softmax with exact expf,
 // O[d] accumulated over the chunk's positions in order.  Fixed order per query -> batch invariant.
 template <int D>
@@ -304,7 +273,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
         const int d = lane + 64 * i;
         if (d < D) {
           float acc = o[i] * alpha;
-          for (int j = 0; j < nvalid; ++j) acc += sp[wave][j] * vc[head_base + (long)(base + j) * D + d];
+          for (int j = 0; j < nvalid; ++j) acc += sp[wave][j] * vc[head_base + (long)d * S + base + j];
           o[i] = acc;
         }
       }

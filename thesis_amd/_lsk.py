@@ -20,7 +20,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 512          # LSK_ATTN_SPLIT
-ATTN_ROWS = 64            # query rows per attention workgroup
+ATTN_ROWS = 16            # query rows per attention workgroup
 ABI_VERSION = 1
 
 # name -> (restype, argtypes)
@@ -130,6 +130,7 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | No
 
 
 def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads, head_dim):
+    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
     _dev(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
     N = qkv.shape[0]
     B, Hkv, S, D = kcache.shape
@@ -141,6 +142,7 @@ def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32,
 
 
 def kv_append(k, v, kcache, vcache, rows_i32, pos_i32):
+    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
     _dev(k, v, kcache, vcache, rows_i32, pos_i32)
     B, Hkv, S, D = kcache.shape
     assert k.is_contiguous() and v.is_contiguous() and k.shape[1:] == (Hkv, D)
@@ -171,7 +173,9 @@ def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
                 scale, workspace=None):
+    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
+    assert vcache.shape == (kcache.shape[0], kcache.shape[1], kcache.shape[3], kcache.shape[2])
     B, Hkv, S, D = kcache.shape
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
@@ -253,6 +257,7 @@ class NativeModel:
         lib = load()
         _dev(cos_tab, sin_tab)
         B, Hkv, S, D = kcache[0].shape
+        assert vcache[0].shape == (B, Hkv, D, S) and vcache[0].is_contiguous(), "V cache must be [B, Hkv, D, S]"
         self._keep = (layers, kcache, vcache, cos_tab, sin_tab)
         h = lib.lsk_model_create(
             dtype_code(dtype), n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, float(eps),

@@ -143,15 +143,23 @@ class LayerWeights:
 
 
 class KVCache:
-    """Static contiguous KV cache: k_all / v_all [L, max_batch, Hkv, max_seq, D]; k[i] / v[i] are views."""
+    """Static contiguous KV cache.  K: k_all [L, max_batch, Hkv, max_seq, D]; V is stored transposed,
+    vt_all [L, max_batch, Hkv, D, max_seq], so the attention kernel reads V^T fragments as 16-byte vectors.
+    k[i] / v[i] / v_all present the reference's [max_batch, Hkv, max_seq, D] view of both."""
 
     def __init__(self, cfg: ModelConfig, max_batch: int, max_seq: int, dtype, device):
         self.max_batch, self.max_seq = max_batch, max_seq
-        shape = (cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq, cfg.head_dim)
-        self.k_all = torch.zeros(shape, dtype=dtype, device=device)
-        self.v_all = torch.zeros(shape, dtype=dtype, device=device)
+        self.k_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq, cfg.head_dim), dtype=dtype,
+                                 device=device)
+        self.vt_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, cfg.head_dim, max_seq), dtype=dtype,
+                                  device=device)
         self.k = [self.k_all[i] for i in range(cfg.n_layers)]
-        self.v = [self.v_all[i] for i in range(cfg.n_layers)]
+        self.vt = [self.vt_all[i] for i in range(cfg.n_layers)]
+        self.v = [t.transpose(-1, -2) for t in self.vt]
+
+    @property
+    def v_all(self) -> Tensor:
+        return self.vt_all.transpose(-1, -2)
 
     @staticmethod
     def bytes_needed(cfg: ModelConfig, max_batch: int, max_seq: int, dtype_bytes: int = 2) -> int:
@@ -287,7 +295,7 @@ class LayerSkipLlama:
         c = self.cfg
         self.native = _lsk.NativeModel(self.dtype, c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim,
                                        c.intermediate_size, c.vocab_size, c.norm_eps, self.layers, self.cache.k,
-                                       self.cache.v, self.rope_cos, self.rope_sin)
+                                       self.cache.vt, self.rope_cos, self.rope_sin)
         return self.cache
 
     def free_cache(self) -> None:
