@@ -7,7 +7,8 @@
 // Layouts
 //   q      [N, Hq, D]            (packed token axis; RoPE applied)
 //   K      [B, Hkv, S, D]        (per layer; the KVCache layout of common/model.py:171-183)
-//   V      [B, Hkv, D, S]        (stored transposed: position-contiguous rows per (head, d))
+//   V      [B, Hkv, S/32, D, 32] (stored in 32-position blocks, each block transposed: element (pos, d)
+//                                 at ((pos / 32) * D + d) * 32 + pos % 32 within a (row, head) stripe)
 //   out    [N, Hq * D]
 //   blocks int32 [nb][4] = {q_start, pos0, T, row}
 //   works  int32 [n_work][8] = {blk, row0, nrows, kv_lo, kv_hi, part, 0, 0}
@@ -20,6 +21,9 @@
 // orders depend only on absolute positions, so the result for a query never depends on which other
 // tokens share its block or batch (batch invariance: a T = 1 decode query and the same query inside a
 // T = 9 verify block give bitwise identical outputs).
+#include <algorithm>
+#include <vector>
+
 #include "lsk_common.h"
 #include "../include/lsk.h"
 
@@ -28,8 +32,9 @@
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// bf16 path.  Cache layouts: K [B, Hkv, S, D], V transposed [B, Hkv, D, S] (V^T), so both MFMA operands
-// come straight from HBM as 16-byte vectors:
+// bf16 path.  Cache layouts: K [B, Hkv, S, D], V in transposed 32-position blocks (V^T per block), so both
+// MFMA operands come straight from HBM as 16-byte vectors and one V^T fragment load of a wave is 1 KiB
+// contiguous:
 //   S^T[pos][q] = K Q^T        v_mfma_f32_16x16x32_bf16, A = K rows (16 positions x 32 d), B = Q^T
 //   O^T[d][q]  += V^T P^T      v_mfma_f32_16x16x32_bf16, A = V^T (16 d x 32 positions), B = P^T
 // Each lane owns one query column (l16), so the running max / row sum are lane-local up to xor shuffles
@@ -56,6 +61,7 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
 
   const int32_t* wk = works + (long)blockIdx.x * 8;
   const int blk = wk[0], row0 = wk[1], nrows = wk[2], kv_lo = wk[3], kv_hi = wk[4], part = wk[5];
+  if (nrows <= 0) return;  // padding item of the XCD-aware work order
   const int32_t* bm = blocks + (long)blk * 4;
   const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
 
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
       }
       lsk_bf16x8 vf[CT];
 #pragma unroll
-      for (int c = 0; c < CT; ++c) vf[c] = *(const lsk_bf16x8*)(vbase + (long)(16 * c + l16) * S + sb + 8 * lg);
+      for (int c = 0; c < CT; ++c) vf[c] = *(const lsk_bf16x8*)(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
       lsk_f32x4 sacc[2];
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
@@ -216,8 +222,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
 }
 
 // ----------------------------------------------------------------------------- fp32 path
-// Straightforward per-query kernel for fp32 models (parity runs; V cache transposed as in the bf16
-// path): one wave per query row, the
+// Straightforward per-query kernel for fp32 models (parity runs; V cache in the same blocked transposed
+// layout as the bf16 path): one wave per query row, the
 // row's positions 0..qpos in 64-position chunks (lane = position), online softmax with exact expf,
 // O[d] accumulated over the chunk's positions in order.  Fixed order per query -> batch invariant.
 template <int D>
@@ -273,7 +279,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
         const int d = lane + 64 * i;
         if (d < D) {
           float acc = o[i] * alpha;
-          for (int j = 0; j < nvalid; ++j) acc += sp[wave][j] * vc[head_base + (long)d * S + base + j];
+          for (int j = 0; j < nvalid; ++j) acc += sp[wave][j] * vc[head_base + (long)base * D + d * 32 + j % 32 + (j / 32) * 32 * D];
           o[i] = acc;
         }
       }
@@ -290,38 +296,82 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
 
 // ----------------------------------------------------------------------------- host planner
 
+// Work order: a "family" is the set of 16-row query tiles of one (block, split); its tiles read the same
+// K/V.  Workgroups are dealt to the 8 XCDs round robin by launch index, so siblings are placed 8 launch
+// slots apart (same XCD, dispatched together: the second read hits that XCD's L2).  Families are sorted
+// by size and dealt in chunks of 8; slots of shorter families in a chunk are padding items (nrows = 0).
 extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
                              int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts) {
   LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
   LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && split % ATTN_TILE == 0, LSK_ESHAPE,
               "lsk_attn_plan: bad arguments (split must be a positive multiple of %d)", ATTN_TILE);
-  int nw = 0, ng = 0, np = 0;
+  struct Item { int b, row0, nrows, lo, hi, part; };
+  std::vector<std::vector<Item>> fams;
+  int ng = 0, np = 0;
   for (int b = 0; b < nb; ++b) {
     const int pos0 = blocks[b * 4 + 1], T = blocks[b * 4 + 2];
     LSK_REQUIRE(T >= 0 && pos0 >= 0, LSK_ESHAPE, "lsk_attn_plan: block %d has T=%d pos0=%d", b, T, pos0);
     const int rows = T * group;
-    for (int row0 = 0; row0 < rows; row0 += ATTN_ROWS) {
-      const int nrows = (rows - row0) < ATTN_ROWS ? (rows - row0) : ATTN_ROWS;
-      const int t_last = (row0 + nrows - 1) / group;
-      const long kv_end = (long)pos0 + t_last + 1;
-      const int ns = (int)((kv_end + split - 1) / split);
-      if (ns > 1) {
+    const int nq = (rows + ATTN_ROWS - 1) / ATTN_ROWS;
+    if (nq == 0) continue;
+    // KV range of the family = the longest tile's range; each tile uses its own end
+    std::vector<int> ns_of(nq);
+    int ns_max = 0;
+    for (int qt = 0; qt < nq; ++qt) {
+      const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+      const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
+      ns_of[qt] = (int)((kv_end + split - 1) / split);
+      ns_max = ns_of[qt] > ns_max ? ns_of[qt] : ns_max;
+    }
+    std::vector<int> part_first(nq);
+    for (int qt = 0; qt < nq; ++qt) {
+      const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+      if (ns_of[qt] > 1) {
         LSK_REQUIRE(groups != nullptr && ng < max_groups, LSK_EWORKSPACE, "lsk_attn_plan: too many combine groups");
         int32_t* gp = groups + (long)ng * 8;
-        gp[0] = b; gp[1] = row0; gp[2] = nrows; gp[3] = np; gp[4] = ns; gp[5] = gp[6] = gp[7] = 0;
+        gp[0] = b; gp[1] = row0; gp[2] = nrows; gp[3] = np; gp[4] = ns_of[qt]; gp[5] = gp[6] = gp[7] = 0;
         ++ng;
+        part_first[qt] = np;
+        np += ns_of[qt];
+      } else {
+        part_first[qt] = -1;
       }
-      for (int s = 0; s < ns; ++s) {
-        LSK_REQUIRE(nw < max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
-        int32_t* wp = works + (long)nw * 8;
-        const long lo = (long)s * split;
-        const long hi = (lo + split < kv_end) ? lo + split : kv_end;
-        wp[0] = b; wp[1] = row0; wp[2] = nrows; wp[3] = (int32_t)lo; wp[4] = (int32_t)hi;
-        wp[5] = ns > 1 ? np + s : -1; wp[6] = wp[7] = 0;
-        ++nw;
-      }
-      if (ns > 1) np += ns;
     }
+    for (int sidx = 0; sidx < ns_max; ++sidx) {
+      std::vector<Item> fam;
+      for (int qt = 0; qt < nq; ++qt) {
+        if (sidx >= ns_of[qt]) continue;
+        const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+        const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
+        const long lo = (long)sidx * split;
+        const long hi = (lo + split < kv_end) ? lo + split : kv_end;
+        fam.push_back({b, row0, nrows, (int)lo, (int)hi, part_first[qt] >= 0 ? part_first[qt] + sidx : -1});
+      }
+      fams.push_back(std::move(fam));
+    }
+  }
+  std::stable_sort(fams.begin(), fams.end(),
+                   [](const std::vector<Item>& a, const std::vector<Item>& b) { return a.size() > b.size(); });
+  int nw = 0;
+  auto emit = [&](const Item* it) -> int {
+    LSK_REQUIRE(nw < max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
+    int32_t* wp = works + (long)nw * 8;
+    if (it) { wp[0] = it->b; wp[1] = it->row0; wp[2] = it->nrows; wp[3] = it->lo; wp[4] = it->hi; wp[5] = it->part; }
+    else { wp[0] = 0; wp[1] = 0; wp[2] = 0; wp[3] = 0; wp[4] = 0; wp[5] = -1; }
+    wp[6] = wp[7] = 0;
+    ++nw;
+    return 0;
+  };
+  for (size_t c0 = 0; c0 < fams.size(); c0 += 8) {
+    const size_t c1 = c0 + 8 < fams.size() ? c0 + 8 : fams.size();
+    size_t depth = 0;
+    for (size_t f = c0; f < c1; ++f) depth = fams[f].size() > depth ? fams[f].size() : depth;
+    for (size_t k = 0; k < depth; ++k)
+      for (size_t f = c0; f < c0 + 8; ++f) {
+        const Item* it = (f < c1 && k < fams[f].size()) ? &fams[f][k] : nullptr;
+        if (it == nullptr && (depth == 1 || f >= c1)) continue;  // no sibling to align: skip the padding
+        if (emit(it)) return LSK_EWORKSPACE;
+      }
   }
   *n_works = nw;
   *n_groups = ng;

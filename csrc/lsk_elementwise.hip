@@ -178,8 +178,8 @@ extern "C" int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, i
 // rnd(sum_s P[s][t][:]) (the QKV GEMM's K-slice partials, s in order) instead of a materialised qkv.
 // q heads:  q_out[t, h]                       = rope(q)   (common/model.py:148-150)
 // k heads:  kcache[row_t, h, pos_t]           = rope(k)   (solutions/packed.py:180)
-// v heads:  vcache[row_t, h, :, pos_t]        = v         (solutions/packed.py:181; V stored transposed,
-//                                                        [B, Hkv, D, S], for the attention kernel)
+// v heads:  V cache (row_t, h, pos_t)          = v         (solutions/packed.py:181; V stored in
+//                                                        transposed 32-position blocks [B, Hkv, S/32, D, 32])
 // rope(x)[j]       = x[j] * c[j]       + (-x[j+D/2]) * s[j]
 // rope(x)[j + D/2] = x[j+D/2] * c[j+D/2] + x[j] * s[j+D/2]
 // with c, s = the fp32 tables at pos_t stored to the model dtype first (solutions/packed.py:106-107)
@@ -221,10 +221,10 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
       Elem<T>::st(dst + j, o1);
       Elem<T>::st(dst + j + half, o2);
     } else {
-      // V cache is stored transposed, [B, Hkv, D, S]
-      T* dst = vc + ((long)row * Hkv + (h - Hq - Hkv)) * (long)D * max_seq + p;
-      Elem<T>::st(dst + (long)j * max_seq, qkv_val(qkv, P, KS, pstride, base + j));
-      Elem<T>::st(dst + (long)(j + half) * max_seq, qkv_val(qkv, P, KS, pstride, base + j + half));
+      // V cache: 32-position blocks, each transposed ([B, Hkv, S/32, D, 32])
+      T* dst = vc + ((long)row * Hkv + (h - Hq - Hkv)) * (long)D * max_seq + (long)(p >> 5) * 32 * D + (p & 31);
+      Elem<T>::st(dst + (long)j * 32, qkv_val(qkv, P, KS, pstride, base + j));
+      Elem<T>::st(dst + (long)(j + half) * 32, qkv_val(qkv, P, KS, pstride, base + j + half));
     }
   }
 }
@@ -281,8 +281,8 @@ extern "C" int lsk_rope_append_partial(int dtype, const float* partials, int ks,
                      n_tokens, n_heads, n_kv_heads, head_dim, max_batch, max_seq, stream);
 }
 
-// Plain KV append (no RoPE): kcache[row_t, h, pos_t] = k[t, h]; vcache[row_t, h, :, pos_t] = v[t, h]
-// (V transposed, [B, Hkv, D, S]).
+// Plain KV append (no RoPE): kcache[row_t, h, pos_t] = k[t, h]; V cache (row_t, h, pos_t) = v[t, h]
+// (V in transposed 32-position blocks, [B, Hkv, S/32, D, 32]).
 // Used for inputs whose RoPE is already applied (solutions/packed.py:180-181 on its own).
 template <typename T>
 __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ k, const T* __restrict__ v,
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ k,
   for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) {
     const int hk = e / D, d = e - hk * D;
     kc[(((long)row * Hkv + hk) * max_seq + p) * D + d] = k[(long)t * Hkv * D + e];
-    vc[(((long)row * Hkv + hk) * D + d) * (long)max_seq + p] = v[(long)t * Hkv * D + e];
+    vc[((long)row * Hkv + hk) * (long)D * max_seq + (long)(p >> 5) * 32 * D + d * 32 + (p & 31)] = v[(long)t * Hkv * D + e];
   }
 }
 

@@ -40,15 +40,16 @@ int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, int n_rows, 
                 long ldo, void* stream);
 
 /* RoPE of q and k + KV append: qkv [N, (Hq+2Hkv)D] -> q_out [N, Hq, D], k into the K cache
- * [B, Hkv, S, D] and v into the V cache, which is stored transposed [B, Hkv, D, S], at (rows[t], pos[t]).  cos/sin tables: fp32 [tab_len, D] (device).
+ * [B, Hkv, S, D] and v into the V cache at (rows[t], pos[t]).  The V cache is stored in 32-position blocks,
+ * each block transposed: [B, Hkv, S/32, D, 32] (S a multiple of 64).  cos/sin tables: fp32 [tab_len, D] (device).
  * Replaces solutions/packed.py:176-181 (split, apply_rope, cache index_put) with
  * common/model.py:143-150 (apply_rope) and solutions/packed.py:106-107 (cos/sin gather + cast). */
 int lsk_rope_append(int dtype, const void* qkv, void* q_out, void* kcache, void* vcache, const float* cos_tab,
                     const float* sin_tab, int tab_len, const int32_t* rows, const int32_t* pos, int n_tokens,
                     int n_heads, int n_kv_heads, int head_dim, int max_batch, int max_seq, void* stream);
 
-/* KV append without RoPE: kcache[rows[t], :, pos[t]] = k[t]; vcache[rows[t], :, :, pos[t]] = v[t]
- * (K [B, Hkv, S, D], V transposed [B, Hkv, D, S]).
+/* KV append without RoPE: kcache[rows[t], :, pos[t]] = k[t]; V cache (rows[t], :, pos[t]) = v[t]
+ * (K [B, Hkv, S, D], V blocked-transposed [B, Hkv, S/32, D, 32]).
  * Replaces solutions/packed.py:180-181 and common/model.py:343-344. */
 int lsk_kv_append(int dtype, const void* k, const void* v, void* kcache, void* vcache, const int32_t* rows,
                   const int32_t* pos, int n_tokens, int n_kv_heads, int head_dim, int max_batch, int max_seq,
@@ -66,7 +67,7 @@ int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* 
 size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
 
 /* Ragged verify/decode attention: a query at position p of row r attends cache[r, :, 0..p].
- * q [N, Hq, D], K [B, Hkv, S, D], V transposed [B, Hkv, D, S], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
+ * q [N, Hq, D], K [B, Hkv, S, D], V blocked-transposed [B, Hkv, S/32, D, 32], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
  * Replaces solutions/packed.py:142-166 (_attend: per-bucket gather + masked SDPA + scatter)
  * and common/model.py:352-364 (the padded path's masked SDPA). */
 int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,

@@ -135,11 +135,11 @@ def test_rope_append_is_bit_exact(cuda, dtype, D):
     kc = torch.zeros(B, Hkv, S, D, dtype=dtype)
     vc = torch.zeros_like(kc)
     kd = kc.to(cuda)
-    vd = torch.zeros(B, Hkv, D, S, dtype=dtype, device=cuda)      # V cache storage is transposed
+    vd = torch.zeros(B, Hkv, S // 32, D, 32, dtype=dtype, device=cuda)      # blocked-transposed V storage
     q_out = torch.empty(N, Hq, D, dtype=dtype, device=cuda)
     lsk.rope_append(qkv.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda),
                     rows.to(torch.int32).to(cuda), pos.to(torch.int32).to(cuda), Hq, Hkv, D)
-    vd = vd.transpose(-1, -2)
+    vd = lsk.v_from_blocked(vd)
     c = cos[pos].to(dtype).unsqueeze(1)
     s = sin[pos].to(dtype).unsqueeze(1)
     q_ref = o_rope(qkv[:, :Hq * D].view(N, Hq, D), c, s)
@@ -162,11 +162,11 @@ def test_kv_append_is_bit_exact(cuda):
     pos = torch.randperm(S, generator=g)[:N]
     kc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
     vc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
-    kd, vd = kc.to(cuda), vc.transpose(-1, -2).contiguous().to(cuda)
+    kd, vd = kc.to(cuda), lsk.v_to_blocked(vc).to(cuda)
     lsk.kv_append(k.to(cuda), v.to(cuda), kd, vd, rows.to(torch.int32).to(cuda), pos.to(torch.int32).to(cuda))
     kc[rows, :, pos] = k
     vc[rows, :, pos] = v
-    assert torch.equal(kd.cpu(), kc) and torch.equal(vd.transpose(-1, -2).cpu(), vc)
+    assert torch.equal(kd.cpu(), kc) and torch.equal(lsk.v_from_blocked(vd).cpu(), vc)
 
 
 # ----------------------------------------------------------------------------- attention
@@ -195,7 +195,7 @@ def _run_attn(lsk, cuda, q, kc, vc, tab, split):
     out = torch.empty(q.shape[0], Hq * D, dtype=q.dtype, device=cuda)
     ws = torch.empty(max(lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=cuda)
     gdev = torch.from_numpy(groups).to(cuda) if len(groups) else None
-    lsk.ragged_attn(q.to(cuda), kc.to(cuda), vc.transpose(-1, -2).contiguous().to(cuda), torch.from_numpy(tab).to(cuda),
+    lsk.ragged_attn(q.to(cuda), kc.to(cuda), lsk.v_to_blocked(vc).to(cuda), torch.from_numpy(tab).to(cuda),
                     torch.from_numpy(works).to(cuda), len(works), gdev, len(groups), n_parts, out, Hq,
                     1.0 / math.sqrt(D), ws)
     return out.cpu()
@@ -363,11 +363,11 @@ def test_rope_append_partial_is_bit_exact(cuda):
     rows = torch.tensor([0, 1, 1, 0, 1])
     pos = torch.tensor([3, 9, 10, 4, 11])
     kd = torch.zeros(B, Hkv, S, D, dtype=BF16, device=cuda)
-    vd = torch.zeros(B, Hkv, D, S, dtype=BF16, device=cuda)
+    vd = torch.zeros(B, Hkv, S // 32, D, 32, dtype=BF16, device=cuda)
     q_out = torch.empty(N, Hq, D, dtype=BF16, device=cuda)
     lsk.rope_append_partial(P.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda), rows.to(torch.int32).to(cuda),
                             pos.to(torch.int32).to(cuda), Hq, Hkv, D)
-    vd = vd.transpose(-1, -2)
+    vd = lsk.v_from_blocked(vd)
     c, s = cos[pos].to(BF16).unsqueeze(1), sin[pos].to(BF16).unsqueeze(1)
     assert torch.equal(q_out.cpu(), o_rope(qkv[:, :Hq * D].view(N, Hq, D), c, s))
     kref = o_rope(qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D), c, s)

@@ -103,6 +103,18 @@ def _stream() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
+def v_to_blocked(v: torch.Tensor) -> torch.Tensor:
+    """[..., S, D] -> the V cache storage [..., S/32, D, 32] (32-position blocks, each transposed)."""
+    *lead, S, D = v.shape
+    return v.reshape(*lead, S // 32, 32, D).transpose(-1, -2).contiguous()
+
+
+def v_from_blocked(vb: torch.Tensor) -> torch.Tensor:
+    """V cache storage [..., S/32, D, 32] -> [..., S, D] (a copy)."""
+    *lead, nb, D, b = vb.shape
+    return vb.transpose(-1, -2).reshape(*lead, nb * b, D)
+
+
 def dtype_code(dtype: torch.dtype) -> int:
     if dtype == torch.bfloat16:
         return DTYPE_BF16
@@ -130,7 +142,7 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | No
 
 
 def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads, head_dim):
-    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
+    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
     N = qkv.shape[0]
     B, Hkv, S, D = kcache.shape
@@ -142,7 +154,7 @@ def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32,
 
 
 def kv_append(k, v, kcache, vcache, rows_i32, pos_i32):
-    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
+    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(k, v, kcache, vcache, rows_i32, pos_i32)
     B, Hkv, S, D = kcache.shape
     assert k.is_contiguous() and v.is_contiguous() and k.shape[1:] == (Hkv, D)
@@ -156,7 +168,7 @@ def attn_plan(blocks: np.ndarray, group: int, split: int):
     nb = blocks.shape[0]
     rows = int(((blocks[:, 2].astype(np.int64) * group + ATTN_ROWS - 1) // ATTN_ROWS).sum()) if nb else 0
     max_ctx = int((blocks[:, 1].astype(np.int64) + blocks[:, 2]).max()) if nb else 0
-    max_works = max(1, rows * max(1, (max_ctx + split - 1) // split))
+    max_works = 8 * max(1, rows * max(1, (max_ctx + split - 1) // split)) + 64   # XCD-order padding
     max_groups = max(1, rows)
     works = np.zeros((max_works, 8), dtype=np.int32)
     groups = np.zeros((max_groups, 8), dtype=np.int32)
@@ -173,9 +185,10 @@ def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
                 scale, workspace=None):
-    """kcache [B, Hkv, S, D]; vcache is the transposed V storage [B, Hkv, D, S]."""
+    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
-    assert vcache.shape == (kcache.shape[0], kcache.shape[1], kcache.shape[3], kcache.shape[2])
+    B_, H_, S_, D_ = kcache.shape
+    assert vcache.shape == (B_, H_, S_ // 32, D_, 32) and S_ % 64 == 0
     B, Hkv, S, D = kcache.shape
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
@@ -257,7 +270,8 @@ class NativeModel:
         lib = load()
         _dev(cos_tab, sin_tab)
         B, Hkv, S, D = kcache[0].shape
-        assert vcache[0].shape == (B, Hkv, D, S) and vcache[0].is_contiguous(), "V cache must be [B, Hkv, D, S]"
+        assert vcache[0].shape == (B, Hkv, S // 32, D, 32) and vcache[0].is_contiguous(), \
+            "V cache must be the blocked-transposed [B, Hkv, S/32, D, 32] storage"
         self._keep = (layers, kcache, vcache, cos_tab, sin_tab)
         h = lib.lsk_model_create(
             dtype_code(dtype), n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, float(eps),

@@ -142,24 +142,41 @@ class LayerWeights:
     ffn_norm: Tensor
 
 
+class _VLayers:
+    """cache.v[i]: layer i's V as the reference's [max_batch, Hkv, max_seq, D] tensor (a copy of the blocked
+    storage; for inspection, the kernels write the storage)."""
+
+    def __init__(self, cache):
+        self.cache = cache
+
+    def __getitem__(self, i):
+        return _lsk.v_from_blocked(self.cache.vb_all[i])
+
+    def __len__(self):
+        return self.cache.vb_all.shape[0]
+
+
 class KVCache:
-    """Static contiguous KV cache.  K: k_all [L, max_batch, Hkv, max_seq, D]; V is stored transposed,
-    vt_all [L, max_batch, Hkv, D, max_seq], so the attention kernel reads V^T fragments as 16-byte vectors.
-    k[i] / v[i] / v_all present the reference's [max_batch, Hkv, max_seq, D] view of both."""
+    """Static contiguous KV cache.  K: k_all [L, max_batch, Hkv, max_seq, D] (k[i] = layer views).
+    V is stored in 32-position blocks, each transposed: vb_all [L, max_batch, Hkv, max_seq/32, D, 32], so the
+    attention kernel reads V^T MFMA fragments as contiguous 16-byte vectors (1 KiB per wave load).
+    v[i] / v_all present V in the reference's [max_batch, Hkv, max_seq, D] layout (copies)."""
 
     def __init__(self, cfg: ModelConfig, max_batch: int, max_seq: int, dtype, device):
+        if max_seq % 64:
+            raise ValueError("max_seq must be a multiple of 64")
         self.max_batch, self.max_seq = max_batch, max_seq
         self.k_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq, cfg.head_dim), dtype=dtype,
                                  device=device)
-        self.vt_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, cfg.head_dim, max_seq), dtype=dtype,
-                                  device=device)
+        self.vb_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq // 32, cfg.head_dim, 32),
+                                  dtype=dtype, device=device)
         self.k = [self.k_all[i] for i in range(cfg.n_layers)]
-        self.vt = [self.vt_all[i] for i in range(cfg.n_layers)]
-        self.v = [t.transpose(-1, -2) for t in self.vt]
+        self.vb = [self.vb_all[i] for i in range(cfg.n_layers)]
+        self.v = _VLayers(self)
 
     @property
     def v_all(self) -> Tensor:
-        return self.vt_all.transpose(-1, -2)
+        return _lsk.v_from_blocked(self.vb_all)
 
     @staticmethod
     def bytes_needed(cfg: ModelConfig, max_batch: int, max_seq: int, dtype_bytes: int = 2) -> int:
@@ -295,7 +312,7 @@ class LayerSkipLlama:
         c = self.cfg
         self.native = _lsk.NativeModel(self.dtype, c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim,
                                        c.intermediate_size, c.vocab_size, c.norm_eps, self.layers, self.cache.k,
-                                       self.cache.vt, self.rope_cos, self.rope_sin)
+                                       self.cache.vb, self.rope_cos, self.rope_sin)
         return self.cache
 
     def free_cache(self) -> None:
