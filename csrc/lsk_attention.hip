@@ -29,6 +29,7 @@
 
 #define ATTN_TILE 64
 #define ATTN_ROWS 16  // query rows per workgroup (one MFMA column tile)
+#define ATTN_MAX_SPLITS 128
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
@@ -192,32 +193,55 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
 //   M = max_s m_s, w_s = exp2(m_s - M) (0 for an empty split, 1 when m_s == M),
 //   out = (sum_s w_s O_s) / (sum_s w_s l_s).
 // A group with a single non-empty split reduces to O_0 / l_0, exactly what the direct path stores.
+// The per-row weights and denominators are computed once into LDS; the O partials stream as float4.
 template <typename T, int D>
 __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __restrict__ blocks,
                                                            const int32_t* __restrict__ groups,
                                                            const float* __restrict__ o_part,
                                                            const float* __restrict__ ml_part, T* __restrict__ out,
                                                            int G, int Hkv) {
+  __shared__ float s_w[ATTN_ROWS][ATTN_MAX_SPLITS];
+  __shared__ float s_L[ATTN_ROWS];
   const int32_t* gp = groups + (long)blockIdx.x * 8;
   const int blk = gp[0], row0 = gp[1], nrows = gp[2], pf = gp[3], ns = gp[4];
   const int kvh = blockIdx.y;
   const int Hq = Hkv * G;
   const int q_start = blocks[(long)blk * 4 + 0];
-  for (int e = threadIdx.x; e < nrows * D; e += blockDim.x) {
-    const int rl = e / D, d = e - rl * D;
+  const int tid = threadIdx.x;
+  if (tid < nrows) {
+    const int rl = tid;
     float M = -INFINITY;
     for (int s = 0; s < ns; ++s) M = fmaxf(M, ml_part[(((long)(pf + s) * Hkv + kvh) * ATTN_ROWS + rl) * 2]);
-    float L = 0.f, O = 0.f;
+    float L = 0.f;
     for (int s = 0; s < ns; ++s) {
       const long slot = ((long)(pf + s) * Hkv + kvh) * ATTN_ROWS + rl;
       const float ms = ml_part[slot * 2], ls = ml_part[slot * 2 + 1];
       const float w = (ms == -INFINITY) ? 0.f : ((ms == M) ? 1.f : fast_exp2(ms - M));
+      s_w[rl][s] = w;
       L = L + w * ls;
-      O = O + w * o_part[slot * D + d];
     }
+    s_L[rl] = L;
+  }
+  __syncthreads();
+  for (int e = tid; e < nrows * (D / 4); e += 256) {
+    const int rl = e / (D / 4), d4 = e - rl * (D / 4);
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s = 0; s < ns; ++s) {
+      const float w = s_w[rl][s];
+      const float4 v = *(const float4*)(o_part + (((long)(pf + s) * Hkv + kvh) * ATTN_ROWS + rl) * D + 4 * d4);
+      O.x = O.x + w * v.x;
+      O.y = O.y + w * v.y;
+      O.z = O.z + w * v.z;
+      O.w = O.w + w * v.w;
+    }
+    const float L = s_L[rl];
     const int r = row0 + rl;
     const int t = r / G, g = r - t * G;
-    Elem<T>::st(out + (long)(q_start + t) * Hq * D + (long)(kvh * G + g) * D + d, O / L);
+    T* o = out + (long)(q_start + t) * Hq * D + (long)(kvh * G + g) * D + 4 * d4;
+    Elem<T>::st(o + 0, O.x / L);
+    Elem<T>::st(o + 1, O.y / L);
+    Elem<T>::st(o + 2, O.z / L);
+    Elem<T>::st(o + 3, O.w / L);
   }
 }
 
@@ -321,6 +345,8 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
       const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
       const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
       ns_of[qt] = (int)((kv_end + split - 1) / split);
+      LSK_REQUIRE(ns_of[qt] <= ATTN_MAX_SPLITS || split >= (1 << 29), LSK_ESHAPE,
+                  "lsk_attn_plan: %d splits of %d positions exceed %d", ns_of[qt], split, ATTN_MAX_SPLITS);
       ns_max = ns_of[qt] > ns_max ? ns_of[qt] : ns_max;
     }
     std::vector<int> part_first(nq);

@@ -19,7 +19,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblsk.so"
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
-ATTN_SPLIT = 512          # LSK_ATTN_SPLIT
+ATTN_SPLIT = 1024         # LSK_ATTN_SPLIT
 ATTN_ROWS = 16            # query rows per attention workgroup
 ABI_VERSION = 1
 
