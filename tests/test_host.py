@@ -1,0 +1,306 @@
+"""Host-side logic and the C ABI without a GPU (CPU only).
+
+  * liblsk.so loads and exports every entry point include/lsk.h declares; argument errors are reported
+    on the host with negative codes before any launch
+  * the attention planner (a host function of the ABI): every query row's KV range [0, pos + 1) is
+    covered exactly once, split boundaries are absolute, siblings sit 8 launch slots apart
+  * the GEMM plan depends on the weight shape only
+  * the product's build_packed equals the oracle's (block order, offsets, buckets, accounting) on
+    random block sets, and rejects bad bucketing / out-of-range blocks
+  * schedulers / cost model against brute force and the reference's unit cases
+  * model config parsing, the product never importing the oracle, bench.py refusing --gpus > 1
+"""
+
+from __future__ import annotations
+
+import ctypes
+import re
+import subprocess
+import sys
+from pathlib import Path
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _lsk():
+    from thesis_amd import _lsk
+
+    _lsk.load()
+    return _lsk
+
+
+def test_library_exports_every_declared_entry_point():
+    lsk = _lsk()
+    header = (ROOT / "include" / "lsk.h").read_text()
+    declared = set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(lsk_[a-z_0-9]+)\s*\(", header, re.M))
+    assert len(declared) >= 20
+    lib = ctypes.CDLL(str(lsk.LIB_PATH))
+    missing = [n for n in sorted(declared) if not hasattr(lib, n)]
+    assert not missing, missing
+    assert declared == set(lsk.EXPORTS), declared ^ set(lsk.EXPORTS)
+    assert lsk.load().lsk_abi_version() == lsk.ABI_VERSION
+
+
+def test_argument_errors_are_reported_on_the_host():
+    lsk = _lsk()
+    lib = lsk.load()
+    assert lib.lsk_gemm(1, None, 64, None, 64, None, 64, None, 0, 4, 64, 64, 0, 0, None) == -1
+    rc = lib.lsk_gemm(1, 8, 64, 8, 64, 8, 64, None, 0, 4, 64, 63, 0, 0, None)       # K % 32 != 0
+    assert rc == -2 and b"K" in lib.lsk_last_error()
+    assert lib.lsk_gemm(1, 8, 64, 8, 64, 8, 64, None, 0, 4, 64, 64, 7, 0, None) == -1  # bad epilogue
+    assert lib.lsk_gemm(5, 8, 64, 8, 64, 8, 64, None, 0, 4, 64, 64, 0, 0, None) == -3  # bad dtype
+    assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
+    assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
+
+
+def _plan(blocks, G, split):
+    return _lsk().attn_plan(np.asarray(blocks, dtype=np.int32), G, split)
+
+
+@pytest.mark.parametrize("G,split", [(4, 1024), (1, 1024), (4, 64), (8, 512)])
+def test_attention_plan_covers_every_row_once(G, split):
+    rng = np.random.default_rng(G + split)
+    nb = 40
+    T = rng.integers(1, 20, nb)
+    pos0 = rng.integers(0, 3000, nb)
+    q_start = np.concatenate([[0], np.cumsum(T)[:-1]])
+    blocks = np.stack([q_start, pos0, T, rng.integers(0, 8, nb)], axis=1)
+    works, groups, n_parts = _plan(blocks, G, split)
+    cover = {}
+    parts_seen = []
+    for w in works:
+        b, row0, nrows, lo, hi, part = (int(v) for v in w[:6])
+        if nrows == 0:
+            continue                                       # padding slot of the XCD order
+        assert lo % split == 0 and hi - lo <= split and lo < hi
+        for r in range(row0, row0 + nrows):
+            cover.setdefault((b, r), []).append((lo, hi))
+        if part >= 0:
+            parts_seen.append(part)
+    assert len(parts_seen) == len(set(parts_seen)) == n_parts
+    for b in range(nb):
+        for r in range(T[b] * G):
+            ivs = sorted(cover[(b, r)])
+            tile = r // 16
+            t_last = min(tile * 16 + 15, T[b] * G - 1) // G
+            end = pos0[b] + t_last + 1                     # the 16-row tile's KV range
+            assert ivs[0][0] == 0 and ivs[-1][1] == end
+            assert all(ivs[i][1] == ivs[i + 1][0] for i in range(len(ivs) - 1))
+    for gp in groups:
+        assert gp[4] >= 2 and gp[3] + gp[4] <= n_parts
+
+
+def test_attention_plan_places_sibling_tiles_eight_slots_apart():
+    blocks = [(0, 50 * i, 9, i) for i in range(16)]         # 36 rows -> 3 sibling tiles, KV < 1024: 1 split
+    works, _, _ = _plan(blocks, 4, 1024)
+    where = {}
+    for idx, w in enumerate(works):
+        if w[2] > 0:
+            where.setdefault(int(w[0]), []).append(idx)
+    for b, idxs in where.items():
+        assert len(idxs) == 3 and all((j - idxs[0]) % 8 == 0 for j in idxs), (b, idxs)
+
+
+def test_gemm_plan_depends_on_shape_only():
+    lsk = _lsk()
+    assert lsk.gemm_plan(28672, 4096) == (4, 1)       # w13 of the 8B shape: wide tiles, whole K
+    assert lsk.gemm_plan(128256, 4096) == (4, 1)      # LM head
+    ns, ks = lsk.gemm_plan(4096, 14336)               # w2: split K
+    assert ns == 2 and ks >= 2 and 14336 % ks == 0 and (14336 // ks) % 128 == 0
+    ns, ks = lsk.gemm_plan(6144, 4096)
+    assert ns == 2 and 4096 % ks == 0
+
+
+# ----------------------------------------------------------------------------- packed metadata
+
+def _stub_model(max_batch=8, max_seq=4096, dtype=torch.bfloat16, G=4):
+    from thesis_amd.common.model import ModelConfig
+
+    cfg = ModelConfig(vocab_size=64, dim=64, n_layers=2, n_heads=G, n_kv_heads=1, head_dim=128,
+                      intermediate_size=128)
+    rope = torch.zeros(max_seq, 128)
+    return SimpleNamespace(device=torch.device("cpu"), dtype=dtype, group=G, cfg=cfg, rope_cos=rope,
+                           rope_sin=rope, cache=SimpleNamespace(max_batch=max_batch, max_seq=max_seq))
+
+
+@pytest.mark.parametrize("bucketing", ["exact", "pad"])
+def test_build_packed_matches_oracle(bucketing):
+    import oracle.model as om
+    from thesis_amd.solutions.packed import Block, build_packed
+
+    rng = np.random.default_rng(1)
+    ocfg = om.OracleConfig(64, 64, 1, 4, 1, 16, 64)
+    orc = om.OracleLlama(ocfg, om.random_weights(ocfg), dtype=torch.float32, max_seq=4096)
+    orc.allocate_cache(8, 4096)
+    stub = _stub_model()
+    for trial in range(20):
+        n = int(rng.integers(1, 9))
+        rows = rng.choice(8, n, replace=False)
+        spec = [(int(r), int(rng.integers(0, 3000)), int(rng.integers(1, 10))) for r in rows]
+        pb = build_packed(stub, [Block(*s) for s in spec], bucketing)
+        ob = om.build_packed(orc, [om.OBlock(*s) for s in spec], bucketing)
+        assert [(b.row, b.pos0, b.T) for b in pb.blocks] == [(b.row, b.pos0, b.T) for b in ob.blocks]
+        assert list(pb.offsets) == list(ob.offsets) and pb.n_tokens == ob.n_tokens
+        assert pb.pos_h.tolist() == ob.pos.tolist() and pb.rows_h.tolist() == ob.rows.tolist()
+        assert (pb.kv_read, pb.kv_read_padded, pb.kv_gathered) == (ob.kv_read, ob.kv_read_padded, ob.kv_gathered)
+        assert [(x.start, x.end, x.b, x.T, x.L, x.b0, x.rows is None) for x in pb.buckets] == \
+               [(x.start, x.end, x.b, x.T, x.L, x.b0, x.rows is None) for x in ob.buckets]
+        for x, y in zip(pb.buckets, ob.buckets):
+            assert (x.pad_index is None) == (y.pad_index is None)
+            if x.pad_index is not None:
+                assert torch.equal(x.pad_index, y.pad_index)
+
+
+def test_build_packed_rejects_bad_input():
+    from thesis_amd.solutions.packed import Block, build_packed
+
+    stub = _stub_model(max_batch=2, max_seq=128)
+    with pytest.raises(ValueError):
+        build_packed(stub, [Block(0, 0, 1)], "ragged")
+    with pytest.raises(ValueError):
+        build_packed(stub, [Block(2, 0, 1)])
+    with pytest.raises(ValueError):
+        build_packed(stub, [Block(0, 120, 9)])
+
+
+def test_packed_metadata_layout():
+    from thesis_amd.solutions.packed import Block, build_packed
+
+    stub = _stub_model()
+    pb = build_packed(stub, [Block(3, 10, 2), Block(1, 700, 1)])
+    meta = pb.meta.numpy()
+    N = pb.n_tokens
+    assert meta[:N].tolist() == pb.rows_h.tolist() and meta[N:2 * N].tolist() == pb.pos_h.tolist()
+    blk = meta[2 * N:2 * N + 4 * pb.nb].reshape(-1, 4)
+    assert blk.tolist() == [[0, 700, 1, 1], [1, 10, 2, 3]]
+    assert meta.size == 2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups)
+    # algorithmic attention work of one launch: K+V of every attended position, Q read and O written
+    assert pb.attn_bytes == (701 + 12) * 1 * 128 * 2 * 2 + N * 4 * 128 * 2 * 2
+
+
+# ----------------------------------------------------------------------------- host policies
+
+def test_expected_token_targets_match_brute_force():
+    from thesis_amd.solutions.schedulers import best_gamma_expected, expected_token_targets
+
+    rng = np.random.default_rng(0)
+    a = rng.uniform(0.05, 0.97, 300)
+    c = rng.uniform(0.02, 0.6, 300)
+    got = expected_token_targets(a, c, 1, 12)
+    ref = np.array([max(1, best_gamma_expected(ai, ci, 12)) for ai, ci in zip(a, c)])
+    assert (np.abs(got - ref) <= 1).mean() > 0.97 and (got == ref).mean() > 0.8
+
+
+def test_m1_rule_direction():
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import synthetic_cost_model
+    from thesis_amd.solutions.schedulers import M1Scheduler
+
+    cm = synthetic_cost_model(PRESETS["llama3-8b"])
+    B = 16
+    d, ctx, dec = np.full(B, 2), np.full(B, 1000), np.ones(B, dtype=bool)
+    s = M1Scheduler(B, cm, 3, d_max=16)
+    s.ema.alpha[:] = 0.98
+    assert not s.decide(d, ctx, dec, 2).any()
+    s.ema.alpha[:] = 0.05
+    assert s.decide(d, ctx, dec, 2).all()
+    d2 = d.copy()
+    d2[0] = 16
+    s.ema.alpha[:] = 0.98
+    assert s.decide(d2, ctx, dec, 2).all()
+
+
+def test_fixed_and_aspire_schedulers():
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import mi355x_cost_model
+    from thesis_amd.solutions.schedulers import make_scheduler
+
+    cm = mi355x_cost_model(PRESETS["llama3-8b"])
+    f = make_scheduler("fixed", 4, cm, 8, gamma=3, d_max=8)
+    dec = np.ones(4, dtype=bool)
+    d = np.array([0, 1, 3, 8])
+    assert f.decide(d, d * 0 + 100, dec, 1).tolist() == [False, False, False, True]
+    assert f.decide(d, d * 0 + 100, dec, 3).tolist() == [False, True, True, True]
+    a = make_scheduler("aspire", 4, cm, 8, d_max=8, min_draft=2, initial_draft=3)
+    v = a.decide(np.array([1, 2, 3, 8]), np.full(4, 500), dec, 0)
+    assert not v[0] and v[3]                             # below the [2, 8] floor never verifies; d_max forces
+    with pytest.raises(ValueError):
+        make_scheduler("nope", 4, cm, 8)
+
+
+def test_cost_model_formula():
+    from thesis_amd.common.model import ModelConfig
+    from thesis_amd.solutions.cost_model import GPUParams, ModelDims, RooflineCostModel
+
+    cfg = ModelConfig(vocab_size=1000, dim=64, n_layers=4, n_heads=4, n_kv_heads=2, head_dim=16,
+                      intermediate_size=128)
+    dims = ModelDims.from_config(cfg)
+    gpu = GPUParams(bw=1e6, flops=1e8, t_op=0.01, n_op_layer=50, n_op_bucket=10, n_op_head=8, n_op_segment=5)
+    cm = RooflineCostModel(gpu, dims, n_max=64)
+    W, P = dims.layer_bytes, dims.layer_params
+    for n in (1, 10, 64, 200):
+        assert np.isclose(cm.layer_gemm_ms(n), max(W / gpu.bw, 2 * P * n / gpu.flops))
+    t = cm.t_segment(3, 10, 500, buckets=2)
+    manual = 3 * (max(W / gpu.bw, 2 * P * 10 / gpu.flops) + 500 * dims.kv_bytes_per_pos / gpu.bw + 60 * 0.01) + 0.05
+    assert np.isclose(t, manual)
+
+
+def test_config_parsing_old_and_new_formats(tmp_path):
+    import json
+
+    from thesis_amd.common.model import ModelConfig
+
+    d = tmp_path / "old"
+    d.mkdir()
+    (d / "config.json").write_text(json.dumps({
+        "vocab_size": 10, "hidden_size": 8, "num_hidden_layers": 2, "num_attention_heads": 2,
+        "intermediate_size": 16, "rope_theta": 500000.0,
+        "rope_scaling": {"rope_type": "llama3", "factor": 32.0}, "eos_token_id": [5, 6]}))
+    c = ModelConfig.from_hf_dir(d)
+    assert c.rope_theta == 500000.0 and c.rope_scaling["factor"] == 32.0 and c.eos_token_ids == (5, 6)
+    d2 = tmp_path / "new"
+    d2.mkdir()
+    (d2 / "config.json").write_text(json.dumps({
+        "vocab_size": 10, "hidden_size": 8, "num_hidden_layers": 2, "num_attention_heads": 2,
+        "intermediate_size": 16, "rope_parameters": {"rope_type": "default", "rope_theta": 1234.0}}))
+    c2 = ModelConfig.from_hf_dir(d2)
+    assert c2.rope_theta == 1234.0 and c2.rope_scaling is None
+
+
+def test_rope_tables_equal_the_oracle_tables():
+    import oracle.model as om
+    from thesis_amd.common.model import PRESETS, build_rope_cache
+
+    c = PRESETS["llama3.2-1b"]
+    cos, sin = build_rope_cache(c, 300, "cpu")
+    oc = om.OracleConfig(c.vocab_size, c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate_size,
+                         rope_theta=c.rope_theta, rope_scaling=c.rope_scaling)
+    ocos, osin = om.rope_tables(oc, 300)
+    assert torch.equal(cos, ocos) and torch.equal(sin, osin)
+
+
+def test_product_does_not_import_the_oracle():
+    for p in (ROOT / "thesis_amd").rglob("*.py"):
+        src = p.read_text()
+        assert not re.search(r"^\s*(from|import)\s+oracle\b", src, re.M), p
+
+
+def test_model_refuses_cpu():
+    from thesis_amd import _lsk
+    from thesis_amd.common.model import LayerSkipLlama, ModelConfig
+
+    cfg = ModelConfig(vocab_size=64, dim=64, n_layers=1, n_heads=4, n_kv_heads=2, head_dim=16, intermediate_size=128)
+    with pytest.raises(_lsk.LskError):
+        LayerSkipLlama(cfg, None, [], None, None, "cpu", torch.float32, 64)
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 2 and "one GPU" in r.stderr
