@@ -37,6 +37,8 @@ sys.path.insert(0, str(ROOT))
 METRIC = "generated tokens/s at 1 GPU (8B-shape, B=32); verify-attn HBM GB/s % of peak"
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
+# HBM bytes per launch of each kernel class, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this benchmark
+TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_8b_b32_traffic.md"
 
 
 def log(*a):
@@ -73,6 +75,22 @@ def engine_step(eng) -> int:
     return committed
 
 
+def calibration_copy(mib: int) -> None:
+    """One plain copy of `mib` MiB (lsk_copy_rows, 16 KiB rows) before the timed steps: the reference
+    size for scaling rocprofv3's FETCH_SIZE / WRITE_SIZE counters, and the marker after which
+    thesis_amd.prof_summary counts dispatches."""
+    from thesis_amd import _lsk
+
+    n = mib * 64
+    src = torch.empty(n, 16384, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    _lsk.copy_rows(dst, None, src, None, n)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def run_main(args):
     from thesis_amd import _lsk
 
@@ -85,6 +103,8 @@ def run_main(args):
     eng.measuring = True
     for _ in range(args.warmup):
         engine_step(eng)
+    if args.copy_calib_mib > 0:
+        calibration_copy(args.copy_calib_mib)
     eng.trace = []
     torch.cuda.synchronize()
     t1 = time.perf_counter()
@@ -109,7 +129,48 @@ def run_main(args):
             engine_step(eng)
         prof = _lsk.Profiler.collect()
         _lsk.Profiler.enable(False)
-    return cfg, model, eng, committed, elapsed, trace, prof
+    replay = replay_w13(model, trace, eng.k, args.replay_steps) if args.replay_steps > 0 else {}
+    return cfg, model, eng, committed, elapsed, trace, prof, replay
+
+
+def replay_w13(model, trace: list, k: int, n_steps: int) -> dict:
+    """Average launch duration of the FFN up-projection GEMM (w13 = [gate; up], silu-mul epilogue, the
+    largest kernel class of the step) over the launches the first `n_steps` timed steps made: the same
+    token counts (shallow segment through layers [0, k), deep segment through [k, L)) and each layer's
+    own weights, issued back to back on the engine's stream between one pair of HIP events.  Events
+    around every single launch would add their own dispatch overhead (a few microseconds) to each."""
+    from thesis_amd import _lsk
+
+    c = model.cfg
+    seq = []
+    for st in trace[:n_steps]:
+        seq += [(len(st["sh"]), i) for i in range(k)]
+        if st["dp"]:
+            seq += [(sum(b[2] for b in st["dp"]), i) for i in range(k, c.n_layers)]
+    if not seq:
+        return {}
+    m_max = max(m for m, _ in seq)
+    g = torch.Generator(device=model.device).manual_seed(1)
+    a = torch.empty(m_max, c.dim, dtype=model.dtype, device=model.device).normal_(generator=g)
+    h = torch.empty(m_max, c.intermediate_size, dtype=model.dtype, device=model.device)
+
+    def run():
+        for m, i in seq:
+            _lsk.gemm(a[:m], model.layers[i].w13, h[:m], epilogue=_lsk.EPI_SILU_MUL)
+
+    run()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    run()
+    e1.record()
+    torch.cuda.synchronize()
+    us = 1e3 * e0.elapsed_time(e1) / len(seq)
+    es = model.dtype.itemsize if hasattr(model.dtype, "itemsize") else 2
+    alg = float(np.mean([es * (2.0 * c.intermediate_size * c.dim + m * c.dim + m * c.intermediate_size)
+                         for m, _ in seq]))
+    return {"launches": len(seq), "avg_us": round(us, 2), "bytes_per_launch": alg,
+            "token_counts": sorted(set(m for m, _ in seq))}
 
 
 def summarize_kernels(prof: dict) -> dict:
@@ -276,37 +337,57 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--profile-steps", type=int, default=40)
     ap.add_argument("--attn-iters", type=int, default=50)
+    ap.add_argument("--replay-steps", type=int, default=20,
+                    help="timed steps whose w13 GEMM launches are replayed for the roofline figure")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--check-attn", action="store_true")
+    ap.add_argument("--attn-only", action="store_true", help="only the verify-attention microbenchmark")
+    ap.add_argument("--copy-calib-mib", type=int, default=0,
+                    help="plain copy of this many MiB before the timed steps (rocprofv3 counter calibration)")
     ap.add_argument("--out", type=str, default=None, help="also write the JSON line to this file")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (requested --gpus {args.gpus}); "
-              "the packed forward shards by request, see DESIGN.md", file=sys.stderr)
+              "the packed forward would shard by request (data parallel over slots)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         sys.exit(2)
 
-    cfg, model, eng, committed, elapsed, trace, prof = run_main(args)
+    if args.attn_only:
+        torch.cuda.set_device(0)
+        if args.copy_calib_mib > 0:
+            calibration_copy(args.copy_calib_mib)
+        txt = json.dumps({"verify_attn": run_attention_bench(args)})
+        print(txt, flush=True)
+        if args.out:
+            Path(args.out).parent.mkdir(parents=True, exist_ok=True)
+            Path(args.out).write_text(txt + "\n")
+        return
+    cfg, model, eng, committed, elapsed, trace, prof, replay = run_main(args)
     kernels = summarize_kernels(prof)
     del model, eng
     torch.cuda.empty_cache()
     attn = None if args.no_attn else run_attention_bench(args)
 
-    # dominant kernel class of the decode step (largest total time in the profiling pass)
+    # roofline of the largest kernel class of the decode step: the w13 GEMM (weight stream, HBM-bound at
+    # these token counts); its average launch duration comes from the back-to-back replay above
     roofline = None
-    if kernels:
-        dom = max(kernels, key=lambda n: kernels[n]["total_ms"])
-        kd = kernels[dom]
-        bound = "hbm" if kd["hbm_frac"] >= kd["mfma_frac"] else "mfma"
-        ach = kd["achieved_GBs"] if bound == "hbm" else kd["achieved_TFLOPs"]
-        peak = HBM_PEAK_GBS if bound == "hbm" else BF16_PEAK_TFLOPS
-        roofline = {"kernel": dom, "bound": bound, "achieved": ach, "peak": peak,
-                    "unit": "GB/s" if bound == "hbm" else "TFLOP/s", "frac": round(ach / peak, 4),
-                    "traffic": None, "avg_launch_us": kd["avg_us"], "bytes_per_launch": kd["bytes_per_launch"]}
+    if replay:
+        from thesis_amd.prof_summary import read_traffic
+
+        b, us = replay["bytes_per_launch"], replay["avg_us"]
+        ach = b / (us * 1e-6) / 1e9
+        traffic = read_traffic(TRAFFIC_SUMMARY, "gemm_w13")
+        roofline = {"kernel": "gemm_w13 (gemm_bf16_kernel, silu-mul epilogue)", "bound": "hbm",
+                    "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_launch_us": us,
+                    "bytes_per_launch": b, "launches_timed": replay["launches"],
+                    "token_counts": replay["token_counts"]}
+        if traffic is not None:
+            roofline["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
 
     line = {
@@ -326,6 +407,7 @@ def main():
     txt = json.dumps(line)
     print(txt, flush=True)
     if args.out:
+        Path(args.out).parent.mkdir(parents=True, exist_ok=True)
         Path(args.out).write_text(txt + "\n")
 
 

@@ -304,3 +304,38 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 2 and "one GPU" in r.stderr
+
+
+def test_rocprof_summary_counts_after_the_calibration_copy(tmp_path, capsys):
+    from thesis_amd import prof_summary as ps
+
+    hdr = ["Correlation_Id", "Dispatch_Id", "Agent_Id", "Queue_Id", "Process_Id", "Thread_Id", "Grid_Size",
+           "Kernel_Id", "Kernel_Name", "Workgroup_Size", "LDS_Block_Size", "Scratch_Size", "VGPR_Count",
+           "Accum_VGPR_Count", "SGPR_Count", "Counter_Name", "Counter_Value", "Start_Timestamp", "End_Timestamp"]
+
+    def write(path, counter, rows):
+        import csv
+
+        with open(path, "w", newline="") as f:
+            w = csv.writer(f)
+            w.writerow(hdr)
+            for d, (name, grid, val) in enumerate(rows, 1):
+                w.writerow([d, d, "Agent 1", 1, 1, 1, grid, 1, name, 256, 0, 0, 0, 0, 0, counter, val, 0, 1])
+
+    gemm = "void gemm_bf16_kernel<2, 2, 2>(unsigned short const*, long)"
+    copy = "void copy_rows_kernel(unsigned char*, long const*)"
+    big = 65536 * 256
+    # before the marker: ignored; the marker copy of 1024 MiB reads 512 MiB on FETCH_SIZE (factor 2)
+    write(tmp_path / "f.csv", "FETCH_SIZE", [(gemm, 448 * 256, 1.0), (copy, big, 512 * 1024.0),
+                                             (gemm, 448 * 256, 100.0), (gemm, 448 * 256, 300.0)])
+    write(tmp_path / "w.csv", "WRITE_SIZE", [(copy, big, 1024 * 1024.0), (gemm, 448 * 256, 8.0),
+                                             (gemm, 448 * 256, 8.0)])
+    ps.main(["pmc", str(tmp_path / "f.csv"), str(tmp_path / "w.csv"), "--calib-mib", "1024"])
+    out = capsys.readouterr().out
+    (tmp_path / "t.md").write_text(out)
+    # fetch: mean 200 KiB x 2; write: 8 KiB x 1
+    assert ps.read_traffic(tmp_path / "t.md", "gemm_w13") == 200 * 1024 * 2 + 8 * 1024
+    assert ps.short_name(gemm) == "gemm_bf16_kernel<2, 2, 2>"
+    assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 192 * 256) == "gemm_qkv"
+    assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 128 * 256) == "gemm_o_w2"
+    assert ps.classify("attn_bf16_kernel<128>") == "attention"
