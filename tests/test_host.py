@@ -339,3 +339,67 @@ def test_rocprof_summary_counts_after_the_calibration_copy(tmp_path, capsys):
     assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 192 * 256) == "gemm_qkv"
     assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 128 * 256) == "gemm_o_w2"
     assert ps.classify("attn_bf16_kernel<128>") == "attention"
+
+
+def test_method_registry():
+    from thesis_amd.common.methods import METHODS, MethodSpec, load_plugins, register
+
+    assert load_plugins(["no_such_module_here"]) == ["thesis_amd.solutions"]
+    assert {"autoregressive", "sync_layerskip", "eesd"} <= set(METHODS)
+    with pytest.raises(ValueError):
+        register(MethodSpec("eesd", "again", lambda g: None, lambda *a: None))
+    spec = METHODS["sync_layerskip"]
+    a = SimpleNamespace(exit_layer=8, gamma=4)
+    assert spec.tag(a) == "-k8-g4" and spec.step_tokens(a) == 5 and spec.params(a) == {"exit_layer": 8, "gamma": 4}
+
+
+def test_sample_tokens_semantics():
+    from thesis_amd.common.engine import sample_tokens
+
+    logits = torch.tensor([[0.0, 3.0, 3.0, 1.0], [5.0, 0.0, 0.0, 0.0]])
+    assert sample_tokens(logits, 0.0, 0, 1.0).tolist() == [1, 0]            # greedy: first index on ties
+    g = torch.Generator().manual_seed(0)
+    draws = torch.stack([sample_tokens(logits, 1.0, 1, 1.0, g) for _ in range(50)])
+    assert set(draws[:, 1].tolist()) == {0} and set(draws[:, 0].tolist()) <= {1, 2}   # top-1 keeps the maxima
+    draws = torch.stack([sample_tokens(logits, 1.0, 0, 0.5, g) for _ in range(50)])
+    assert set(draws[:, 0].tolist()) <= {1, 2}                              # nucleus 0.5 drops the tail
+
+
+def test_decode_engine_driver_on_a_stub_model():
+    """Cyclic replay bookkeeping of DecodeEngine.run (warm-up completions, refill, static pass) with a
+    CPU stub: every step commits one token per active slot."""
+    from thesis_amd.common.data import Prompt
+    from thesis_amd.common.engine import DecodeEngine, RunConfig, StepRecord
+
+    class Stub:
+        device = torch.device("cpu")
+
+        def allocate_cache(self, b, s):
+            self.cache = SimpleNamespace(max_seq=s)
+
+        def prefill(self, tokens, slot, capture_exits=False):
+            return torch.nn.functional.one_hot(torch.tensor(len(tokens) % 7), 7).float(), None
+
+    class Counting(DecodeEngine):
+        def _iteration(self, measured):
+            c = 0
+            for i in self._active():
+                s = self.slots[i]
+                s.pos += 1
+                c += self._commit(i, [s.pos % 7])
+            self.records.append(StepRecord("ar", 1.0, len(self._active()), 0, 0, 0, measured))
+            return c
+
+    prompts = [Prompt(f"p{i}", list(range(3 + i))) for i in range(5)]
+    eng = Counting(Stub(), 2, 16, 4, (), ignore_eos=True)
+    res = eng.run(prompts, RunConfig(mode="static", keep_outputs=True))
+    assert res["metrics"]["stop_reason"] == "pool_exhausted"
+    assert sorted(c["pid"] for c in res["completions"]) == [f"p{i}" for i in range(5)]
+    assert all(c["generated"] == 4 and c["finish_reason"] == "length" for c in res["completions"])
+    assert res["metrics"]["measured_tokens"] == 5 * 3                    # first tokens come from prefill
+    eng = Counting(Stub(), 2, 16, 4, (), ignore_eos=True)
+    res = eng.run(prompts, RunConfig(mode="cyclic", warmup_samples=2, warmup_per_slot=1.0, converge=False,
+                                     max_eval_samples=6, converge_min_samples=1, min_eval_per_slot=0.0))
+    assert res["metrics"]["stop_reason"] == "max_eval_samples"
+    assert res["metrics"]["evaluated_completions"] == 6
+    assert sum(1 for c in res["completions"] if not c["measured"]) == 2

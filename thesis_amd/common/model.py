@@ -408,8 +408,13 @@ class LayerSkipLlama:
 
         b, T, dim = h.shape
         x = h.reshape(b * T, dim).contiguous()
-        if layer_hook is None and capture is None:
-            return packed_layers(self, x, ctx.pb, start, end).view(b, T, dim)
+        if layer_hook is None:
+            if capture is None:
+                return packed_layers(self, x, ctx.pb, start, end).view(b, T, dim)
+            cap = {}
+            out = packed_layers(self, x, ctx.pb, start, end, cap, tuple(range(start + 1, end + 1)))
+            capture.extend(cap[j].view(b, T, dim) for j in range(start + 1, end + 1))
+            return out.view(b, T, dim)
         for i in range(start, end):
             if layer_hook is not None:
                 layer_hook(i, "pre")
