@@ -31,8 +31,16 @@
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// Two workgroups per CU where the tile's registers fit 256 VGPRs (two fragment buffers of 32 VGPRs
+// per weight row group and per token group, plus 4 accumulators per pair), else one.
 template <int NS, int MS, int EPI>
-__global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
+constexpr int gemm_occupancy() {
+  constexpr int NT = EPI == LSK_EPI_SILU_MUL ? 2 * NS : NS;
+  return 32 * (NT + MS) + 4 * NT * MS <= 240 ? 2 : 1;
+}
+
+template <int NS, int MS, int EPI>
+__global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI>())) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
                                                         const uint16_t* __restrict__ W, long ldw,
                                                         uint16_t* __restrict__ C, long ldc,
                                                         const uint16_t* __restrict__ R, long ldr,
@@ -43,7 +51,8 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: loop bounds and branches are scalar
   const int l16 = lane & 15, lg = lane >> 4;
   const int n0 = blockIdx.x * 16 * NS;
   const int m0 = blockIdx.y * 16 * MS;
@@ -74,39 +83,38 @@ __global__ __launch_bounds__(256) void gemm_bf16_kernel(const uint16_t* __restri
     for (int t = 0; t < MS; ++t) acc[a][t] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 
   const int nk32 = (k1 - k0) / 32;
-  const int nfull = nk32 / 4;  // full 128-element chunks of the slice
-  lsk_bf16x8 wf[2][4][NT], af[2][4][MS];
-  auto load = [&](int buf, int c) {
+  const int nfull = nk32 / 4;                                 // full 128-element chunks of the slice
+  const int my_n = nfull > wave ? (nfull - wave + 3) / 4 : 0;  // this wave's chunks: wave, wave + 4, ...
+  lsk_bf16x8 wA[4][NT], aA[4][MS], wB[4][NT], aB[4][MS];
+  auto load = [&](lsk_bf16x8 (&wf)[4][NT], lsk_bf16x8 (&af)[4][MS], int c) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const int k = c * 128 + ks * 32;
 #pragma unroll
-      for (int a = 0; a < NT; ++a) wf[buf][ks][a] = *(const lsk_bf16x8*)(wrow[a] + k);
+      for (int a = 0; a < NT; ++a) wf[ks][a] = *(const lsk_bf16x8*)(wrow[a] + k);
 #pragma unroll
-      for (int t = 0; t < MS; ++t) af[buf][ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
+      for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
     }
   };
-  auto comp = [&](int buf) {
+  auto comp = [&](lsk_bf16x8 (&wf)[4][NT], lsk_bf16x8 (&af)[4][MS]) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
       for (int a = 0; a < NT; ++a)
 #pragma unroll
         for (int t = 0; t < MS; ++t)
-          acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[buf][ks][a], af[buf][ks][t], acc[a][t], 0, 0, 0);
+          acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ks][a], af[ks][t], acc[a][t], 0, 0, 0);
   };
-  // full chunks c = wave, wave + 4, ... with the next chunk in flight while computing the current one
-  {
-    int c = wave;
-    if (c < nfull) load(0, c);
-    for (; c < nfull; c += 8) {
-      if (c + 4 < nfull) load(1, c + 4);
-      comp(0);
-      if (c + 4 >= nfull) break;
-      if (c + 8 < nfull) load(0, c + 8);
-      comp(1);
-    }
+  // two register buffers: the next chunk is in flight while the current one is multiplied
+  if (my_n > 0) load(wA, aA, wave);
+  int i = 0;
+  for (; i + 2 <= my_n; i += 2) {
+    load(wB, aB, wave + 4 * (i + 1));
+    comp(wA, aA);
+    if (i + 2 < my_n) load(wA, aA, wave + 4 * (i + 2));
+    comp(wB, aB);
   }
+  if (i < my_n) comp(wA, aA);
   // tail chunk (slice length % 128 != 0): owned by wave nfull % 4, k-steps in order
   if (wave == (nfull & 3)) {
     for (int kk = nfull * 4; kk < nk32; ++kk) {
@@ -296,9 +304,10 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 
 // ----------------------------------------------------------------------------- host side
 
-// Canonical tiling of a weight shape (N rows x K): NS = 4 when that still yields >= 256 row tiles,
-// else NS = 2 with KS = the smallest power of two giving >= 512 workgroups (K/KS a multiple of 128).
-// Depends on (N, K) only, never on M.
+// K-split plan of a weight shape (N rows x K); it fixes the reduction order of every output.  KS = 1
+// when the matrix has >= 256 row tiles of 64; otherwise KS = the smallest power of two giving >= 512
+// (32-row tile, slice) pairs, K / KS a multiple of 128.  ns_out is the row-tile width (in 16-row groups)
+// of that rule.  Depends on (N, K) only, never on M; a launch's own tile width (tile_ns) may follow M.
 extern "C" int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out) {
   LSK_REQUIRE(ns_out && ks_out && N > 0 && K > 0, LSK_EARG, "lsk_gemm_plan: bad arguments");
   int ns, ks = 1;
@@ -317,6 +326,18 @@ extern "C" int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out) {
 
 static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 
+// Tile width of a launch (16 * NS weight rows per workgroup; n = output columns, ffn for silu-mul).
+// Every row tile reads the whole M x K-slice activation block, so wide tiles cut those re-reads;
+// measured on MI355X at the 8B shapes, 64-row tiles beat 32-row ones for qkv, o, w2 and the head at
+// M <= 64, and 4+4 row groups for w13 at M <= 32 (2+2 above, where the token tile doubles).  The
+// reduction order of an output does not depend on NS or MS (only on K and the plan's KS), so the
+// tile may follow M without breaking batch invariance.
+static int tile_ns(int n, int M, int epi) {
+  int ns = (epi == LSK_EPI_SILU_MUL) ? (M <= 32 ? 4 : 2) : 4;
+  while (ns > 1 && n % (16 * ns) != 0) ns >>= 1;
+  return ns;
+}
+
 template <int NS, int MS>
 static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                         uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
@@ -325,7 +346,7 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
     gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
                                                                     ffn, kslice);
   else if (epi == LSK_EPI_SILU_MUL) {
-    if constexpr (NS <= 2)
+    if constexpr (NS <= 2 || MS <= 2)  // 2 * NS row groups: NS = 4 only with small token tiles (LDS, VGPRs)
       gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
                                                                       K, ffn, kslice);
   } else if (epi == EPI_PARTIAL)
@@ -369,11 +390,8 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
     LSK_REQUIRE(K % 32 == 0 && lda % 8 == 0 && ldw % 8 == 0, LSK_ESHAPE,
                 "lsk_gemm: bf16 needs K %% 32 == 0 and 16-byte aligned rows (K=%d)", K);
     LSK_REQUIRE(N % 16 == 0, LSK_ESHAPE, "lsk_gemm: bf16 needs N %% 16 == 0 (N=%d)", N);
-    // whole-K workgroups; the tile follows the plan of the weight shape (W rows = 2N for silu-mul)
-    int ns, ks;
-    lsk_gemm_plan(epilogue == LSK_EPI_SILU_MUL ? 2 * N : N, K, &ns, &ks);
-    if (epilogue == LSK_EPI_SILU_MUL) ns = ns >= 4 ? 2 : (ns == 2 ? 1 : 1);  // 2*NS rows per tile = the plan's width
-    while (N % (16 * ns) != 0) ns >>= 1;
+    // whole-K workgroups
+    const int ns = tile_ns(N, M, epilogue);
     const int ms = ms_for(M);
     dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), 1);
     dispatch_bf16(ns, ms, epilogue, grid, s, A, lda, W, ldw, C, ldc, R, ldr, nullptr, nullptr, nullptr, M, N, K, ffn, K);
@@ -404,9 +422,7 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
                   N % 16 == 0 && lda % 8 == 0 && ldw % 8 == 0,
               LSK_ESHAPE, "lsk_gemm_partial: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
-  int ns, kp;
-  lsk_gemm_plan(N, K, &ns, &kp);
-  while (N % (16 * ns) != 0) ns >>= 1;
+  const int ns = tile_ns(N, M, EPI_PARTIAL);
   const int ms = ms_for(M);
   dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks);
   dispatch_bf16(ns, ms, EPI_PARTIAL, grid, (hipStream_t)stream, A, lda, W, ldw, nullptr, 0, nullptr, 0, P, nullptr,

@@ -82,8 +82,9 @@ int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vc
 int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc, const void* R, long ldr,
              int M, int N, int K, int epilogue, int ffn, void* stream);
 
-/* Canonical bf16 tiling of a weight shape (N rows x K): 16*ns weight rows per workgroup and ks K slices.
- * Chosen from (N, K) only, so the per-element reduction order never depends on the token count M. */
+/* K-split plan of a bf16 weight shape (N rows x K): ks K slices (this fixes the per-element reduction
+ * order) and ns, the 16-row-group tile width the rule is based on.  Chosen from (N, K) only, so the
+ * reduction order never depends on the token count M; each launch picks its own tile width from M. */
 int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out);
 
 /* bf16 GEMM into fp32 K-slice partials: P[s][m][n] = sum over k in slice s of A[m][k] W[n][k], s < ks
