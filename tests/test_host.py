@@ -126,7 +126,8 @@ def _stub_model(max_batch=8, max_seq=4096, dtype=torch.bfloat16, G=4):
                       intermediate_size=128)
     rope = torch.zeros(max_seq, 128)
     return SimpleNamespace(device=torch.device("cpu"), dtype=dtype, group=G, cfg=cfg, rope_cos=rope,
-                           rope_sin=rope, cache=SimpleNamespace(max_batch=max_batch, max_seq=max_seq))
+                           rope_sin=rope, cache=SimpleNamespace(max_batch=max_batch, max_seq=max_seq,
+                                                                      attn_split=1024))
 
 
 @pytest.mark.parametrize("bucketing", ["exact", "pad"])

@@ -7,9 +7,10 @@ Same object surface as the reference model (common/model.py:218-403): `cfg`, `de
 `prefill()`, `n_layers`.  The padded per-call path (`make_ctx` / `forward_layers`) runs on the same
 ragged kernels as the packed path: a [b, T] call is b blocks of T tokens.
 
-HBM layout: K and V caches are two tensors [L, max_batch, Hkv, max_seq, D] (one allocation each;
-`cache.k[i]` is layer i's view), so one (request, KV head) is a contiguous max_seq x D stripe that
-the attention kernel streams once.  Weights keep the reference's fused row-major layout
+HBM layout: the K cache is one tensor [L, max_batch, Hkv, max_seq, D] (`cache.k[i]` is layer i's view),
+so one (request, KV head) is a contiguous max_seq x D stripe that the attention kernel streams once; the
+V cache holds the same stripes in transposed 32-position blocks [L, max_batch, Hkv, max_seq/32, D, 32]
+(`cache.v[i]` returns the reference layout as a copy).  Weights keep the reference's fused row-major layout
 (wqkv = [q; k; v], w13 = [gate; up], [out, in]).  The RoPE tables are built on the CPU with the
 reference's op sequence (common/model.py:113-140) and copied, so they are bitwise the CPU tables.
 """
@@ -173,6 +174,15 @@ class KVCache:
         self.k = [self.k_all[i] for i in range(cfg.n_layers)]
         self.vb = [self.vb_all[i] for i in range(cfg.n_layers)]
         self.v = _VLayers(self)
+        # KV positions per flash-decoding split of the attention kernel, fixed for the cache's lifetime so
+        # that a query's result never depends on the batch it is packed in.  Few (request, KV head) pairs
+        # leave most CUs idle with 1024-position splits, so small caches split every 256 positions
+        # (measured on MI355X: B=32 x 8 KV heads, 1-9 rows per request, 41 -> 33 us per launch); the fp32
+        # path does not split.
+        if dtype == torch.bfloat16:
+            self.attn_split = _lsk.ATTN_SPLIT if max_batch * cfg.n_kv_heads >= 1024 else 256
+        else:
+            self.attn_split = 1 << 30
 
     @property
     def v_all(self) -> Tensor:

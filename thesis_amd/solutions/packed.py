@@ -132,7 +132,7 @@ def pack_blocks(model, ordered: list, groups: Optional[list] = None, bucketing: 
     pos_h = np.repeat(pos0, Ts) + within
     rows_h = np.repeat(rws, Ts)
     blk = np.stack([offsets[:-1], pos0, Ts, rws], axis=1).astype(np.int32) if nb else np.zeros((0, 4), np.int32)
-    split = _lsk.ATTN_SPLIT if model.dtype == torch.bfloat16 else (1 << 30)
+    split = model.cache.attn_split
     works, grps, n_parts = _lsk.attn_plan(blk, model.group, split) if nb else (np.zeros((0, 8), np.int32),) * 2 + (0,)
     meta = np.concatenate([rows_h.astype(np.int32), pos_h.astype(np.int32), blk.ravel(), works.ravel(),
                            grps.ravel()]).astype(np.int32)
