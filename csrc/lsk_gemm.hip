@@ -33,20 +33,29 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 
 // Two workgroups per CU where the tile's registers fit 256 VGPRs (two fragment buffers of 32 VGPRs
 // per weight row group and per token group, plus 4 accumulators per pair), else one.
+// k-steps of 32 per pipeline unit: half chunks (64 k) for large tiles, whole 128-k chunks otherwise.
+// A unit is the granularity of the register double buffer only; every accumulator still sees the
+// k-steps in the same order (chunk by chunk, 32 at a time), so the result does not depend on it.
 template <int NS, int MS, int EPI>
-constexpr int gemm_occupancy() {
+constexpr int gemm_unit() {
   constexpr int NT = EPI == LSK_EPI_SILU_MUL ? 2 * NS : NS;
-  return 32 * (NT + MS) + 4 * NT * MS <= 240 ? 2 : 1;
+  return NT + MS > 6 ? 2 : 4;
 }
 
-template <int NS, int MS, int EPI>
-__global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI>())) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
+template <int NS, int MS, int EPI, int CK>
+constexpr int gemm_occupancy() {
+  constexpr int NT = EPI == LSK_EPI_SILU_MUL ? 2 * NS : NS;
+  return 8 * CK * (NT + MS) + 4 * NT * MS <= 240 ? 2 : 1;
+}
+
+template <int NS, int MS, int EPI, int CK = gemm_unit<NS, MS, EPI>()>
+__global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
                                                         const uint16_t* __restrict__ W, long ldw,
                                                         uint16_t* __restrict__ C, long ldc,
                                                         const uint16_t* __restrict__ R, long ldr,
                                                         float* __restrict__ P, float* __restrict__ amax_v,
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
-                                                        int kslice) {
+                                                        int kslice, int n_tiles, int m_tiles) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
@@ -54,8 +63,18 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI>())) void gemm_bf1
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: loop bounds and branches are scalar
   const int l16 = lane & 15, lg = lane >> 4;
-  const int n0 = blockIdx.x * 16 * NS;
-  const int m0 = blockIdx.y * 16 * MS;
+  // workgroup -> (row tile, token tile).  With several token tiles, the token tiles of one row tile
+  // take launch slots 8 apart: consecutive slots go to different XCDs, so they run side by side on one
+  // XCD and the second and later reads of the weight tile hit that XCD's L2 instead of HBM.
+  int tn = blockIdx.x, tm = 0;
+  if (m_tiles > 1) {
+    const int slot = blockIdx.x >> 3;
+    tm = slot % m_tiles;
+    tn = (slot / m_tiles) * 8 + (blockIdx.x & 7);
+    if (tn >= n_tiles) return;  // padding slot of the last group of 8
+  }
+  const int n0 = tn * 16 * NS;
+  const int m0 = tm * 16 * MS;
   const int s = blockIdx.z;
   const int k0 = s * kslice;
   const int k1 = min(K, k0 + kslice);
@@ -85,36 +104,40 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI>())) void gemm_bf1
   const int nk32 = (k1 - k0) / 32;
   const int nfull = nk32 / 4;                                 // full 128-element chunks of the slice
   const int my_n = nfull > wave ? (nfull - wave + 3) / 4 : 0;  // this wave's chunks: wave, wave + 4, ...
-  lsk_bf16x8 wA[4][NT], aA[4][MS], wB[4][NT], aB[4][MS];
-  auto load = [&](lsk_bf16x8 (&wf)[4][NT], lsk_bf16x8 (&af)[4][MS], int c) {
+  constexpr int UPC = 4 / CK;                                 // units per chunk
+  const int my_u = my_n * UPC;
+  lsk_bf16x8 wA[CK][NT], aA[CK][MS], wB[CK][NT], aB[CK][MS];
+  // unit u of this wave: chunk wave + 4 * (u / UPC), k-steps (u % UPC) * CK ...
+  auto load = [&](lsk_bf16x8 (&wf)[CK][NT], lsk_bf16x8 (&af)[CK][MS], int u) {
+    const int kb = (wave + 4 * (u / UPC)) * 128 + (u % UPC) * CK * 32;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const int k = c * 128 + ks * 32;
+    for (int ks = 0; ks < CK; ++ks) {
+      const int k = kb + ks * 32;
 #pragma unroll
       for (int a = 0; a < NT; ++a) wf[ks][a] = *(const lsk_bf16x8*)(wrow[a] + k);
 #pragma unroll
       for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
     }
   };
-  auto comp = [&](lsk_bf16x8 (&wf)[4][NT], lsk_bf16x8 (&af)[4][MS]) {
+  auto comp = [&](lsk_bf16x8 (&wf)[CK][NT], lsk_bf16x8 (&af)[CK][MS]) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+    for (int ks = 0; ks < CK; ++ks)
 #pragma unroll
       for (int a = 0; a < NT; ++a)
 #pragma unroll
         for (int t = 0; t < MS; ++t)
           acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ks][a], af[ks][t], acc[a][t], 0, 0, 0);
   };
-  // two register buffers: the next chunk is in flight while the current one is multiplied
-  if (my_n > 0) load(wA, aA, wave);
+  // two register buffers: the next unit is in flight while the current one is multiplied
+  if (my_u > 0) load(wA, aA, 0);
   int i = 0;
-  for (; i + 2 <= my_n; i += 2) {
-    load(wB, aB, wave + 4 * (i + 1));
+  for (; i + 2 <= my_u; i += 2) {
+    load(wB, aB, i + 1);
     comp(wA, aA);
-    if (i + 2 < my_n) load(wA, aA, wave + 4 * (i + 2));
+    if (i + 2 < my_u) load(wA, aA, i + 2);
     comp(wB, aB);
   }
-  if (i < my_n) comp(wA, aA);
+  if (i < my_u) comp(wA, aA);
   // tail chunk (slice length % 128 != 0): owned by wave nfull % 4, k-steps in order
   if (wave == (nfull & 3)) {
     for (int kk = nfull * 4; kk < nk32; ++kk) {
@@ -175,8 +198,8 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI>())) void gemm_bf1
             bi = n;
           }
         }
-        amax_v[(long)m * gridDim.x + blockIdx.x] = best;
-        amax_i[(long)m * gridDim.x + blockIdx.x] = bi;
+        amax_v[(long)m * n_tiles + tn] = best;
+        amax_i[(long)m * n_tiles + tn] = bi;
       }
     }
     return;
@@ -328,12 +351,14 @@ static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 
 // Tile width of a launch (16 * NS weight rows per workgroup; n = output columns, ffn for silu-mul).
 // Every row tile reads the whole M x K-slice activation block, so wide tiles cut those re-reads;
-// measured on MI355X at the 8B shapes, 64-row tiles beat 32-row ones for qkv, o, w2 and the head at
-// M <= 64, and 4+4 row groups for w13 at M <= 32 (2+2 above, where the token tile doubles).  The
-// reduction order of an output does not depend on NS or MS (only on K and the plan's KS), so the
-// tile may follow M without breaking batch invariance.
+// measured on MI355X at the 8B shapes (M = 32 .. 64), 64-row tiles beat 32-row ones for qkv, o, w2 and
+// the head, and 4 + 4 row groups (gate, up) for w13.  The reduction order of an output does not depend
+// on NS or MS (only on K and the plan's KS), so the tile could follow M without breaking batch
+// invariance.
 static int tile_ns(int n, int M, int epi) {
-  int ns = (epi == LSK_EPI_SILU_MUL) ? (M <= 32 ? 4 : 2) : 4;
+  (void)M;
+  (void)epi;
+  int ns = 4;
   while (ns > 1 && n % (16 * ns) != 0) ns >>= 1;
   return ns;
 }
@@ -341,34 +366,35 @@ static int tile_ns(int n, int M, int epi) {
 template <int NS, int MS>
 static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                         uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
-                        int N, int K, int ffn, int kslice) {
+                        int N, int K, int ffn, int kslice, int nt, int mt) {
   if (epi == LSK_EPI_RESIDUAL)
     gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                    ffn, kslice);
+                                                                    ffn, kslice, nt, mt);
   else if (epi == LSK_EPI_SILU_MUL) {
-    if constexpr (NS <= 2 || MS <= 2)  // 2 * NS row groups: NS = 4 only with small token tiles (LDS, VGPRs)
-      gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
-                                                                      K, ffn, kslice);
+    gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
+                                                                      K, ffn, kslice, nt, mt);
   } else if (epi == EPI_PARTIAL)
     gemm_bf16_kernel<NS, MS, EPI_PARTIAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                               kslice);
+                                                               kslice, nt, mt);
   else if (epi == EPI_ARGMAX)
     gemm_bf16_kernel<NS, MS, EPI_ARGMAX><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                              kslice);
+                                                              kslice, nt, mt);
   else
     gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                ffn, kslice);
+                                                                ffn, kslice, nt, mt);
 }
 
-static void dispatch_bf16(int ns, int ms, int epi, dim3 grid, hipStream_t s, const void* A, long lda, const void* W,
-                          long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av, int* ai, int M,
-                          int N, int K, int ffn, int kslice) {
+// Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).
+static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipStream_t s, const void* A, long lda,
+                          const void* W, long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av,
+                          int* ai, int M, int N, int K, int ffn, int kslice) {
+  const dim3 grid(mt > 1 ? (unsigned)(((nt + 7) / 8) * 8 * mt) : (unsigned)nt, 1, (unsigned)ks);
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)W;
   uint16_t* c = (uint16_t*)C;
   const uint16_t* r = (const uint16_t*)R;
 #define LSK_GEMM_CASE(NS_, MS_) \
-  if (ns == NS_ && ms == MS_) launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice);
+  if (ns == NS_ && ms == MS_) launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt);
   LSK_GEMM_CASE(1, 1) LSK_GEMM_CASE(1, 2) LSK_GEMM_CASE(1, 4)
   LSK_GEMM_CASE(2, 1) LSK_GEMM_CASE(2, 2) LSK_GEMM_CASE(2, 4)
   LSK_GEMM_CASE(4, 1) LSK_GEMM_CASE(4, 2) LSK_GEMM_CASE(4, 4)
@@ -393,8 +419,8 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
     // whole-K workgroups
     const int ns = tile_ns(N, M, epilogue);
     const int ms = ms_for(M);
-    dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), 1);
-    dispatch_bf16(ns, ms, epilogue, grid, s, A, lda, W, ldw, C, ldc, R, ldr, nullptr, nullptr, nullptr, M, N, K, ffn, K);
+    dispatch_bf16(ns, ms, epilogue, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, C, ldc, R, ldr,
+                  nullptr, nullptr, nullptr, M, N, K, ffn, K);
     return lsk_check_launch("lsk_gemm(bf16)");
   }
   if (dtype == LSK_DTYPE_F32) {
@@ -424,9 +450,8 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
   if (M == 0) return 0;
   const int ns = tile_ns(N, M, EPI_PARTIAL);
   const int ms = ms_for(M);
-  dim3 grid(N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks);
-  dispatch_bf16(ns, ms, EPI_PARTIAL, grid, (hipStream_t)stream, A, lda, W, ldw, nullptr, 0, nullptr, 0, P, nullptr,
-                nullptr, M, N, K, 0, K / ks);
+  dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,
+                ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, K / ks);
   return lsk_check_launch("lsk_gemm_partial");
 }
 
@@ -453,8 +478,8 @@ extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W
   float* av = (float*)workspace;
   int* ai = (int*)((char*)workspace + half);
   const int ms = ms_for(M);
-  dim3 grid(nt, (M + 16 * ms - 1) / (16 * ms), 1);
-  dispatch_bf16(4, ms, EPI_ARGMAX, grid, s, A, lda, W, ldw, logits, ldl, nullptr, 0, nullptr, av, ai, M, N, K, 0, K);
+  dispatch_bf16(4, ms, EPI_ARGMAX, nt, (M + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, logits, ldl, nullptr, 0,
+                nullptr, av, ai, M, N, K, 0, K);
   int rc = lsk_check_launch("lsk_head_argmax(gemm)");
   if (rc) return rc;
   argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
