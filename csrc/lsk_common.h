@@ -16,6 +16,7 @@
 typedef __bf16 lsk_bf16x8 __attribute__((ext_vector_type(8)));
 typedef short lsk_s16x4 __attribute__((ext_vector_type(4)));
 typedef float lsk_f32x4 __attribute__((ext_vector_type(4)));
+typedef int lsk_i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 

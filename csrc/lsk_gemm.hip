@@ -2,20 +2,29 @@
 // common/model.py:330):  C[m][n] = epilogue( sum_k A[m][k] * W[n][k] )   (F.linear, W = [out, in]).
 //
 // bf16 path (gfx950 MFMA v_mfma_f32_16x16x32_bf16, fp32 accumulation).  Decode GEMMs are skinny
-// (M = 1..~300 tokens against 6k-128k weight rows), so the kernel is a weight stream: both operands
-// are K-contiguous and every lane fetches its MFMA fragment with one 16-byte load (no LDS staging);
-// a workgroup of 4 waves owns a (16*NS weight rows) x (16*MS tokens) tile, the waves split K into
-// 128-element chunks (wave w takes chunks w, w+4, ... of its K slice, with the next chunk prefetched
-// into registers) and their partial sums are added in wave order through LDS.  Wide tiles (NS = 4)
-// cut the re-reads of the token rows; weight matrices with few rows (qkv, o, w2 of the 8B shape)
-// use NS = 2 and a fixed split of K into KS slices whose fp32 partial sums the NEXT kernel reduces
-// in slice order (RoPE + append, add + RMSNorm), because a cross-workgroup reduction inside the GEMM
+// (M = 1..~300 tokens against 6k-128k weight rows), so the kernel is a weight stream.
+//
+// Weight storage (bf16): fragment-major, written once by lsk_pack_weight.  Fragment (g, j) holds rows
+// 16g .. 16g+15 and k = 32j .. 32j+31 of W as 1 KiB in MFMA lane order: lane l's 16 bytes are
+// W[16g + l % 16][32j + 8 (l / 16) .. +7], fragments ordered [g][j].  A wave's fragment load is then one
+// contiguous 1 KiB request stream, and the k-steps of a row group follow each other in memory; the
+// row-major [out, in] layout instead makes every load touch 16 rows 64 bytes at a time (an 8 KiB
+// stride at K = 4096), which measured ~25 % slower on MI355X.  Weights are read with non-temporal
+// loads (each byte is used once per launch); the activations use ordinary loads (re-read from L2 by
+// every row tile).
+//
+// A workgroup of 4 waves owns a tile of (16*NS weight rows) x (16*MS tokens); every lane fetches its
+// MFMA fragments with 16-byte loads (no LDS staging); the waves split K into 128-element chunks (wave
+// w takes chunks w, w+4, ... of its K slice, with the next pipeline unit in flight) and their partial
+// sums are added in wave order through LDS.  Weight matrices with few rows (qkv, o, w2 of the 8B
+// shape) use a fixed split of K into KS slices whose fp32 partial sums the NEXT kernel reduces in
+// slice order (RoPE + append, add + RMSNorm), because a cross-workgroup reduction inside the GEMM
 // needs device-scope fences that cost more than the split saves on MI355X.
 //
-// Batch invariance: (NS, KS) are chosen from the weight shape (N, K) only (lsk_gemm_plan) and the
-// reduction order of every output element is fixed by (K, KS): chunks in order within a wave, waves in
-// order, slices in order.  It does not depend on M or on which rows share a tile, so a token's result
-// is bitwise the same whether it is decoded alone or inside a packed verify batch.
+// Batch invariance: KS is chosen from the weight shape (N, K) only (lsk_gemm_plan) and the reduction
+// order of every output element is fixed by (K, KS): chunks in order within a wave, waves in order,
+// slices in order.  It does not depend on M or on which rows share a tile, so a token's result is
+// bitwise the same whether it is decoded alone or inside a packed verify batch.
 //
 // Epilogues (the reference's dtype rounding points):
 //   NONE      C = rnd(acc)
@@ -30,6 +39,12 @@
 #define EPI_ARGMAX 4
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+
+// One lane's 16 bytes of a weight fragment, non-temporal (streamed once per launch).
+__device__ __forceinline__ lsk_bf16x8 ld_w(const uint16_t* p) {
+  const lsk_i32x4 v = __builtin_nontemporal_load((const lsk_i32x4*)p);
+  return __builtin_bit_cast(lsk_bf16x8, v);
+}
 
 // Two workgroups per CU where the tile's registers fit 256 VGPRs (two fragment buffers of 32 VGPRs
 // per weight row group and per token group, plus 4 accumulators per pair), else one.
@@ -79,13 +94,15 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
   const int k0 = s * kslice;
   const int k1 = min(K, k0 + kslice);
 
+  // fragment-major weights: row group g, k-step j at W + (g * nks + j) * 512 (+ 8 * lane for this lane)
+  const int nks = K >> 5;
   const uint16_t* wrow[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
-    int n = (t < NS) ? (n0 + 16 * t + l16) : (ffn + n0 + 16 * (t - NS) + l16);
-    const int nmax = (EPI == LSK_EPI_SILU_MUL) ? (t < NS ? ffn - 1 : 2 * ffn - 1) : N - 1;
-    n = n < nmax ? n : nmax;  // clamp: padded rows load a valid row, results discarded
-    wrow[t] = W + (long)n * ldw + k0 + 8 * lg;
+    int gi = (t < NS) ? (n0 / 16 + t) : ((ffn + n0) / 16 + (t - NS));
+    const int gmax = (EPI == LSK_EPI_SILU_MUL) ? (t < NS ? ffn / 16 - 1 : 2 * ffn / 16 - 1) : N / 16 - 1;
+    gi = gi < gmax ? gi : gmax;  // clamp: padded row groups load a valid group, results discarded
+    wrow[t] = W + ((long)gi * nks + (k0 >> 5)) * 512 + 8 * lane;
   }
   const uint16_t* arow[MS];
 #pragma unroll
@@ -114,7 +131,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
     for (int ks = 0; ks < CK; ++ks) {
       const int k = kb + ks * 32;
 #pragma unroll
-      for (int a = 0; a < NT; ++a) wf[ks][a] = *(const lsk_bf16x8*)(wrow[a] + k);
+      for (int a = 0; a < NT; ++a) wf[ks][a] = ld_w(wrow[a] + (long)k * 16);
 #pragma unroll
       for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
     }
@@ -144,7 +161,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
       const int k = kk * 32;
       lsk_bf16x8 w1[NT], a1[MS];
 #pragma unroll
-      for (int a = 0; a < NT; ++a) w1[a] = *(const lsk_bf16x8*)(wrow[a] + k);
+      for (int a = 0; a < NT; ++a) w1[a] = ld_w(wrow[a] + (long)k * 16);
 #pragma unroll
       for (int t = 0; t < MS; ++t) a1[t] = *(const lsk_bf16x8*)(arow[t] + k);
 #pragma unroll
@@ -325,6 +342,24 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
   }
 }
 
+// ----------------------------------------------------------------------------- weight packing
+// One thread per 16-byte lane slice: packed element offset 8 * o, o = (g * nks + j) * 64 + l  <->  row
+// 16 g + l % 16, columns 32 j + 8 (l / 16) .. +7 of the row-major matrix.  Both directions are pure copies.
+template <bool PACK>
+__global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                                          long ld, int nks, long n_slices) {
+  const long o = (long)blockIdx.x * 256 + threadIdx.x;
+  if (o >= n_slices) return;
+  const int l = (int)(o & 63);
+  const long f = o >> 6;
+  const long g = f / nks, j = f - g * nks;
+  const long rm = (16 * g + (l & 15)) * ld + 32 * j + 8 * (l >> 4);  // row-major element offset
+  if (PACK)
+    *(uint4*)(dst + 8 * o) = *(const uint4*)(src + rm);
+  else
+    *(uint4*)(dst + rm) = *(const uint4*)(src + 8 * o);
+}
+
 // ----------------------------------------------------------------------------- host side
 
 // K-split plan of a weight shape (N rows x K); it fixes the reduction order of every output.  KS = 1
@@ -413,8 +448,9 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
   if (M == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == LSK_DTYPE_BF16) {
-    LSK_REQUIRE(K % 32 == 0 && lda % 8 == 0 && ldw % 8 == 0, LSK_ESHAPE,
-                "lsk_gemm: bf16 needs K %% 32 == 0 and 16-byte aligned rows (K=%d)", K);
+    LSK_REQUIRE(K % 32 == 0 && lda % 8 == 0 && ldw == K, LSK_ESHAPE,
+                "lsk_gemm: bf16 needs K %% 32 == 0, 16-byte aligned A rows and a packed W (ldw == K; K=%d ldw=%ld)", K,
+                ldw);
     LSK_REQUIRE(N % 16 == 0, LSK_ESHAPE, "lsk_gemm: bf16 needs N %% 16 == 0 (N=%d)", N);
     // whole-K workgroups
     const int ns = tile_ns(N, M, epilogue);
@@ -444,8 +480,8 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
 extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P, int M, int N, int K, int ks,
                                 void* stream) {
   LSK_REQUIRE(A && W && P, LSK_EARG, "lsk_gemm_partial: null pointer");
-  LSK_REQUIRE(M >= 0 && N > 0 && K > 0 && lda >= K && ldw >= K && ks >= 1 && K % ks == 0 && (K / ks) % 32 == 0 &&
-                  N % 16 == 0 && lda % 8 == 0 && ldw % 8 == 0,
+  LSK_REQUIRE(M >= 0 && N > 0 && K > 0 && lda >= K && ldw == K && ks >= 1 && K % ks == 0 && (K / ks) % 32 == 0 &&
+                  N % 16 == 0 && lda % 8 == 0,
               LSK_ESHAPE, "lsk_gemm_partial: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
   const int ns = tile_ns(N, M, EPI_PARTIAL);
@@ -469,8 +505,8 @@ extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W
   if (M == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   LSK_REQUIRE(dtype == LSK_DTYPE_BF16, LSK_EUNSUPPORTED, "lsk_head_argmax: bf16 only (fp32 uses lsk_gemm + lsk_argmax)");
-  LSK_REQUIRE(K % 32 == 0 && N % 64 == 0 && lda % 8 == 0 && ldw % 8 == 0, LSK_ESHAPE,
-              "lsk_head_argmax: needs K %% 32 == 0 and N %% 64 == 0 (N=%d K=%d)", N, K);
+  LSK_REQUIRE(K % 32 == 0 && N % 64 == 0 && lda % 8 == 0 && ldw == K, LSK_ESHAPE,
+              "lsk_head_argmax: needs K %% 32 == 0, N %% 64 == 0 and a packed W (ldw == K; N=%d K=%d)", N, K);
   const int nt = N / 64;
   const size_t half = lsk_align_up((size_t)M * nt * 4, 256);
   LSK_REQUIRE(workspace != nullptr && ws_bytes >= 2 * half, LSK_EWORKSPACE, "lsk_head_argmax: workspace %zu < %zu",
@@ -484,4 +520,28 @@ extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W
   if (rc) return rc;
   argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
   return lsk_check_launch("lsk_head_argmax(pick)");
+}
+
+static int pack_common(bool pack, const void* src, void* dst, long ld, int N, int K, void* stream) {
+  const char* what = pack ? "lsk_pack_weight" : "lsk_unpack_weight";
+  LSK_REQUIRE(src && dst && src != dst, LSK_EARG, "%s: null or aliased pointers", what);
+  LSK_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && ld >= K && ld % 8 == 0, LSK_ESHAPE,
+              "%s: needs N %% 16 == 0, K %% 32 == 0, ld >= K, ld %% 8 == 0 (N=%d K=%d ld=%ld)", what, N, K, ld);
+  const long n_slices = (long)N * K / 8;
+  const unsigned grid = (unsigned)((n_slices + 255) / 256);
+  if (pack)
+    pack_weight_kernel<true><<<grid, 256, 0, (hipStream_t)stream>>>((const uint16_t*)src, (uint16_t*)dst, ld, K / 32,
+                                                                    n_slices);
+  else
+    pack_weight_kernel<false><<<grid, 256, 0, (hipStream_t)stream>>>((const uint16_t*)src, (uint16_t*)dst, ld, K / 32,
+                                                                     n_slices);
+  return lsk_check_launch(what);
+}
+
+extern "C" int lsk_pack_weight(const void* W, long ldw, void* Wp, int N, int K, void* stream) {
+  return pack_common(true, W, Wp, ldw, N, K, stream);
+}
+
+extern "C" int lsk_unpack_weight(const void* Wp, void* W, long ldw, int N, int K, void* stream) {
+  return pack_common(false, Wp, W, ldw, N, K, stream);
 }

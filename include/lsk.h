@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 1
+#define LSK_ABI_VERSION 2
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -75,7 +75,17 @@ int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vc
                     int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
                     size_t ws_bytes, void* stream);
 
-/* GEMM C = epilogue(A W^T), A [M,K] (lda), W [N_w,K] (ldw), C [M,N] (ldc), R residual [M,N] (ldr).
+/* bf16 weight storage of the GEMMs: W [N, K] row-major (ldw) <-> fragment-major Wp (N*K elements, no
+ * padding): fragment (g, j) = rows 16g..16g+15 x k 32j..32j+31 is 1 KiB, lane l's 8 elements being
+ * W[16g + l%16][32j + 8(l/16) .. +7], fragments in [g][j] order.  N % 16 == 0, K % 32 == 0.
+ * Pure copies (bit-exact both ways).  Has no reference counterpart: the reference keeps F.linear's
+ * [out, in] tensors (common/model.py:259-276); the packed form is what lsk_gemm, lsk_gemm_partial,
+ * lsk_head_argmax and the layer runner read for bf16, and unpacking restores the reference tensor. */
+int lsk_pack_weight(const void* W, long ldw, void* Wp, int N, int K, void* stream);
+int lsk_unpack_weight(const void* Wp, void* W, long ldw, int N, int K, void* stream);
+
+/* GEMM C = epilogue(A W^T), A [M,K] (lda), W [N_w,K], C [M,N] (ldc), R residual [M,N] (ldr).
+ * bf16: W is the packed storage (lsk_pack_weight) and ldw must equal K; fp32: W row-major with stride ldw.
  * For LSK_EPI_SILU_MUL, W has 2*ffn rows [gate; up] and N == ffn.
  * Replaces F.linear at solutions/packed.py:175 (wqkv), 182 (wo + residual), 183-185 (w13, silu*mul,
  * w2 + residual) and common/model.py:330 (lm_head). */
@@ -87,13 +97,13 @@ int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* 
  * reduction order never depends on the token count M; each launch picks its own tile width from M. */
 int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out);
 
-/* bf16 GEMM into fp32 K-slice partials: P[s][m][n] = sum over k in slice s of A[m][k] W[n][k], s < ks
+/* bf16 GEMM into fp32 K-slice partials (W packed, ldw == K): P[s][m][n] = sum over k in slice s of A[m][k] W[n][k], s < ks
  * (ks must equal lsk_gemm_plan's for this shape to keep the canonical reduction order; the consumer adds
  * the slices in order).  Replaces F.linear at solutions/packed.py:175 (wqkv), 182 (wo), 185 (w2). */
 int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P, int M, int N, int K, int ks,
                      void* stream);
 
-/* LM head + greedy pick: out[dst_idx ? dst_idx[m] : m] = argmax_n rnd(A[m] . W[n]) (first index on ties),
+/* LM head + greedy pick (W packed, ldw == K): out[dst_idx ? dst_idx[m] : m] = argmax_n rnd(A[m] . W[n]) (first index on ties),
  * optionally also storing the bf16 logits [M, ldl].  workspace >= lsk_head_workspace_bytes(M, N).
  * Replaces F.linear(.., lm_head) + .argmax(-1) (common/model.py:330, solutions/engine.py:255,352,463). */
 size_t lsk_head_workspace_bytes(int M, int N);
@@ -140,7 +150,8 @@ int lsk_greedy_accept(const int64_t* Yv, int64_t* seq_buf, int Dm1, const int32_
 int lsk_kv_rollback(int64_t* kv_len, const int32_t* slots, const int64_t* accepted, int nv, void* stream);
 
 /* ---- native layer-range runner (solutions/packed.py:169-196, packed_layer / packed_layers) ----
- * A model handle holds host copies of per-layer device pointers (weights [out, in] row-major,
+ * A model handle holds host copies of per-layer device pointers (weights [out, in]: packed for bf16,
+ * row-major for fp32,
  * KV caches [B, Hkv, S, D], fp32 RoPE tables [tab_len, D]); it owns no device memory.
  * Returns a handle > 0, or a negative error code. */
 long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, int n_kv_heads, int head_dim, int ffn, int vocab,

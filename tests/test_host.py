@@ -54,6 +54,10 @@ def test_argument_errors_are_reported_on_the_host():
     assert rc == -2 and b"K" in lib.lsk_last_error()
     assert lib.lsk_gemm(1, 8, 64, 8, 64, 8, 64, None, 0, 4, 64, 64, 7, 0, None) == -1  # bad epilogue
     assert lib.lsk_gemm(5, 8, 64, 8, 64, 8, 64, None, 0, 4, 64, 64, 0, 0, None) == -3  # bad dtype
+    assert lib.lsk_gemm(1, 8, 64, 8, 128, 8, 64, None, 0, 4, 64, 64, 0, 0, None) == -2  # bf16 W not packed (ldw != K)
+    assert lib.lsk_pack_weight(None, 64, 8, 64, 64, None) == -1
+    assert lib.lsk_pack_weight(8, 64, 16, 40, 64, None) == -2                          # N % 16 != 0
+    assert lib.lsk_unpack_weight(8, 16, 64, 64, 48, None) == -2                        # K % 32 != 0
     assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
     assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0

@@ -41,7 +41,7 @@ def test_gemm_bf16_none_matches_fp32_reference(cuda, M, N, K):
     a = torch.randn(M, K, generator=g).to(BF16)
     w = torch.randn(N, K, generator=g).to(BF16)
     ref = a.float() @ w.float().t()                      # exact products, fp32 accumulation
-    got = lsk.gemm(a.to(cuda), w.to(cuda)).cpu().float()
+    got = lsk.gemm(a.to(cuda), lsk.PackedWeight(w.to(cuda))).cpu().float()
     # bf16 output rounding (2^-8 relative) + fp32 accumulation-order error
     tol = 2.0 ** -8 * ref.abs() + 1e-3 * math.sqrt(K)
     assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max()
@@ -53,7 +53,7 @@ def test_gemm_bf16_is_batch_invariant(cuda):
     g = _gen(3)
     K, N = 1024, 384
     a = torch.randn(200, K, generator=g).to(BF16).to(cuda)
-    w = torch.randn(N, K, generator=g).to(BF16).to(cuda)
+    w = lsk.PackedWeight(torch.randn(N, K, generator=g).to(BF16).to(cuda))
     full = lsk.gemm(a, w)
     for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104)]:
         part = lsk.gemm(a[lo:hi].contiguous(), w)
@@ -70,14 +70,39 @@ def test_gemm_bf16_epilogues_match_reference_rounding(cuda):
     r = torch.randn(M, 2 * F_, generator=g).to(BF16)
     acc = (a.float() @ w13.float().t())
     # residual: compare with the same formula on the CPU from the fp32 accumulation
-    got_r = lsk.gemm(a.to(cuda), w13.to(cuda), residual=r.to(cuda), epilogue=lsk.EPI_RESIDUAL).cpu()
+    w13p = lsk.PackedWeight(w13.to(cuda))
+    got_r = lsk.gemm(a.to(cuda), w13p, residual=r.to(cuda), epilogue=lsk.EPI_RESIDUAL).cpu()
     ref_r = (r.float() + acc.to(BF16).float()).to(BF16)
     close = (got_r.float() - ref_r.float()).abs() <= 2.0 ** -7 * ref_r.float().abs() + 1e-2
     assert close.all()
-    got_s = lsk.gemm(a.to(cuda), w13.to(cuda), epilogue=lsk.EPI_SILU_MUL).cpu()
+    got_s = lsk.gemm(a.to(cuda), w13p, epilogue=lsk.EPI_SILU_MUL).cpu()
     gg, uu = acc.to(BF16).chunk(2, dim=-1)
     ref_s = F.silu(gg) * uu                               # torch bf16 ops: the reference's rounding points
     assert ((got_s.float() - ref_s.float()).abs() <= 2.0 ** -6 * ref_s.float().abs() + 2e-3).all()
+
+
+@pytest.mark.parametrize("N,K,ld", [(16, 32, 32), (48, 96, 128), (6144, 4096, 4096)])
+def test_pack_weight_layout_and_round_trip(cuda, N, K, ld):
+    """Packed storage follows the documented fragment order (computed here in numpy) and unpacks bit-exact."""
+    lsk = _lsk()
+    g = _gen(N + K)
+    full = torch.randn(N, ld, generator=g).to(BF16)
+    w = full[:, :K]
+    wp = lsk.PackedWeight(w.to(cuda))
+    # fragment (g, j) = rows 16g.., k 32j..; lane l holds row 16g + l % 16, k 32j + 8 (l // 16) .. +7
+    gi, j, l, e = np.meshgrid(np.arange(N // 16), np.arange(K // 32), np.arange(64), np.arange(8), indexing="ij")
+    rows = 16 * gi + l % 16
+    cols = 32 * j + 8 * (l // 16) + e
+    want = w.view(torch.int16).numpy()[rows.reshape(-1), cols.reshape(-1)]
+    assert np.array_equal(wp.data.cpu().view(torch.int16).numpy(), want)
+    assert torch.equal(wp.unpack().cpu(), w)
+
+
+def test_bf16_gemm_rejects_unpacked_weights(cuda):
+    lsk = _lsk()
+    a = torch.zeros(4, 64, dtype=BF16, device=cuda)
+    with pytest.raises(lsk.LskError):
+        lsk.gemm(a, torch.zeros(64, 64, dtype=BF16, device=cuda))
 
 
 @pytest.mark.parametrize("M,N,K", [(1, 8, 16), (7, 64, 64), (33, 100, 130)])
@@ -318,14 +343,15 @@ def test_gemm_partial_slices(cuda, M, N, K):
     g = _gen(M + N)
     a = torch.randn(M, K, generator=g).to(BF16)
     w = torch.randn(N, K, generator=g).to(BF16)
-    P = lsk.gemm_partial(a.to(cuda), w.to(cuda), ks).cpu()
+    wp = lsk.PackedWeight(w.to(cuda))
+    P = lsk.gemm_partial(a.to(cuda), wp, ks).cpu()
     assert P.shape == (ks, M, N)
     ref = a.float() @ w.float().t()
     tot = P[0].clone()
     for s in range(1, ks):
         tot = tot + P[s]
     assert torch.allclose(tot, ref, rtol=1e-4, atol=1e-3 * math.sqrt(K))
-    sub = lsk.gemm_partial(a[3:5].contiguous().to(cuda), w.to(cuda), ks).cpu()
+    sub = lsk.gemm_partial(a[3:5].contiguous().to(cuda), wp, ks).cpu()
     assert torch.equal(sub, P[:, 3:5])
 
 
@@ -384,7 +410,7 @@ def test_head_argmax_matches_logits_argmax(cuda):
     w = torch.randn(V, K, generator=g).to(BF16)
     w[3000] = w[100]                      # duplicate rows -> exact ties, the first index must win
     w[4100] = w[100]
-    wd = w.to(cuda)
+    wd = lsk.PackedWeight(w.to(cuda))
     logits = lsk.gemm(a, wd)
     ref = logits.float().argmax(-1)
     out = torch.empty(M, dtype=torch.long, device=cuda)

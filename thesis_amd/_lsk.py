@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 1024         # LSK_ATTN_SPLIT
 ATTN_ROWS = 16            # query rows per attention workgroup
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -34,6 +34,8 @@ _SIGS = {
     "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
     "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z, _P]),
+    "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
+    "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
     "lsk_gemm_plan": (_I, [_I, _I, _P, _P]),
     "lsk_gemm_partial": (_I, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _P]),
@@ -129,6 +131,61 @@ def _dev(*ts):
             raise LskError(f"liblsk kernels need CUDA (HIP) tensors, got {t.device}")
 
 
+# ----------------------------------------------------------------------------- weights
+
+class PackedWeight:
+    """A bf16 weight matrix [N, K] (F.linear's [out, in]) in the GEMM kernels' fragment-major storage
+    (lsk_pack_weight): every 16-row x 32-column MFMA fragment is 1 KiB contiguous in lane order, so each
+    wave's weight load is one contiguous 1 KiB stream.  `unpack()` returns the [N, K] tensor (a copy)."""
+
+    def __init__(self, w: torch.Tensor):
+        _dev(w)
+        if w.dtype != torch.bfloat16 or w.dim() != 2 or w.stride(1) != 1:
+            raise LskError("PackedWeight: a 2-D bf16 tensor with unit column stride is needed")
+        N, K = w.shape
+        self.shape = (N, K)
+        self.dtype = w.dtype
+        self.device = w.device
+        self.data = torch.empty(N * K, dtype=w.dtype, device=w.device)
+        _check(load().lsk_pack_weight(_ptr(w), w.stride(0), _ptr(self.data), N, K, _stream()), "lsk_pack_weight")
+
+    def data_ptr(self) -> int:
+        return self.data.data_ptr()
+
+    def stride(self, dim: int) -> int:
+        return self.shape[1] if dim == 0 else 1
+
+    def dim(self) -> int:
+        return 2
+
+    def numel(self) -> int:
+        return self.shape[0] * self.shape[1]
+
+    def element_size(self) -> int:
+        return 2
+
+    def unpack(self) -> torch.Tensor:
+        N, K = self.shape
+        out = torch.empty(N, K, dtype=self.dtype, device=self.device)
+        _check(load().lsk_unpack_weight(_ptr(self.data), _ptr(out), K, N, K, _stream()), "lsk_unpack_weight")
+        return out
+
+    def __repr__(self) -> str:
+        return f"PackedWeight(shape={self.shape}, dtype={self.dtype}, device={self.device})"
+
+
+def as_gemm_weight(w: torch.Tensor):
+    """The storage the GEMMs read for a weight of this dtype: PackedWeight for bf16, the tensor for fp32."""
+    return PackedWeight(w) if w.dtype == torch.bfloat16 else w.contiguous()
+
+
+def _check_weight(a: torch.Tensor, w) -> None:
+    if a.dtype == torch.bfloat16 and not isinstance(w, PackedWeight):
+        raise LskError("bf16 GEMMs read packed weights: wrap the [out, in] tensor in PackedWeight")
+    if a.dtype != torch.bfloat16 and isinstance(w, PackedWeight):
+        raise LskError("packed weights are bf16 only")
+
+
 # ----------------------------------------------------------------------------- ops
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | None = None) -> torch.Tensor:
@@ -199,6 +256,7 @@ def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n
 def gemm(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
          epilogue: int = EPI_NONE) -> torch.Tensor:
     _dev(a, w, out, residual)
+    _check_weight(a, w)
     assert a.dim() == 2 and w.dim() == 2 and a.stride(1) == 1 and w.stride(1) == 1
     M, K = a.shape
     if epilogue == EPI_SILU_MUL:
@@ -346,8 +404,9 @@ def gemm_plan(N: int, K: int) -> tuple:
 
 
 def gemm_partial(a: torch.Tensor, w: torch.Tensor, ks: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """fp32 K-slice partials [ks, M, N] of a @ w.T (bf16)."""
+    """fp32 K-slice partials [ks, M, N] of a @ w.T (bf16, w packed)."""
     _dev(a, w, out)
+    _check_weight(a, w)
     M, K = a.shape
     N = w.shape[0]
     if out is None:
@@ -360,6 +419,7 @@ def gemm_partial(a: torch.Tensor, w: torch.Tensor, ks: int, out: torch.Tensor | 
 def head_argmax(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, dst_idx: torch.Tensor | None = None,
                 logits: torch.Tensor | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     _dev(a, w, out, dst_idx, logits, workspace)
+    _check_weight(a, w)
     M, K = a.shape
     N = w.shape[0]
     need = int(load().lsk_head_workspace_bytes(M, N))

@@ -10,9 +10,11 @@ ragged kernels as the packed path: a [b, T] call is b blocks of T tokens.
 HBM layout: the K cache is one tensor [L, max_batch, Hkv, max_seq, D] (`cache.k[i]` is layer i's view),
 so one (request, KV head) is a contiguous max_seq x D stripe that the attention kernel streams once; the
 V cache holds the same stripes in transposed 32-position blocks [L, max_batch, Hkv, max_seq/32, D, 32]
-(`cache.v[i]` returns the reference layout as a copy).  Weights keep the reference's fused row-major layout
-(wqkv = [q; k; v], w13 = [gate; up], [out, in]).  The RoPE tables are built on the CPU with the
-reference's op sequence (common/model.py:113-140) and copied, so they are bitwise the CPU tables.
+(`cache.v[i]` returns the reference layout as a copy).  Weights keep the reference's fusion (wqkv = [q; k; v],
+w13 = [gate; up], [out, in]); bf16 projection and LM-head weights are stored in the GEMMs' fragment-major
+form (`_lsk.PackedWeight`, every 16 x 32 MFMA fragment 1 KiB contiguous), whose `unpack()` gives the
+[out, in] tensor back bit for bit; fp32 weights stay row-major.  The RoPE tables are built on the CPU with
+the reference's op sequence (common/model.py:113-140) and copied, so they are bitwise the CPU tables.
 """
 
 from __future__ import annotations
@@ -135,12 +137,20 @@ def build_rope_cache(cfg: ModelConfig, max_seq: int, device) -> tuple[Tensor, Te
 
 @dataclass
 class LayerWeights:
-    wqkv: Tensor
-    wo: Tensor
-    w13: Tensor
-    w2: Tensor
+    """One layer's weights (common/model.py:161-168).  The four projections are GEMM weights: a
+    `_lsk.PackedWeight` for bf16 (`.unpack()` -> [out, in]), the row-major tensor for fp32."""
+    wqkv: object
+    wo: object
+    w13: object
+    w2: object
     attn_norm: Tensor
     ffn_norm: Tensor
+
+    @classmethod
+    def from_dense(cls, wqkv: Tensor, wo: Tensor, w13: Tensor, w2: Tensor, attn_norm: Tensor,
+                   ffn_norm: Tensor) -> "LayerWeights":
+        g = _lsk.as_gemm_weight
+        return cls(g(wqkv), g(wo), g(w13), g(w2), attn_norm, ffn_norm)
 
 
 class _VLayers:
@@ -261,12 +271,14 @@ class LayerSkipLlama:
                               weights[p + "self_attn.v_proj.weight"]], dim=0).to(device=device, dtype=dtype)
             w13 = torch.cat([weights[p + "mlp.gate_proj.weight"], weights[p + "mlp.up_proj.weight"]],
                             dim=0).to(device=device, dtype=dtype)
-            layers.append(LayerWeights(wqkv.contiguous(), take(p + "self_attn.o_proj.weight"), w13.contiguous(),
-                                       take(p + "mlp.down_proj.weight"), take(p + "input_layernorm.weight"),
-                                       take(p + "post_attention_layernorm.weight")))
+            layers.append(LayerWeights.from_dense(wqkv.contiguous(), take(p + "self_attn.o_proj.weight"),
+                                                  w13.contiguous(), take(p + "mlp.down_proj.weight"),
+                                                  take(p + "input_layernorm.weight"),
+                                                  take(p + "post_attention_layernorm.weight")))
+            del wqkv, w13
         embed = take("model.embed_tokens.weight")
         norm = take("model.norm.weight")
-        lm_head = take("lm_head.weight") if "lm_head.weight" in weights else embed
+        lm_head = _lsk.as_gemm_weight(take("lm_head.weight") if "lm_head.weight" in weights else embed)
         return cls(cfg, embed, layers, norm, lm_head, device, dtype, max_seq or cfg.max_position_embeddings)
 
     @classmethod
@@ -300,11 +312,12 @@ class LayerSkipLlama:
         def ones(n):
             return torch.ones(n, dtype=dtype, device=device)
 
-        layers = [LayerWeights(mat(qd + 2 * kvd, cfg.dim), mat(cfg.dim, qd), mat(2 * cfg.intermediate_size, cfg.dim),
-                               mat(cfg.dim, cfg.intermediate_size), ones(cfg.dim), ones(cfg.dim))
+        layers = [LayerWeights.from_dense(mat(qd + 2 * kvd, cfg.dim), mat(cfg.dim, qd),
+                                          mat(2 * cfg.intermediate_size, cfg.dim), mat(cfg.dim, cfg.intermediate_size),
+                                          ones(cfg.dim), ones(cfg.dim))
                   for _ in range(cfg.n_layers)]
         embed = mat(cfg.vocab_size, cfg.dim)
-        lm_head = embed if cfg.tie_word_embeddings else mat(cfg.vocab_size, cfg.dim)
+        lm_head = _lsk.as_gemm_weight(embed if cfg.tie_word_embeddings else mat(cfg.vocab_size, cfg.dim))
         return cls(cfg, embed, layers, ones(cfg.dim), lm_head, device, dtype, max_seq or cfg.max_position_embeddings)
 
     @property
