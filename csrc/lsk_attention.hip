@@ -89,67 +89,113 @@ __global__ __launch_bounds__(256) void attn_bf16_kernel(
   // MFMA row l16 of S^T sub-tile a <-> position 8 * (l16 / 4) + 4 * a + l16 % 4 of the 32-position step
   const int krow0 = 8 * (l16 >> 2) + (l16 & 3);
 
-  for (int tb = kv_lo + ATTN_TILE * wave; tb < kv_hi; tb += 4 * ATTN_TILE) {
+#ifndef LSK_ATTN_PIPE
+#define LSK_ATTN_PIPE 1
+#endif
+#ifndef LSK_ATTN_NT
+#define LSK_ATTN_NT 0
+#endif
+#ifndef LSK_ATTN_KFRAG
+#define LSK_ATTN_KFRAG 0
+#endif
+  auto ldkv = [&](const uint16_t* p) -> lsk_bf16x8 {
+#if LSK_ATTN_NT
+    return __builtin_bit_cast(lsk_bf16x8, __builtin_nontemporal_load((const lsk_i32x4*)p));
+#else
+    return *(const lsk_bf16x8*)p;
+#endif
+  };
+  lsk_bf16x8 kf[2][KSTEPS];
+  lsk_bf16x8 vf[CT];
+  auto load_k = [&](int sb) {
+#if LSK_ATTN_KFRAG
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int sb = tb + 32 * h;  // 32-position step
-      if (sb >= kv_hi) break;
-      lsk_bf16x8 kf[2][KSTEPS];
+    for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        const uint16_t* krow = kbase + (long)(sb + krow0 + 4 * a) * D + 8 * lg;
+      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(kbase + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
+#else
 #pragma unroll
-        for (int j = 0; j < KSTEPS; ++j) kf[a][j] = *(const lsk_bf16x8*)(krow + 32 * j);
-      }
-      lsk_bf16x8 vf[CT];
+    for (int a = 0; a < 2; ++a) {
+      const uint16_t* krow = kbase + (long)(sb + krow0 + 4 * a) * D + 8 * lg;
 #pragma unroll
-      for (int c = 0; c < CT; ++c) vf[c] = *(const lsk_bf16x8*)(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
-      lsk_f32x4 sacc[2];
-#pragma unroll
-      for (int a = 0; a < 2; ++a) {
-        sacc[a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < KSTEPS; ++j)
-          sacc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[j], sacc[a], 0, 0, 0);
-      }
-      // sacc[a][i] <-> position sb + 8 lg + 4 a + i, query l16
-      float sv[8];
-      float mt = -INFINITY;
-#pragma unroll
-      for (int a = 0; a < 2; ++a)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kp = sb + 8 * lg + 4 * a + i;
-          const bool ok = qvalid && kp < kv_hi && kp <= qpos;
-          const float sc = ok ? sacc[a][i] * scale_log2 : -INFINITY;
-          sv[4 * a + i] = sc;
-          mt = fmaxf(mt, sc);
-        }
-      mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-      mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-      const float m_new = fmaxf(m_run, mt);
-      const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
-      float rs = 0.f;
-      lsk_bf16x8 pb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float pe = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
-        rs += pe;
-        pb[e] = __builtin_bit_cast(__bf16, f2bf(pe));
-      }
-      rs += __shfl_xor(rs, 16, 64);
-      rs += __shfl_xor(rs, 32, 64);
-      l_run = l_run * alpha + rs;
-      m_run = m_new;
-#pragma unroll
-      for (int c = 0; c < CT; ++c) {
-        oacc[c][0] *= alpha;
-        oacc[c][1] *= alpha;
-        oacc[c][2] *= alpha;
-        oacc[c][3] *= alpha;
-        oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[c], pb, oacc[c], 0, 0, 0);
-      }
+      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(krow + 32 * j);
     }
+#endif
+  };
+  auto load_v = [&](int sb) {
+#pragma unroll
+    for (int c = 0; c < CT; ++c) vf[c] = ldkv(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
+  };
+  // this wave's 32-position steps: both halves of tiles wave, wave + 4, ... of the range, in order
+  auto step_pos = [&](int i) { return kv_lo + ATTN_TILE * (wave + 4 * (i >> 1)) + 32 * (i & 1); };
+  int sb = step_pos(0);
+  if (sb < kv_hi) {
+    load_k(sb);
+    load_v(sb);
+  }
+  for (int i = 0; sb < kv_hi; ++i) {
+    const int sn = step_pos(i + 1);
+    const bool more = sn < kv_hi;
+#if !LSK_ATTN_PIPE
+    (void)more;
+#endif
+    lsk_f32x4 sacc[2];
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      sacc[a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int j = 0; j < KSTEPS; ++j)
+        sacc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[j], sacc[a], 0, 0, 0);
+    }
+#if LSK_ATTN_PIPE
+    if (more) load_k(sn);  // next step's K streams in during this step's softmax and P.V
+#endif
+    // sacc[a][i] <-> position sb + 8 lg + 4 a + i, query l16
+    float sv[8];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int kp = sb + 8 * lg + 4 * a + e;
+        const bool ok = qvalid && kp < kv_hi && kp <= qpos;
+        const float sc = ok ? sacc[a][e] * scale_log2 : -INFINITY;
+        sv[4 * a + e] = sc;
+        mt = fmaxf(mt, sc);
+      }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
+    float rs = 0.f;
+    lsk_bf16x8 pb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float pe = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
+      rs += pe;
+      pb[e] = __builtin_bit_cast(__bf16, f2bf(pe));
+    }
+    rs += __shfl_xor(rs, 16, 64);
+    rs += __shfl_xor(rs, 32, 64);
+    l_run = l_run * alpha + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) {
+      oacc[c][0] *= alpha;
+      oacc[c][1] *= alpha;
+      oacc[c][2] *= alpha;
+      oacc[c][3] *= alpha;
+      oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[c], pb, oacc[c], 0, 0, 0);
+    }
+#if LSK_ATTN_PIPE
+    if (more) load_v(sn);
+#else
+    if (more) {
+      load_k(sn);
+      load_v(sn);
+    }
+#endif
+    sb = sn;
   }
   // ---- merge the four waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
   if (lg == 0) {

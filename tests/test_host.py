@@ -162,6 +162,31 @@ def test_build_packed_matches_oracle(bucketing):
                 assert torch.equal(x.pad_index, y.pad_index)
 
 
+@pytest.mark.parametrize("bucketing", ["exact", "pad"])
+def test_build_packed_arrays_matches_block_path(bucketing):
+    """The engine's array path gives the block path's order, metadata and accounting; `order` maps
+    packed blocks back to the caller's indices and tags follow their blocks."""
+    from thesis_amd.solutions.packed import Block, build_packed, build_packed_arrays
+
+    rng = np.random.default_rng(7)
+    stub = _stub_model()
+    for trial in range(20):
+        n = int(rng.integers(1, 12))
+        rows = rng.integers(0, 8, n)                  # repeated rows: ties broken by pos0, then input order
+        pos0 = rng.integers(0, 3000, n)
+        T = rng.integers(1, 10, n)
+        tags = [("t", j) for j in range(n)]
+        ref = build_packed(stub, [Block(int(r), int(p), int(t), g) for r, p, t, g in zip(rows, pos0, T, tags)],
+                           bucketing)
+        got = build_packed_arrays(stub, rows, pos0, T, bucketing, tags=tags, upload_meta=False)
+        assert [(b.row, b.pos0, b.T, b.tag) for b in got.blocks] == [(b.row, b.pos0, b.T, b.tag) for b in ref.blocks]
+        assert [tags[j] for j in got.order] == [b.tag for b in ref.blocks]
+        assert np.array_equal(got.meta_host, ref.meta.numpy()) and got.meta is None
+        assert (got.kv_read, got.kv_read_padded, got.kv_gathered) == (ref.kv_read, ref.kv_read_padded, ref.kv_gathered)
+        assert [(x.start, x.end, x.b, x.T, x.L, x.b0) for x in got.buckets] == \
+               [(x.start, x.end, x.b, x.T, x.L, x.b0) for x in ref.buckets]
+
+
 def test_build_packed_rejects_bad_input():
     from thesis_amd.solutions.packed import Block, build_packed
 

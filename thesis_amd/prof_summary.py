@@ -50,7 +50,7 @@ def short_name(name: str) -> str:
 def classify(short: str, grid_x_threads=None) -> str:
     """Kernel class; the split-K GEMMs of qkv and of o / w2 are told apart by their grid's x extent
     (weight row tiles), which the counter CSV does not carry (it reports the total grid)."""
-    m = re.match(r"gemm_bf16_kernel<(\d+), (\d+), (\d+)>", short)
+    m = re.match(r"gemm_bf16_kernel<(\d+), (\d+), (\d+)(?:, \d+)*>", short)
     if m:
         cls = _EPI.get(m.group(3), "gemm")
         if cls == "gemm_partial":

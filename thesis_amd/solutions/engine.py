@@ -32,7 +32,7 @@ import torch
 
 from .. import _lsk
 from ..common.timing import Interval
-from .packed import Block, build_packed, packed_layers, upload
+from .packed import Block, build_packed, build_packed_arrays, packed_layers, upload, upload_many
 from .schedulers import make_scheduler
 
 FREE, PREFILL, DECODE = 0, 1, 2
@@ -298,37 +298,42 @@ class EESDEngine:
         dslots = np.flatnonzero(dec)
         if len(dslots) == 0:
             return 0, []
-        blocks = [Block(int(i), int(self.pos[i] + d[i]), 1, ("sh", int(i))) for i in dslots]
-        pb = build_packed(m, blocks, cfg.bucketing)
+        # shallow blocks: every decoding slot, T = 1 at pos + d (packed order: by slot)
+        pb = build_packed_arrays(m, dslots, self.pos[dslots] + d[dslots], np.ones(len(dslots), dtype=np.int64),
+                                 cfg.bucketing, upload_meta=False)
         self._kv(pb, k)
         N = pb.n_tokens
-        sl = np.fromiter((b.tag[1] for b in pb.blocks), dtype=np.int64, count=N)   # T = 1: token j <-> block j
+        sl = dslots[pb.order]                                                    # T = 1: token j <-> block j
         sel = sl * Dm1 + d[sl]
         drf_src = np.flatnonzero(Dr[sl])
         drf_dst = sel[drf_src] + 1
         nd = len(drf_src)
-        glue = upload(np.concatenate([sel, drf_src, drf_dst]), self.dev)
-        sel_t, drf_src_t, drf_dst_t = glue[:N], glue[N:N + nd], glue[N + nd:]
+        pb.meta, sel_t, drf_src_t, drf_dst_t = upload_many(
+            [pb.meta_host, sel, drf_src.astype(np.int64), drf_dst], self.dev)
         sb, exh = self._flat()
         iv = Interval(self.dev).start()
         x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
         _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
         h = packed_layers(m, x, pb, 0, k)
         _lsk.copy_rows(exh, sel_t, h, None, N)                                   # exit_h[i, d_i] = h
-        if nd:
-            hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
-            _lsk.copy_rows(hx, None, h, drf_src_t, nd)
-            m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                         # seq_buf[i, d_i + 1] = draft
         readback = None
         n_v_tok = 0
         if deep:
-            readback, n_v_tok, vinfo = self._deep(V, d)
+            # the drafts are first read next step, so their head shares the verify head's launch (one pass
+            # over the LM head weights per step); the batch-invariant GEMM gives every row the same result
+            readback, n_v_tok, vinfo = self._deep(V, d, (h, drf_src_t, drf_dst_t, nd))
+        elif nd:
+            hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
+            _lsk.copy_rows(hx, None, h, drf_src_t, nd)
+            m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                         # seq_buf[i, d_i + 1] = draft
         iv.stop()
         self._rec("deep" if deep else "shallow", iv, n_sh=N, n_dp=n_v_tok, plan_ms=plan_ms)
         self.d[Dr] += 1
         if self.trace is not None:
-            self.trace.append({"sh": [(b.row, b.pos0, b.T) for b in pb.blocks], "n_draft": nd,
-                               "dp": [(int(i), int(self.pos[i]), int(d[i]) + 1) for i in np.flatnonzero(V)],
+            vs = np.flatnonzero(V)
+            self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
+                               "n_draft": nd,
+                               "dp": list(zip(vs.tolist(), self.pos[vs].tolist(), (d[vs] + 1).tolist())),
                                "committed": 0})
         if not deep:
             self.steps_since_deep += 1
@@ -361,33 +366,40 @@ class EESDEngine:
         self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms)
         return committed, done
 
-    def _deep(self, V, d):
-        """Deep segment (inside the step's interval).  Returns the int64 readback
-        [accepted per verifier | committed/verified tokens], the verify token count and verifier info."""
+    def _deep(self, V, d, draft):
+        """Deep segment (inside the step's interval) and the step's one LM-head launch: rows [0, nd) are the
+        drafting slots' layer-k states (draft = (h, src rows, seq_buf destinations, nd)), rows nd.. the deep
+        outputs.  Returns the int64 readback [accepted per verifier | committed/verified tokens], the verify
+        token count and verifier info."""
         m, k, L, Dm1 = self.m, self.k, self.L, self.Dm1
-        vb = [Block(int(i), int(self.pos[i]), int(d[i]) + 1, ("v", int(i))) for i in np.flatnonzero(V)]
-        pb = build_packed(m, vb, self.cfg.bucketing)
+        vs = np.flatnonzero(V)
+        pb = build_packed_arrays(m, vs, self.pos[vs], d[vs] + 1, self.cfg.bucketing, upload_meta=False)
         self._kv(pb, L - k)
-        nv, n = len(pb.blocks), pb.n_tokens
-        vslots = [b.tag[1] for b in pb.blocks]
-        vT = [b.T for b in pb.blocks]
-        vstarts = [int(o) for o in pb.offsets[:-1]]
-        slots_a = np.asarray(vslots, dtype=np.int64)
-        T_a = np.asarray(vT, dtype=np.int64)
-        src = np.repeat(slots_a * Dm1, T_a) + (np.arange(n) - np.repeat(pb.offsets[:-1], T_a))
+        nv, n = pb.nb, pb.n_tokens
+        slots_a = vs[pb.order]
+        T_a = pb.blk_T
+        starts_a = pb.offsets[:-1]
+        vslots, vT, vstarts = slots_a.tolist(), T_a.tolist(), starts_a.tolist()
+        src = np.repeat(slots_a * Dm1 - starts_a, T_a) + np.arange(n)
         if self.forced is not None:
             forced = np.array([self.forced.draw(self.req[i].key) for i in vslots], dtype=np.int64)
         else:
             forced = np.full(nv, -1, dtype=np.int64)
-        src_t = upload(src, self.dev)
-        info = upload(np.concatenate([slots_a, np.asarray(vstarts, dtype=np.int64), T_a, forced]), self.dev,
-                      dtype=torch.int32)
+        pb.meta, src_t, info = upload_many(
+            [pb.meta_host, src, np.concatenate([slots_a, starts_a, T_a, forced]).astype(np.int32)], self.dev)
         slots_t, starts_t, T_t, forced_t = info[:nv], info[nv:2 * nv], info[2 * nv:3 * nv], info[3 * nv:4 * nv]
         sb, exh = self._flat()
+        h, drf_src_t, drf_dst_t, nd = draft
+        xh = m.buffer("x_head", (nd + n, m.cfg.dim), m.dtype)
+        if nd:
+            _lsk.copy_rows(xh, None, h, drf_src_t, nd)                            # drafting slots' states
         x = m.buffer("x_deep", (n, m.cfg.dim), m.dtype)
         _lsk.copy_rows(x, None, exh, src_t, n)                                    # x = exit_h[i, 0..d_i]
-        hd = packed_layers(m, x, pb, k, L)
-        Yv = m.head_argmax(hd)
+        packed_layers(m, x, pb, k, L, out=xh[nd:])
+        ids = m.head_argmax(xh, out=m.buffer("head_ids", (nd + n,), torch.long))
+        if nd:
+            _lsk.copy_rows(sb.view(-1, 1), drf_dst_t, ids.view(-1, 1), None, nd)  # seq_buf[i, d_i + 1] = draft
+        Yv = ids[nd:]
         rb = torch.empty(nv + n, dtype=torch.long, device=self.dev)
         _lsk.greedy_accept(Yv, sb, Dm1, slots_t, starts_t, T_t, forced_t, nv, rb[:nv], rb[nv:])
         return rb.cpu(), n, (vslots, vstarts, vT)

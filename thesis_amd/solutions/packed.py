@@ -37,6 +37,25 @@ def upload(arr, device: torch.device, dtype=torch.long) -> torch.Tensor:
     return t
 
 
+_NP_TO_TORCH = {np.dtype(np.int32): torch.int32, np.dtype(np.int64): torch.int64}
+
+
+def upload_many(arrays: list, device: torch.device) -> list:
+    """Several int32 / int64 numpy arrays -> device tensors through ONE pinned staging buffer and ONE
+    non_blocking copy (each array 8-byte aligned in the buffer); returns the device views in order."""
+    offs, total = [], 0
+    for a in arrays:
+        total = (total + 7) // 8 * 8
+        offs.append(total)
+        total += a.nbytes
+    host = torch.empty(max(total, 8), dtype=torch.uint8, pin_memory=True)
+    hv = host.numpy()
+    for a, o in zip(arrays, offs):
+        hv[o:o + a.nbytes] = np.ascontiguousarray(a).view(np.uint8).reshape(-1)
+    dev = host.to(device, non_blocking=True)
+    return [dev[o:o + a.nbytes].view(_NP_TO_TORCH[a.dtype]) for a, o in zip(arrays, offs)]
+
+
 def qo_indptr(lengths) -> np.ndarray:
     """cumsum of per-request token counts with a leading 0 (solutions/packed.py:199-201)."""
     return np.concatenate([[0], np.cumsum(np.asarray(lengths, dtype=np.int64))]).astype(np.int64)
@@ -65,10 +84,16 @@ class Bucket:
 
 @dataclass
 class PackedBatch:
-    blocks: list
+    """Packed segment metadata.  Per-block arrays are in packed order; `blocks` lists them as Block
+    objects (built on first access when the batch came from arrays).  `order[j]` is the caller's index
+    of packed block j."""
     offsets: np.ndarray
     pos_h: np.ndarray                 # [N] positions (host)
     rows_h: np.ndarray                # [N] cache rows (host)
+    blk_rows: np.ndarray = None
+    blk_pos0: np.ndarray = None
+    blk_T: np.ndarray = None
+    order: np.ndarray = None
     buckets: list = field(default_factory=list)
     n_tokens: int = 0
     kv_read: int = 0
@@ -76,6 +101,7 @@ class PackedBatch:
     kv_gathered: int = 0
     # kernel metadata (device int32): [rows N][pos N][blocks nb*4][works nw*8][groups ng*8]
     meta: Optional[torch.Tensor] = None
+    meta_host: Optional[np.ndarray] = None
     nb: int = 0
     n_works: int = 0
     n_groups: int = 0
@@ -83,6 +109,16 @@ class PackedBatch:
     attn_bytes: float = 0.0
     attn_flops: float = 0.0
     _model: object = None
+    _blocks: Optional[list] = None
+    _tags: Optional[list] = None
+
+    @property
+    def blocks(self) -> list:
+        if self._blocks is None:
+            tags = self._tags
+            self._blocks = [Block(int(r), int(p), int(t), tags[j] if tags is not None else None)
+                            for j, (r, p, t) in enumerate(zip(self.blk_rows, self.blk_pos0, self.blk_T))]
+        return self._blocks
 
     def block_slice(self, i: int) -> slice:
         return slice(int(self.offsets[i]), int(self.offsets[i + 1]))
@@ -106,26 +142,58 @@ class PackedBatch:
         return m.rope_sin[self.pos].to(m.dtype).unsqueeze(1)
 
 
-def _validate(model, blocks) -> None:
+def _validate(model, rows: np.ndarray, pos0: np.ndarray, T: np.ndarray) -> None:
     cache = model.cache
     if cache is None:
         raise ValueError("allocate_cache() first")
-    for b in blocks:
-        if not (0 <= b.row < cache.max_batch):
-            raise ValueError(f"block row {b.row} outside the cache's {cache.max_batch} rows")
-        if b.T < 1 or b.pos0 < 0 or b.pos0 + b.T > cache.max_seq:
-            raise ValueError(f"block positions [{b.pos0}, {b.pos0 + b.T}) outside max_seq={cache.max_seq}")
-    if blocks and max(b.pos0 + b.T for b in blocks) > model.rope_cos.shape[0]:
+    if len(rows) == 0:
+        return
+    bad = (rows < 0) | (rows >= cache.max_batch)
+    if bad.any():
+        raise ValueError(f"block row {int(rows[bad][0])} outside the cache's {cache.max_batch} rows")
+    bad = (T < 1) | (pos0 < 0) | (pos0 + T > cache.max_seq)
+    if bad.any():
+        j = int(np.flatnonzero(bad)[0])
+        raise ValueError(f"block positions [{int(pos0[j])}, {int(pos0[j] + T[j])}) outside max_seq={cache.max_seq}")
+    if int((pos0 + T).max()) > model.rope_cos.shape[0]:
         raise ValueError("positions beyond the RoPE table")
 
 
-def pack_blocks(model, ordered: list, groups: Optional[list] = None, bucketing: str = "exact") -> PackedBatch:
-    """Build the packed batch for blocks already in packed order (groups = bucket partition)."""
-    _validate(model, ordered)
-    nb = len(ordered)
-    Ts = np.fromiter((b.T for b in ordered), dtype=np.int64, count=nb)
-    pos0 = np.fromiter((b.pos0 for b in ordered), dtype=np.int64, count=nb)
-    rws = np.fromiter((b.row for b in ordered), dtype=np.int64, count=nb)
+def packed_order(rows, pos0, T, bucketing: str = "exact") -> np.ndarray:
+    """Packed block order of solutions/packed.py:95-101: "exact" groups by T ascending, each group by
+    (row, pos0); "pad" is one (row, pos0)-ordered group.  Stable, like the reference's sorted()."""
+    if bucketing == "exact":
+        return np.lexsort((pos0, rows, T))
+    if bucketing == "pad":
+        return np.lexsort((pos0, rows))
+    raise ValueError(bucketing)
+
+
+def build_packed_arrays(model, rows, pos0, T, bucketing: str = "exact", tags: Optional[list] = None,
+                        upload_meta: bool = True) -> PackedBatch:
+    """build_packed over per-block arrays (row, pos0, T) in caller order.  With upload_meta=False the
+    kernel metadata stays in `meta_host` for the caller to upload (e.g. with upload_many) into `meta`."""
+    rows = np.asarray(rows, dtype=np.int64)
+    pos0 = np.asarray(pos0, dtype=np.int64)
+    T = np.asarray(T, dtype=np.int64)
+    order = packed_order(rows, pos0, T, bucketing)
+    rws, p0, Ts = rows[order], pos0[order], T[order]
+    if bucketing == "exact" and len(Ts):
+        cut = np.flatnonzero(np.diff(Ts)) + 1
+        bounds = np.concatenate([[0], cut, [len(Ts)]])
+    else:
+        bounds = np.array([0, len(Ts)]) if len(Ts) else np.array([0])
+    otags = [tags[i] for i in order] if tags is not None else None
+    pb = _pack(model, rws, p0, Ts, bounds, bucketing, upload_meta)
+    pb.order = order
+    pb._tags = otags
+    return pb
+
+
+def _pack(model, rws: np.ndarray, pos0: np.ndarray, Ts: np.ndarray, bounds: np.ndarray, bucketing: str,
+          upload_meta: bool) -> PackedBatch:
+    _validate(model, rws, pos0, Ts)
+    nb = len(Ts)
     offsets = qo_indptr(Ts)
     N = int(offsets[-1])
     within = np.arange(N, dtype=np.int64) - np.repeat(offsets[:-1], Ts)
@@ -136,67 +204,81 @@ def pack_blocks(model, ordered: list, groups: Optional[list] = None, bucketing: 
     works, grps, n_parts = _lsk.attn_plan(blk, model.group, split) if nb else (np.zeros((0, 8), np.int32),) * 2 + (0,)
     meta = np.concatenate([rows_h.astype(np.int32), pos_h.astype(np.int32), blk.ravel(), works.ravel(),
                            grps.ravel()]).astype(np.int32)
-    pb = PackedBatch(list(ordered), offsets, pos_h, rows_h, n_tokens=N, nb=nb, n_works=len(works),
-                     n_groups=len(grps), n_parts=n_parts, _model=model)
+    pb = PackedBatch(offsets, pos_h, rows_h, rws, pos0, Ts, n_tokens=N, nb=nb, n_works=len(works),
+                     n_groups=len(grps), n_parts=n_parts, _model=model, meta_host=meta)
     # algorithmic work of one attention launch (per layer): K+V of every attended position read once per
     # (block, KV head), Q read and O written once; flops = 4 Hq D per (query, attended position)
     c = model.cfg
     es = model.dtype.itemsize
     pb.attn_bytes = float((pos0 + Ts).sum()) * c.n_kv_heads * c.head_dim * 2 * es + N * c.n_heads * c.head_dim * 2 * es
     pb.attn_flops = 4.0 * c.n_heads * c.head_dim * float((Ts * pos0 + Ts * (Ts + 1) // 2).sum())
-    pb.meta = upload(meta, model.device, dtype=torch.int32) if N else None
+    if upload_meta and N:
+        pb.meta = upload(meta, model.device, dtype=torch.int32)
     # ---- reference bucket bookkeeping (solutions/packed.py:109-138), host only
-    if groups is None:
-        groups = [ordered] if ordered else []
     max_seq = model.cache.max_seq
-    first = 0
-    for g in groups:
-        n = len(g)
-        start, end = int(offsets[first]), int(offsets[first + n])
-        Tm = max(b.T for b in g)
-        L = min((max(b.pos0 + b.T - 1 for b in g) + 1 + 63) // 64 * 64, max_seq)
-        rl = [b.row for b in g]
-        contiguous = rl == list(range(rl[0], rl[0] + n))
+    for gi in range(len(bounds) - 1):
+        a, b = int(bounds[gi]), int(bounds[gi + 1])
+        n = b - a
+        gr, gp, gt = rws[a:b], pos0[a:b], Ts[a:b]
+        start, end = int(offsets[a]), int(offsets[b])
+        Tm = int(gt.max())
+        L = min((int((gp + gt).max()) + 63) // 64 * 64, max_seq)
+        contiguous = bool((gr == np.arange(gr[0], gr[0] + n)).all())
         pad = None
-        if bucketing == "pad" and any(b.T != Tm for b in g):
+        if bucketing == "pad" and (gt != Tm).any():
             pad = torch.full((n, Tm), -1, dtype=torch.long)
             for j in range(n):
-                pad[j, :g[j].T] = torch.arange(int(offsets[first + j]), int(offsets[first + j + 1]))
-        pb.buckets.append(Bucket(start, end, n, Tm, L, None if contiguous else torch.tensor(rl), rl[0], None, pad))
-        pb.kv_read += sum(b.pos0 + b.T for b in g)
+                pad[j, :int(gt[j])] = torch.arange(int(offsets[a + j]), int(offsets[a + j + 1]))
+        pb.buckets.append(Bucket(start, end, n, Tm, L, None if contiguous else torch.as_tensor(gr), int(gr[0]), None,
+                                 pad))
+        pb.kv_read += int((gp + gt).sum())
         pb.kv_read_padded += n * L
         if not contiguous:
             pb.kv_gathered += n * L
-        first += n
+    return pb
+
+
+def pack_blocks(model, ordered: list, groups: Optional[list] = None, bucketing: str = "exact") -> PackedBatch:
+    """Build the packed batch for blocks already in packed order (groups = bucket partition)."""
+    nb = len(ordered)
+    rws = np.fromiter((b.row for b in ordered), dtype=np.int64, count=nb)
+    pos0 = np.fromiter((b.pos0 for b in ordered), dtype=np.int64, count=nb)
+    Ts = np.fromiter((b.T for b in ordered), dtype=np.int64, count=nb)
+    if groups is None:
+        bounds = np.array([0, nb]) if nb else np.array([0])
+    else:
+        bounds = np.concatenate([[0], np.cumsum([len(g) for g in groups])]).astype(np.int64)
+    pb = _pack(model, rws, pos0, Ts, bounds, bucketing, True)
+    pb._blocks = list(ordered)
+    pb.order = np.arange(nb)
     return pb
 
 
 def build_packed(model, blocks: list, bucketing: str = "exact") -> PackedBatch:
     """Order the blocks bucket-major (by T, then row) and build all attention metadata
     (solutions/packed.py:81-139)."""
-    key = lambda b: (b.row, b.pos0)  # noqa: E731
-    if bucketing == "exact":
-        by_T: dict = {}
-        for b in blocks:
-            by_T.setdefault(b.T, []).append(b)
-        groups = [sorted(by_T[T], key=key) for T in sorted(by_T)]
-    elif bucketing == "pad":
-        groups = [sorted(blocks, key=key)] if blocks else []
-    else:
-        raise ValueError(bucketing)
-    ordered = [b for g in groups for b in g]
-    return pack_blocks(model, ordered, groups, bucketing)
+    nb = len(blocks)
+    rows = np.fromiter((b.row for b in blocks), dtype=np.int64, count=nb)
+    pos0 = np.fromiter((b.pos0 for b in blocks), dtype=np.int64, count=nb)
+    T = np.fromiter((b.T for b in blocks), dtype=np.int64, count=nb)
+    pb = build_packed_arrays(model, rows, pos0, T, bucketing)
+    pb._blocks = [blocks[i] for i in pb.order]
+    return pb
 
 
 def packed_layers(model, x: torch.Tensor, pb: PackedBatch, start: int, end: int, capture: Optional[dict] = None,
-                  capture_layers: tuple = ()) -> torch.Tensor:
+                  capture_layers: tuple = (), out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Run layers [start, end) on packed tokens x [N, dim] (one native call).  capture[k] = hidden state
-    entering exit layer k (output of layer k-1) for every k in capture_layers with start < k <= end."""
+    entering exit layer k (output of layer k-1) for every k in capture_layers with start < k <= end.
+    `out` (optional, contiguous [N, dim], not aliasing x) receives the result."""
     N = pb.n_tokens
     if x.shape != (N, model.cfg.dim) or x.dtype != model.dtype or x.device != model.device:
         raise ValueError(f"x must be [{N}, {model.cfg.dim}] {model.dtype} on {model.device}")
     x = x.contiguous()
-    out = torch.empty_like(x)
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype or not out.is_contiguous() or out.data_ptr() == x.data_ptr():
+        raise ValueError("out must be a contiguous tensor shaped like x that does not alias it")
     if N == 0 or start == end:
         out.copy_(x)
         if capture is not None:
