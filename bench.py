@@ -209,7 +209,7 @@ def run_attention_bench(args):
     S = int(math.ceil((ctx + T).max() / 64) * 64)
     N = int(T.sum())
     g = torch.Generator(device=dev).manual_seed(args.seed)
-    kc = torch.empty(B, Hkv, S, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    kc = torch.empty(B, Hkv, S // 32, D // 16, 64, 8, dtype=torch.bfloat16, device=dev).normal_(generator=g)  # frag K
     vc = torch.empty(B, Hkv, S // 32, D, 32, dtype=torch.bfloat16, device=dev).normal_(generator=g)  # blocked V^T
     q = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
     k_new = torch.empty(N, Hkv, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
@@ -268,7 +268,7 @@ def run_attention_bench(args):
         from oracle.model import brute_attention
 
         got = out.float().cpu()
-        kh, vh, qh = kc.cpu(), _lsk.v_from_blocked(vc.cpu()), q.cpu()
+        kh, vh, qh = _lsk.k_from_frag(kc.cpu()), _lsk.v_from_blocked(vc.cpu()), q.cpu()
         worst = 0.0
         for r in (0, B // 2, B - 1):
             sl = slice(int(offs[r]), int(offs[r] + T[r]))

@@ -6,12 +6,14 @@
 //
 // Layouts
 //   q      [N, Hq, D]            (packed token axis; RoPE applied)
-//   K      [B, Hkv, S, D]        (per layer; the KVCache layout of common/model.py:171-183)
+//   K      bf16: [B, Hkv, S/32, 2 D/32, 64, 8] fragment-major blocks (k_cache_offset in lsk_common.h);
+//          fp32: [B, Hkv, S, D] (the KVCache layout of common/model.py:171-183)
 //   V      [B, Hkv, S/32, D, 32] (stored in 32-position blocks, each block transposed: element (pos, d)
 //                                 at ((pos / 32) * D + d) * 32 + pos % 32 within a (row, head) stripe)
 //   out    [N, Hq * D]
 //   blocks int32 [nb][4] = {q_start, pos0, T, row}
-//   works  int32 [n_work][8] = {blk, row0, nrows, kv_lo, kv_hi, part, 0, 0}
+//   works  int32 [n_work][8] = {q_start, row0, nrows, kv_lo, kv_hi, part, pos0, row} (the block's fields
+//                                 copied in, so a workgroup reads one record before its first load)
 //   groups int32 [n_group][8] = {blk, row0, nrows, part_first, n_split, 0, 0, 0}
 // The G query heads of a KV head are folded into query rows: row = t * G + g (t = token of the
 // block, g = head within the group); a workgroup serves 16 rows, so one KV read serves G*T <= 16 rows.
@@ -27,188 +29,204 @@
 #include "lsk_common.h"
 #include "../include/lsk.h"
 
-#define ATTN_TILE 64
-#define ATTN_ROWS 16  // query rows per workgroup (one MFMA column tile)
+#define ATTN_TILE 64   // work ranges are split at multiples of this (planner granularity)
+#define ATTN_STEP 32   // KV positions per step of a wave
+#define ATTN_QT 2      // 16-row MFMA column tiles per work item
+#define ATTN_ROWS (16 * ATTN_QT)  // query rows per work item
 #define ATTN_MAX_SPLITS 128
+#define ATTN_DEEP_PREFETCH_MAX_WGS 256  // launches up to this many workgroups use the PF = 3 kernel
+
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// bf16 path.  Cache layouts: K [B, Hkv, S, D], V in transposed 32-position blocks (V^T per block), so both
-// MFMA operands come straight from HBM as 16-byte vectors and one V^T fragment load of a wave is 1 KiB
-// contiguous:
+// bf16 path.  Cache layouts: K in fragment-major 32-position blocks (k_cache_offset), V in transposed
+// 32-position blocks (V^T per block), so both MFMA operands come straight from HBM as 16-byte vectors and
+// every K or V^T fragment load of a wave is 1 KiB contiguous (read non-temporally: each byte once per launch):
 //   S^T[pos][q] = K Q^T        v_mfma_f32_16x16x32_bf16, A = K rows (16 positions x 32 d), B = Q^T
 //   O^T[d][q]  += V^T P^T      v_mfma_f32_16x16x32_bf16, A = V^T (16 d x 32 positions), B = P^T
-// Each lane owns one query column (l16), so the running max / row sum are lane-local up to xor shuffles
-// over the four 16-lane groups.  A 32-position step uses two S^T sub-tiles whose MFMA rows are mapped to
-// positions so that lane group g holds positions 8g .. 8g+7 of the step: exactly the 8 consecutive
-// positions its P^T fragment and its 16-byte V^T load need.
-// The 4 waves of a workgroup take the 64-position tiles of the work item's KV range round robin
-// (tile index within the split mod 4) and are merged in wave order through LDS.
-template <int D>
-__global__ __launch_bounds__(256) void attn_bf16_kernel(
+// Each lane owns one query column (l16) of each column tile, so the running max / row sum are lane-local
+// up to xor shuffles over the four 16-lane groups.  A 32-position step uses two S^T sub-tiles whose MFMA
+// rows are mapped to positions so that lane group g holds positions 8g .. 8g+7 of the step: exactly the 8
+// consecutive positions its P^T fragment and its 16-byte V^T load need.
+// A work item carries up to 32 query rows (two column tiles sharing every K / V fragment), so the KV of a
+// (block, KV head) is read by one workgroup for blocks of up to 32 / G tokens.  The 4 waves take the
+// 32-position steps of the item's KV range round robin (step index within the split mod 4), keep the next
+// step's K and V loads in flight while they compute, and are merged in wave order through LDS.
+// PF = steps of K / V loads each wave keeps in flight (register ring).  PF = 1 (two workgroups per CU) for
+// large launches; PF = 3 (one workgroup per CU) for launches that fit the CUs once, where each wave's chain
+// of dependent steps, not the number of loads in flight, sets the time.  PF changes only when loads are
+// issued, never the arithmetic, so both give bitwise the same result.
+template <int D, int PF>
+__global__ __launch_bounds__(256, PF == 1 ? 2 : 1) void attn_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
-    const int32_t* __restrict__ blocks, const int32_t* __restrict__ works, uint16_t* __restrict__ out,
-    float* __restrict__ o_part, float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
+    const int32_t* __restrict__ works, uint16_t* __restrict__ out, float* __restrict__ o_part,
+    float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
   constexpr int KSTEPS = D / 32;
   constexpr int CT = D / 16;
   __shared__ float s_ml[4][2][ATTN_ROWS];
   __shared__ __attribute__((aligned(16))) float s_o[4][ATTN_ROWS][D + 4];
 
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int kvh = blockIdx.y;
   const int Hq = Hkv * G;
 
   const int32_t* wk = works + (long)blockIdx.x * 8;
-  const int blk = wk[0], row0 = wk[1], nrows = wk[2], kv_lo = wk[3], kv_hi = wk[4], part = wk[5];
+  const int q_start = wk[0], row0 = wk[1], nrows = wk[2], kv_lo = wk[3], kv_hi = wk[4], part = wk[5];
+  const int pos0 = wk[6], crow = wk[7];
   if (nrows <= 0) return;  // padding item of the XCD-aware work order
-  const int32_t* bm = blocks + (long)blk * 4;
-  const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
+  const int nq = (nrows + 15) >> 4;  // column tiles in use (wave-uniform)
 
-  const bool qvalid = l16 < nrows;
-  const int r = row0 + (qvalid ? l16 : 0);
-  const int t = r / G, g = r - t * G;
-  const int qpos = pos0 + t;
-  const int hq = kvh * G + g;
-
-  lsk_bf16x8 qf[KSTEPS];
-  {
-    const uint16_t* qrow = q + ((long)(q_start + t) * Hq + hq) * D;
+  lsk_bf16x8 qf[ATTN_QT][KSTEPS];
+  int qpos[ATTN_QT];
 #pragma unroll
-    for (int j = 0; j < KSTEPS; ++j) qf[j] = qvalid ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
+  for (int qt = 0; qt < ATTN_QT; ++qt) {
+    const bool valid = 16 * qt + l16 < nrows;
+    const int r = row0 + 16 * qt + (valid ? l16 : 0);
+    const int t = r / G, g = r - t * G;
+    qpos[qt] = valid ? pos0 + t : -1;  // invalid rows: every score masked
+    const uint16_t* qrow = q + ((long)(q_start + t) * Hq + kvh * G + g) * D;
+#pragma unroll
+    for (int j = 0; j < KSTEPS; ++j)
+      qf[qt][j] = (valid && qt < nq) ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
   }
-  lsk_f32x4 oacc[CT];
+  lsk_f32x4 oacc[ATTN_QT][CT];
+  float m_run[ATTN_QT], l_run[ATTN_QT];
 #pragma unroll
-  for (int c = 0; c < CT; ++c) oacc[c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  for (int qt = 0; qt < ATTN_QT; ++qt) {
+    m_run[qt] = -INFINITY;
+    l_run[qt] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CT; ++c) oacc[qt][c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+  }
+  // positions every valid row of the item may read without masking: <= the first row's position, < kv_hi
+  const int full_lim = min(kv_hi - 1, pos0 + row0 / G);
 
   const long head = (long)crow * Hkv + kvh;
   const uint16_t* kbase = kc + head * (long)S * D;
   const uint16_t* vbase = vt + head * (long)D * S;
-  // MFMA row l16 of S^T sub-tile a <-> position 8 * (l16 / 4) + 4 * a + l16 % 4 of the 32-position step
-  const int krow0 = 8 * (l16 >> 2) + (l16 & 3);
+  // MFMA row l16 of S^T sub-tile a <-> position 8 * (l16 / 4) + 4 * a + l16 % 4 of the 32-position step (the
+  // order the K cache stores each block's fragments in)
 
-#ifndef LSK_ATTN_PIPE
-#define LSK_ATTN_PIPE 1
-#endif
-#ifndef LSK_ATTN_NT
-#define LSK_ATTN_NT 0
-#endif
-#ifndef LSK_ATTN_KFRAG
-#define LSK_ATTN_KFRAG 0
-#endif
   auto ldkv = [&](const uint16_t* p) -> lsk_bf16x8 {
-#if LSK_ATTN_NT
     return __builtin_bit_cast(lsk_bf16x8, __builtin_nontemporal_load((const lsk_i32x4*)p));
-#else
-    return *(const lsk_bf16x8*)p;
-#endif
   };
-  lsk_bf16x8 kf[2][KSTEPS];
-  lsk_bf16x8 vf[CT];
-  auto load_k = [&](int sb) {
-#if LSK_ATTN_KFRAG
+  lsk_bf16x8 kf[PF][2][KSTEPS];
+  lsk_bf16x8 vf[PF][CT];
+  auto load_k = [&](lsk_bf16x8 (&kr)[2][KSTEPS], int sb) {
+    // fragment-major K cache: fragment (a, j) of the step's 32-position block is 1 KiB in lane order
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(kbase + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
-#else
+      for (int j = 0; j < KSTEPS; ++j) kr[a][j] = ldkv(kbase + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
+  };
+  auto load_v = [&](lsk_bf16x8 (&vr)[CT], int sb) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      const uint16_t* krow = kbase + (long)(sb + krow0 + 4 * a) * D + 8 * lg;
+    for (int c = 0; c < CT; ++c) vr[c] = ldkv(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
+  };
+  // this wave's steps: 32-position steps wave, wave + 4, ... of the range, in order
+  auto step_pos = [&](int i) { return kv_lo + ATTN_STEP * (wave + 4 * i); };
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(krow + 32 * j);
+  for (int u = 0; u < PF; ++u) {
+    const int sp = step_pos(u);
+    if (sp < kv_hi) {
+      load_k(kf[u], sp);
+      load_v(vf[u], sp);
     }
-#endif
-  };
-  auto load_v = [&](int sb) {
-#pragma unroll
-    for (int c = 0; c < CT; ++c) vf[c] = ldkv(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
-  };
-  // this wave's 32-position steps: both halves of tiles wave, wave + 4, ... of the range, in order
-  auto step_pos = [&](int i) { return kv_lo + ATTN_TILE * (wave + 4 * (i >> 1)) + 32 * (i & 1); };
-  int sb = step_pos(0);
-  if (sb < kv_hi) {
-    load_k(sb);
-    load_v(sb);
   }
-  for (int i = 0; sb < kv_hi; ++i) {
-    const int sn = step_pos(i + 1);
-    const bool more = sn < kv_hi;
-#if !LSK_ATTN_PIPE
-    (void)more;
-#endif
-    lsk_f32x4 sacc[2];
+  for (int i0 = 0; step_pos(i0) < kv_hi; i0 += PF) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a) {
-      sacc[a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < PF; ++u) {
+      const int sb = step_pos(i0 + u);
+      if (sb >= kv_hi) break;
+      const int sn = step_pos(i0 + u + PF);  // the step whose loads reuse this ring slot
+      const bool more = sn < kv_hi;
+      lsk_f32x4 sacc[ATTN_QT][2];
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j)
-        sacc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[j], sacc[a], 0, 0, 0);
-    }
-#if LSK_ATTN_PIPE
-    if (more) load_k(sn);  // next step's K streams in during this step's softmax and P.V
-#endif
-    // sacc[a][i] <-> position sb + 8 lg + 4 a + i, query l16
-    float sv[8];
-    float mt = -INFINITY;
+      for (int qt = 0; qt < ATTN_QT; ++qt) {
+        if (qt < nq) {
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+          for (int a = 0; a < 2; ++a) {
+            sacc[qt][a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int kp = sb + 8 * lg + 4 * a + e;
-        const bool ok = qvalid && kp < kv_hi && kp <= qpos;
-        const float sc = ok ? sacc[a][e] * scale_log2 : -INFINITY;
-        sv[4 * a + e] = sc;
-        mt = fmaxf(mt, sc);
+            for (int j = 0; j < KSTEPS; ++j)
+              sacc[qt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][a][j], qf[qt][j], sacc[qt][a], 0, 0, 0);
+          }
+        }
       }
-    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
-    const float m_new = fmaxf(m_run, mt);
-    const float alpha = (m_new == m_run) ? 1.f : fast_exp2(m_run - m_new);
-    float rs = 0.f;
-    lsk_bf16x8 pb;
+      if (more) load_k(kf[u], sn);  // streams in while later steps are computed
+      const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
+      lsk_bf16x8 pb[ATTN_QT];
+      float alpha[ATTN_QT];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float pe = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
-      rs += pe;
-      pb[e] = __builtin_bit_cast(__bf16, f2bf(pe));
-    }
-    rs += __shfl_xor(rs, 16, 64);
-    rs += __shfl_xor(rs, 32, 64);
-    l_run = l_run * alpha + rs;
-    m_run = m_new;
+      for (int qt = 0; qt < ATTN_QT; ++qt) {
+        if (qt < nq) {
+          // sacc[qt][a][e] <-> position sb + 8 lg + 4 a + e, query column l16 of tile qt
+          float sv[8];
+          float mt = -INFINITY;
 #pragma unroll
-    for (int c = 0; c < CT; ++c) {
-      oacc[c][0] *= alpha;
-      oacc[c][1] *= alpha;
-      oacc[c][2] *= alpha;
-      oacc[c][3] *= alpha;
-      oacc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[c], pb, oacc[c], 0, 0, 0);
+          for (int a = 0; a < 2; ++a)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              float sc = sacc[qt][a][e] * scale_log2;
+              if (!full) {
+                const int kp = sb + 8 * lg + 4 * a + e;
+                sc = (kp < kv_hi && kp <= qpos[qt]) ? sc : -INFINITY;
+              }
+              sv[4 * a + e] = sc;
+              mt = fmaxf(mt, sc);
+            }
+          mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          const float m_new = fmaxf(m_run[qt], mt);
+          alpha[qt] = (m_new == m_run[qt]) ? 1.f : fast_exp2(m_run[qt] - m_new);
+          float rs = 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float pe = (sv[e] == -INFINITY) ? 0.f : fast_exp2(sv[e] - m_new);
+            rs += pe;
+            pb[qt][e] = static_cast<__bf16>(pe);
+          }
+          rs += __shfl_xor(rs, 16, 64);
+          rs += __shfl_xor(rs, 32, 64);
+          l_run[qt] = l_run[qt] * alpha[qt] + rs;
+          m_run[qt] = m_new;
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < ATTN_QT; ++qt) {
+        if (qt < nq) {
+#pragma unroll
+          for (int c = 0; c < CT; ++c) {
+            oacc[qt][c][0] *= alpha[qt];
+            oacc[qt][c][1] *= alpha[qt];
+            oacc[qt][c][2] *= alpha[qt];
+            oacc[qt][c][3] *= alpha[qt];
+            oacc[qt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[u][c], pb[qt], oacc[qt][c], 0, 0, 0);
+          }
+        }
+      }
+      if (more) load_v(vf[u], sn);
     }
-#if LSK_ATTN_PIPE
-    if (more) load_v(sn);
-#else
-    if (more) {
-      load_k(sn);
-      load_v(sn);
-    }
-#endif
-    sb = sn;
   }
   // ---- merge the four waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
-  if (lg == 0) {
-    s_ml[wave][0][l16] = m_run;
-    s_ml[wave][1][l16] = l_run;
-  }
 #pragma unroll
-  for (int c = 0; c < CT; ++c)
-    *(float4*)(&s_o[wave][l16][16 * c + 4 * lg]) = make_float4(oacc[c][0], oacc[c][1], oacc[c][2], oacc[c][3]);
+  for (int qt = 0; qt < ATTN_QT; ++qt) {
+    if (qt < nq) {
+      if (lg == 0) {
+        s_ml[wave][0][16 * qt + l16] = m_run[qt];
+        s_ml[wave][1][16 * qt + l16] = l_run[qt];
+      }
+#pragma unroll
+      for (int c = 0; c < CT; ++c)
+        *(float4*)(&s_o[wave][16 * qt + l16][16 * c + 4 * lg]) =
+            make_float4(oacc[qt][c][0], oacc[qt][c][1], oacc[qt][c][2], oacc[qt][c][3]);
+    }
+  }
   __syncthreads();
-  for (int e = tid; e < ATTN_ROWS * D; e += 256) {
+  for (int e = tid; e < nrows * D; e += 256) {
     const int qr = e / D, d = e - qr * D;
-    if (qr >= nrows) continue;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][0][qr]);
@@ -299,7 +317,6 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
 template <int D>
 __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
                                                        const float* __restrict__ vc,
-                                                       const int32_t* __restrict__ blocks,
                                                        const int32_t* __restrict__ works, float* __restrict__ out,
                                                        int G, int Hkv, int S, float scale) {
   constexpr int DPL = (D + 63) / 64;  // d values per lane
@@ -308,9 +325,7 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
   const int kvh = blockIdx.y;
   const int Hq = Hkv * G;
   const int32_t* wk = works + (long)blockIdx.x * 8;
-  const int blk = wk[0], row0 = wk[1], nrows = wk[2];
-  const int32_t* bm = blocks + (long)blk * 4;
-  const int q_start = bm[0], pos0 = bm[1], crow = bm[3];
+  const int q_start = wk[0], row0 = wk[1], nrows = wk[2], pos0 = wk[6], crow = wk[7];
   const long head_base = ((long)crow * Hkv + kvh) * (long)S * D;
   for (int rl = wave; rl < nrows; rl += 4) {
     const int r = row0 + rl;
@@ -375,7 +390,7 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
   LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
   LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && split % ATTN_TILE == 0, LSK_ESHAPE,
               "lsk_attn_plan: bad arguments (split must be a positive multiple of %d)", ATTN_TILE);
-  struct Item { int b, row0, nrows, lo, hi, part; };
+  struct Item { int b, row0, nrows, lo, hi, part; };  // b: block index (its fields are copied into the record)
   std::vector<std::vector<Item>> fams;
   int ng = 0, np = 0;
   for (int b = 0; b < nb; ++b) {
@@ -428,9 +443,13 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
   auto emit = [&](const Item* it) -> int {
     LSK_REQUIRE(nw < max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
     int32_t* wp = works + (long)nw * 8;
-    if (it) { wp[0] = it->b; wp[1] = it->row0; wp[2] = it->nrows; wp[3] = it->lo; wp[4] = it->hi; wp[5] = it->part; }
-    else { wp[0] = 0; wp[1] = 0; wp[2] = 0; wp[3] = 0; wp[4] = 0; wp[5] = -1; }
-    wp[6] = wp[7] = 0;
+    if (it) {
+      const int32_t* bm = blocks + (long)it->b * 4;
+      wp[0] = bm[0]; wp[1] = it->row0; wp[2] = it->nrows; wp[3] = it->lo; wp[4] = it->hi; wp[5] = it->part;
+      wp[6] = bm[1]; wp[7] = bm[3];
+    } else {
+      wp[0] = 0; wp[1] = 0; wp[2] = 0; wp[3] = 0; wp[4] = 0; wp[5] = -1; wp[6] = 0; wp[7] = 0;
+    }
     ++nw;
     return 0;
   };
@@ -483,14 +502,21 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
       ml_part = (float*)((char*)workspace + lsk_align_up(rows * head_dim * sizeof(float), 256));
     }
     const float scale_log2 = scale * 1.4426950408889634f;
-    if (head_dim == 128)
-      attn_bf16_kernel<128><<<grid, 256, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                  (const uint16_t*)vcache, blocks, works, (uint16_t*)out, o_part,
-                                                  ml_part, G, n_kv_heads, max_seq, scale_log2);
-    else
-      attn_bf16_kernel<64><<<grid, 256, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                 (const uint16_t*)vcache, blocks, works, (uint16_t*)out, o_part,
-                                                 ml_part, G, n_kv_heads, max_seq, scale_log2);
+    // a launch that fits the CUs once (one workgroup each) is bound by each wave's chain of steps: keep three
+    // steps of loads in flight per wave; larger launches run two workgroups per CU with one step in flight
+    const bool deep_prefetch = (long)n_works * n_kv_heads <= ATTN_DEEP_PREFETCH_MAX_WGS;
+    const uint16_t* qb = (const uint16_t*)q;
+    const uint16_t* kb = (const uint16_t*)kcache;
+    const uint16_t* vb = (const uint16_t*)vcache;
+    uint16_t* ob = (uint16_t*)out;
+#define LSK_ATTN_LAUNCH(D_, PF_) \
+  attn_bf16_kernel<D_, PF_><<<grid, 256, 0, s>>>(qb, kb, vb, works, ob, o_part, ml_part, G, n_kv_heads, max_seq, scale_log2)
+    if (head_dim == 128) {
+      if (deep_prefetch) LSK_ATTN_LAUNCH(128, 3); else LSK_ATTN_LAUNCH(128, 1);
+    } else {
+      if (deep_prefetch) LSK_ATTN_LAUNCH(64, 3); else LSK_ATTN_LAUNCH(64, 1);
+    }
+#undef LSK_ATTN_LAUNCH
     int rc = lsk_check_launch("lsk_ragged_attn");
     if (rc) return rc;
     if (n_groups > 0) {
@@ -508,10 +534,10 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
   if (dtype == LSK_DTYPE_F32) {
     LSK_REQUIRE(n_parts == 0, LSK_EARG, "lsk_ragged_attn: the fp32 path takes unsplit plans");
     switch (head_dim) {
-      case 16: attn_f32_kernel<16><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
-      case 32: attn_f32_kernel<32><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
-      case 64: attn_f32_kernel<64><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
-      case 128: attn_f32_kernel<128><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, blocks, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 16: attn_f32_kernel<16><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 32: attn_f32_kernel<32><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 64: attn_f32_kernel<64><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
+      case 128: attn_f32_kernel<128><<<grid, 256, 0, s>>>((const float*)q, (const float*)kcache, (const float*)vcache, works, (float*)out, G, n_kv_heads, max_seq, scale); break;
       default: LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_ragged_attn: fp32 head_dim %d", head_dim);
     }
     return lsk_check_launch("lsk_ragged_attn(f32)");

@@ -30,6 +30,25 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // Round a float through bf16 and back (value of the float once stored in a bf16 tensor).
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// Offset of K cache element (position p, dim d) within one (row, KV head) stripe of S positions x D.
+// bf16: fragment-major 32-position blocks of 32 D elements, each block 2 (D / 32) MFMA fragments of 1 KiB:
+//   fragment (a, j), lane l = 16 lg + l16 holds positions 8 (l16 / 4) + 4 a + l16 % 4 of the block and
+//   d = 32 j + 8 lg .. +7, so a wave's K fragment load is one contiguous 1 KiB request (D % 32 == 0).
+// fp32: the reference's row-major [S, D].
+template <typename T>
+__device__ __forceinline__ long k_cache_offset(int p, int d, int D);
+template <>
+__device__ __forceinline__ long k_cache_offset<uint16_t>(int p, int d, int D) {
+  const int pp = p & 31;
+  const int a = (pp >> 2) & 1, l16 = ((pp >> 3) << 2) | (pp & 3);
+  const int j = d >> 5, lg = (d >> 3) & 3;
+  return (long)(p >> 5) * 32 * D + (long)((a * (D >> 5) + j) * 64 + lg * 16 + l16) * 8 + (d & 7);
+}
+template <>
+__device__ __forceinline__ long k_cache_offset<float>(int p, int d, int D) {
+  return (long)p * D + d;
+}
+
 // Loads/stores of "dtype T" elements expressed as float.
 template <typename T> struct Elem;
 template <> struct Elem<float> {

@@ -216,10 +216,15 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
       const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
       const float a2 = Elem<T>::round(x2 * c2), b2 = Elem<T>::round(x1 * s2);
       const float o1 = a1 + b1, o2 = a2 + b2;
-      T* dst = (h < Hq) ? q_out + ((long)t * Hq + h) * D
-                        : kc + (((long)row * Hkv + (h - Hq)) * max_seq + p) * D;
-      Elem<T>::st(dst + j, o1);
-      Elem<T>::st(dst + j + half, o2);
+      if (h < Hq) {
+        T* dst = q_out + ((long)t * Hq + h) * D;
+        Elem<T>::st(dst + j, o1);
+        Elem<T>::st(dst + j + half, o2);
+      } else {
+        T* dst = kc + ((long)row * Hkv + (h - Hq)) * (long)max_seq * D;
+        Elem<T>::st(dst + k_cache_offset<T>(p, j, D), o1);
+        Elem<T>::st(dst + k_cache_offset<T>(p, j + half, D), o2);
+      }
     } else {
       // V cache: 32-position blocks, each transposed ([B, Hkv, S/32, D, 32])
       T* dst = vc + ((long)row * Hkv + (h - Hq - Hkv)) * (long)D * max_seq + (long)(p >> 5) * 32 * D + (p & 31);
@@ -247,7 +252,7 @@ static int rope_common(int dtype, const void* qkv, const float* P, int KS, void*
               "lsk_rope_append: null pointer");
   LSK_REQUIRE(n_tokens >= 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && (head_dim % 2) == 0 &&
                   head_dim <= 512 && n_heads % n_kv_heads == 0 && max_batch > 0 && max_seq > 0 && tab_len > 0 &&
-                  KS >= 1,
+                  KS >= 1 && max_seq % 32 == 0 && (dtype != LSK_DTYPE_BF16 || head_dim % 32 == 0),
               LSK_ESHAPE, "lsk_rope_append: bad shape");
   if (n_tokens == 0) return 0;
   const long pstride = (long)n_tokens * (n_heads + 2 * n_kv_heads) * head_dim;
@@ -295,7 +300,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ k,
   if (row < 0 || row >= max_batch || p < 0 || p >= max_seq) return;
   for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) {
     const int hk = e / D, d = e - hk * D;
-    kc[(((long)row * Hkv + hk) * max_seq + p) * D + d] = k[(long)t * Hkv * D + e];
+    kc[((long)row * Hkv + hk) * (long)max_seq * D + k_cache_offset<T>(p, d, D)] = k[(long)t * Hkv * D + e];
     vc[((long)row * Hkv + hk) * (long)D * max_seq + (long)(p >> 5) * 32 * D + d * 32 + (p & 31)] = v[(long)t * Hkv * D + e];
   }
 }
@@ -304,8 +309,9 @@ extern "C" int lsk_kv_append(int dtype, const void* k, const void* v, void* kcac
                              const int32_t* pos, int n_tokens, int n_kv_heads, int head_dim, int max_batch,
                              int max_seq, void* stream) {
   LSK_REQUIRE(k && v && kcache && vcache && rows && pos, LSK_EARG, "lsk_kv_append: null pointer");
-  LSK_REQUIRE(n_tokens >= 0 && n_kv_heads > 0 && head_dim > 0 && max_batch > 0 && max_seq > 0, LSK_ESHAPE,
-              "lsk_kv_append: bad shape");
+  LSK_REQUIRE(n_tokens >= 0 && n_kv_heads > 0 && head_dim > 0 && max_batch > 0 && max_seq > 0 && max_seq % 32 == 0 &&
+                  (dtype != LSK_DTYPE_BF16 || head_dim % 32 == 0),
+              LSK_ESHAPE, "lsk_kv_append: bad shape (bf16 needs head_dim %% 32 == 0; max_seq %% 32 == 0)");
   if (n_tokens == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == LSK_DTYPE_BF16)

@@ -63,6 +63,22 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
 
 
+@pytest.mark.parametrize("D", [64, 128])
+def test_k_fragment_layout(D):
+    """k_to_frag follows the documented lane order (computed here element by element) and inverts exactly."""
+    lsk = _lsk()
+    S = 64
+    k = torch.arange(2 * S * D, dtype=torch.float32).view(2, S, D)
+    kf = lsk.k_to_frag(k)
+    assert kf.shape == (2, S // 32, D // 16, 64, 8)
+    for blk, a, j, lane, e in [(0, 0, 0, 0, 0), (1, 1, D // 32 - 1, 63, 7), (0, 1, 0, 21, 3), (1, 0, 1, 42, 5)]:
+        l16, lg = lane % 16, lane // 16
+        p = 32 * blk + 8 * (l16 // 4) + 4 * a + l16 % 4
+        d = 32 * j + 8 * lg + e
+        assert kf[1, blk, a * (D // 32) + j, lane, e] == k[1, p, d]
+    assert torch.equal(lsk.k_from_frag(kf), k)
+
+
 def _plan(blocks, G, split):
     return _lsk().attn_plan(np.asarray(blocks, dtype=np.int32), G, split)
 
@@ -76,13 +92,17 @@ def test_attention_plan_covers_every_row_once(G, split):
     q_start = np.concatenate([[0], np.cumsum(T)[:-1]])
     blocks = np.stack([q_start, pos0, T, rng.integers(0, 8, nb)], axis=1)
     works, groups, n_parts = _plan(blocks, G, split)
+    R = _lsk().ATTN_ROWS
+    by_start = {int(qs): b for b, qs in enumerate(q_start)}
     cover = {}
     parts_seen = []
     for w in works:
-        b, row0, nrows, lo, hi, part = (int(v) for v in w[:6])
+        qs, row0, nrows, lo, hi, part, p0, row = (int(v) for v in w)
         if nrows == 0:
             continue                                       # padding slot of the XCD order
-        assert lo % split == 0 and hi - lo <= split and lo < hi
+        b = by_start[qs]                                   # the record carries its block's fields
+        assert (p0, row) == (pos0[b], blocks[b][3])
+        assert lo % split == 0 and hi - lo <= split and lo < hi and nrows <= R
         for r in range(row0, row0 + nrows):
             cover.setdefault((b, r), []).append((lo, hi))
         if part >= 0:
@@ -91,9 +111,9 @@ def test_attention_plan_covers_every_row_once(G, split):
     for b in range(nb):
         for r in range(T[b] * G):
             ivs = sorted(cover[(b, r)])
-            tile = r // 16
-            t_last = min(tile * 16 + 15, T[b] * G - 1) // G
-            end = pos0[b] + t_last + 1                     # the 16-row tile's KV range
+            tile = r // R
+            t_last = min(tile * R + R - 1, T[b] * G - 1) // G
+            end = pos0[b] + t_last + 1                     # the row tile's KV range
             assert ivs[0][0] == 0 and ivs[-1][1] == end
             assert all(ivs[i][1] == ivs[i + 1][0] for i in range(len(ivs) - 1))
     for gp in groups:
@@ -101,7 +121,9 @@ def test_attention_plan_covers_every_row_once(G, split):
 
 
 def test_attention_plan_places_sibling_tiles_eight_slots_apart():
-    blocks = [(0, 50 * i, 9, i) for i in range(16)]         # 36 rows -> 3 sibling tiles, KV < 1024: 1 split
+    R = _lsk().ATTN_ROWS
+    T = (2 * R + 4) // 4                                     # G = 4: 2 R + 4 rows -> 3 sibling tiles
+    blocks = [(T * i, 50 * i, T, i) for i in range(16)]      # KV < 1024: 1 split
     works, _, _ = _plan(blocks, 4, 1024)
     where = {}
     for idx, w in enumerate(works):

@@ -31,6 +31,15 @@ def _gen(seed):
     return torch.Generator().manual_seed(seed)
 
 
+def _kstore(lsk, k):
+    """K cache storage the kernels read: fragment-major for bf16, row-major for fp32."""
+    return lsk.k_to_frag(k) if k.dtype == BF16 else k
+
+
+def _kview(lsk, kstore):
+    return lsk.k_from_frag(kstore) if kstore.dtype == BF16 else kstore
+
+
 # ----------------------------------------------------------------------------- GEMM
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 64), (5, 128, 256), (16, 64, 96), (17, 256, 512), (33, 128, 4160),
@@ -159,7 +168,7 @@ def test_rope_append_is_bit_exact(cuda, dtype, D):
     pos = torch.randperm(S, generator=g)[:N]             # distinct (row, pos) slots
     kc = torch.zeros(B, Hkv, S, D, dtype=dtype)
     vc = torch.zeros_like(kc)
-    kd = kc.to(cuda)
+    kd = _kstore(lsk, kc).to(cuda)                                          # fragment-major for bf16
     vd = torch.zeros(B, Hkv, S // 32, D, 32, dtype=dtype, device=cuda)      # blocked-transposed V storage
     q_out = torch.empty(N, Hq, D, dtype=dtype, device=cuda)
     lsk.rope_append(qkv.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda),
@@ -173,7 +182,7 @@ def test_rope_append_is_bit_exact(cuda, dtype, D):
     assert torch.equal(q_out.cpu(), q_ref)
     kc[rows, :, pos] = k_ref
     vc[rows, :, pos] = v_ref
-    assert torch.equal(kd.cpu(), kc)
+    assert torch.equal(_kview(lsk, kd.cpu()), kc)
     assert torch.equal(vd.cpu(), vc)
 
 
@@ -187,11 +196,11 @@ def test_kv_append_is_bit_exact(cuda):
     pos = torch.randperm(S, generator=g)[:N]
     kc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
     vc = torch.randn(B, Hkv, S, D, generator=g).to(BF16)
-    kd, vd = kc.to(cuda), lsk.v_to_blocked(vc).to(cuda)
+    kd, vd = lsk.k_to_frag(kc).to(cuda), lsk.v_to_blocked(vc).to(cuda)
     lsk.kv_append(k.to(cuda), v.to(cuda), kd, vd, rows.to(torch.int32).to(cuda), pos.to(torch.int32).to(cuda))
     kc[rows, :, pos] = k
     vc[rows, :, pos] = v
-    assert torch.equal(kd.cpu(), kc) and torch.equal(lsk.v_from_blocked(vd).cpu(), vc)
+    assert torch.equal(lsk.k_from_frag(kd.cpu()), kc) and torch.equal(lsk.v_from_blocked(vd).cpu(), vc)
 
 
 # ----------------------------------------------------------------------------- attention
@@ -220,11 +229,13 @@ def _run_attn(lsk, cuda, q, kc, vc, tab, split):
     out = torch.empty(q.shape[0], Hq * D, dtype=q.dtype, device=cuda)
     ws = torch.empty(max(lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=cuda)
     gdev = torch.from_numpy(groups).to(cuda) if len(groups) else None
-    lsk.ragged_attn(q.to(cuda), kc.to(cuda), lsk.v_to_blocked(vc).to(cuda), torch.from_numpy(tab).to(cuda),
+    lsk.ragged_attn(q.to(cuda), _kstore(lsk, kc).to(cuda), lsk.v_to_blocked(vc).to(cuda), torch.from_numpy(tab).to(cuda),
                     torch.from_numpy(works).to(cuda), len(works), gdev, len(groups), n_parts, out, Hq,
                     1.0 / math.sqrt(D), ws)
     return out.cpu()
 
+
+ATTN_TEST_SPLIT = 1024   # KV positions per split in these cases (block ranges cross split boundaries)
 
 ATTN_CASES = [
     # (B, Hq, Hkv, D, S, blocks)
@@ -240,7 +251,7 @@ def test_ragged_attention_bf16_matches_brute_force(cuda, case):
     lsk = _lsk()
     B, Hq, Hkv, D, S, blocks = ATTN_CASES[case]
     q, kc, vc, tab, ref = _attn_case(case, BF16, B, Hq, Hkv, D, S, blocks)
-    got = _run_attn(lsk, cuda, q, kc, vc, tab, lsk.ATTN_SPLIT).double()
+    got = _run_attn(lsk, cuda, q, kc, vc, tab, ATTN_TEST_SPLIT).double()
     # bf16 inputs are exact in the fp64 reference; the kernel rounds P to bf16 and the output to bf16
     err = (got - ref).abs()
     assert err.max() < 2e-2, err.max()
@@ -261,13 +272,32 @@ def test_ragged_attention_bf16_is_batch_invariant(cuda):
     B, Hq, Hkv, D, S = 2, 32, 8, 128, 2048
     blocks = [(0, 505, 9), (1, 1020, 8)]
     q, kc, vc, tab, _ = _attn_case(21, BF16, B, Hq, Hkv, D, S, blocks)
-    full = _run_attn(lsk, cuda, q, kc, vc, tab, lsk.ATTN_SPLIT)
+    full = _run_attn(lsk, cuda, q, kc, vc, tab, ATTN_TEST_SPLIT)
     off = 0
     for (r, p0, T) in blocks:
         for t in range(T):
             one = np.array([(0, p0 + t, 1, r)], dtype=np.int32)
-            got = _run_attn(lsk, cuda, q[off + t:off + t + 1].contiguous(), kc, vc, one, lsk.ATTN_SPLIT)
+            got = _run_attn(lsk, cuda, q[off + t:off + t + 1].contiguous(), kc, vc, one, ATTN_TEST_SPLIT)
             assert torch.equal(got[0], full[off + t]), (r, p0, t)
+        off += T
+
+
+def test_ragged_attention_launch_size_variants_agree_bitwise(cuda):
+    """Launches of more than 256 workgroups run the one-step-in-flight kernel, smaller ones the deep-prefetch
+    kernel; a block gives bitwise the same output in both."""
+    lsk = _lsk()
+    B, Hq, Hkv, D, S = 40, 32, 8, 128, 1024
+    rng = np.random.default_rng(5)
+    blocks = [(r, int(rng.integers(0, 900)), int(rng.integers(1, 9))) for r in range(B)]
+    q, kc, vc, tab, _ = _attn_case(33, BF16, B, Hq, Hkv, D, S, blocks)
+    works, _, _ = lsk.attn_plan(tab, Hq // Hkv, lsk.ATTN_SPLIT)
+    assert len(works) * Hkv > 256                                  # the large-launch kernel
+    full = _run_attn(lsk, cuda, q, kc, vc, tab, lsk.ATTN_SPLIT)
+    off = 0
+    for i, (r, p0, T) in enumerate(blocks[:6]):
+        one = np.array([(0, p0, T, r)], dtype=np.int32)
+        got = _run_attn(lsk, cuda, q[off:off + T].contiguous(), kc, vc, one, lsk.ATTN_SPLIT)
+        assert torch.equal(got, full[off:off + T]), (r, p0, T)
         off += T
 
 
@@ -388,7 +418,7 @@ def test_rope_append_partial_is_bit_exact(cuda):
     qkv = (P[0] + P[1]).to(BF16)
     rows = torch.tensor([0, 1, 1, 0, 1])
     pos = torch.tensor([3, 9, 10, 4, 11])
-    kd = torch.zeros(B, Hkv, S, D, dtype=BF16, device=cuda)
+    kd = lsk.k_to_frag(torch.zeros(B, Hkv, S, D, dtype=BF16)).to(cuda)
     vd = torch.zeros(B, Hkv, S // 32, D, 32, dtype=BF16, device=cuda)
     q_out = torch.empty(N, Hq, D, dtype=BF16, device=cuda)
     lsk.rope_append_partial(P.to(cuda), q_out, kd, vd, cos.to(cuda), sin.to(cuda), rows.to(torch.int32).to(cuda),
@@ -397,7 +427,7 @@ def test_rope_append_partial_is_bit_exact(cuda):
     c, s = cos[pos].to(BF16).unsqueeze(1), sin[pos].to(BF16).unsqueeze(1)
     assert torch.equal(q_out.cpu(), o_rope(qkv[:, :Hq * D].view(N, Hq, D), c, s))
     kref = o_rope(qkv[:, Hq * D:(Hq + Hkv) * D].view(N, Hkv, D), c, s)
-    assert torch.equal(kd.cpu()[rows, :, pos], kref)
+    assert torch.equal(lsk.k_from_frag(kd.cpu())[rows, :, pos], kref)
     assert torch.equal(vd.cpu()[rows, :, pos], qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D))
 
 

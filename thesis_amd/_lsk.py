@@ -19,8 +19,8 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblsk.so"
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
-ATTN_SPLIT = 1024         # LSK_ATTN_SPLIT
-ATTN_ROWS = 16            # query rows per attention workgroup
+ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
+ATTN_ROWS = 32            # query rows per attention work item
 ABI_VERSION = 2
 
 # name -> (restype, argtypes)
@@ -109,6 +109,43 @@ def _stream() -> int:
     if _raw_stream is not None:
         return _raw_stream(torch._C._cuda_getDevice())
     return torch.cuda.current_stream().cuda_stream
+
+
+def k_to_frag(k: torch.Tensor) -> torch.Tensor:
+    """[..., S, D] -> the bf16 K cache storage [..., S/32, D/16, 64, 8]: per 32-position block, 2 D/32 MFMA
+    fragments (a, j) of 1 KiB; lane 16 lg + 4 q + r of fragment (a, j) holds position 8 q + 4 a + r of the
+    block and d = 32 j + 8 lg .. +7."""
+    *lead, S, D = k.shape
+    n = len(lead)
+    x = k.reshape(*lead, S // 32, 4, 2, 4, D // 32, 4, 8)          # blk, q, a, r, j, lg, e
+    perm = list(range(n)) + [n + i for i in (0, 2, 4, 5, 1, 3, 6)]  # blk, a, j, lg, q, r, e
+    return x.permute(*perm).reshape(*lead, S // 32, D // 16, 64, 8).contiguous()
+
+
+def k_from_frag(kf: torch.Tensor) -> torch.Tensor:
+    """bf16 K cache storage [..., S/32, D/16, 64, 8] -> [..., S, D] (a copy)."""
+    *lead, nb, nf, _, _ = kf.shape
+    n = len(lead)
+    D = nf * 16
+    x = kf.reshape(*lead, nb, 2, D // 32, 4, 4, 4, 8)               # blk, a, j, lg, q, r, e
+    perm = list(range(n)) + [n + i for i in (0, 4, 1, 5, 2, 3, 6)]  # blk, q, a, r, j, lg, e
+    return x.permute(*perm).reshape(*lead, nb * 32, D)
+
+
+def k_dims(kcache: torch.Tensor) -> tuple:
+    """(B, Hkv, S, D) of a K cache: fragment-major bf16 storage [B, Hkv, S/32, D/16, 64, 8] or row-major
+    [B, Hkv, S, D] (fp32)."""
+    if kcache.dim() == 6:
+        B, Hkv, nb, nf = kcache.shape[:4]
+        return B, Hkv, nb * 32, nf * 16
+    return tuple(kcache.shape)
+
+
+def _check_kcache(dtype: torch.dtype, kcache: torch.Tensor) -> None:
+    if dtype == torch.bfloat16 and kcache.dim() != 6:
+        raise LskError("bf16 K caches use the fragment-major storage [B, Hkv, S/32, D/16, 64, 8] (k_to_frag)")
+    if dtype != torch.bfloat16 and kcache.dim() != 4:
+        raise LskError("fp32 K caches are row-major [B, Hkv, S, D]")
 
 
 def v_to_blocked(v: torch.Tensor) -> torch.Tensor:
@@ -205,10 +242,11 @@ def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, out: torch.Tensor | No
 
 
 def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads, head_dim):
-    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
+    """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
+    _check_kcache(q_out.dtype, kcache)
     N = qkv.shape[0]
-    B, Hkv, S, D = kcache.shape
+    B, Hkv, S, D = k_dims(kcache)
     assert qkv.is_contiguous() and q_out.is_contiguous() and kcache.is_contiguous() and vcache.is_contiguous()
     assert cos_tab.dtype == torch.float32 and cos_tab.is_contiguous() and cos_tab.shape[1] == head_dim
     _check(load().lsk_rope_append(dtype_code(qkv.dtype), _ptr(qkv), _ptr(q_out), _ptr(kcache), _ptr(vcache),
@@ -217,9 +255,10 @@ def rope_append(qkv, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32,
 
 
 def kv_append(k, v, kcache, vcache, rows_i32, pos_i32):
-    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
+    """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(k, v, kcache, vcache, rows_i32, pos_i32)
-    B, Hkv, S, D = kcache.shape
+    _check_kcache(k.dtype, kcache)
+    B, Hkv, S, D = k_dims(kcache)
     assert k.is_contiguous() and v.is_contiguous() and k.shape[1:] == (Hkv, D)
     _check(load().lsk_kv_append(dtype_code(k.dtype), _ptr(k), _ptr(v), _ptr(kcache), _ptr(vcache), _ptr(rows_i32),
                                 _ptr(pos_i32), k.shape[0], Hkv, D, B, S, _stream()), "lsk_kv_append")
@@ -248,11 +287,12 @@ def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
                 scale, workspace=None):
-    """kcache [B, Hkv, S, D]; vcache is the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
+    """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
-    B_, H_, S_, D_ = kcache.shape
+    _check_kcache(q.dtype, kcache)
+    B_, H_, S_, D_ = k_dims(kcache)
     assert vcache.shape == (B_, H_, S_ // 32, D_, 32) and S_ % 64 == 0
-    B, Hkv, S, D = kcache.shape
+    B, Hkv, S, D = k_dims(kcache)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
                                   _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(out), n_heads,
@@ -333,7 +373,8 @@ class NativeModel:
                  cos_tab, sin_tab):
         lib = load()
         _dev(cos_tab, sin_tab)
-        B, Hkv, S, D = kcache[0].shape
+        _check_kcache(dtype, kcache[0])
+        B, Hkv, S, D = k_dims(kcache[0])
         assert vcache[0].shape == (B, Hkv, S // 32, D, 32) and vcache[0].is_contiguous(), \
             "V cache must be the blocked-transposed [B, Hkv, S/32, D, 32] storage"
         self._keep = (layers, kcache, vcache, cos_tab, sin_tab)
@@ -451,8 +492,9 @@ def add_rmsnorm(x: torch.Tensor, partials: torch.Tensor | None, w: torch.Tensor 
 def rope_append_partial(partials, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads,
                         head_dim):
     _dev(partials, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
+    _check_kcache(q_out.dtype, kcache)
     ks, N, _ = partials.shape
-    B, Hkv, S, D = kcache.shape
+    B, Hkv, S, D = k_dims(kcache)
     _check(load().lsk_rope_append_partial(dtype_code(q_out.dtype), _ptr(partials), ks, _ptr(q_out), _ptr(kcache),
                                           _ptr(vcache), _ptr(cos_tab), _ptr(sin_tab), cos_tab.shape[0],
                                           _ptr(rows_i32), _ptr(pos_i32), N, n_heads, n_kv_heads, head_dim, B, S,

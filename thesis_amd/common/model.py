@@ -7,10 +7,10 @@ Same object surface as the reference model (common/model.py:218-403): `cfg`, `de
 `prefill()`, `n_layers`.  The padded per-call path (`make_ctx` / `forward_layers`) runs on the same
 ragged kernels as the packed path: a [b, T] call is b blocks of T tokens.
 
-HBM layout: the K cache is one tensor [L, max_batch, Hkv, max_seq, D] (`cache.k[i]` is layer i's view),
-so one (request, KV head) is a contiguous max_seq x D stripe that the attention kernel streams once; the
-V cache holds the same stripes in transposed 32-position blocks [L, max_batch, Hkv, max_seq/32, D, 32]
-(`cache.v[i]` returns the reference layout as a copy).  Weights keep the reference's fusion (wqkv = [q; k; v],
+HBM layout: one (request, KV head) of a layer is a contiguous max_seq x D stripe that the attention kernel
+streams once.  Inside a stripe the bf16 K cache keeps 32-position blocks in MFMA-fragment order and the V
+cache keeps 32-position blocks transposed (`KVCache`); `cache.k[i]` / `cache.v[i]` return the reference
+[max_batch, Hkv, max_seq, D] layout.  Weights keep the reference's fusion (wqkv = [q; k; v],
 w13 = [gate; up], [out, in]); bf16 projection and LM-head weights are stored in the GEMMs' fragment-major
 form (`_lsk.PackedWeight`, every 16 x 32 MFMA fragment 1 KiB contiguous), whose `unpack()` gives the
 [out, in] tensor back bit for bit; fp32 weights stay row-major.  The RoPE tables are built on the CPU with
@@ -153,46 +153,62 @@ class LayerWeights:
         return cls(g(wqkv), g(wo), g(w13), g(w2), attn_norm, ffn_norm)
 
 
-class _VLayers:
-    """cache.v[i]: layer i's V as the reference's [max_batch, Hkv, max_seq, D] tensor (a copy of the blocked
-    storage; for inspection, the kernels write the storage)."""
+class _Decoded:
+    """cache.k[i] / cache.v[i] of a layout the kernels store differently: layer i in the reference's
+    [max_batch, Hkv, max_seq, D] layout, as a copy (for inspection; the kernels write the storage)."""
 
-    def __init__(self, cache):
-        self.cache = cache
+    def __init__(self, store: Tensor, decode):
+        self.store, self.decode = store, decode
 
     def __getitem__(self, i):
-        return _lsk.v_from_blocked(self.cache.vb_all[i])
+        return self.decode(self.store[i])
 
     def __len__(self):
-        return self.cache.vb_all.shape[0]
+        return self.store.shape[0]
 
 
 class KVCache:
-    """Static contiguous KV cache.  K: k_all [L, max_batch, Hkv, max_seq, D] (k[i] = layer views).
-    V is stored in 32-position blocks, each transposed: vb_all [L, max_batch, Hkv, max_seq/32, D, 32], so the
-    attention kernel reads V^T MFMA fragments as contiguous 16-byte vectors (1 KiB per wave load).
-    v[i] / v_all present V in the reference's [max_batch, Hkv, max_seq, D] layout (copies)."""
+    """Static contiguous KV cache, per layer, zero-initialised.
+    K (bf16): kf_all [L, max_batch, Hkv, max_seq/32, D/16, 64, 8], fragment-major 32-position blocks (every
+      16-position x 32-d MFMA fragment 1 KiB contiguous in lane order, `_lsk.k_to_frag`); K (fp32): k_all
+      [L, max_batch, Hkv, max_seq, D] row-major.
+    V: vb_all [L, max_batch, Hkv, max_seq/32, D, 32], 32-position blocks each transposed, so every V^T MFMA
+      fragment is 1 KiB contiguous as well.
+    `kstore[i]` / `vb[i]` are the per-layer storage tensors the kernels use; k[i] / v[i] and k_all / v_all
+    present the reference's [max_batch, Hkv, max_seq, D] layout (views for fp32 K, copies otherwise)."""
 
     def __init__(self, cfg: ModelConfig, max_batch: int, max_seq: int, dtype, device):
         if max_seq % 64:
             raise ValueError("max_seq must be a multiple of 64")
         self.max_batch, self.max_seq = max_batch, max_seq
-        self.k_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq, cfg.head_dim), dtype=dtype,
-                                 device=device)
-        self.vb_all = torch.zeros((cfg.n_layers, max_batch, cfg.n_kv_heads, max_seq // 32, cfg.head_dim, 32),
-                                  dtype=dtype, device=device)
-        self.k = [self.k_all[i] for i in range(cfg.n_layers)]
-        self.vb = [self.vb_all[i] for i in range(cfg.n_layers)]
-        self.v = _VLayers(self)
-        # KV positions per flash-decoding split of the attention kernel, fixed for the cache's lifetime so
-        # that a query's result never depends on the batch it is packed in.  Few (request, KV head) pairs
-        # leave most CUs idle with 1024-position splits, so small caches split every 256 positions
-        # (measured on MI355X: B=32 x 8 KV heads, 1-9 rows per request, 41 -> 33 us per launch); the fp32
-        # path does not split.
+        L, Hkv, D = cfg.n_layers, cfg.n_kv_heads, cfg.head_dim
+        self.frag_k = dtype == torch.bfloat16
+        if self.frag_k:
+            if D % 32:
+                raise ValueError("bf16 caches need head_dim % 32 == 0")
+            self.kf_all = torch.zeros((L, max_batch, Hkv, max_seq // 32, D // 16, 64, 8), dtype=dtype, device=device)
+            self.kstore = [self.kf_all[i] for i in range(L)]
+            self.k = _Decoded(self.kf_all, _lsk.k_from_frag)
+        else:
+            self._k_rows = torch.zeros((L, max_batch, Hkv, max_seq, D), dtype=dtype, device=device)
+            self.kstore = [self._k_rows[i] for i in range(L)]
+            self.k = self.kstore
+        self.vb_all = torch.zeros((L, max_batch, Hkv, max_seq // 32, D, 32), dtype=dtype, device=device)
+        self.vb = [self.vb_all[i] for i in range(L)]
+        self.v = _Decoded(self.vb_all, _lsk.v_from_blocked)
+        # KV positions per flash-decoding split of the attention kernel, fixed for the cache's lifetime so that
+        # a query's result never depends on the batch it is packed in.  Measured on MI355X: 256 requests x 8 KV
+        # heads with median-1500 contexts stream best with 4096-position splits (fewer work items, fewer
+        # prologues); a B = 32 decode batch runs unsplit up to 2048 positions, its launches using the
+        # deep-prefetch kernel.  The fp32 path does not split.
         if dtype == torch.bfloat16:
-            self.attn_split = _lsk.ATTN_SPLIT if max_batch * cfg.n_kv_heads >= 1024 else 256
+            self.attn_split = _lsk.ATTN_SPLIT if max_batch * cfg.n_kv_heads >= 1024 else 2048
         else:
             self.attn_split = 1 << 30
+
+    @property
+    def k_all(self) -> Tensor:
+        return _lsk.k_from_frag(self.kf_all) if self.frag_k else self._k_rows
 
     @property
     def v_all(self) -> Tensor:
@@ -334,7 +350,7 @@ class LayerSkipLlama:
         self.cache = KVCache(self.cfg, max_batch, max_seq, self.dtype, self.device)
         c = self.cfg
         self.native = _lsk.NativeModel(self.dtype, c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim,
-                                       c.intermediate_size, c.vocab_size, c.norm_eps, self.layers, self.cache.k,
+                                       c.intermediate_size, c.vocab_size, c.norm_eps, self.layers, self.cache.kstore,
                                        self.cache.vb, self.rope_cos, self.rope_sin)
         return self.cache
 
