@@ -34,7 +34,7 @@
 #define ATTN_QT 2      // 16-row MFMA column tiles per work item
 #define ATTN_ROWS (16 * ATTN_QT)  // query rows per work item
 #define ATTN_MAX_SPLITS 128
-#define ATTN_DEEP_PREFETCH_MAX_WGS 256  // launches up to this many workgroups use the PF = 3 kernel
+#define ATTN_WAVES 8   // waves per work item; fixed, because it fixes which wave accumulates which step
 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -49,98 +49,106 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // rows are mapped to positions so that lane group g holds positions 8g .. 8g+7 of the step: exactly the 8
 // consecutive positions its P^T fragment and its 16-byte V^T load need.
 // A work item carries up to 32 query rows (two column tiles sharing every K / V fragment), so the KV of a
-// (block, KV head) is read by one workgroup for blocks of up to 32 / G tokens.  The 4 waves take the
-// 32-position steps of the item's KV range round robin (step index within the split mod 4), keep the next
-// step's K and V loads in flight while they compute, and are merged in wave order through LDS.
-// PF = steps of K / V loads each wave keeps in flight (register ring).  PF = 1 (two workgroups per CU) for
-// large launches; PF = 3 (one workgroup per CU) for launches that fit the CUs once, where each wave's chain
-// of dependent steps, not the number of loads in flight, sets the time.  PF changes only when loads are
-// issued, never the arithmetic, so both give bitwise the same result.
-template <int D, int PF>
-__global__ __launch_bounds__(256, PF == 1 ? 2 : 1) void attn_bf16_kernel(
+// (block, KV head) is read by one workgroup for blocks of up to 32 / G tokens.  The 8 waves take the
+// 32-position steps of the item's KV range round robin (step index within the split mod 8), keep the next
+// step's K and V loads in flight while they compute, and are merged in wave order through LDS; 8 waves keep
+// the chain of dependent steps short when a decode batch has few (block, KV head) pairs.
+template <int D>
+__global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
-    const int32_t* __restrict__ works, uint16_t* __restrict__ out, float* __restrict__ o_part,
-    float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
+    const int32_t* __restrict__ works, const int32_t* __restrict__ sched, const int32_t* __restrict__ slot_off,
+    uint16_t* __restrict__ out, float* __restrict__ o_part, float* __restrict__ ml_part, int G, int Hkv, int S,
+    float scale_log2) {
   constexpr int KSTEPS = D / 32;
   constexpr int CT = D / 16;
-  __shared__ float s_ml[4][2][ATTN_ROWS];
-  __shared__ __attribute__((aligned(16))) float s_o[4][ATTN_ROWS][D + 4];
+  constexpr int NW = ATTN_WAVES;
+  __shared__ float s_ml[NW][2][ATTN_ROWS];
+  __shared__ __attribute__((aligned(16))) float s_o[NW][ATTN_ROWS][D + 4];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
-  const int kvh = blockIdx.y;
   const int Hq = Hkv * G;
+  const int i_beg = slot_off[blockIdx.x], i_end = slot_off[blockIdx.x + 1];
+  if (i_beg >= i_end) return;
 
-  const int32_t* wk = works + (long)blockIdx.x * 8;
-  const int q_start = wk[0], row0 = wk[1], nrows = wk[2], kv_lo = wk[3], kv_hi = wk[4], part = wk[5];
-  const int pos0 = wk[6], crow = wk[7];
-  if (nrows <= 0) return;  // padding item of the XCD-aware work order
-  const int nq = (nrows + 15) >> 4;  // column tiles in use (wave-uniform)
+  struct Item {
+    int q_start, row0, nrows, kv_lo, kv_hi, part, pos0, crow, kvh;
+  };
+  auto fetch = [&](int i) {
+    const int id = sched[i];
+    const int wi = id / Hkv;
+    const int32_t* wk = works + (long)wi * 8;
+    Item it;
+    it.q_start = wk[0]; it.row0 = wk[1]; it.nrows = wk[2]; it.kv_lo = wk[3]; it.kv_hi = wk[4]; it.part = wk[5];
+    it.pos0 = wk[6]; it.crow = wk[7]; it.kvh = id - wi * Hkv;
+    return it;
+  };
+  auto kbase_of = [&](const Item& it) { return kc + ((long)it.crow * Hkv + it.kvh) * (long)S * D; };
+  auto vbase_of = [&](const Item& it) { return vt + ((long)it.crow * Hkv + it.kvh) * (long)D * S; };
 
   lsk_bf16x8 qf[ATTN_QT][KSTEPS];
   int qpos[ATTN_QT];
+  auto load_q = [&](const Item& it) {
 #pragma unroll
-  for (int qt = 0; qt < ATTN_QT; ++qt) {
-    const bool valid = 16 * qt + l16 < nrows;
-    const int r = row0 + 16 * qt + (valid ? l16 : 0);
-    const int t = r / G, g = r - t * G;
-    qpos[qt] = valid ? pos0 + t : -1;  // invalid rows: every score masked
-    const uint16_t* qrow = q + ((long)(q_start + t) * Hq + kvh * G + g) * D;
+    for (int qt = 0; qt < ATTN_QT; ++qt) {
+      const bool valid = 16 * qt + l16 < it.nrows;
+      const int r = it.row0 + 16 * qt + (valid ? l16 : 0);
+      const int t = r / G, g = r - t * G;
+      qpos[qt] = valid ? it.pos0 + t : -1;  // invalid rows: every score masked
+      const uint16_t* qrow = q + ((long)(it.q_start + t) * Hq + it.kvh * G + g) * D;
 #pragma unroll
-    for (int j = 0; j < KSTEPS; ++j)
-      qf[qt][j] = (valid && qt < nq) ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
-  }
-  lsk_f32x4 oacc[ATTN_QT][CT];
-  float m_run[ATTN_QT], l_run[ATTN_QT];
-#pragma unroll
-  for (int qt = 0; qt < ATTN_QT; ++qt) {
-    m_run[qt] = -INFINITY;
-    l_run[qt] = 0.f;
-#pragma unroll
-    for (int c = 0; c < CT; ++c) oacc[qt][c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
-  }
-  // positions every valid row of the item may read without masking: <= the first row's position, < kv_hi
-  const int full_lim = min(kv_hi - 1, pos0 + row0 / G);
-
-  const long head = (long)crow * Hkv + kvh;
-  const uint16_t* kbase = kc + head * (long)S * D;
-  const uint16_t* vbase = vt + head * (long)D * S;
-  // MFMA row l16 of S^T sub-tile a <-> position 8 * (l16 / 4) + 4 * a + l16 % 4 of the 32-position step (the
-  // order the K cache stores each block's fragments in)
-
+      for (int j = 0; j < KSTEPS; ++j)
+        qf[qt][j] = valid ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
+    }
+  };
   auto ldkv = [&](const uint16_t* p) -> lsk_bf16x8 {
     return __builtin_bit_cast(lsk_bf16x8, __builtin_nontemporal_load((const lsk_i32x4*)p));
   };
-  lsk_bf16x8 kf[PF][2][KSTEPS];
-  lsk_bf16x8 vf[PF][CT];
-  auto load_k = [&](lsk_bf16x8 (&kr)[2][KSTEPS], int sb) {
-    // fragment-major K cache: fragment (a, j) of the step's 32-position block is 1 KiB in lane order
+  lsk_bf16x8 kf[2][KSTEPS];
+  lsk_bf16x8 vf[CT];
+  // fragment-major K cache: fragment (a, j) of the step's 32-position block is 1 KiB in lane order
+  auto load_k = [&](const uint16_t* kb, int sb) {
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) kr[a][j] = ldkv(kbase + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
+      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(kb + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
   };
-  auto load_v = [&](lsk_bf16x8 (&vr)[CT], int sb) {
+  auto load_v = [&](const uint16_t* vb, int sb) {
 #pragma unroll
-    for (int c = 0; c < CT; ++c) vr[c] = ldkv(vbase + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
+    for (int c = 0; c < CT; ++c) vf[c] = ldkv(vb + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
   };
-  // this wave's steps: 32-position steps wave, wave + 4, ... of the range, in order
-  auto step_pos = [&](int i) { return kv_lo + ATTN_STEP * (wave + 4 * i); };
-#pragma unroll
-  for (int u = 0; u < PF; ++u) {
-    const int sp = step_pos(u);
-    if (sp < kv_hi) {
-      load_k(kf[u], sp);
-      load_v(vf[u], sp);
+  // a wave's steps of an item: 32-position steps wave, wave + NW, ... of the item's range, in order
+  auto first_step = [&](const Item& it) { return it.kv_lo + ATTN_STEP * wave; };
+  auto issue_first = [&](const Item& it) {
+    load_q(it);
+    const int sb = first_step(it);
+    if (sb < it.kv_hi) {
+      load_k(kbase_of(it), sb);
+      load_v(vbase_of(it), sb);
     }
-  }
-  for (int i0 = 0; step_pos(i0) < kv_hi; i0 += PF) {
+  };
+
+  Item cur = fetch(i_beg);
+  issue_first(cur);
+  for (int i = i_beg; i < i_end; ++i) {
+    const int nq = (cur.nrows + 15) >> 4;  // column tiles in use (wave-uniform)
+    const int kv_hi = cur.kv_hi;
+    const uint16_t* kb = kbase_of(cur);
+    const uint16_t* vb = vbase_of(cur);
+    // positions every valid row of the item may read without masking: <= the first row's position, < kv_hi
+    const int full_lim = min(kv_hi - 1, cur.pos0 + cur.row0 / G);
+    lsk_f32x4 oacc[ATTN_QT][CT];
+    float m_run[ATTN_QT], l_run[ATTN_QT];
 #pragma unroll
-    for (int u = 0; u < PF; ++u) {
-      const int sb = step_pos(i0 + u);
-      if (sb >= kv_hi) break;
-      const int sn = step_pos(i0 + u + PF);  // the step whose loads reuse this ring slot
+    for (int qt = 0; qt < ATTN_QT; ++qt) {
+      m_run[qt] = -INFINITY;
+      l_run[qt] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CT; ++c) oacc[qt][c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+    }
+    for (int sb = first_step(cur); sb < kv_hi; sb += ATTN_STEP * NW) {
+      const int sn = sb + ATTN_STEP * NW;
       const bool more = sn < kv_hi;
       lsk_f32x4 sacc[ATTN_QT][2];
 #pragma unroll
@@ -151,11 +159,11 @@ __global__ __launch_bounds__(256, PF == 1 ? 2 : 1) void attn_bf16_kernel(
             sacc[qt][a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
-              sacc[qt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[u][a][j], qf[qt][j], sacc[qt][a], 0, 0, 0);
+              sacc[qt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[qt][j], sacc[qt][a], 0, 0, 0);
           }
         }
       }
-      if (more) load_k(kf[u], sn);  // streams in while later steps are computed
+      if (more) load_k(kb, sn);  // the next step's K streams in during this step's softmax and P.V
       const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
       lsk_bf16x8 pb[ATTN_QT];
       float alpha[ATTN_QT];
@@ -203,53 +211,60 @@ __global__ __launch_bounds__(256, PF == 1 ? 2 : 1) void attn_bf16_kernel(
             oacc[qt][c][1] *= alpha[qt];
             oacc[qt][c][2] *= alpha[qt];
             oacc[qt][c][3] *= alpha[qt];
-            oacc[qt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[u][c], pb[qt], oacc[qt][c], 0, 0, 0);
+            oacc[qt][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf[c], pb[qt], oacc[qt][c], 0, 0, 0);
           }
         }
       }
-      if (more) load_v(vf[u], sn);
+      if (more) load_v(vb, sn);
     }
-  }
-  // ---- merge the four waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
-#pragma unroll
-  for (int qt = 0; qt < ATTN_QT; ++qt) {
-    if (qt < nq) {
-      if (lg == 0) {
-        s_ml[wave][0][16 * qt + l16] = m_run[qt];
-        s_ml[wave][1][16 * qt + l16] = l_run[qt];
-      }
-#pragma unroll
-      for (int c = 0; c < CT; ++c)
-        *(float4*)(&s_o[wave][16 * qt + l16][16 * c + 4 * lg]) =
-            make_float4(oacc[qt][c][0], oacc[qt][c][1], oacc[qt][c][2], oacc[qt][c][3]);
+    // the next item's Q and first K / V loads fly while this item is merged
+    const Item done = cur;
+    if (i + 1 < i_end) {
+      cur = fetch(i + 1);
+      issue_first(cur);
     }
-  }
-  __syncthreads();
-  for (int e = tid; e < nrows * D; e += 256) {
-    const int qr = e / D, d = e - qr * D;
-    float M = -INFINITY;
+    // ---- merge the waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][0][qr]);
-    float L = 0.f, O = 0.f;
+    for (int qt = 0; qt < ATTN_QT; ++qt) {
+      if (qt < nq) {
+        if (lg == 0) {
+          s_ml[wave][0][16 * qt + l16] = m_run[qt];
+          s_ml[wave][1][16 * qt + l16] = l_run[qt];
+        }
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float mw = s_ml[w][0][qr];
-      const float ew = (mw == -INFINITY) ? 0.f : ((mw == M) ? 1.f : fast_exp2(mw - M));
-      L = L + ew * s_ml[w][1][qr];
-      O = O + ew * s_o[w][qr][d];
-    }
-    const int rr = row0 + qr;
-    const int tt = rr / G, gg = rr - tt * G;
-    if (part < 0) {
-      out[(long)(q_start + tt) * Hq * D + (long)(kvh * G + gg) * D + d] = f2bf(O / L);
-    } else {
-      const long slot = ((long)part * Hkv + kvh) * ATTN_ROWS + qr;
-      o_part[slot * D + d] = O;
-      if (d == 0) {
-        ml_part[slot * 2 + 0] = M;
-        ml_part[slot * 2 + 1] = L;
+        for (int c = 0; c < CT; ++c)
+          *(float4*)(&s_o[wave][16 * qt + l16][16 * c + 4 * lg]) =
+              make_float4(oacc[qt][c][0], oacc[qt][c][1], oacc[qt][c][2], oacc[qt][c][3]);
       }
     }
+    __syncthreads();
+    for (int e = tid; e < done.nrows * D; e += 64 * NW) {
+      const int qr = e / D, d = e - qr * D;
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][0][qr]);
+      float L = 0.f, O = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        const float mw = s_ml[w][0][qr];
+        const float ew = (mw == -INFINITY) ? 0.f : ((mw == M) ? 1.f : fast_exp2(mw - M));
+        L = L + ew * s_ml[w][1][qr];
+        O = O + ew * s_o[w][qr][d];
+      }
+      const int rr = done.row0 + qr;
+      const int tt = rr / G, gg = rr - tt * G;
+      if (done.part < 0) {
+        out[(long)(done.q_start + tt) * Hq * D + (long)(done.kvh * G + gg) * D + d] = f2bf(O / L);
+      } else {
+        const long slot = ((long)done.part * Hkv + done.kvh) * ATTN_ROWS + qr;
+        o_part[slot * D + d] = O;
+        if (d == 0) {
+          ml_part[slot * 2 + 0] = M;
+          ml_part[slot * 2 + 1] = L;
+        }
+      }
+    }
+    __syncthreads();  // the merge has read s_o / s_ml before the next item writes them
   }
 }
 
@@ -470,6 +485,52 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
   return 0;
 }
 
+// Static schedule of a plan over n_slots persistent workgroups (one per CU): items are (work, KV head)
+// pairs of non-padding works, costed by their KV steps per wave plus a fixed per-item overhead, and dealt
+// longest first to the least-loaded slot (ties: lowest slot; equal costs keep plan order).  Output:
+// sched[] = work * n_kv_heads + head, grouped by slot in processing order; slot_off[s] .. slot_off[s + 1]
+// are slot s's items.  Which workgroup computes an item never changes its result.
+extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* sched,
+                                 int max_items, int32_t* slot_off, int* n_items) {
+  LSK_REQUIRE(works && sched && slot_off && n_items, LSK_EARG, "lsk_attn_schedule: null pointer");
+  LSK_REQUIRE(n_works >= 0 && n_kv_heads > 0 && n_slots > 0, LSK_ESHAPE, "lsk_attn_schedule: bad arguments");
+  struct It { int id, cost; };
+  std::vector<It> items;
+  for (int w = 0; w < n_works; ++w) {
+    const int32_t* wp = works + (long)w * 8;
+    if (wp[2] <= 0) continue;
+    const int steps = (wp[4] - wp[3] + ATTN_STEP * ATTN_WAVES - 1) / (ATTN_STEP * ATTN_WAVES);
+    for (int h = 0; h < n_kv_heads; ++h) items.push_back({w * n_kv_heads + h, steps + 2});
+  }
+  LSK_REQUIRE((int)items.size() <= max_items, LSK_EWORKSPACE, "lsk_attn_schedule: %zu items > %d", items.size(),
+              max_items);
+  std::stable_sort(items.begin(), items.end(), [](const It& a, const It& b) { return a.cost > b.cost; });
+  // min-heap of (load, slot)
+  std::vector<std::pair<long, int>> heap;
+  heap.reserve(n_slots);
+  for (int sl = 0; sl < n_slots; ++sl) heap.push_back({0, sl});
+  auto cmp = [](const std::pair<long, int>& a, const std::pair<long, int>& b) {
+    return a.first > b.first || (a.first == b.first && a.second > b.second);
+  };
+  std::make_heap(heap.begin(), heap.end(), cmp);
+  std::vector<std::vector<int>> per(n_slots);
+  for (const It& it : items) {
+    std::pop_heap(heap.begin(), heap.end(), cmp);
+    auto& top = heap.back();
+    per[top.second].push_back(it.id);
+    top.first += it.cost;
+    std::push_heap(heap.begin(), heap.end(), cmp);
+  }
+  int k = 0;
+  for (int sl = 0; sl < n_slots; ++sl) {
+    slot_off[sl] = k;
+    for (int id : per[sl]) sched[k++] = id;
+  }
+  slot_off[n_slots] = k;
+  *n_items = k;
+  return 0;
+}
+
 extern "C" size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim) {
   // o_part [n_parts][Hkv][64][D] fp32, ml_part [n_parts][Hkv][64][2] fp32
   const size_t rows = (size_t)n_parts * n_kv_heads * ATTN_ROWS;
@@ -478,9 +539,12 @@ extern "C" size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head
 
 extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache,
                                const int32_t* blocks, const int32_t* works, int n_works, const int32_t* groups,
-                               int n_groups, int n_parts, void* out, int n_heads, int n_kv_heads, int head_dim,
-                               int max_seq, float scale, void* workspace, size_t ws_bytes, void* stream) {
+                               int n_groups, int n_parts, const int32_t* sched, const int32_t* slot_off, int n_slots,
+                               void* out, int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale,
+                               void* workspace, size_t ws_bytes, void* stream) {
   LSK_REQUIRE(q && kcache && vcache && blocks && works && out, LSK_EARG, "lsk_ragged_attn: null pointer");
+  LSK_REQUIRE(dtype != LSK_DTYPE_BF16 || n_works == 0 || (sched && slot_off && n_slots > 0), LSK_EARG,
+              "lsk_ragged_attn: the bf16 path needs a schedule (lsk_attn_schedule)");
   LSK_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && max_seq > 0 && n_works >= 0,
               LSK_ESHAPE, "lsk_ragged_attn: bad shape");
   if (n_works == 0) return 0;
@@ -502,21 +566,17 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
       ml_part = (float*)((char*)workspace + lsk_align_up(rows * head_dim * sizeof(float), 256));
     }
     const float scale_log2 = scale * 1.4426950408889634f;
-    // a launch that fits the CUs once (one workgroup each) is bound by each wave's chain of steps: keep three
-    // steps of loads in flight per wave; larger launches run two workgroups per CU with one step in flight
-    const bool deep_prefetch = (long)n_works * n_kv_heads <= ATTN_DEEP_PREFETCH_MAX_WGS;
-    const uint16_t* qb = (const uint16_t*)q;
-    const uint16_t* kb = (const uint16_t*)kcache;
-    const uint16_t* vb = (const uint16_t*)vcache;
-    uint16_t* ob = (uint16_t*)out;
-#define LSK_ATTN_LAUNCH(D_, PF_) \
-  attn_bf16_kernel<D_, PF_><<<grid, 256, 0, s>>>(qb, kb, vb, works, ob, o_part, ml_part, G, n_kv_heads, max_seq, scale_log2)
-    if (head_dim == 128) {
-      if (deep_prefetch) LSK_ATTN_LAUNCH(128, 3); else LSK_ATTN_LAUNCH(128, 1);
-    } else {
-      if (deep_prefetch) LSK_ATTN_LAUNCH(64, 3); else LSK_ATTN_LAUNCH(64, 1);
-    }
-#undef LSK_ATTN_LAUNCH
+    const dim3 pgrid(n_slots);
+    if (head_dim == 128)
+      attn_bf16_kernel<128><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
+                                                              (const uint16_t*)vcache, works, sched, slot_off,
+                                                              (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
+                                                              max_seq, scale_log2);
+    else
+      attn_bf16_kernel<64><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
+                                                             (const uint16_t*)vcache, works, sched, slot_off,
+                                                             (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
+                                                             max_seq, scale_log2);
     int rc = lsk_check_launch("lsk_ragged_attn");
     if (rc) return rc;
     if (n_groups > 0) {

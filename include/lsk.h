@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 2
+#define LSK_ABI_VERSION 3
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -63,6 +63,13 @@ int lsk_kv_append(int dtype, const void* k, const void* v, void* kcache, void* v
 int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
                   int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts);
 
+/* Static schedule of a plan's (work, KV head) items over n_slots persistent workgroups (host pointers):
+ * longest first to the least-loaded slot.  sched[] = work * n_kv_heads + head grouped by slot,
+ * slot_off [n_slots + 1].  Has no reference counterpart (the reference runs one SDPA per bucket); it
+ * only decides which workgroup computes an item, never the result. */
+int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* sched, int max_items,
+                      int32_t* slot_off, int* n_items);
+
 /* Workspace bytes for the split partials of a plan with n_parts partial slots. */
 size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
 
@@ -71,9 +78,10 @@ size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
  * Replaces solutions/packed.py:142-166 (_attend: per-bucket gather + masked SDPA + scatter)
  * and common/model.py:352-364 (the padded path's masked SDPA). */
 int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
-                    const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts, void* out,
-                    int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
-                    size_t ws_bytes, void* stream);
+                    const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
+                    const int32_t* sched, const int32_t* slot_off, int n_slots, void* out, int n_heads,
+                    int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes,
+                    void* stream);
 
 /* bf16 weight storage of the GEMMs: W [N, K] row-major (ldw) <-> fragment-major Wp (N*K elements, no
  * padding): fragment (g, j) = rows 16g..16g+15 x k 32j..32j+31 is 1 KiB, lane l's 8 elements being
@@ -165,12 +173,14 @@ int lsk_model_destroy(long handle);
 size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts);
 
 /* Layers [start, end) over n_tokens packed tokens: x_out = layers(x_in) (x_in is not modified).
- * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8] (see lsk_attn_plan).
+ * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8][sched n_items]
+ * [slot_off n_slots+1] (see lsk_attn_plan, lsk_attn_schedule).
  * capture: NULL or a host array of n_layers device pointers; capture[i] != NULL receives layer i's output
  * (solutions/packed.py:190-195).  Replaces packed_layers (solutions/packed.py:188-196). */
 int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
-                       const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, void* workspace,
-                       size_t ws_bytes, void* const* capture, double attn_bytes, double attn_flops, void* stream);
+                       const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, int n_items, int n_slots,
+                       void* workspace, size_t ws_bytes, void* const* capture, double attn_bytes, double attn_flops,
+                       void* stream);
 
 /* ---- optional per-launch profiling (no reference counterpart: measurement support) ----
  * When enabled, the layer runner (and callers using lsk_prof_start/stop around their own launches)

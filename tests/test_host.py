@@ -59,7 +59,9 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_pack_weight(8, 64, 16, 40, 64, None) == -2                          # N % 16 != 0
     assert lib.lsk_unpack_weight(8, 16, 64, 64, 48, None) == -2                        # K % 32 != 0
     assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
-    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 8, 1, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, None, 0, 8, 32, 8, 128, 64, 0.1, None, 0,
+                               None) == -1                                            # bf16 without a schedule
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
 
 
@@ -118,6 +120,28 @@ def test_attention_plan_covers_every_row_once(G, split):
             assert all(ivs[i][1] == ivs[i + 1][0] for i in range(len(ivs) - 1))
     for gp in groups:
         assert gp[4] >= 2 and gp[3] + gp[4] <= n_parts
+
+
+@pytest.mark.parametrize("n_slots", [1, 7, 256])
+def test_attention_schedule_covers_every_item_once_longest_first(n_slots):
+    lsk = _lsk()
+    rng = np.random.default_rng(n_slots)
+    nb = 60
+    T = rng.integers(1, 12, nb)
+    pos0 = rng.integers(0, 9000, nb)
+    blocks = np.stack([np.concatenate([[0], np.cumsum(T)[:-1]]), pos0, T, rng.integers(0, 8, nb)], axis=1)
+    works, _, _ = _plan(blocks, 4, 4096)
+    Hkv = 8
+    sched, slot_off = lsk.attn_schedule(works, Hkv, n_slots)
+    real = [w for w in range(len(works)) if works[w][2] > 0]
+    assert sorted(sched.tolist()) == sorted(w * Hkv + h for w in real for h in range(Hkv))
+    assert slot_off[0] == 0 and slot_off[-1] == len(sched) and (np.diff(slot_off) >= 0).all()
+    cost = lambda i: -(-(works[i // Hkv][4] - works[i // Hkv][3]) // 256) + 2  # noqa: E731
+    loads = [sum(cost(i) for i in sched[slot_off[s]:slot_off[s + 1]]) for s in range(n_slots)]
+    # greedy longest-first bound: no slot exceeds the mean by more than the largest item
+    assert max(loads) <= sum(loads) / n_slots + max(cost(i) for i in sched)
+    again, off2 = lsk.attn_schedule(works, Hkv, n_slots)
+    assert np.array_equal(again, sched) and np.array_equal(off2, slot_off)   # deterministic
 
 
 def test_attention_plan_places_sibling_tiles_eight_slots_apart():
@@ -231,7 +255,10 @@ def test_packed_metadata_layout():
     assert meta[:N].tolist() == pb.rows_h.tolist() and meta[N:2 * N].tolist() == pb.pos_h.tolist()
     blk = meta[2 * N:2 * N + 4 * pb.nb].reshape(-1, 4)
     assert blk.tolist() == [[0, 700, 1, 1], [1, 10, 2, 3]]
-    assert meta.size == 2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups)
+    assert meta.size == 2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups) + pb.n_items + pb.n_slots + 1
+    assert pb.n_items == 2 * 1                                       # (work, KV head) pairs: 2 works x 1 head
+    tail = meta[2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups):]
+    assert sorted(tail[:pb.n_items].tolist()) == [0, 1] and tail[pb.n_items + pb.n_slots] == pb.n_items
     # algorithmic attention work of one launch: K+V of every attended position, Q read and O written
     assert pb.attn_bytes == (701 + 12) * 1 * 128 * 2 * 2 + N * 4 * 128 * 2 * 2
 

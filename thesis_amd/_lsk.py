@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 32            # query rows per attention work item
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -32,8 +32,10 @@ _SIGS = {
     "lsk_rope_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lsk_kv_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
+    "lsk_attn_schedule": (_I, [_P, _I, _I, _I, _P, _I, _P, _P]),
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
-    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z, _P]),
+    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _I, _F, _P, _Z,
+                             _P]),
     "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
     "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
@@ -51,7 +53,7 @@ _SIGS = {
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
     "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
-    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _P, _Z, _P, ctypes.c_double,
+    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P, ctypes.c_double,
                                 ctypes.c_double, _P]),
     "lsk_prof_enable": (_I, [_I]),
     "lsk_prof_start": (_I, [_I, ctypes.c_double, ctypes.c_double, _P]),
@@ -281,12 +283,42 @@ def attn_plan(blocks: np.ndarray, group: int, split: int):
     return works[:nw.value], groups[:ng.value], npart.value
 
 
+_CU_COUNT: dict = {}
+
+
+def cu_count(device) -> int:
+    """Compute units of the device (the persistent attention kernel runs one workgroup per CU); 256 (MI355X)
+    for a non-CUDA device, where plans are only built, never run."""
+    device = torch.device(device)
+    if device.type != "cuda":
+        return 256
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    n = _CU_COUNT.get(idx)
+    if n is None:
+        n = _CU_COUNT[idx] = int(torch.cuda.get_device_properties(idx).multi_processor_count)
+    return n
+
+
+def attn_schedule(works: np.ndarray, n_kv_heads: int, n_slots: int):
+    """Static longest-first schedule of (work, KV head) items over n_slots persistent workgroups
+    -> (sched int32 [n_items], slot_off int32 [n_slots + 1])."""
+    works = np.ascontiguousarray(works, dtype=np.int32)
+    max_items = max(1, len(works) * n_kv_heads)
+    sched = np.zeros(max_items, dtype=np.int32)
+    slot_off = np.zeros(n_slots + 1, dtype=np.int32)
+    n = ctypes.c_int(0)
+    _check(load().lsk_attn_schedule(works.ctypes.data if len(works) else None, len(works), n_kv_heads, n_slots,
+                                    sched.ctypes.data, max_items, slot_off.ctypes.data, ctypes.byref(n)),
+           "lsk_attn_schedule")
+    return sched[:n.value], slot_off
+
+
 def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
     return int(load().lsk_attn_workspace_bytes(n_parts, n_kv_heads, head_dim))
 
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
-                scale, workspace=None):
+                scale, workspace=None, sched_dev=None, slot_off_dev=None, n_slots=0):
     """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
     _check_kcache(q.dtype, kcache)
@@ -295,8 +327,9 @@ def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n
     B, Hkv, S, D = k_dims(kcache)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
-                                  _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(out), n_heads,
-                                  Hkv, D, S, float(scale), _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
+                                  _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(sched_dev),
+                                  _ptr(slot_off_dev), n_slots, _ptr(out), n_heads, Hkv, D, S, float(scale),
+                                  _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
 
 
 def gemm(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
@@ -394,13 +427,14 @@ class NativeModel:
     def workspace_bytes(self, n_tokens: int, n_parts: int) -> int:
         return int(load().lsk_segment_workspace_bytes(self.handle, n_tokens, n_parts))
 
-    def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, workspace,
-                       capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
+    def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, n_items,
+                       n_slots, workspace, capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
         _dev(x_in, x_out, meta_dev, workspace)
         cap = _ptr_array(capture_ptrs) if capture_ptrs is not None else None
         ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
         _check(load().lsk_forward_layers(self.handle, _ptr(x_in), _ptr(x_out), n_tokens, start, end, _ptr(meta_dev),
-                                         nb, n_works, n_groups, n_parts, _ptr(workspace), ws_bytes, cap,
+                                         nb, n_works, n_groups, n_parts, n_items, n_slots, _ptr(workspace), ws_bytes,
+                                         cap,
                                          float(attn_bytes), float(attn_flops), _stream()),
                "lsk_forward_layers")
 
