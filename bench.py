@@ -39,6 +39,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 # HBM bytes per launch of each kernel class, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this benchmark
 TRAFFIC_SUMMARY = ROOT / "profiles" / "decode_8b_b32_traffic.md"
+ATTN_TRAFFIC_SUMMARY = ROOT / "profiles" / "verify_attn_ubench_traffic.md"
 
 
 def log(*a):
@@ -267,6 +268,12 @@ def run_attention_bench(args):
         "kv_append_us": round(1e3 * t_append, 2), "kv_append_GBs": round(app_bytes / (t_append * 1e-3) / 1e9, 1),
         "rollback_us": round(1e3 * t_rb, 2), "rollback_bytes": int(B * 8),
     }
+    from thesis_amd.prof_summary import read_traffic
+
+    traffic = read_traffic(ATTN_TRAFFIC_SUMMARY, "attention")
+    if traffic is not None:
+        res["traffic"] = traffic
+        res["traffic_source"] = str(ATTN_TRAFFIC_SUMMARY.relative_to(ROOT))
     # size-independent property at full size: a sample of requests against the fp64 brute force
     if args.check_attn:
         from oracle.model import brute_attention

@@ -127,10 +127,16 @@ def read_counter(path: str, counter):
 
 
 def _bench(path):
+    """Per-class figures of a bench.py JSON line: its `kernels` table, or, for an --attn-only run, the
+    verify-attention launch (algorithmic bytes and the HIP-event average, which covers attention + combine)."""
     if not path:
         return {}
-    txt = Path(path).read_text().strip().splitlines()[-1]
-    return json.loads(txt).get("kernels", {}) or {}
+    line = json.loads(Path(path).read_text().strip().splitlines()[-1])
+    out = dict(line.get("kernels") or {})
+    va = line.get("verify_attn")
+    if va and "attention" not in out:
+        out["attention"] = {"bytes_per_launch": va["attn_bytes"], "avg_us": va["attn_us"]}
+    return out
 
 
 def cmd_trace(a):
