@@ -43,7 +43,8 @@ def _kview(lsk, kstore):
 # ----------------------------------------------------------------------------- GEMM
 
 @pytest.mark.parametrize("M,N,K", [(1, 64, 64), (5, 128, 256), (16, 64, 96), (17, 256, 512), (33, 128, 4160),
-                                   (64, 4096, 256), (100, 320, 1024), (288, 512, 2048)])
+                                   (64, 4096, 256), (65, 256, 512), (100, 320, 1024), (128, 1024, 256),
+                                   (129, 128, 512), (288, 512, 2048)])
 def test_gemm_bf16_none_matches_fp32_reference(cuda, M, N, K):
     lsk = _lsk()
     g = _gen(M * 7 + N)
@@ -57,23 +58,31 @@ def test_gemm_bf16_none_matches_fp32_reference(cuda, M, N, K):
 
 
 def test_gemm_bf16_is_batch_invariant(cuda):
-    """Every row's result is bitwise independent of M and of which rows share a tile."""
+    """Every row's result is bitwise independent of M and of which rows share a tile (16- to 128-token tiles,
+    one or several token tiles, every epilogue)."""
     lsk = _lsk()
     g = _gen(3)
     K, N = 1024, 384
-    a = torch.randn(200, K, generator=g).to(BF16).to(cuda)
+    a = torch.randn(300, K, generator=g).to(BF16).to(cuda)
     w = lsk.PackedWeight(torch.randn(N, K, generator=g).to(BF16).to(cuda))
+    w13 = lsk.PackedWeight(torch.randn(2 * N, K, generator=g).to(BF16).to(cuda))
     full = lsk.gemm(a, w)
-    for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104)]:
-        part = lsk.gemm(a[lo:hi].contiguous(), w)
-        assert torch.equal(part, full[lo:hi]), (lo, hi)
+    full_s = lsk.gemm(a, w13, epilogue=lsk.EPI_SILU_MUL)
+    ns, ks = lsk.gemm_plan(N, K)
+    full_p = lsk.gemm_partial(a, w, ks)
+    for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104), (10, 130), (0, 300)]:
+        sub = a[lo:hi].contiguous()
+        assert torch.equal(lsk.gemm(sub, w), full[lo:hi]), (lo, hi)
+        assert torch.equal(lsk.gemm(sub, w13, epilogue=lsk.EPI_SILU_MUL), full_s[lo:hi]), (lo, hi)
+        assert torch.equal(lsk.gemm_partial(sub, w, ks), full_p[:, lo:hi]), (lo, hi)
 
 
-def test_gemm_bf16_epilogues_match_reference_rounding(cuda):
+@pytest.mark.parametrize("big", [0, 1])
+def test_gemm_bf16_epilogues_match_reference_rounding(cuda, big):
     """RESIDUAL: rnd(R + rnd(acc)); SILU_MUL: rnd(rnd(silu(rnd(g))) * rnd(u))  (solutions/packed.py:182-185)."""
     lsk = _lsk()
     g = _gen(11)
-    M, K, F_ = 37, 512, 256
+    M, K, F_ = 37 + 64 * big, 512, 256
     a = torch.randn(M, K, generator=g).to(BF16)
     w13 = (torch.randn(2 * F_, K, generator=g) * 0.05).to(BF16)
     r = torch.randn(M, 2 * F_, generator=g).to(BF16)
@@ -434,11 +443,12 @@ def test_rope_append_partial_is_bit_exact(cuda):
     assert torch.equal(vd.cpu()[rows, :, pos], qkv[:, (Hq + Hkv) * D:].view(N, Hkv, D))
 
 
-def test_head_argmax_matches_logits_argmax(cuda):
+@pytest.mark.parametrize("M", [37, 100, 150])
+def test_head_argmax_matches_logits_argmax(cuda, M):
     """Fused head + pick == argmax over the materialised bf16 logits (first index on ties)."""
     lsk = _lsk()
     g = _gen(12)
-    M, V, K = 37, 4096 + 64, 512
+    V, K = 4096 + 64, 512
     a = torch.randn(M, K, generator=g).to(BF16).to(cuda)
     w = torch.randn(V, K, generator=g).to(BF16)
     w[3000] = w[100]                      # duplicate rows -> exact ties, the first index must win

@@ -219,6 +219,9 @@ class PackedWeight:
         return f"PackedWeight(shape={self.shape}, dtype={self.dtype}, device={self.device})"
 
 
+GEMM_TOKEN_TILE = 64       # tokens per GEMM token tile: launches of up to this many rows read each weight once
+
+
 def as_gemm_weight(w: torch.Tensor):
     """The storage the GEMMs read for a weight of this dtype: PackedWeight for bf16, the tensor for fp32."""
     return PackedWeight(w) if w.dtype == torch.bfloat16 else w.contiguous()

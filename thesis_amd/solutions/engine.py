@@ -318,14 +318,18 @@ class EESDEngine:
         _lsk.copy_rows(exh, sel_t, h, None, N)                                   # exit_h[i, d_i] = h
         readback = None
         n_v_tok = 0
-        if deep:
-            # the drafts are first read next step, so their head shares the verify head's launch (one pass
-            # over the LM head weights per step); the batch-invariant GEMM gives every row the same result
-            readback, n_v_tok, vinfo = self._deep(V, d, (h, drf_src_t, drf_dst_t, nd))
-        elif nd:
+        n_verify = int((d[V] + 1).sum()) if deep else 0
+        merge_heads = deep and nd + n_verify <= _lsk.GEMM_TOKEN_TILE
+        if nd and not merge_heads:
             hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
             _lsk.copy_rows(hx, None, h, drf_src_t, nd)
             m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                         # seq_buf[i, d_i + 1] = draft
+        if deep:
+            # the drafts are first read next step, so when the rows fit one GEMM token tile their head shares
+            # the verify head's launch (one pass over the LM head weights per step); the batch-invariant GEMM
+            # gives every row the same result either way
+            draft = (h, drf_src_t, drf_dst_t, nd) if merge_heads else (h, None, None, 0)
+            readback, n_v_tok, vinfo = self._deep(V, d, draft)
         iv.stop()
         self._rec("deep" if deep else "shallow", iv, n_sh=N, n_dp=n_v_tok, plan_ms=plan_ms)
         self.d[Dr] += 1
