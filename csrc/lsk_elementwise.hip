@@ -512,6 +512,39 @@ extern "C" int lsk_greedy_accept(const int64_t* Yv, int64_t* seq_buf, int Dm1, c
   return lsk_check_launch("lsk_greedy_accept");
 }
 
+// ----------------------------------------------------------------------------- M2 probe agreement
+// pred [nc][nvt]: greedy tokens of the nc candidate exits on the nvt verify tokens; Yv [nvt]: the full model's
+// tokens; acc [nv] accepted counts; blk [nvt] / jl [nvt]: verifier and position within its block of each verify
+// token.  out[c] = #{t : jl[t] <= acc[blk[t]] and pred[c][t] == Yv[t]}, out[nc] = #{t : jl[t] <= acc[blk[t]]}
+// (solutions/engine.py:491-514: agreement on the positions whose prefix is correct).  One workgroup per output;
+// integer sums, so the order of the additions does not matter.
+__global__ __launch_bounds__(256) void probe_matches_kernel(const int64_t* __restrict__ pred,
+                                                            const int64_t* __restrict__ Yv,
+                                                            const int64_t* __restrict__ acc,
+                                                            const int32_t* __restrict__ blk,
+                                                            const int32_t* __restrict__ jl, int nc, int nvt,
+                                                            int64_t* __restrict__ out) {
+  const int c = blockIdx.x;
+  int cnt = 0;
+  for (int t = threadIdx.x; t < nvt; t += 256) {
+    const bool valid = jl[t] <= acc[blk[t]];
+    cnt += (c == nc) ? (int)valid : (int)(valid && pred[(long)c * nvt + t] == Yv[t]);
+  }
+  for (int o = 32; o >= 1; o >>= 1) cnt += __shfl_xor(cnt, o, 64);
+  __shared__ int part[4];
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = cnt;
+  __syncthreads();
+  if (threadIdx.x == 0) out[c] = (int64_t)(part[0] + part[1] + part[2] + part[3]);
+}
+
+extern "C" int lsk_probe_matches(const int64_t* pred, const int64_t* Yv, const int64_t* acc, const int32_t* blk,
+                                 const int32_t* jl, int nc, int nvt, int64_t* out, void* stream) {
+  LSK_REQUIRE(out && (nvt == 0 || (pred && Yv && acc && blk && jl)), LSK_EARG, "lsk_probe_matches: null pointer");
+  LSK_REQUIRE(nc >= 0 && nvt >= 0, LSK_ESHAPE, "lsk_probe_matches: bad shape");
+  probe_matches_kernel<<<nc + 1, 256, 0, (hipStream_t)stream>>>(pred, Yv, acc, blk, jl, nc, nvt, out);
+  return lsk_check_launch("lsk_probe_matches");
+}
+
 // ----------------------------------------------------------------------------- rollback
 // Pointer rollback (solutions/engine.py:12-14, 381-384): the committed length of slot i becomes
 // kv_len[i] + acc_j + 1; the KV of the rejected suffix stays where it is (never read: a query reads

@@ -153,6 +153,13 @@ int lsk_greedy_accept(const int64_t* Yv, int64_t* seq_buf, int Dm1, const int32_
                       const int32_t* Ts, const int32_t* forced, int nv, int64_t* acc_out, int64_t* y_out,
                       int64_t* kv_len, void* stream);
 
+/* M2 probe agreement: out[c] = number of verify tokens t with a correct prefix (jl[t] <= acc[blk[t]]) on which
+ * candidate exit c's greedy token pred[c * nvt + t] equals the full model's Yv[t]; out[nc] = number of tokens
+ * with a correct prefix.  int64 tokens and counts, int32 blk / jl.
+ * Replaces the match counting of solutions/engine.py:491-514 (_probe_counts). */
+int lsk_probe_matches(const int64_t* pred, const int64_t* Yv, const int64_t* acc, const int32_t* blk, const int32_t* jl,
+                      int nc, int nvt, int64_t* out, void* stream);
+
 /* Pointer rollback: kv_len[slots[j]] += accepted[j] + 1; moves no KV.
  * Replaces solutions/engine.py:381-384 (pos += a + 1; d = 0) for a device-resident length array. */
 int lsk_kv_rollback(int64_t* kv_len, const int32_t* slots, const int64_t* accepted, int nv, void* stream);

@@ -482,3 +482,53 @@ def test_decode_engine_driver_on_a_stub_model():
     assert res["metrics"]["stop_reason"] == "max_eval_samples"
     assert res["metrics"]["evaluated_completions"] == 6
     assert sum(1 for c in res["completions"] if not c["measured"]) == 2
+
+
+# ----------------------------------------------------------------------------- M2 / M3 policies (host)
+
+def test_m3_budget_respects_the_knee():
+    """c == 0 or (c + shallow tokens and c + deep tokens stay within knee * safety) (tests/test_eesd.py:357-363)."""
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import synthetic_cost_model
+    from thesis_amd.solutions.prefill import M3Planner
+
+    cm = synthetic_cost_model(PRESETS["llama3.2-1b"])
+    cm.gpu.knee_measured = 12.0
+    for safety in (0.5, 0.9):
+        p = M3Planner(cm, knee_safety=safety)
+        bound = 12.0 * safety
+        for n_sh in range(0, 14):
+            for n_dp in range(0, 14):
+                c = p.budget(n_sh, n_dp, 0)
+                assert c == 0 or (c + n_sh <= bound and c + n_dp <= bound)
+
+
+def test_exit_controller_probe_cadence_ema_and_switch():
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import synthetic_cost_model
+    from thesis_amd.solutions.exit_select import ExitController
+
+    cm = synthetic_cost_model(PRESETS["llama3.2-1b"])
+    ec = ExitController(cm, 4, [2, 6], probe_every=3, margin=0.05, omega=0.5)
+    assert ec.cands == [2, 4, 6]
+    wants = []
+    for _ in range(6):
+        wants.append(ec.want_probe())
+        ec.after_deep_step()
+    assert wants == [False, False, True, False, False, True]
+    assert ec.maybe_switch(8, 800.0, True) is None                # no probe yet
+    ec.observe_probe([1, 4, 8], 8)
+    assert ec.alpha == {2: 0.125, 4: 0.5, 6: 1.0}
+    ec.observe_probe([3, 4, 8], 8)
+    assert ec.alpha[2] == 0.5 * 0.125 + 0.5 * 0.375            # EMA with omega = 0.5
+    ec.observe_probe([0, 0, 0], 0)                              # no correct-prefix position: ignored
+    assert ec.probes == 2
+    new = ec.maybe_switch(8, 800.0, True)
+    rates = ec.last_rates
+    best = max(rates, key=rates.get)
+    assert new == (best if best != 4 and rates[best] > 1.05 * rates[4] else None)
+    assert ec.maybe_switch(8, 800.0, False) is None             # a half-done prefill blocks switches
+    cyc = ExitController(cm, 4, [2, 6], probe_every=1, force="cycle")
+    cyc.after_deep_step()
+    cyc.observe_probe([1, 1, 1], 2)
+    assert cyc.maybe_switch(8, 800.0, True) == 6 and cyc.timeline == [(0, 4), (1, 6)]

@@ -50,6 +50,7 @@ _SIGS = {
     "lsk_argmax": (_I, [_I, _P, _L, _I, _I, _P, _P, _P]),
     "lsk_greedy_accept": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
     "lsk_kv_rollback": (_I, [_P, _P, _P, _I, _P]),
+    "lsk_probe_matches": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P]),
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
     "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
@@ -386,6 +387,12 @@ def greedy_accept(Yv, seq_buf, Dm1, slots, starts, Ts, forced, nv, acc_out, y_ou
     _dev(Yv, seq_buf, slots, starts, Ts, forced, acc_out, y_out, kv_len)
     _check(load().lsk_greedy_accept(_ptr(Yv), _ptr(seq_buf), Dm1, _ptr(slots), _ptr(starts), _ptr(Ts), _ptr(forced),
                                     nv, _ptr(acc_out), _ptr(y_out), _ptr(kv_len), _stream()), "lsk_greedy_accept")
+
+
+def probe_matches(pred, Yv, acc, blk_i32, jl_i32, nc: int, nvt: int, out) -> None:
+    _dev(pred, Yv, acc, blk_i32, jl_i32, out)
+    _check(load().lsk_probe_matches(_ptr(pred), _ptr(Yv), _ptr(acc), _ptr(blk_i32), _ptr(jl_i32), nc, nvt, _ptr(out),
+                                    _stream()), "lsk_probe_matches")
 
 
 def kv_rollback(kv_len, slots, accepted, nv):

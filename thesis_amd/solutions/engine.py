@@ -14,10 +14,17 @@ Device glue (id assembly + embedding, exit_h staging, draft head + argmax scatte
 gathers, greedy acceptance) runs in liblsk; the host reads the device once per deep step (accepted
 counts + verified tokens) and never in a shallow step.
 
+M2 (exit="m2", solutions/engine.py:284-288, 312-313, 458, 491-514): every probe_every-th deep step the
+verifiers run all d + 1 tokens through the shallow layers, the hidden states entering every candidate exit are
+captured in both segments, the shared head runs on all of them and lsk_probe_matches counts the agreement with Y on
+the correct-prefix positions; ExitController may then switch the exit layer (pending drafts are dropped).
+M3 (prefill="m3", solutions/engine.py:289-305, 353-354, 424-426, 477-480): chunks of an admitted prompt ride on the
+shallow segment (prompt ids through [0, k), layer-k states kept) and on the next deep segment (those states through
+[k, L)); the last chunk's head gives the request's first token.
+
 Harness hook with no reference counterpart: `forced_accept_p` replaces each verifier's acceptance by
 a seeded draw min(Geometric(p) - 1, d) and commits drafts[0..a-1] + Yv[a] (the tokens whose KV the deep
 segment wrote), as the measured configurations prescribe.
-Not built yet (raise NotImplementedError): exit="m2" (probe steps) and prefill="m3" (piggyback chunks).
 """
 
 from __future__ import annotations
@@ -33,6 +40,8 @@ import torch
 from .. import _lsk
 from ..common.timing import Interval
 from .packed import Block, build_packed, build_packed_arrays, packed_layers, upload, upload_many
+from .exit_select import ExitController
+from .prefill import M3Planner
 from .schedulers import make_scheduler
 
 FREE, PREFILL, DECODE = 0, 1, 2
@@ -127,10 +136,10 @@ class EESDEngine:
                  stop_for: Optional[Callable] = None, ref: Optional[dict] = None):
         if cfg.mode == "ar" and cfg.prefill != "separate":
             raise ValueError("AR mode supports --prefill separate only")
-        if cfg.exit != "fixed":
-            raise NotImplementedError("exit='m2' (probe steps) is not built in this engine yet")
-        if cfg.prefill != "separate":
-            raise NotImplementedError("prefill='m3' (piggyback chunks) is not built in this engine yet")
+        if cfg.exit not in ("fixed", "m2"):
+            raise ValueError(f"unknown exit policy {cfg.exit!r}")
+        if cfg.prefill not in ("separate", "m3"):
+            raise ValueError(f"unknown prefill policy {cfg.prefill!r}")
         self.m, self.dev, self.B, self.cfg, self.cm = model, model.device, B, cfg, cost_model
         self.max_new, self.eos = max_new, set(eos_ids)
         self.stop_for = stop_for or (lambda pid: None)
@@ -154,8 +163,10 @@ class EESDEngine:
         self.sched = make_scheduler(cfg.sched, B, cost_model, self.k, gamma=cfg.gamma, d_max=Dm,
                                     sla_steps=cfg.sla_steps, initial_draft=cfg.initial_draft, omega=cfg.omega,
                                     alpha0=cfg.alpha0, min_draft=cfg.min_draft) if cfg.mode == "spec" else None
-        self.exitc = None
-        self.m3 = None
+        self.exitc = ExitController(cost_model, self.k, [c for c in cfg.k_cands if 1 <= c < self.L], cfg.probe_every,
+                                    cfg.switch_margin, cfg.omega, Dm, cfg.m2_force) if cfg.exit == "m2" else None
+        self.m3 = M3Planner(cost_model, cfg.max_wait, cfg.m3_chunk_cap, cfg.prefill_chunk,
+                            cfg.knee_safety) if cfg.prefill == "m3" else None
         self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
         self._keys = 0
         self.measuring = False
@@ -220,6 +231,17 @@ class EESDEngine:
         self.req[slot] = req
         self.pending[slot] = []
         self.d[slot] = 0
+        if self.m3 is not None and (self.state == DECODE).any():
+            dec = self.state == DECODE
+            n_dec = int(dec.sum())
+            ok, why = self.m3.admit(len(req.prompt), n_dec, n_dec * (self.round_len + 1), self.k,
+                                    float((self.pos + self.d)[dec].sum()))
+            if ok:
+                self.state[slot] = PREFILL
+                req.pf_sh = req.pf_dp = 0
+                return 0
+            self.stats["m3_fallbacks"] += 1
+            self.fallback_reasons[why] = self.fallback_reasons.get(why, 0) + 1
         return self._prefill_separate(slot)
 
     @torch.inference_mode()
@@ -291,48 +313,96 @@ class EESDEngine:
         ctx = np.where(dec, self.pos + d, 0)
         V = self.sched.decide(d, ctx, dec, self.steps_since_deep) if dec.any() else np.zeros(self.B, dtype=bool)
         V = (V | (dec & (d >= cfg.d_max))) & dec & (d >= 1)
-        deep = bool(V.any())
+        # M3 progress guarantee: with no decoding slot, pending prompts run both segments in this step
+        flush = (not dec.any()) and bool((self.state == PREFILL).any())
+        deep = bool(V.any()) or flush
         Dr = dec & ~V
+        probe = deep and self.exitc is not None and self.exitc.want_probe() and bool(V.any())
+        chunks = self._plan_chunks(dec, d, V, deep, probe, flush, ctx) if self.m3 is not None else []
         plan_ms = 1000 * (time.perf_counter() - t0)
 
+        # ---- shallow segment: one block per decoding slot (T = 1 at pos + d, or all d + 1 tokens of a probed
+        # verifier), plus the M3 chunks
         dslots = np.flatnonzero(dec)
-        if len(dslots) == 0:
-            return 0, []
-        # shallow blocks: every decoding slot, T = 1 at pos + d (packed order: by slot)
-        pb = build_packed_arrays(m, dslots, self.pos[dslots] + d[dslots], np.ones(len(dslots), dtype=np.int64),
-                                 cfg.bucketing, upload_meta=False)
+        chunk_slices = []
+        if not probe and not chunks:
+            # every block is one token at pos + d: token j <-> packed block j
+            if len(dslots) == 0:
+                return 0, []
+            pb = build_packed_arrays(m, dslots, self.pos[dslots] + d[dslots], np.ones(len(dslots), dtype=np.int64),
+                                     cfg.bucketing, upload_meta=False)
+            kb = sb_slot = None
+            N = pb.n_tokens
+            sl = dslots[pb.order]
+            sel = sl * Dm1 + d[sl]
+            drf_src = np.flatnonzero(Dr[sl])
+            drf_dst = sel[drf_src] + 1
+            nd, nex = len(drf_src), N
+            pb.meta, sel_t, drf_src_t, drf_dst_t = upload_many([pb.meta_host, sel, drf_src, drf_dst], self.dev)
+            alt_t, ex_dst_t, ex_src_t = sel_t, sel_t, None
+        else:
+            full = V[dslots] if probe else np.zeros(len(dslots), dtype=bool)
+            rows = np.concatenate([dslots, np.array([c[0] for c in chunks], dtype=np.int64)])
+            pos0 = np.concatenate([np.where(full, self.pos[dslots], self.pos[dslots] + d[dslots]),
+                                   np.array([c[1] for c in chunks], dtype=np.int64)])
+            T = np.concatenate([np.where(full, d[dslots] + 1, 1), np.array([c[2] for c in chunks], dtype=np.int64)])
+            kind = np.concatenate([np.where(full, 1, 0), np.full(len(chunks), 2)]).astype(np.int64)  # sh/full/chunk
+            pb = build_packed_arrays(m, rows, pos0, T, cfg.bucketing, upload_meta=False)
+            N = pb.n_tokens
+            kb, sb_slot = kind[pb.order], rows[pb.order]
+            tb = np.repeat(np.arange(pb.nb), pb.blk_T)                   # block of every token
+            j = np.arange(N) - pb.offsets[:-1][tb]                       # position within its block
+            kt, st = kb[tb], sb_slot[tb]
+            dst_d = np.where(kt == 1, j, d[st])                          # exit_h / seq_buf column of the token
+            sel = np.where(kt == 2, -1, st * Dm1 + dst_d)
+            alt = np.zeros(N, dtype=np.int64)
+            for bi in np.flatnonzero(kb == 2):
+                s0, i, p = int(pb.offsets[bi]), int(sb_slot[bi]), int(pb.blk_pos0[bi])
+                c = int(pb.blk_T[bi])
+                alt[s0:s0 + c] = self.req[i].prompt[p:p + c]
+                chunk_slices.append((i, p, c, s0))
+            ex_src = np.flatnonzero(kt != 2)
+            ex_dst = st[ex_src] * Dm1 + dst_d[ex_src]
+            drf_src = np.flatnonzero((kt == 0) & Dr[st])
+            drf_dst = st[drf_src] * Dm1 + d[st[drf_src]] + 1
+            nd, nex = len(drf_src), len(ex_src)
+            pb.meta, sel_t, alt_t, ex_dst_t, ex_src_t, drf_src_t, drf_dst_t = upload_many(
+                [pb.meta_host, sel.astype(np.int64), alt, ex_dst.astype(np.int64), ex_src.astype(np.int64),
+                 drf_src.astype(np.int64), drf_dst.astype(np.int64)], self.dev)
         self._kv(pb, k)
-        N = pb.n_tokens
-        sl = dslots[pb.order]                                                    # T = 1: token j <-> block j
-        sel = sl * Dm1 + d[sl]
-        drf_src = np.flatnonzero(Dr[sl])
-        drf_dst = sel[drf_src] + 1
-        nd = len(drf_src)
-        pb.meta, sel_t, drf_src_t, drf_dst_t = upload_many(
-            [pb.meta_host, sel, drf_src.astype(np.int64), drf_dst], self.dev)
         sb, exh = self._flat()
         iv = Interval(self.dev).start()
         x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
-        _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
-        h = packed_layers(m, x, pb, 0, k)
-        _lsk.copy_rows(exh, sel_t, h, None, N)                                   # exit_h[i, d_i] = h
-        readback = None
-        n_v_tok = 0
+        _lsk.embed(m.embed_w, alt_t, x, sb, sel_t)                        # seq_buf ids, or prompt ids for chunks
+        cap_sh = {} if probe else None
+        h = packed_layers(m, x, pb, 0, k, cap_sh, tuple(c for c in self.exitc.cands if c < k) if probe else ())
+        if nex:
+            _lsk.copy_rows(exh, ex_dst_t, h, ex_src_t, nex)               # exit_h[i, d_i] (all j of a probe) = h
+        for (i, p, c, s0) in chunk_slices:
+            self.pending[i].append((p, c, h[s0:s0 + c]))                  # layer-k states wait for the deep segment
         n_verify = int((d[V] + 1).sum()) if deep else 0
-        merge_heads = deep and nd + n_verify <= _lsk.GEMM_TOKEN_TILE
+        merge_heads = deep and not probe and nd + n_verify <= _lsk.GEMM_TOKEN_TILE
         if nd and not merge_heads:
             hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
             _lsk.copy_rows(hx, None, h, drf_src_t, nd)
-            m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                         # seq_buf[i, d_i + 1] = draft
+            m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                  # seq_buf[i, d_i + 1] = draft
+        readback, n_v_tok, vinfo, cfin = None, 0, ([], [], []), []
         if deep:
             # the drafts are first read next step, so when the rows fit one GEMM token tile their head shares
             # the verify head's launch (one pass over the LM head weights per step); the batch-invariant GEMM
             # gives every row the same result either way
             draft = (h, drf_src_t, drf_dst_t, nd) if merge_heads else (h, None, None, 0)
-            readback, n_v_tok, vinfo = self._deep(V, d, draft)
+            probe_ctx = (pb, kb, sb_slot, cap_sh) if probe else None
+            readback, n_v_tok, vinfo, cfin = self._deep(V, d, draft, probe_ctx)
         iv.stop()
-        self._rec("deep" if deep else "shallow", iv, n_sh=N, n_dp=n_v_tok, plan_ms=plan_ms)
+        n_chunk = sum(c[2] for c in chunks)
+        self._rec("probe" if probe else ("deep" if deep else "shallow"), iv, n_sh=N, n_dp=n_v_tok, n_chunk=n_chunk,
+                  plan_ms=plan_ms)
         self.d[Dr] += 1
+        if self.measuring:
+            self.stats["piggyback_tokens"] += n_chunk
+        for (i, _, c) in chunks:
+            self.req[i].piggybacked += c
         if self.trace is not None:
             vs = np.flatnonzero(V)
             self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
@@ -350,10 +420,10 @@ class EESDEngine:
         Y = rb[nv:nv + n_v_tok]
         accepted = np.zeros(self.B, dtype=np.int64)
         committed, done = 0, []
-        for j, i in enumerate(vslots):
-            a = int(acc[j])
+        for jv, i in enumerate(vslots):
+            a = int(acc[jv])
             accepted[i] = a
-            toks = Y[vstarts[j]:vstarts[j] + a + 1]
+            toks = Y[vstarts[jv]:vstarts[jv] + a + 1]
             self.pos[i] += a + 1
             self.d[i] = 0
             committed += self._commit(i, toks)
@@ -362,51 +432,189 @@ class EESDEngine:
                 self.stats["accepted"] += a
             if self.req[i].finish:
                 done.append(i)
+        off = nv + n_v_tok
+        for jf, i in enumerate(cfin):                                     # M3: prompts whose last chunk finished
+            committed += self._first_token(i, int(rb[off + jf]))
+            if self.req[i].finish:
+                done.append(i)
+        off += len(cfin)
         self.sched.observe(V, accepted, d)
         if self.trace is not None:
             self.trace[-1]["committed"] = committed
         self.round_len = self.steps_since_deep
         self.steps_since_deep = 0
-        self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms)
+        t2 = time.perf_counter()
+        if self.exitc is not None:
+            if probe:
+                nc = len(self.exitc.cands)
+                self.exitc.observe_probe(rb[off:off + nc], int(rb[off + nc]))
+            self.exitc.after_deep_step()
+            dec_now = self.state == DECODE
+            new = self.exitc.maybe_switch(int(dec_now.sum()), float((self.pos + self.d)[dec_now].sum()),
+                                          can_switch=not (self.state == PREFILL).any())
+            if new is not None:
+                self._switch_exit(new)
+        plan_ms += 1000 * (time.perf_counter() - t2)
+        self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms, probe=probe)
         return committed, done
 
-    def _deep(self, V, d, draft):
-        """Deep segment (inside the step's interval) and the step's one LM-head launch: rows [0, nd) are the
-        drafting slots' layer-k states (draft = (h, src rows, seq_buf destinations, nd)), rows nd.. the deep
-        outputs.  Returns the int64 readback [accepted per verifier | committed/verified tokens], the verify
-        token count and verifier info."""
+    def _plan_chunks(self, dec, d, V, deep, probe, flush, ctx) -> list:
+        """M3 chunks riding on this step's shallow segment: [(slot, pos0, c)] (solutions/engine.py:289-305)."""
+        pf = np.flatnonzero(self.state == PREFILL)
+        if not len(pf):
+            return []
+        n_sh = int(dec.sum()) + (int((d[V] + 1).sum() - V.sum()) if probe else 0)
+        n_dp_est = int((d[V] + 1).sum()) if deep else int(dec.sum()) * (max(self.round_len, 1) + 1)
+        pend = sum(c for i in range(self.B) for (_, c, _) in self.pending[i])
+        chunks = []
+        for i in pf:
+            r = self.req[i]
+            rem = len(r.prompt) - r.pf_sh
+            if rem <= 0:
+                continue
+            c = min(rem, self.m3.budget(0 if flush else n_sh, 0 if flush else n_dp_est, 0 if flush else pend))
+            if flush and c <= 0:
+                c = min(rem, self.cfg.prefill_chunk)
+            if c <= 0:
+                continue
+            chunks.append((int(i), r.pf_sh, c))
+            r.pf_sh += c
+            n_sh += c
+            pend += c
+        return chunks
+
+    def _deep(self, V, d, draft, probe_ctx):
+        """Deep segment (inside the step's interval) and the step's LM-head launch.  Blocks: every verifier's
+        d + 1 tokens (inputs exit_h[i, 0..d]) and the pending M3 chunks (inputs their layer-k states).  Head rows:
+        [drafts (when merged) | verify tokens | last token of every finished prompt]; with a probe, one more head
+        launch over every candidate exit's states of the verify tokens.  Returns the int64 readback
+        [accepted per verifier | committed/verified tokens | first tokens | probe matches per candidate, total],
+        the verify token count, verifier info and the slots whose prompt finished."""
         m, k, L, Dm1 = self.m, self.k, self.L, self.Dm1
         vs = np.flatnonzero(V)
-        pb = build_packed_arrays(m, vs, self.pos[vs], d[vs] + 1, self.cfg.bucketing, upload_meta=False)
+        crow, cpos, cT, chid = [], [], [], []
+        if self.m3 is not None:
+            for i in range(self.B):
+                for (p0, c, hk) in self.pending[i]:
+                    crow.append(i)
+                    cpos.append(p0)
+                    cT.append(c)
+                    chid.append(hk)
+        nvb = len(vs)
+        rows = np.concatenate([vs, np.array(crow, dtype=np.int64)])
+        pos0 = np.concatenate([self.pos[vs], np.array(cpos, dtype=np.int64)])
+        T = np.concatenate([d[vs] + 1, np.array(cT, dtype=np.int64)])
+        pb = build_packed_arrays(m, rows, pos0, T, self.cfg.bucketing, upload_meta=False)
         self._kv(pb, L - k)
-        nv, n = pb.nb, pb.n_tokens
-        slots_a = vs[pb.order]
-        T_a = pb.blk_T
-        starts_a = pb.offsets[:-1]
-        vslots, vT, vstarts = slots_a.tolist(), T_a.tolist(), starts_a.tolist()
-        src = np.repeat(slots_a * Dm1 - starts_a, T_a) + np.arange(n)
+        n = pb.n_tokens
+        is_v = pb.order < nvb
+        vb = np.flatnonzero(is_v)                                         # verify blocks in packed order
+        slots_a = rows[pb.order[vb]]
+        T_a = pb.blk_T[vb]
+        nv = len(vb)
+        vstarts_a = np.concatenate([[0], np.cumsum(T_a)[:-1]]).astype(np.int64)
+        nvt = int(T_a.sum())
+        blk_of = np.repeat(np.arange(nv), T_a)
+        jl = np.arange(nvt) - vstarts_a[blk_of]                             # position within its verify block
+        vtok = pb.offsets[vb][blk_of] + jl                                 # packed index of every verify token
+        src = slots_a[blk_of] * Dm1 + jl                                   # exit_h row of every verify token
+        cfin, cfin_row = [], []
+        for b in np.flatnonzero(~is_v):
+            ci = int(pb.order[b]) - nvb
+            i = crow[ci]
+            if cpos[ci] + cT[ci] >= len(self.req[i].prompt):
+                cfin.append(i)
+                cfin_row.append(int(pb.offsets[b]) + cT[ci] - 1)
         if self.forced is not None:
-            forced = np.array([self.forced.draw(self.req[i].key) for i in vslots], dtype=np.int64)
+            forced = np.array([self.forced.draw(self.req[i].key) for i in slots_a.tolist()], dtype=np.int64)
         else:
             forced = np.full(nv, -1, dtype=np.int64)
-        pb.meta, src_t, info = upload_many(
-            [pb.meta_host, src, np.concatenate([slots_a, starts_a, T_a, forced]).astype(np.int32)], self.dev)
+        fast = len(crow) == 0
+        pb.meta, src_t, vtok_t, cfin_t, cfin_dst_t, info = upload_many(
+            [pb.meta_host, src.astype(np.int64), vtok.astype(np.int64), np.array(cfin_row, dtype=np.int64),
+             np.array(cfin, dtype=np.int64) * Dm1,
+             np.concatenate([slots_a, vstarts_a, T_a, forced, blk_of, jl]).astype(np.int32)], self.dev)
         slots_t, starts_t, T_t, forced_t = info[:nv], info[nv:2 * nv], info[2 * nv:3 * nv], info[3 * nv:4 * nv]
+        blk_t, jl_t = info[4 * nv:4 * nv + nvt], info[4 * nv + nvt:4 * nv + 2 * nvt]
         sb, exh = self._flat()
-        h, drf_src_t, drf_dst_t, nd = draft
-        xh = m.buffer("x_head", (nd + n, m.cfg.dim), m.dtype)
-        if nd:
-            _lsk.copy_rows(xh, None, h, drf_src_t, nd)                            # drafting slots' states
+        h_sh, drf_src_t, drf_dst_t, nd = draft
         x = m.buffer("x_deep", (n, m.cfg.dim), m.dtype)
-        _lsk.copy_rows(x, None, exh, src_t, n)                                    # x = exit_h[i, 0..d_i]
-        packed_layers(m, x, pb, k, L, out=xh[nd:])
-        ids = m.head_argmax(xh, out=m.buffer("head_ids", (nd + n,), torch.long))
+        if fast:
+            _lsk.copy_rows(x, None, exh, src_t, n)                        # x = exit_h[i, 0..d_i]
+        else:
+            if nvt:
+                _lsk.copy_rows(x, vtok_t, exh, src_t, nvt)
+            for b in np.flatnonzero(~is_v):
+                s0, ci = int(pb.offsets[b]), int(pb.order[b]) - nvb
+                _lsk.copy_rows(x[s0:s0 + cT[ci]], None, chid[ci], None, cT[ci])
+        probe = probe_ctx is not None
+        cands = self.exitc.cands if probe else ()
+        cap_dp = {} if probe else None
+        nh = nd + nvt + len(cfin)
+        xh = m.buffer("x_head", (nh, m.cfg.dim), m.dtype)
         if nd:
-            _lsk.copy_rows(sb.view(-1, 1), drf_dst_t, ids.view(-1, 1), None, nd)  # seq_buf[i, d_i + 1] = draft
-        Yv = ids[nd:]
-        rb = torch.empty(nv + n, dtype=torch.long, device=self.dev)
-        _lsk.greedy_accept(Yv, sb, Dm1, slots_t, starts_t, T_t, forced_t, nv, rb[:nv], rb[nv:])
-        return rb.cpu(), n, (vslots, vstarts, vT)
+            _lsk.copy_rows(xh, None, h_sh, drf_src_t, nd)                 # drafting slots' layer-k states
+        if fast and not probe:
+            packed_layers(m, x, pb, k, L, out=xh[nd:])
+            hd = xh[nd:]
+        else:
+            hd = packed_layers(m, x, pb, k, L, cap_dp, tuple(c for c in cands if c > k))
+            if nvt:
+                _lsk.copy_rows(xh[nd:], None, hd, vtok_t, nvt)
+            if cfin:
+                _lsk.copy_rows(xh[nd + nvt:], None, hd, cfin_t, len(cfin))
+        nc = len(cands)
+        rb = torch.empty(nv + nvt + len(cfin) + (nc + 1 if probe else 0), dtype=torch.long, device=self.dev)
+        if nh:
+            ids = m.head_argmax(xh, out=m.buffer("head_ids", (nh,), torch.long))
+            if nd:
+                _lsk.copy_rows(sb.view(-1, 1), drf_dst_t, ids.view(-1, 1), None, nd)   # seq_buf[i, d_i + 1] = draft
+            Yv = ids[nd:nd + nvt]
+            if nv:
+                _lsk.greedy_accept(Yv, sb, Dm1, slots_t, starts_t, T_t, forced_t, nv, rb[:nv], rb[nv:nv + nvt])
+            if cfin:
+                y0 = ids[nd + nvt:]
+                _lsk.copy_rows(sb.view(-1, 1), cfin_dst_t, y0.view(-1, 1), None, len(cfin))  # seq_buf[i, 0] = y0
+                _lsk.copy_rows(rb[nv + nvt:nv + nvt + len(cfin)].view(-1, 1), None, y0.view(-1, 1), None, len(cfin))
+        if probe:
+            self._probe_counts(probe_ctx, cands, slots_a, T_a, vtok_t, x, cap_dp, Yv, rb, nv, nvt, blk_t, jl_t,
+                               rb[nv + nvt + len(cfin):])
+        if crow:                                                          # pending chunks are consumed here
+            for i in range(self.B):
+                for (p0, c, _) in self.pending[i]:
+                    self.req[i].pf_dp = p0 + c
+                self.pending[i] = []
+        return rb.cpu(), nvt, (slots_a.tolist(), vstarts_a.tolist(), T_a.tolist()), cfin
+
+    def _probe_counts(self, probe_ctx, cands, slots_a, T_a, vtok_t, x_k, cap_dp, Yv, rb, nv, nvt, blk_t, jl_t, out):
+        """Agreement of every candidate exit with Y on the correct-prefix positions (solutions/engine.py:491-514):
+        the hidden state entering candidate c of each verify token (shallow capture for c < k, the deep segment's
+        input for c = k, deep capture for c > k) goes through the shared head; lsk_probe_matches counts."""
+        m, k = self.m, self.k
+        pb_sh, kb_sh, slot_sh, cap_sh = probe_ctx
+        full_start = {int(slot_sh[b]): int(pb_sh.offsets[b]) for b in np.flatnonzero(kb_sh == 1)}
+        sh_idx = np.concatenate([full_start[int(i)] + np.arange(t) for i, t in zip(slots_a, T_a)])
+        sh_t = upload(sh_idx, self.dev)
+        nc = len(cands)
+        xp = m.buffer("x_probe", (nc * nvt, m.cfg.dim), m.dtype)
+        for ci, c in enumerate(cands):
+            dst = xp[ci * nvt:(ci + 1) * nvt]
+            if c < k:
+                _lsk.copy_rows(dst, None, cap_sh[c], sh_t, nvt)
+            elif c == k:
+                _lsk.copy_rows(dst, None, x_k, vtok_t, nvt)
+            else:
+                _lsk.copy_rows(dst, None, cap_dp[c], vtok_t, nvt)
+        pred = m.head_argmax(xp, out=m.buffer("probe_ids", (nc * nvt,), torch.long))
+        _lsk.probe_matches(pred, Yv, rb[:nv], blk_t, jl_t, nc, nvt, out)
+
+    def _switch_exit(self, new_k: int) -> None:
+        """Exit switch (solutions/engine.py:522-527): drafts in flight are dropped (lossless), every slot restarts
+        drafting from its last committed token with the new exit layer."""
+        self.stats["dropped_drafts"] += int(self.d[self.state == DECODE].sum())
+        self.d[:] = 0
+        self.k = new_k
+        self.sched.set_exit(new_k, self.exitc.alpha.get(new_k))
 
     def _kv(self, pb, n_layers: int) -> None:
         if self.measuring:
@@ -619,7 +827,9 @@ class EESDEngine:
             "ttft_ms_p99": float(np.percentile(ttft, 99)) if ttft else None,
             "tpot_ms_mean": float(np.mean(tpot)) if tpot else None,
             "tpot_ms_p99": float(np.percentile(tpot, 99)) if tpot else None,
-            "k_final": self.k, "k_timeline": [(0, self.k)], "k_alpha": None,
+            "k_final": self.k,
+            "k_timeline": list(self.exitc.timeline) if self.exitc is not None else [(0, self.k)],
+            "k_alpha": dict(self.exitc.alpha) if self.exitc is not None else None,
             "probe_steps": st["probe_steps"], "dropped_drafts_at_switch": st["dropped_drafts"],
             "m3_fallbacks": st["m3_fallbacks"], "m3_fallback_reasons": dict(self.fallback_reasons),
             "oracle_coverage": None,
