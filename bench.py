@@ -48,10 +48,20 @@ def log(*a):
 
 # ----------------------------------------------------------------------------- main workload
 
-def build_engine(seed: int, max_new: int, B: int):
+def bench_cost_model(cfg, kind: str):
+    """The aspire policy's cost model: the package's MI355X calibration of this shape (written by
+    `python -m thesis_amd.solutions.calibrate --model llama3-8b`) in the given kind, or with 'peaks' the
+    uncalibrated model of published peaks x the fractions the kernels reach."""
+    from thesis_amd.solutions.cost_model import default_cost_model, mi355x_cost_model
+
+    if kind == "peaks":
+        return mi355x_cost_model(cfg), "roofline, MI355X published peaks x achieved fractions"
+    return default_cost_model(cfg, kind)
+
+
+def build_engine(seed: int, max_new: int, B: int, cost_kind: str = "roofline"):
     from thesis_amd.common.data import synthetic_prompts
     from thesis_amd.common.model import PRESETS, LayerSkipLlama
-    from thesis_amd.solutions.cost_model import mi355x_cost_model
     from thesis_amd.solutions.engine import EESDEngine, EngineConfig, Request
 
     cfg = PRESETS["llama3-8b"]
@@ -59,7 +69,10 @@ def build_engine(seed: int, max_new: int, B: int):
     prompts = synthetic_prompts(B, cfg.vocab_size, 128, 1024, seed=seed + 1)
     ecfg = EngineConfig(sched="aspire", k=8, d_max=8, min_draft=2, initial_draft=3, forced_accept_p=0.3,
                         forced_seed=seed)
-    eng = EESDEngine(model, B, 1024, max_new, (), ecfg, mi355x_cost_model(cfg))
+    cm, cm_src = bench_cost_model(cfg, cost_kind)
+    log(f"[bench] cost model: {cm_src}")
+    eng = EESDEngine(model, B, 1024, max_new, (), ecfg, cm)
+    eng.cost_model_source = cm_src
     for i, p in enumerate(prompts):
         eng.assign(i, Request(p.pid, list(p.tokens)))
     return cfg, model, eng, prompts
@@ -98,7 +111,7 @@ def run_main(args):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     t0 = time.time()
-    cfg, model, eng, prompts = build_engine(args.seed, args.max_new, args.batch)
+    cfg, model, eng, prompts = build_engine(args.seed, args.max_new, args.batch, args.cost_model)
     torch.cuda.synchronize()
     log(f"[bench] model + prefill of {len(prompts)} prompts: {time.time() - t0:.1f}s")
     eng.measuring = True
@@ -355,6 +368,9 @@ def main():
     ap.add_argument("--no-attn", action="store_true")
     ap.add_argument("--check-attn", action="store_true")
     ap.add_argument("--attn-only", action="store_true", help="only the verify-attention microbenchmark")
+    ap.add_argument("--cost-model", default="roofline", choices=["roofline", "roofline-peak", "linear", "peaks"],
+                    help="aspire's cost model: a kind of the package's MI355X calibration, or 'peaks' for the "
+                         "uncalibrated published-peak model")
     ap.add_argument("--copy-calib-mib", type=int, default=0,
                     help="plain copy of this many MiB before the timed steps (rocprofv3 counter calibration)")
     ap.add_argument("--out", type=str, default=None, help="also write the JSON line to this file")
@@ -379,6 +395,7 @@ def main():
         return
     cfg, model, eng, committed, elapsed, trace, prof, replay = run_main(args)
     kernels = summarize_kernels(prof)
+    cost_model_source = eng.cost_model_source
     del model, eng
     torch.cuda.empty_cache()
     attn = None if args.no_attn else run_attention_bench(args)
@@ -408,7 +425,8 @@ def main():
         "config": {"workload": "llama3-8b-shape packed self-speculative decode (EESD)", "B": args.batch,
                    "prompt_len": [128, 1024], "max_new": args.max_new, "exit_layer": 8, "draft_len": [2, 8],
                    "scheduler": "aspire (latency-aware)", "acceptance": "forced geometric p=0.3",
-                   "weights": "random init bf16", "parallelism": "single GPU"},
+                   "cost_model": cost_model_source, "weights": "random init bf16",
+                   "parallelism": "single GPU"},
         "roofline": roofline, "cpu_baseline": cpu, "verify_attn": attn, "kernels": kernels,
         "steps_detail": {"committed_tokens": committed, "deep_steps": sum(1 for s in trace if s["dp"]),
                          "mean_shallow_rows": float(np.mean([len(s["sh"]) for s in trace])) if trace else None,

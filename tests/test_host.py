@@ -330,6 +330,74 @@ def test_cost_model_formula():
     assert np.isclose(t, manual)
 
 
+def test_hinge_knee_recovers_a_planted_knee():
+    from thesis_amd.solutions.calibrate import N_GRID, hinge_knee
+
+    n = np.array(N_GRID, dtype=np.float64)
+    for knee, a, b in ((96.0, 0.5, 0.004), (32.0, 0.12, 0.01), (256.0, 2.0, 0.02)):
+        t = a + b * np.maximum(n - knee, 0.0)
+        kn, coef = hinge_knee(N_GRID, t)
+        assert kn == knee and np.allclose(coef, [a, b])
+    # a falling line has no knee with a non-negative slope
+    with pytest.raises(ValueError):
+        hinge_knee(N_GRID, 1.0 - 1e-3 * n)
+
+
+def test_linear_fit_recovers_planted_coefficients():
+    from thesis_amd.solutions.calibrate import ape_summary, fit_linear
+
+    rng = np.random.default_rng(0)
+    rows = [{"n": int(nn), "kv": int(kv), "ms": 0.3 + 0.002 * nn + 5e-6 * kv}
+            for nn, kv in zip(rng.integers(1, 600, 40), rng.integers(100, 200000, 40))]
+    heads = [{"n": nn, "ms": 0.25 + 0.001 * nn} for nn in (1, 8, 64, 256)]
+    fit = fit_linear(rows, heads)
+    assert np.allclose([fit["a"], fit["b"], fit["c"], fit["head_a"], fit["head_b"]],
+                       [0.3, 0.002, 5e-6, 0.25, 0.001])
+    val = [{"kind": "deep", "n": 100, "ms": 2.0, "m": 2.2}, {"kind": "shallow", "n": 8, "ms": 1.0, "m": 0.9}]
+    s = ape_summary(val, ["m"])
+    assert np.isclose(s["m_all"]["mape"], 0.1) and np.isclose(s["m_deep"]["max_ape"], 0.1)
+    assert s["m_n64_256"]["n"] == 1 and "m_prefill" not in s
+
+
+def test_calibration_record_loads_as_cost_models(tmp_path):
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import (GPUParams, LinearCostModel, RooflineCostModel, load_cost_model,
+                                                 save_json)
+
+    cfg = PRESETS["llama3-8b"]
+    gpu = GPUParams(bw=5.5e9, flops=1.6e12, t_op=0.003, n_op_layer=8, n_op_bucket=0, n_op_head=3, n_op_segment=1,
+                    meta={"host": "x"}, flops_eff=9e11, knee_measured=120.0)
+    p = tmp_path / "c.json"
+    save_json(p, {"model": "llama3-8b", "gpu": gpu,
+                  "linear": {"a": 0.09, "b": 1e-4, "c": 2e-8, "head_a": 0.2, "head_b": 1e-3}})
+    cm = load_cost_model(p, cfg)
+    assert isinstance(cm, RooflineCostModel) and cm.F == 9e11 and cm.knee() == 120.0
+    assert load_cost_model(p, cfg, "roofline-peak").F == 1.6e12
+    lin = load_cost_model(p, cfg, "linear")
+    assert isinstance(lin, LinearCostModel) and np.isclose(lin.layer_gemm_ms(10), 0.09 + 1e-3)
+
+
+def test_committed_mi355x_calibration_is_the_default_and_fits_its_measurements():
+    import csv
+
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import RooflineCostModel, calibration_path, default_cost_model
+
+    cfg = PRESETS["llama3-8b"]
+    cm, src = default_cost_model(cfg)
+    assert isinstance(cm, RooflineCostModel) and "calibrated" in src
+    # the measured single-layer times of the knee grid (128 cached positions per request)
+    grid = cm.gpu.meta["knee_layer_grid"]
+    for r in grid:
+        pred = float(cm.t_segment(1, r["n"], 128 * r["n"])) - cm.segment_ops_ms()
+        assert abs(pred - r["ms"]) / r["ms"] < 0.5, (r, pred)
+    # the validation steps written beside it: the roofline model within 40 % of every measured step
+    with open(calibration_path("llama3-8b").with_name("llama3-8b_mi355x_validation.csv")) as f:
+        rows = list(csv.DictReader(f))
+    assert len(rows) >= 90
+    assert max(abs(float(r["roofline"]) - float(r["ms"])) / float(r["ms"]) for r in rows) < 0.4
+
+
 def test_config_parsing_old_and_new_formats(tmp_path):
     import json
 

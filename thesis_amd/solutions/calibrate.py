@@ -1,0 +1,343 @@
+"""Calibrate the cost models on this GPU by timing the native packed path, and report their prediction
+error (solutions/calibrate.py:1-20 semantics).
+
+    python -m thesis_amd.solutions.calibrate --model llama3-8b              # writes the calibration JSON
+    python -m thesis_amd.solutions.calibrate --model llama3-8b --validate   # + measured steps -> MAPE table
+
+Measured, each with HIP events on the stream liblsk launches on (median of repetitions):
+  bw         weight-streaming rate of lsk_gemm at n = 1 through a packed 28672 x 8192 bf16 weight
+             (solutions/calibrate.py:59-62)
+  flops      8192^3 bf16 matmul through torch (hipBLASLt): the device's dense rate as a library reaches
+             it, kept only for the roofline-peak variant (solutions/calibrate.py:63-66)
+  flops_eff  highest flop rate of the model's own layer GEMMs (qkv, o, w13 + silu-mul, w2) through
+             lsk_gemm for n = 1..512 tokens (solutions/calibrate.py:126-140)
+  knee       hinge fit t = a + b max(n - knee, 0) of one real packed layer timed for n = 1..512
+             single-token requests (solutions/calibrate.py:143-172)
+  t_op       back-to-back tiny liblsk launches (a one-row lsk_copy_rows) (solutions/calibrate.py:67-72)
+  n_op       kernels issued by one packed layer (one and two query-length buckets), by the head and by
+             the metadata build, counted with the torch profiler (solutions/calibrate.py:78-99)
+  linear     a + b n + c KV least squares over a (requests, tokens, context) grid of packed-layer times
+             and a + b n for the head (solutions/calibrate.py:102-123, 175-181)
+Validation times shallow steps, deep steps and prefill chunks of the packed path over a grid and reports
+MAPE / max APE of each model overall, per step kind and for n = 64..256 (solutions/calibrate.py:184-236).
+Random-init weights of the named shape are used: timing does not depend on the values.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import socket
+import time
+from pathlib import Path
+from typing import Callable, Optional
+
+import numpy as np
+import torch
+
+from .. import _lsk
+from .cost_model import GPUParams, LinearCostModel, ModelDims, RooflineCostModel, calibration_path, save_json
+from .packed import Block, build_packed, packed_layer, packed_layers
+
+N_GRID = (1, 2, 4, 8, 16, 24, 32, 48, 64, 80, 96, 112, 128, 160, 192, 224, 256, 320, 384, 448, 512)
+
+
+def default_path(model_name: str) -> Path:
+    """Where a calibration of `model_name` on an MI355X is kept (loaded by bench.py and the eesd method)."""
+    return calibration_path(model_name)
+
+
+def timed_ms(fn: Callable[[], object], reps: int = 20, warm: int = 5) -> float:
+    """Median over `reps` runs of fn, each bracketed by HIP events on the current stream (liblsk launches
+    on it), after `warm` untimed runs."""
+    for _ in range(warm):
+        fn()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for e0, e1 in ev:
+        e0.record()
+        fn()
+        e1.record()
+    torch.cuda.synchronize()
+    return float(np.median([e0.elapsed_time(e1) for e0, e1 in ev]))
+
+
+# ----------------------------------------------------------------------------- device constants
+
+def micro(dev, bw_shape=(28672, 8192), mm: int = 8192, n_tiny: int = 1000) -> dict:
+    """bw (bytes/ms), flops (flop/ms), t_op (ms per launch)."""
+    W = _lsk.as_gemm_weight(torch.randn(*bw_shape, device=dev, dtype=torch.bfloat16))
+    x = torch.randn(1, bw_shape[1], device=dev, dtype=torch.bfloat16)
+    y = torch.empty(1, bw_shape[0], device=dev, dtype=torch.bfloat16)
+    bw = bw_shape[0] * bw_shape[1] * 2 / timed_ms(lambda: _lsk.gemm(x, W, out=y))
+    del W
+    A = torch.randn(mm, mm, device=dev, dtype=torch.bfloat16)
+    Bm = torch.randn(mm, mm, device=dev, dtype=torch.bfloat16)
+    flops = 2.0 * mm ** 3 / timed_ms(lambda: torch.mm(A, Bm), reps=10)
+    del A, Bm
+    src = torch.zeros(1, 16, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+
+    def tiny():
+        for _ in range(n_tiny):
+            _lsk.copy_rows(dst, None, src, None, 1)
+    t_op = timed_ms(tiny, reps=5, warm=1) / n_tiny
+    torch.cuda.empty_cache()
+    return {"bw": bw, "flops": flops, "t_op": t_op}
+
+
+def count_kernels(fn: Callable[[], object]) -> int:
+    """Device activities (kernels and copies) one call of fn issues, from the torch profiler."""
+    from torch.profiler import ProfilerActivity, profile
+
+    fn()
+    torch.cuda.synchronize()
+    with profile(activities=[ProfilerActivity.CUDA]) as prof:
+        fn()
+        torch.cuda.synchronize()
+    return sum(1 for e in prof.events() if e.device_type.name == "CUDA")
+
+
+def trace_ops(m) -> dict:
+    """n_op terms: one packed layer with one and with two query-length buckets, the head, the metadata
+    build (solutions/calibrate.py:88-99)."""
+    m.allocate_cache(4, 512)
+    one = build_packed(m, [Block(0, 100, 1), Block(1, 100, 1)])
+    two = build_packed(m, [Block(0, 100, 1), Block(1, 100, 3)])
+    x1 = torch.randn(one.n_tokens, m.cfg.dim, device=m.device, dtype=m.dtype)
+    x2 = torch.randn(two.n_tokens, m.cfg.dim, device=m.device, dtype=m.dtype)
+    with torch.inference_mode():
+        n1 = count_kernels(lambda: packed_layer(m, 0, x1, one))
+        n2 = count_kernels(lambda: packed_layer(m, 0, x2, two))
+        nh = count_kernels(lambda: m.head_argmax(x1))
+        ns = count_kernels(lambda: build_packed(m, [Block(0, 100, 1), Block(1, 100, 1)]))
+    m.free_cache()
+    return {"n_op_layer": n1, "n_op_bucket": max(n2 - n1, 0), "n_op_head": nh, "n_op_segment": ns}
+
+
+def _layer_gemms(m) -> list:
+    """(weight, input width, epilogue) of the four projections of layer 0, as the layer runner calls them."""
+    lw, c = m.layers[0], m.cfg
+    return [(lw.wqkv, c.dim, _lsk.EPI_NONE), (lw.wo, m.q_size, _lsk.EPI_NONE),
+            (lw.w13, c.dim, _lsk.EPI_SILU_MUL), (lw.w2, c.intermediate_size, _lsk.EPI_NONE)]
+
+
+def measure_flops_eff(m, ns=N_GRID) -> dict:
+    """F_eff: the highest flop rate the model's own layer GEMMs reach for n = 1..512 tokens.  At small n
+    they stream the weights (rate grows with n); past the ridge they are MFMA-bound."""
+    shapes = _layer_gemms(m)
+    params = sum(w.shape[0] * w.shape[1] for w, _, _ in shapes)
+    rows = []
+    with torch.inference_mode():
+        for n in ns:
+            xs = [torch.randn(n, k, device=m.device, dtype=m.dtype) for _, k, _ in shapes]
+            outs = [torch.empty(n, w.shape[0] // (2 if e == _lsk.EPI_SILU_MUL else 1), device=m.device,
+                                dtype=m.dtype) for w, _, e in shapes]
+
+            def run():
+                for (w, _, e), x, o in zip(shapes, xs, outs):
+                    _lsk.gemm(x, w, out=o, epilogue=e)
+            ms = timed_ms(run)
+            rows.append({"n": n, "ms": ms, "flop_per_ms": 2.0 * params * n / ms})
+    best = max(rows, key=lambda r: r["flop_per_ms"])
+    return {"flops_eff": best["flop_per_ms"], "flops_eff_at_n": best["n"], "gemm_grid": rows}
+
+
+def hinge_knee(ns, ms, grid=None) -> tuple:
+    """Knee of t = a + b max(n - knee, 0), b >= 0, fitted in relative error (weights 1/t) over a grid
+    of knees (solutions/calibrate.py:143-157).  Returns (knee, [a, b])."""
+    n = np.asarray(ns, dtype=np.float64)
+    t = np.asarray(ms, dtype=np.float64)
+    w = 1.0 / t
+    cands = np.arange(4.0, n.max(), 2.0) if grid is None else np.asarray(grid, dtype=np.float64)
+    best = None
+    for kn in cands:
+        X = np.stack([np.ones_like(n), np.maximum(n - kn, 0.0)], axis=1) * w[:, None]
+        coef = np.linalg.lstsq(X, t * w, rcond=None)[0]
+        if coef[1] < 0:
+            continue
+        err = float(np.sum((X @ coef - t * w) ** 2))
+        if best is None or err < best[0]:
+            best = (err, float(kn), [float(coef[0]), float(coef[1])])
+    if best is None:
+        raise ValueError("no knee with a non-negative slope")
+    return best[1], best[2]
+
+
+def measure_knee(m, ns=N_GRID, ctx: int = 128) -> dict:
+    """One real packed decoder layer, n single-token requests at a short context, n = 1..512."""
+    rows = []
+    with torch.inference_mode():
+        m.allocate_cache(max(ns), ctx + 64)
+        for n in ns:
+            pb = build_packed(m, [Block(b, ctx, 1) for b in range(n)])
+            x = torch.randn(n, m.cfg.dim, device=m.device, dtype=m.dtype)
+            rows.append({"n": n, "ms": timed_ms(lambda: packed_layer(m, 1, x, pb))})
+        m.free_cache()
+    knee, coef = hinge_knee([r["n"] for r in rows], [r["ms"] for r in rows])
+    return {"knee_measured": knee, "knee_fit": {"a": coef[0], "b": coef[1]}, "layer_grid": rows}
+
+
+def layer_grid(m, Bs=(1, 4, 16, 32, 64), Ts=(1, 4, 8, 17), ctxs=(256, 1024, 2048), log=None) -> tuple:
+    """Packed-layer times over (requests B, tokens T per request, context) and head times over n = B T."""
+    rows, heads = [], []
+    with torch.inference_mode():
+        for C in ctxs:
+            for B in Bs:
+                m.allocate_cache(B, C + 64)
+                for T in Ts:
+                    pb = build_packed(m, [Block(b, C - T, T) for b in range(B)])
+                    x = torch.randn(pb.n_tokens, m.cfg.dim, device=m.device, dtype=m.dtype)
+                    ms = timed_ms(lambda: packed_layer(m, 1, x, pb), reps=10, warm=3)
+                    rows.append({"n": B * T, "kv": pb.kv_read, "ms": ms, "B": B, "T": T, "ctx": C})
+                    if C == ctxs[0]:
+                        heads.append({"n": B * T, "ms": timed_ms(lambda: m.head_argmax(x), reps=10, warm=3)})
+                m.free_cache()
+            if log:
+                log(f"[calibrate] layer grid: context {C} done")
+    return rows, heads
+
+
+def fit_linear(rows, heads) -> dict:
+    """Least squares of t_layer = a + b n + c KV and t_head = head_a + head_b n
+    (solutions/calibrate.py:175-181)."""
+    X = np.array([[1.0, r["n"], r["kv"]] for r in rows])
+    a, b, c = np.linalg.lstsq(X, np.array([r["ms"] for r in rows]), rcond=None)[0]
+    Xh = np.array([[1.0, h["n"]] for h in heads])
+    ha, hb = np.linalg.lstsq(Xh, np.array([h["ms"] for h in heads]), rcond=None)[0]
+    return {"a": float(a), "b": float(b), "c": float(c), "head_a": float(ha), "head_b": float(hb)}
+
+
+# ----------------------------------------------------------------------------- validation
+
+def ape_summary(rows: list, names) -> dict:
+    """MAPE and max APE of each prediction column in `rows` against the measured `ms`, overall, per
+    step kind and for 64 <= n <= 256 (solutions/calibrate.py:223-235)."""
+    out = {}
+    for name in names:
+        for kind in ("shallow", "deep", "prefill", "all", "n64_256"):
+            if kind == "n64_256":
+                sel = [r for r in rows if 64 <= r["n"] <= 256]
+            else:
+                sel = [r for r in rows if kind == "all" or r["kind"] == kind]
+            if sel:
+                ape = np.array([abs(r[name] - r["ms"]) / r["ms"] for r in sel])
+                out[f"{name}_{kind}"] = {"n": len(sel), "mape": float(ape.mean()), "max_ape": float(ape.max())}
+    return out
+
+
+def validate(m, cms: dict, k: int, out_csv: Optional[Path], ctxs=(256, 1024, 2048), Bs=(1, 4, 8, 16, 32),
+             Ts=(2, 4, 6, 9, 17), prefill=(64, 256, 1024), log=None) -> dict:
+    """Time the engine's packed step shapes and compare with every model's prediction
+    (solutions/calibrate.py:184-221): shallow = B draft tokens through [0, k) + head; deep = the latest
+    draft through [0, k), then B T tokens through [k, L) + head; prefill = one chunk of n tokens through
+    [0, L) + the head of its last row."""
+    L = m.n_layers
+    rows = []
+    with torch.inference_mode():
+        for C in ctxs:
+            for B in Bs:
+                m.allocate_cache(B, C + max(max(Ts), max(prefill) if prefill else 0) + 64)
+                pb = build_packed(m, [Block(b, C, 1) for b in range(B)])
+                x = torch.randn(B, m.cfg.dim, device=m.device, dtype=m.dtype)
+                ms = timed_ms(lambda: m.head_argmax(packed_layers(m, x, pb, 0, k)), reps=10, warm=3)
+                rows.append({"kind": "shallow", "B": B, "ctx": C, "T": 1, "n": B, "ms": ms,
+                             **{nm: float(c.t_sh(B, k, pb.kv_read)) for nm, c in cms.items()}})
+                for T in Ts:
+                    pbs = build_packed(m, [Block(b, C + T - 1, 1) for b in range(B)])
+                    pbd = build_packed(m, [Block(b, C, T) for b in range(B)])
+                    xd = torch.randn(B * T, m.cfg.dim, device=m.device, dtype=m.dtype)
+
+                    def deep():
+                        packed_layers(m, x, pbs, 0, k)
+                        m.head_argmax(packed_layers(m, xd, pbd, k, L))
+                    ms = timed_ms(deep, reps=10, warm=3)
+                    rows.append({"kind": "deep", "B": B, "ctx": C, "T": T, "n": B * T, "ms": ms,
+                                 **{nm: float(c.t_deep(B * T, k, pbd.kv_read, B)) for nm, c in cms.items()}})
+                if B == 1:
+                    for n_tok in prefill:
+                        pbp = build_packed(m, [Block(0, C, n_tok)])
+                        xp = torch.randn(n_tok, m.cfg.dim, device=m.device, dtype=m.dtype)
+                        ms = timed_ms(lambda: m.head_argmax(packed_layers(m, xp, pbp, 0, L)[-1:]), reps=5, warm=2)
+                        rows.append({"kind": "prefill", "B": 1, "ctx": C, "T": n_tok, "n": n_tok, "ms": ms,
+                                     **{nm: float(c.t_prefill(n_tok, pbp.kv_read)) for nm, c in cms.items()}})
+                m.free_cache()
+                if log:
+                    log(f"[calibrate] validation: context {C}, B {B} done")
+    if out_csv is not None:
+        out_csv.parent.mkdir(parents=True, exist_ok=True)
+        with open(out_csv, "w", newline="") as f:
+            wr = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+            wr.writeheader()
+            wr.writerows(rows)
+    return {"rows": rows, "summary": ape_summary(rows, cms.keys())}
+
+
+# ----------------------------------------------------------------------------- driver
+
+def calibrate(model, name: str, *, linear: bool = True, do_validate: bool = False, k: int = 8,
+              ns=N_GRID, grid: Optional[dict] = None, val: Optional[dict] = None, bw_shape=(28672, 8192),
+              mm: int = 8192, val_csv: Optional[Path] = None, log=print) -> dict:
+    """Run every measurement on `model` and return the calibration record (JSON-ready)."""
+    t0 = time.time()
+    mic = micro(model.device, bw_shape=bw_shape, mm=mm)
+    ops = trace_ops(model)
+    fe = measure_flops_eff(model, ns)
+    kn = measure_knee(model, ns)
+    gpu = GPUParams(**mic, **ops, flops_eff=fe["flops_eff"], knee_measured=kn["knee_measured"],
+                    meta={"host": socket.gethostname(), "device": torch.cuda.get_device_name(model.device),
+                          "torch": torch.__version__, "hip": torch.version.hip,
+                          "flops_eff_at_n": fe["flops_eff_at_n"], "knee_fit": kn["knee_fit"],
+                          "knee_analytic_peak": mic["flops"] / mic["bw"],
+                          "gemm_grid": fe["gemm_grid"], "knee_layer_grid": kn["layer_grid"]})
+    dims = ModelDims.from_config(model.cfg)
+    res = {"model": name, "gpu": gpu, "model_dims": dims.__dict__}
+    log(f"[calibrate] BW {mic['bw'] / 1e9:.2f} TB/s, F {mic['flops'] / 1e9:.1f} TFLOP/s, F_eff "
+        f"{fe['flops_eff'] / 1e9:.1f} TFLOP/s (n={fe['flops_eff_at_n']}), knee {kn['knee_measured']:.0f} tokens, "
+        f"t_op {mic['t_op'] * 1e3:.2f} us, n_op layer/bucket/head/segment {ops['n_op_layer']}/"
+        f"{ops['n_op_bucket']}/{ops['n_op_head']}/{ops['n_op_segment']} ({time.time() - t0:.0f}s)")
+    if linear:
+        rows, heads = layer_grid(model, **(grid or {}), log=log)
+        res["linear"] = {**fit_linear(rows, heads), "n_layers": model.n_layers, "model_name": name}
+        res["linear_grid"] = rows
+        log(f"[calibrate] linear a {res['linear']['a'] * 1e3:.1f} us, b {res['linear']['b'] * 1e3:.3f} us/token, "
+            f"c {res['linear']['c'] * 1e6:.3f} ns/pos, head {res['linear']['head_a'] * 1e3:.1f} us "
+            f"+ {res['linear']['head_b'] * 1e3:.3f} us/token ({time.time() - t0:.0f}s)")
+    if do_validate:
+        cms = {"roofline": RooflineCostModel(gpu, dims, variant="measured"),
+               "roofline_peak": RooflineCostModel(gpu, dims, variant="peak")}
+        if linear:
+            lin = res["linear"]
+            cms["linear"] = LinearCostModel(lin["a"], lin["b"], lin["c"], lin["head_a"], lin["head_b"], dims)
+        v = validate(model, cms, k, val_csv, **(val or {}), log=log)
+        res["validation"] = v["summary"]
+        for key, s in v["summary"].items():
+            log(f"[calibrate] {key:26s} n={s['n']:3d}  MAPE {100 * s['mape']:5.1f}%  max {100 * s['max_ape']:5.1f}%")
+    return res
+
+
+def main(argv=None) -> None:
+    from ..common.model import PRESETS, LayerSkipLlama
+
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--model", default="llama3-8b", choices=sorted(PRESETS))
+    ap.add_argument("--k", type=int, default=8, help="exit layer of the validation steps")
+    ap.add_argument("--validate", action="store_true")
+    ap.add_argument("--skip-linear", action="store_true", help="device constants only (no layer grid)")
+    ap.add_argument("--out", default=None, help="JSON path (default: the package's calibration directory)")
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args(argv)
+    if not torch.cuda.is_available():
+        raise SystemExit("calibration needs the GPU")
+    torch.manual_seed(args.seed)
+    out = Path(args.out) if args.out else default_path(args.model)
+    model = LayerSkipLlama.random(PRESETS[args.model], seed=args.seed, dtype=torch.bfloat16, max_seq=4096)
+    res = calibrate(model, args.model, linear=not args.skip_linear, do_validate=args.validate, k=args.k,
+                    val_csv=out.with_name(out.stem + "_validation.csv") if args.validate else None,
+                    log=lambda s: print(s, flush=True))
+    save_json(out, res)
+    print(f"[calibrate] wrote {out}", flush=True)
+
+
+if __name__ == "__main__":
+    main()

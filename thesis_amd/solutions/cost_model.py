@@ -173,6 +173,27 @@ def mi355x_cost_model(cfg, bw_frac: float = 0.7, flops_frac: float = 0.5, t_op_m
     return RooflineCostModel(gpu, dims)
 
 
+CALIBRATION_DIR = Path(__file__).resolve().parent / "calibration"
+
+
+def calibration_path(model_name: str) -> Path:
+    """Where the MI355X calibration of a preset model shape is kept (written by thesis_amd.solutions.calibrate)."""
+    return CALIBRATION_DIR / f"{model_name}_mi355x.json"
+
+
+def default_cost_model(cfg, kind: str = "roofline"):
+    """(model, source): the MI355X calibration of the preset whose shape equals cfg when one is kept in the
+    package (as the reference's drivers load <calibration dir>/<model>.json, solutions/run_ablation.py:183-195),
+    else `mi355x_cost_model`."""
+    from ..common.model import PRESETS
+
+    for name, pc in PRESETS.items():
+        p = calibration_path(name)
+        if pc == cfg and p.exists():
+            return load_cost_model(p, cfg, kind), f"{kind}, calibrated on MI355X ({name})"
+    return mi355x_cost_model(cfg), "roofline, MI355X published peaks x achieved fractions"
+
+
 def load_cost_model(path, cfg, kind: str = "roofline"):
     d = json.loads(Path(path).read_text())
     dims = ModelDims.from_config(cfg)

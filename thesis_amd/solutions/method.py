@@ -13,7 +13,7 @@ import torch
 
 from ..common.engine import DecodeEngine, SlotState, StepRecord
 from ..common.methods import MethodSpec, register
-from .cost_model import load_cost_model, mi355x_cost_model
+from .cost_model import default_cost_model, load_cost_model
 from .engine import FREE, EESDEngine, EngineConfig, Request
 
 
@@ -100,7 +100,7 @@ def _config(args) -> EngineConfig:
 
 def _build(model, args, batch_size, max_prompt_len, eos):
     cfg = _config(args)
-    cm = load_cost_model(args.cost_model, model.cfg) if args.cost_model else mi355x_cost_model(model.cfg)
+    cm = load_cost_model(args.cost_model, model.cfg) if args.cost_model else default_cost_model(model.cfg)[0]
     return EESDDecodeEngine(model, batch_size, max_prompt_len, args.max_new_tokens, eos, cfg, cm,
                             ignore_eos=args.ignore_eos)
 
