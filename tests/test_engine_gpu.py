@@ -160,6 +160,19 @@ def test_engine_spec_equals_ar_on_gpu(cuda, dtype, sched):
     assert sp == ar
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32])
+def test_shallow_step_graphs_replay_the_eager_steps(cuda, dtype):
+    """Fixed-shape shallow steps replayed as captured HIP graphs give the tokens of eager steps, with eager
+    work and synchronisations between replays; the graphs really replay."""
+    ocfg = small_cfg()
+    _, g = _pair(ocfg, dtype, std=0.1)
+    prompts = _prompts(6, ocfg.vocab_size, seed=7)
+    eager, _, _ = _run_gpu(g, prompts, 3, 24, sched="fixed", k=2, gamma=4, d_max=6, graphs=False)
+    graph, eng, _ = _run_gpu(g, prompts, 3, 24, sched="fixed", k=2, gamma=4, d_max=6, graphs=True)
+    assert graph == eager
+    assert eng.graphs.captures >= 1 and eng.graphs.replays > eng.graphs.captures
+
+
 def test_rollback_moves_no_kv(cuda):
     """Rejected drafts are rolled back by the position pointer only: a step never rewrites cached positions
     below a slot's committed position, and pos == prompt_len + generated - 1 (tests/test_eesd.py:145-171)."""

@@ -270,6 +270,9 @@ class LayerSkipLlama:
         self.native: Optional[_lsk.NativeModel] = None
         self._ws: Optional[Tensor] = None
         self._bufs: dict = {}
+        # bumped whenever a reusable device buffer, the cache or the native handle is (re)allocated: captured
+        # step graphs hold their addresses and are dropped when it changes
+        self.buf_epoch = 0
 
     # ---------------------------------------------------------------- construction
     @classmethod
@@ -347,6 +350,7 @@ class LayerSkipLlama:
             self.rope_cos, self.rope_sin = build_rope_cache(self.cfg, max_seq, self.device)
         self.cache = None
         self.native = None
+        self.buf_epoch += 1
         self.cache = KVCache(self.cfg, max_batch, max_seq, self.dtype, self.device)
         c = self.cfg
         self.native = _lsk.NativeModel(self.dtype, c.n_layers, c.dim, c.n_heads, c.n_kv_heads, c.head_dim,
@@ -357,12 +361,14 @@ class LayerSkipLlama:
     def free_cache(self) -> None:
         self.cache = None
         self.native = None
+        self.buf_epoch += 1
         torch.cuda.empty_cache()
 
     # ---------------------------------------------------------------- scratch
     def workspace(self, nbytes: int) -> Tensor:
         if self._ws is None or self._ws.numel() < nbytes:
             self._ws = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=self.device)
+            self.buf_epoch += 1
         return self._ws
 
     def buffer(self, name: str, shape: tuple, dtype) -> Tensor:
@@ -372,6 +378,7 @@ class LayerSkipLlama:
         if b is None or b.numel() < n:
             b = torch.empty(max(n, 1), dtype=dtype, device=self.device)
             self._bufs[(name, dtype)] = b
+            self.buf_epoch += 1
         return b[:n].view(shape)
 
     # ---------------------------------------------------------------- building blocks

@@ -43,6 +43,7 @@ from .packed import Block, build_packed, build_packed_arrays, packed_layers, upl
 from .exit_select import ExitController
 from .prefill import M3Planner
 from .schedulers import make_scheduler
+from .step_graph import ShallowGraphs
 
 FREE, PREFILL, DECODE = 0, 1, 2
 
@@ -53,8 +54,8 @@ class EngineConfig:
     sched: str = "fixed"            # fixed | aspire | m1 | fsm-sync | aspire-fsm
     gamma: int = 4
     k: int = 3
-    exit: str = "fixed"             # fixed (m2: not built)
-    prefill: str = "separate"       # separate (m3: not built)
+    exit: str = "fixed"             # fixed | m2
+    prefill: str = "separate"       # separate | m3
     d_max: int = 16
     sla_steps: int = 32
     initial_draft: int = 3
@@ -72,6 +73,7 @@ class EngineConfig:
     m2_force: Optional[str] = None
     forced_accept_p: Optional[float] = None
     forced_seed: int = 0
+    graphs: bool = True             # replay fixed-shape shallow steps as captured HIP graphs
 
     def label(self) -> str:
         if self.mode == "ar":
@@ -168,6 +170,7 @@ class EESDEngine:
         self.m3 = M3Planner(cost_model, cfg.max_wait, cfg.m3_chunk_cap, cfg.prefill_chunk,
                             cfg.knee_safety) if cfg.prefill == "m3" else None
         self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
+        self.graphs = ShallowGraphs(self.dev) if cfg.graphs and cfg.mode == "spec" else None
         self._keys = 0
         self.measuring = False
         self.stats = {"steps": 0, "deep_steps": 0, "probe_steps": 0, "deep_tokens": 0, "verifiers": 0, "drafted": 0,
@@ -325,6 +328,7 @@ class EESDEngine:
         # verifier), plus the M3 chunks
         dslots = np.flatnonzero(dec)
         chunk_slices = []
+        gentry = None
         if not probe and not chunks:
             # every block is one token at pos + d: token j <-> packed block j
             if len(dslots) == 0:
@@ -338,7 +342,13 @@ class EESDEngine:
             drf_src = np.flatnonzero(Dr[sl])
             drf_dst = sel[drf_src] + 1
             nd, nex = len(drf_src), N
-            pb.meta, sel_t, drf_src_t, drf_dst_t = upload_many([pb.meta_host, sel, drf_src, drf_dst], self.dev)
+            if not deep and self.graphs is not None and not _lsk.Profiler.enabled:
+                # shallow-only step of a fixed shape: staged at fixed addresses, replayed as a graph below
+                gkey = (N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_items, pb.n_slots, nd, k)
+                (pb.meta, sel_t, drf_src_t, drf_dst_t), gentry = self.graphs.stage(
+                    gkey, [pb.meta_host, sel, drf_src, drf_dst])
+            else:
+                pb.meta, sel_t, drf_src_t, drf_dst_t = upload_many([pb.meta_host, sel, drf_src, drf_dst], self.dev)
             alt_t, ex_dst_t, ex_src_t = sel_t, sel_t, None
         else:
             full = V[dslots] if probe else np.zeros(len(dslots), dtype=bool)
@@ -372,6 +382,26 @@ class EESDEngine:
         self._kv(pb, k)
         sb, exh = self._flat()
         iv = Interval(self.dev).start()
+        if gentry is not None:
+            def shallow_gpu():
+                xg = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+                _lsk.embed(m.embed_w, sel_t, xg, sb, sel_t)
+                hg = packed_layers(m, xg, pb, 0, k)
+                _lsk.copy_rows(exh, sel_t, hg, None, N)
+                if nd:
+                    hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
+                    _lsk.copy_rows(hx, None, hg, drf_src_t, nd)
+                    m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)
+            self.graphs.run(gentry, lambda: m.buf_epoch, shallow_gpu)
+            iv.stop()
+            self._rec("shallow", iv, n_sh=N, n_dp=0, n_chunk=0, plan_ms=plan_ms)
+            self.d[Dr] += 1
+            if self.trace is not None:
+                self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
+                                   "n_draft": nd, "dp": [], "committed": 0})
+            self.steps_since_deep += 1
+            self._account(0, deep=False, plan_ms=plan_ms)
+            return 0, []
         x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
         _lsk.embed(m.embed_w, alt_t, x, sb, sel_t)                        # seq_buf ids, or prompt ids for chunks
         cap_sh = {} if probe else None
