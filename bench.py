@@ -243,12 +243,12 @@ def run_attention_bench(args):
     kv_len = torch.from_numpy(ctx.copy()).to(dev)
 
     n_slots = _lsk.cu_count(dev)
-    sched, slot_off = _lsk.attn_schedule(works, Hkv, n_slots)
-    sched_d, slot_d = torch.from_numpy(sched).to(dev), torch.from_numpy(slot_off).to(dev)
+    recs, n_rounds = _lsk.attn_schedule(works, Hkv, n_slots)
+    recs_d = torch.from_numpy(recs).to(dev)
 
     def attn():
         _lsk.ragged_attn(q, kc, vc, blk_d, wk_d, len(works), gr_d, len(groups), n_parts, out, Hq,
-                         1.0 / math.sqrt(D), ws, sched_d, slot_d, n_slots)
+                         1.0 / math.sqrt(D), ws, recs_d, n_rounds, n_slots)
 
     def timed(fn, iters):
         for _ in range(5):

@@ -13,7 +13,11 @@
 //   out    [N, Hq * D]
 //   blocks int32 [nb][4] = {q_start, pos0, T, row}
 //   works  int32 [n_work][8] = {q_start, row0, nrows, kv_lo, kv_hi, part, pos0, row} (the block's fields
-//                                 copied in, so a workgroup reads one record before its first load)
+//                                 copied in; the fp32 kernel reads them directly)
+//   recs   int32 [n_slots][n_rounds][8]: the bf16 kernel's static schedule, one record per (work, KV head)
+//                                 = the work record with nrows | kvh << 8 in field 2; slot s runs its records
+//                                 in order and stops at the first with nrows = 0, so a workgroup's first
+//                                 load depends on nothing but its own index
 //   groups int32 [n_group][8] = {blk, row0, nrows, part_first, n_split, 0, 0, 0}
 // The G query heads of a KV head are folded into query rows: row = t * G + g (t = token of the
 // block, g = head within the group); a workgroup serves 16 rows, so one KV read serves G*T <= 16 rows.
@@ -56,9 +60,8 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 template <int D>
 __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
-    const int32_t* __restrict__ works, const int32_t* __restrict__ sched, const int32_t* __restrict__ slot_off,
-    uint16_t* __restrict__ out, float* __restrict__ o_part, float* __restrict__ ml_part, int G, int Hkv, int S,
-    float scale_log2) {
+    const int32_t* __restrict__ recs, int n_rounds, uint16_t* __restrict__ out, float* __restrict__ o_part,
+    float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
   constexpr int KSTEPS = D / 32;
   constexpr int CT = D / 16;
   constexpr int NW = ATTN_WAVES;
@@ -69,19 +72,21 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l16 = lane & 15, lg = lane >> 4;
   const int Hq = Hkv * G;
-  const int i_beg = slot_off[blockIdx.x], i_end = slot_off[blockIdx.x + 1];
-  if (i_beg >= i_end) return;
+  const int32_t* my_recs = recs + (long)blockIdx.x * n_rounds * 8;
 
   struct Item {
     int q_start, row0, nrows, kv_lo, kv_hi, part, pos0, crow, kvh;
   };
-  auto fetch = [&](int i) {
-    const int id = sched[i];
-    const int wi = id / Hkv;
-    const int32_t* wk = works + (long)wi * 8;
+  // record r of this slot (nrows = 0 past the slot's last item)
+  auto fetch = [&](int r) {
     Item it;
-    it.q_start = wk[0]; it.row0 = wk[1]; it.nrows = wk[2]; it.kv_lo = wk[3]; it.kv_hi = wk[4]; it.part = wk[5];
-    it.pos0 = wk[6]; it.crow = wk[7]; it.kvh = id - wi * Hkv;
+    if (r >= n_rounds) {
+      it.nrows = 0;
+      return it;
+    }
+    const int32_t* wk = my_recs + (long)r * 8;
+    it.q_start = wk[0]; it.row0 = wk[1]; it.nrows = wk[2] & 255; it.kvh = wk[2] >> 8; it.kv_lo = wk[3];
+    it.kv_hi = wk[4]; it.part = wk[5]; it.pos0 = wk[6]; it.crow = wk[7];
     return it;
   };
   auto kbase_of = [&](const Item& it) { return kc + ((long)it.crow * Hkv + it.kvh) * (long)S * D; };
@@ -129,9 +134,11 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     }
   };
 
-  Item cur = fetch(i_beg);
+  Item cur = fetch(0);
+  if (cur.nrows == 0) return;
   issue_first(cur);
-  for (int i = i_beg; i < i_end; ++i) {
+  Item nxt = fetch(1);  // the next record is read while this item streams
+  for (int r = 0; cur.nrows > 0; ++r) {
     const int nq = (cur.nrows + 15) >> 4;  // column tiles in use (wave-uniform)
     const int kv_hi = cur.kv_hi;
     const uint16_t* kb = kbase_of(cur);
@@ -219,9 +226,10 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     }
     // the next item's Q and first K / V loads fly while this item is merged
     const Item done = cur;
-    if (i + 1 < i_end) {
-      cur = fetch(i + 1);
+    cur = nxt;
+    if (cur.nrows > 0) {
       issue_first(cur);
+      nxt = fetch(r + 2);
     }
     // ---- merge the waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
 #pragma unroll
@@ -485,25 +493,26 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
   return 0;
 }
 
-// Static schedule of a plan over n_slots persistent workgroups (one per CU): items are (work, KV head)
-// pairs of non-padding works, costed by their KV steps per wave plus a fixed per-item overhead, and dealt
-// longest first to the least-loaded slot (ties: lowest slot; equal costs keep plan order).  Output:
-// sched[] = work * n_kv_heads + head, grouped by slot in processing order; slot_off[s] .. slot_off[s + 1]
-// are slot s's items.  Which workgroup computes an item never changes its result.
-extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* sched,
-                                 int max_items, int32_t* slot_off, int* n_items) {
-  LSK_REQUIRE(works && sched && slot_off && n_items, LSK_EARG, "lsk_attn_schedule: null pointer");
-  LSK_REQUIRE(n_works >= 0 && n_kv_heads > 0 && n_slots > 0, LSK_ESHAPE, "lsk_attn_schedule: bad arguments");
+// Static schedule of a plan over n_slots persistent workgroups (one per CU): items are (work, KV head) pairs
+// of non-padding works, costed by their KV steps per wave plus a fixed per-item overhead, and dealt longest
+// first to the least-loaded slot (ties: lowest slot; equal costs keep plan order).  Output: records
+// recs[slot][round][8] (the work record with nrows | kvh << 8 in field 2), each slot's items in processing
+// order from round 0, padded with nrows = 0 records up to n_rounds = the largest item count of a slot.
+// With recs == NULL only n_rounds is computed.  Which workgroup computes an item never changes its result.
+extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* recs,
+                                 int max_recs, int* n_rounds) {
+  LSK_REQUIRE(n_rounds && (works || n_works == 0), LSK_EARG, "lsk_attn_schedule: null pointer");
+  LSK_REQUIRE(n_works >= 0 && n_kv_heads > 0 && n_kv_heads < (1 << 23) && n_slots > 0, LSK_ESHAPE,
+              "lsk_attn_schedule: bad arguments");
   struct It { int id, cost; };
   std::vector<It> items;
   for (int w = 0; w < n_works; ++w) {
     const int32_t* wp = works + (long)w * 8;
     if (wp[2] <= 0) continue;
+    LSK_REQUIRE(wp[2] <= ATTN_ROWS, LSK_ESHAPE, "lsk_attn_schedule: work %d has %d rows", w, wp[2]);
     const int steps = (wp[4] - wp[3] + ATTN_STEP * ATTN_WAVES - 1) / (ATTN_STEP * ATTN_WAVES);
     for (int h = 0; h < n_kv_heads; ++h) items.push_back({w * n_kv_heads + h, steps + 2});
   }
-  LSK_REQUIRE((int)items.size() <= max_items, LSK_EWORKSPACE, "lsk_attn_schedule: %zu items > %d", items.size(),
-              max_items);
   std::stable_sort(items.begin(), items.end(), [](const It& a, const It& b) { return a.cost > b.cost; });
   // min-heap of (load, slot)
   std::vector<std::pair<long, int>> heap;
@@ -521,13 +530,24 @@ extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_hea
     top.first += it.cost;
     std::push_heap(heap.begin(), heap.end(), cmp);
   }
-  int k = 0;
-  for (int sl = 0; sl < n_slots; ++sl) {
-    slot_off[sl] = k;
-    for (int id : per[sl]) sched[k++] = id;
-  }
-  slot_off[n_slots] = k;
-  *n_items = k;
+  int R = 0;
+  for (int sl = 0; sl < n_slots; ++sl) R = (int)per[sl].size() > R ? (int)per[sl].size() : R;
+  *n_rounds = R;
+  if (recs == nullptr) return 0;
+  LSK_REQUIRE((long)n_slots * R <= max_recs, LSK_EWORKSPACE, "lsk_attn_schedule: %ld records > %d",
+              (long)n_slots * R, max_recs);
+  for (int sl = 0; sl < n_slots; ++sl)
+    for (int r = 0; r < R; ++r) {
+      int32_t* rp = recs + ((long)sl * R + r) * 8;
+      if (r < (int)per[sl].size()) {
+        const int id = per[sl][r], w = id / n_kv_heads, h = id - w * n_kv_heads;
+        const int32_t* wp = works + (long)w * 8;
+        rp[0] = wp[0]; rp[1] = wp[1]; rp[2] = wp[2] | (h << 8); rp[3] = wp[3];
+        rp[4] = wp[4]; rp[5] = wp[5]; rp[6] = wp[6]; rp[7] = wp[7];
+      } else {
+        for (int f = 0; f < 8; ++f) rp[f] = 0;
+      }
+    }
   return 0;
 }
 
@@ -539,11 +559,11 @@ extern "C" size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head
 
 extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache,
                                const int32_t* blocks, const int32_t* works, int n_works, const int32_t* groups,
-                               int n_groups, int n_parts, const int32_t* sched, const int32_t* slot_off, int n_slots,
-                               void* out, int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale,
-                               void* workspace, size_t ws_bytes, void* stream) {
+                               int n_groups, int n_parts, const int32_t* recs, int n_rounds, int n_slots, void* out,
+                               int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
+                               size_t ws_bytes, void* stream) {
   LSK_REQUIRE(q && kcache && vcache && blocks && works && out, LSK_EARG, "lsk_ragged_attn: null pointer");
-  LSK_REQUIRE(dtype != LSK_DTYPE_BF16 || n_works == 0 || (sched && slot_off && n_slots > 0), LSK_EARG,
+  LSK_REQUIRE(dtype != LSK_DTYPE_BF16 || n_works == 0 || (recs && n_rounds > 0 && n_slots > 0), LSK_EARG,
               "lsk_ragged_attn: the bf16 path needs a schedule (lsk_attn_schedule)");
   LSK_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && max_seq > 0 && n_works >= 0,
               LSK_ESHAPE, "lsk_ragged_attn: bad shape");
@@ -569,12 +589,12 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
     const dim3 pgrid(n_slots);
     if (head_dim == 128)
       attn_bf16_kernel<128><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                              (const uint16_t*)vcache, works, sched, slot_off,
+                                                              (const uint16_t*)vcache, recs, n_rounds,
                                                               (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
                                                               max_seq, scale_log2);
     else
       attn_bf16_kernel<64><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                             (const uint16_t*)vcache, works, sched, slot_off,
+                                                             (const uint16_t*)vcache, recs, n_rounds,
                                                              (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
                                                              max_seq, scale_log2);
     int rc = lsk_check_launch("lsk_ragged_attn");

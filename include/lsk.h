@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 3
+#define LSK_ABI_VERSION 4
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -39,8 +39,8 @@ int lsk_abi_version(void);
 int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, int n_rows, int dim, float eps, long ldx,
                 long ldo, void* stream);
 
-/* RoPE of q and k + KV append: qkv [N, (Hq+2Hkv)D] -> q_out [N, Hq, D], k into the K cache
- * [B, Hkv, S, D] and v into the V cache at (rows[t], pos[t]).  The V cache is stored in 32-position blocks,
+/* RoPE of q and k + KV append: qkv [N, (Hq+2Hkv)D] -> q_out [N, Hq, D], k into the K cache (bf16
+ * fragment-major [B, Hkv, S/32, D/16, 64, 8], fp32 [B, Hkv, S, D]) and v into the V cache at (rows[t], pos[t]).  The V cache is stored in 32-position blocks,
  * each block transposed: [B, Hkv, S/32, D, 32] (S a multiple of 64).  cos/sin tables: fp32 [tab_len, D] (device).
  * Replaces solutions/packed.py:176-181 (split, apply_rope, cache index_put) with
  * common/model.py:143-150 (apply_rope) and solutions/packed.py:106-107 (cos/sin gather + cast). */
@@ -49,8 +49,8 @@ int lsk_rope_append(int dtype, const void* qkv, void* q_out, void* kcache, void*
                     int n_heads, int n_kv_heads, int head_dim, int max_batch, int max_seq, void* stream);
 
 /* KV append without RoPE: kcache[rows[t], :, pos[t]] = k[t]; V cache (rows[t], :, pos[t]) = v[t]
- * (K [B, Hkv, S, D], V blocked-transposed [B, Hkv, S/32, D, 32]).
- * Replaces solutions/packed.py:180-181 and common/model.py:343-344. */
+ * (K: bf16 fragment-major [B, Hkv, S/32, D/16, 64, 8] / fp32 [B, Hkv, S, D]; V blocked-transposed
+ * [B, Hkv, S/32, D, 32]).  Replaces solutions/packed.py:180-181 and common/model.py:343-344. */
 int lsk_kv_append(int dtype, const void* k, const void* v, void* kcache, void* vcache, const int32_t* rows,
                   const int32_t* pos, int n_tokens, int n_kv_heads, int head_dim, int max_batch, int max_seq,
                   void* stream);
@@ -64,24 +64,27 @@ int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* 
                   int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts);
 
 /* Static schedule of a plan's (work, KV head) items over n_slots persistent workgroups (host pointers):
- * longest first to the least-loaded slot.  sched[] = work * n_kv_heads + head grouped by slot,
- * slot_off [n_slots + 1].  Has no reference counterpart (the reference runs one SDPA per bucket); it
- * only decides which workgroup computes an item, never the result. */
-int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* sched, int max_items,
-                      int32_t* slot_off, int* n_items);
+ * longest first to the least-loaded slot.  Writes recs int32 [n_slots][n_rounds][8]: slot s's items in
+ * processing order from round 0, each the work record with field 2 = nrows | kv_head << 8, padded with
+ * all-zero records; n_rounds = the largest item count of a slot (recs == NULL: only n_rounds is written).
+ * max_recs = capacity in records.  Has no reference counterpart (the reference runs one SDPA per bucket);
+ * it only decides which workgroup computes an item, never the result. */
+int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* recs, int max_recs,
+                      int* n_rounds);
 
 /* Workspace bytes for the split partials of a plan with n_parts partial slots. */
 size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
 
 /* Ragged verify/decode attention: a query at position p of row r attends cache[r, :, 0..p].
- * q [N, Hq, D], K [B, Hkv, S, D], V blocked-transposed [B, Hkv, S/32, D, 32], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
+ * q [N, Hq, D], K: bf16 fragment-major [B, Hkv, S/32, D/16, 64, 8] / fp32 [B, Hkv, S, D],
+ * V blocked-transposed [B, Hkv, S/32, D, 32], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
+ * bf16 runs n_slots persistent workgroups over the schedule records (recs, n_rounds); fp32 reads works.
  * Replaces solutions/packed.py:142-166 (_attend: per-bucket gather + masked SDPA + scatter)
  * and common/model.py:352-364 (the padded path's masked SDPA). */
 int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
                     const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
-                    const int32_t* sched, const int32_t* slot_off, int n_slots, void* out, int n_heads,
-                    int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes,
-                    void* stream);
+                    const int32_t* recs, int n_rounds, int n_slots, void* out, int n_heads, int n_kv_heads,
+                    int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes, void* stream);
 
 /* bf16 weight storage of the GEMMs: W [N, K] row-major (ldw) <-> fragment-major Wp (N*K elements, no
  * padding): fragment (g, j) = rows 16g..16g+15 x k 32j..32j+31 is 1 KiB, lane l's 8 elements being
@@ -180,12 +183,12 @@ int lsk_model_destroy(long handle);
 size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts);
 
 /* Layers [start, end) over n_tokens packed tokens: x_out = layers(x_in) (x_in is not modified).
- * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8][sched n_items]
- * [slot_off n_slots+1] (see lsk_attn_plan, lsk_attn_schedule).
+ * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8]
+ * [recs n_slots*n_rounds*8] (see lsk_attn_plan, lsk_attn_schedule).
  * capture: NULL or a host array of n_layers device pointers; capture[i] != NULL receives layer i's output
  * (solutions/packed.py:190-195).  Replaces packed_layers (solutions/packed.py:188-196). */
 int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
-                       const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, int n_items, int n_slots,
+                       const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, int n_rounds, int n_slots,
                        void* workspace, size_t ws_bytes, void* const* capture, double attn_bytes, double attn_flops,
                        void* stream);
 

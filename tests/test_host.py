@@ -59,8 +59,8 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_pack_weight(8, 64, 16, 40, 64, None) == -2                          # N % 16 != 0
     assert lib.lsk_unpack_weight(8, 16, 64, 64, 48, None) == -2                        # K % 32 != 0
     assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
-    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 8, 1, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
-    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, None, 0, 8, 32, 8, 128, 64, 0.1, None, 0,
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, 0, 0, 8, 32, 8, 128, 64, 0.1, None, 0,
                                None) == -1                                            # bf16 without a schedule
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
 
@@ -132,16 +132,32 @@ def test_attention_schedule_covers_every_item_once_longest_first(n_slots):
     blocks = np.stack([np.concatenate([[0], np.cumsum(T)[:-1]]), pos0, T, rng.integers(0, 8, nb)], axis=1)
     works, _, _ = _plan(blocks, 4, 4096)
     Hkv = 8
-    sched, slot_off = lsk.attn_schedule(works, Hkv, n_slots)
+    recs, R = lsk.attn_schedule(works, Hkv, n_slots)
+    recs = recs.reshape(n_slots, R, 8)
     real = [w for w in range(len(works)) if works[w][2] > 0]
-    assert sorted(sched.tolist()) == sorted(w * Hkv + h for w in real for h in range(Hkv))
-    assert slot_off[0] == 0 and slot_off[-1] == len(sched) and (np.diff(slot_off) >= 0).all()
+    per_slot = []
+    for sl in range(n_slots):
+        ids = []
+        for r in range(R):
+            rec = recs[sl, r]
+            if rec[2] & 255 == 0:
+                assert not rec.any() and not recs[sl, r:].any()      # padding only after the slot's items
+                break
+            kvh = rec[2] >> 8
+            # the record is the work record with the KV head folded into field 2
+            w = next(i for i in real if np.array_equal(np.delete(works[i], 2), np.delete(rec, 2))
+                     and works[i][2] == rec[2] & 255)
+            ids.append(w * Hkv + kvh)
+        per_slot.append(ids)
+    assert max(len(x) for x in per_slot) == R
+    flat = [i for x in per_slot for i in x]
+    assert sorted(flat) == sorted(w * Hkv + h for w in real for h in range(Hkv))
     cost = lambda i: -(-(works[i // Hkv][4] - works[i // Hkv][3]) // 256) + 2  # noqa: E731
-    loads = [sum(cost(i) for i in sched[slot_off[s]:slot_off[s + 1]]) for s in range(n_slots)]
+    loads = [sum(cost(i) for i in x) for x in per_slot]
     # greedy longest-first bound: no slot exceeds the mean by more than the largest item
-    assert max(loads) <= sum(loads) / n_slots + max(cost(i) for i in sched)
-    again, off2 = lsk.attn_schedule(works, Hkv, n_slots)
-    assert np.array_equal(again, sched) and np.array_equal(off2, slot_off)   # deterministic
+    assert max(loads) <= sum(loads) / n_slots + max(cost(i) for i in flat)
+    again, R2 = lsk.attn_schedule(works, Hkv, n_slots)
+    assert R2 == R and np.array_equal(again.reshape(n_slots, R, 8), recs)   # deterministic
 
 
 def test_attention_plan_places_sibling_tiles_eight_slots_apart():
@@ -255,10 +271,12 @@ def test_packed_metadata_layout():
     assert meta[:N].tolist() == pb.rows_h.tolist() and meta[N:2 * N].tolist() == pb.pos_h.tolist()
     blk = meta[2 * N:2 * N + 4 * pb.nb].reshape(-1, 4)
     assert blk.tolist() == [[0, 700, 1, 1], [1, 10, 2, 3]]
-    assert meta.size == 2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups) + pb.n_items + pb.n_slots + 1
-    assert pb.n_items == 2 * 1                                       # (work, KV head) pairs: 2 works x 1 head
-    tail = meta[2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups):]
-    assert sorted(tail[:pb.n_items].tolist()) == [0, 1] and tail[pb.n_items + pb.n_slots] == pb.n_items
+    assert meta.size == 2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups) + 8 * pb.n_slots * pb.n_rounds
+    assert pb.n_rounds == 1 and pb.n_slots >= 2                      # 2 (work, KV head) items over the slots
+    works = meta[2 * N + 4 * pb.nb:2 * N + 4 * pb.nb + 8 * pb.n_works].reshape(-1, 8)
+    recs = meta[2 * N + 4 * pb.nb + 8 * (pb.n_works + pb.n_groups):].reshape(pb.n_slots, pb.n_rounds, 8)
+    live = recs[recs[:, 0, 2] != 0, 0]
+    assert sorted(map(tuple, live.tolist())) == sorted(map(tuple, works[works[:, 2] > 0].tolist()))  # kvh = 0
     # algorithmic attention work of one launch: K+V of every attended position, Q read and O written
     assert pb.attn_bytes == (701 + 12) * 1 * 128 * 2 * 2 + N * 4 * 128 * 2 * 2
 

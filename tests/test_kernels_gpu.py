@@ -239,11 +239,10 @@ def _run_attn(lsk, cuda, q, kc, vc, tab, split):
     ws = torch.empty(max(lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=cuda)
     gdev = torch.from_numpy(groups).to(cuda) if len(groups) else None
     n_slots = lsk.cu_count(cuda)
-    sched, slot_off = lsk.attn_schedule(works, Hkv, n_slots)
+    recs, n_rounds = lsk.attn_schedule(works, Hkv, n_slots)
     lsk.ragged_attn(q.to(cuda), _kstore(lsk, kc).to(cuda), lsk.v_to_blocked(vc).to(cuda), torch.from_numpy(tab).to(cuda),
                     torch.from_numpy(works).to(cuda), len(works), gdev, len(groups), n_parts, out, Hq,
-                    1.0 / math.sqrt(D), ws, torch.from_numpy(sched).to(cuda), torch.from_numpy(slot_off).to(cuda),
-                    n_slots)
+                    1.0 / math.sqrt(D), ws, torch.from_numpy(recs).to(cuda), n_rounds, n_slots)
     return out.cpu()
 
 

@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 32            # query rows per attention work item
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -32,9 +32,9 @@ _SIGS = {
     "lsk_rope_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lsk_kv_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
-    "lsk_attn_schedule": (_I, [_P, _I, _I, _I, _P, _I, _P, _P]),
+    "lsk_attn_schedule": (_I, [_P, _I, _I, _I, _P, _I, _P]),
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
-    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _P, _I, _P, _I, _I, _I, _I, _F, _P, _Z,
+    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z,
                              _P]),
     "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
     "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
@@ -305,16 +305,16 @@ def cu_count(device) -> int:
 
 def attn_schedule(works: np.ndarray, n_kv_heads: int, n_slots: int):
     """Static longest-first schedule of (work, KV head) items over n_slots persistent workgroups
-    -> (sched int32 [n_items], slot_off int32 [n_slots + 1])."""
+    -> (recs int32 [n_slots * n_rounds * 8], n_rounds): slot s's records are recs[s * n_rounds * 8 ...]."""
     works = np.ascontiguousarray(works, dtype=np.int32)
-    max_items = max(1, len(works) * n_kv_heads)
-    sched = np.zeros(max_items, dtype=np.int32)
-    slot_off = np.zeros(n_slots + 1, dtype=np.int32)
-    n = ctypes.c_int(0)
-    _check(load().lsk_attn_schedule(works.ctypes.data if len(works) else None, len(works), n_kv_heads, n_slots,
-                                    sched.ctypes.data, max_items, slot_off.ctypes.data, ctypes.byref(n)),
-           "lsk_attn_schedule")
-    return sched[:n.value], slot_off
+    lib = load()
+    wp = works.ctypes.data if len(works) else None
+    R = ctypes.c_int(0)
+    _check(lib.lsk_attn_schedule(wp, len(works), n_kv_heads, n_slots, None, 0, ctypes.byref(R)), "lsk_attn_schedule")
+    recs = np.zeros(max(n_slots * R.value * 8, 8), dtype=np.int32)
+    _check(lib.lsk_attn_schedule(wp, len(works), n_kv_heads, n_slots, recs.ctypes.data, n_slots * R.value,
+                                 ctypes.byref(R)), "lsk_attn_schedule")
+    return recs[:n_slots * R.value * 8], R.value
 
 
 def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
@@ -322,7 +322,7 @@ def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
 
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
-                scale, workspace=None, sched_dev=None, slot_off_dev=None, n_slots=0):
+                scale, workspace=None, recs_dev=None, n_rounds=0, n_slots=0):
     """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
     _check_kcache(q.dtype, kcache)
@@ -331,8 +331,8 @@ def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n
     B, Hkv, S, D = k_dims(kcache)
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
-                                  _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(sched_dev),
-                                  _ptr(slot_off_dev), n_slots, _ptr(out), n_heads, Hkv, D, S, float(scale),
+                                  _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(recs_dev),
+                                  n_rounds, n_slots, _ptr(out), n_heads, Hkv, D, S, float(scale),
                                   _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
 
 
@@ -437,13 +437,13 @@ class NativeModel:
     def workspace_bytes(self, n_tokens: int, n_parts: int) -> int:
         return int(load().lsk_segment_workspace_bytes(self.handle, n_tokens, n_parts))
 
-    def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, n_items,
+    def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, n_rounds,
                        n_slots, workspace, capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
         _dev(x_in, x_out, meta_dev, workspace)
         cap = _ptr_array(capture_ptrs) if capture_ptrs is not None else None
         ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
         _check(load().lsk_forward_layers(self.handle, _ptr(x_in), _ptr(x_out), n_tokens, start, end, _ptr(meta_dev),
-                                         nb, n_works, n_groups, n_parts, n_items, n_slots, _ptr(workspace), ws_bytes,
+                                         nb, n_works, n_groups, n_parts, n_rounds, n_slots, _ptr(workspace), ws_bytes,
                                          cap,
                                          float(attn_bytes), float(attn_flops), _stream()),
                "lsk_forward_layers")

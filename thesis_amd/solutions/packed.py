@@ -99,15 +99,15 @@ class PackedBatch:
     kv_read: int = 0
     kv_read_padded: int = 0
     kv_gathered: int = 0
-    # kernel metadata (device int32): [rows N][pos N][blocks nb*4][works nw*8][groups ng*8][sched n_items]
-    # [slot_off n_slots+1]
+    # kernel metadata (device int32): [rows N][pos N][blocks nb*4][works nw*8][groups ng*8]
+    # [schedule records n_slots*n_rounds*8]
     meta: Optional[torch.Tensor] = None
     meta_host: Optional[np.ndarray] = None
     nb: int = 0
     n_works: int = 0
     n_groups: int = 0
     n_parts: int = 0
-    n_items: int = 0
+    n_rounds: int = 0
     n_slots: int = 0
     attn_bytes: float = 0.0
     attn_flops: float = 0.0
@@ -206,11 +206,11 @@ def _pack(model, rws: np.ndarray, pos0: np.ndarray, Ts: np.ndarray, bounds: np.n
     split = model.cache.attn_split
     works, grps, n_parts = _lsk.attn_plan(blk, model.group, split) if nb else (np.zeros((0, 8), np.int32),) * 2 + (0,)
     n_slots = _lsk.cu_count(model.device)
-    sched, slot_off = _lsk.attn_schedule(works, model.cfg.n_kv_heads, n_slots)
+    recs, n_rounds = _lsk.attn_schedule(works, model.cfg.n_kv_heads, n_slots)
     meta = np.concatenate([rows_h.astype(np.int32), pos_h.astype(np.int32), blk.ravel(), works.ravel(),
-                           grps.ravel(), sched, slot_off]).astype(np.int32)
+                           grps.ravel(), recs]).astype(np.int32)
     pb = PackedBatch(offsets, pos_h, rows_h, rws, pos0, Ts, n_tokens=N, nb=nb, n_works=len(works),
-                     n_groups=len(grps), n_parts=n_parts, n_items=len(sched), n_slots=n_slots, _model=model,
+                     n_groups=len(grps), n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots, _model=model,
                      meta_host=meta)
     # algorithmic work of one attention launch (per layer): K+V of every attended position read once per
     # (block, KV head), Q read and O written once; flops = 4 Hq D per (query, attended position)
@@ -303,7 +303,7 @@ def packed_layers(model, x: torch.Tensor, pb: PackedBatch, start: int, end: int,
                     cap_ptrs[k - 1] = t.data_ptr()
     ws = model.workspace(model.native.workspace_bytes(N, pb.n_parts))
     model.native.forward_layers(x, out, N, start, end, pb.meta, pb.nb, pb.n_works, pb.n_groups, pb.n_parts,
-                                pb.n_items, pb.n_slots, ws, cap_ptrs, pb.attn_bytes, pb.attn_flops)
+                                pb.n_rounds, pb.n_slots, ws, cap_ptrs, pb.attn_bytes, pb.attn_flops)
     return out
 
 
