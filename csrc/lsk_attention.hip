@@ -404,17 +404,20 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
 
 // ----------------------------------------------------------------------------- host planner
 
-// Work order: a "family" is the set of 16-row query tiles of one (block, split); its tiles read the same
-// K/V.  Workgroups are dealt to the 8 XCDs round robin by launch index, so siblings are placed 8 launch
-// slots apart (same XCD, dispatched together: the second read hits that XCD's L2).  Families are sorted
-// by size and dealt in chunks of 8; slots of shorter families in a chunk are padding items (nrows = 0).
-extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
-                             int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts) {
-  LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
+// Work order: a "family" is the set of query tiles of one (block, split); its tiles read the same K/V.
+// Families are sorted by size and dealt in chunks of 8 launch slots; slots of shorter families in a chunk are
+// padding items (nrows = 0), so sibling tiles sit 8 slots apart.  Output appended to `works` / `groups`.
+static int plan_into(const int32_t* blocks, int nb, int group, int split, std::vector<int32_t>& works,
+                     std::vector<int32_t>& groups, int* n_parts) {
   LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && split % ATTN_TILE == 0, LSK_ESHAPE,
               "lsk_attn_plan: bad arguments (split must be a positive multiple of %d)", ATTN_TILE);
   struct Item { int b, row0, nrows, lo, hi, part; };  // b: block index (its fields are copied into the record)
-  std::vector<std::vector<Item>> fams;
+  thread_local std::vector<Item> items;               // families back to back
+  thread_local std::vector<int> fam_off, fam_order, part_first, ns_of;
+  items.clear();
+  fam_off.clear();
+  works.clear();
+  groups.clear();
   int ng = 0, np = 0;
   for (int b = 0; b < nb; ++b) {
     const int pos0 = blocks[b * 4 + 1], T = blocks[b * 4 + 2];
@@ -423,23 +426,24 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
     const int nq = (rows + ATTN_ROWS - 1) / ATTN_ROWS;
     if (nq == 0) continue;
     // KV range of the family = the longest tile's range; each tile uses its own end
-    std::vector<int> ns_of(nq);
     int ns_max = 0;
     for (int qt = 0; qt < nq; ++qt) {
       const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
       const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
-      ns_of[qt] = (int)((kv_end + split - 1) / split);
-      LSK_REQUIRE(ns_of[qt] <= ATTN_MAX_SPLITS || split >= (1 << 29), LSK_ESHAPE,
-                  "lsk_attn_plan: %d splits of %d positions exceed %d", ns_of[qt], split, ATTN_MAX_SPLITS);
-      ns_max = ns_of[qt] > ns_max ? ns_of[qt] : ns_max;
+      const int ns = (int)((kv_end + split - 1) / split);
+      LSK_REQUIRE(ns <= ATTN_MAX_SPLITS || split >= (1 << 29), LSK_ESHAPE,
+                  "lsk_attn_plan: %d splits of %d positions exceed %d", ns, split, ATTN_MAX_SPLITS);
+      ns_max = ns > ns_max ? ns : ns_max;
     }
-    std::vector<int> part_first(nq);
+    part_first.resize(nq);
+    ns_of.resize(nq);
     for (int qt = 0; qt < nq; ++qt) {
       const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+      const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
+      ns_of[qt] = (int)((kv_end + split - 1) / split);
       if (ns_of[qt] > 1) {
-        LSK_REQUIRE(groups != nullptr && ng < max_groups, LSK_EWORKSPACE, "lsk_attn_plan: too many combine groups");
-        int32_t* gp = groups + (long)ng * 8;
-        gp[0] = b; gp[1] = row0; gp[2] = nrows; gp[3] = np; gp[4] = ns_of[qt]; gp[5] = gp[6] = gp[7] = 0;
+        const int32_t g[8] = {b, row0, nrows, np, ns_of[qt], 0, 0, 0};
+        groups.insert(groups.end(), g, g + 8);
         ++ng;
         part_first[qt] = np;
         np += ns_of[qt];
@@ -448,45 +452,61 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
       }
     }
     for (int sidx = 0; sidx < ns_max; ++sidx) {
-      std::vector<Item> fam;
+      fam_off.push_back((int)items.size());
       for (int qt = 0; qt < nq; ++qt) {
         if (sidx >= ns_of[qt]) continue;
         const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
         const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
         const long lo = (long)sidx * split;
         const long hi = (lo + split < kv_end) ? lo + split : kv_end;
-        fam.push_back({b, row0, nrows, (int)lo, (int)hi, part_first[qt] >= 0 ? part_first[qt] + sidx : -1});
+        items.push_back({b, row0, nrows, (int)lo, (int)hi, part_first[qt] >= 0 ? part_first[qt] + sidx : -1});
       }
-      fams.push_back(std::move(fam));
     }
   }
-  std::stable_sort(fams.begin(), fams.end(),
-                   [](const std::vector<Item>& a, const std::vector<Item>& b) { return a.size() > b.size(); });
-  int nw = 0;
-  auto emit = [&](const Item* it) -> int {
-    LSK_REQUIRE(nw < max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
-    int32_t* wp = works + (long)nw * 8;
+  const int nf = (int)fam_off.size();
+  fam_off.push_back((int)items.size());
+  fam_order.resize(nf);
+  for (int f = 0; f < nf; ++f) fam_order[f] = f;
+  auto fsize = [&](int f) { return fam_off[f + 1] - fam_off[f]; };
+  std::stable_sort(fam_order.begin(), fam_order.end(), [&](int a, int b) { return fsize(a) > fsize(b); });
+  auto emit = [&](const Item* it) {
+    int32_t w[8] = {0, 0, 0, 0, 0, -1, 0, 0};
     if (it) {
       const int32_t* bm = blocks + (long)it->b * 4;
-      wp[0] = bm[0]; wp[1] = it->row0; wp[2] = it->nrows; wp[3] = it->lo; wp[4] = it->hi; wp[5] = it->part;
-      wp[6] = bm[1]; wp[7] = bm[3];
-    } else {
-      wp[0] = 0; wp[1] = 0; wp[2] = 0; wp[3] = 0; wp[4] = 0; wp[5] = -1; wp[6] = 0; wp[7] = 0;
+      w[0] = bm[0]; w[1] = it->row0; w[2] = it->nrows; w[3] = it->lo; w[4] = it->hi; w[5] = it->part;
+      w[6] = bm[1]; w[7] = bm[3];
     }
-    ++nw;
-    return 0;
+    works.insert(works.end(), w, w + 8);
   };
-  for (size_t c0 = 0; c0 < fams.size(); c0 += 8) {
-    const size_t c1 = c0 + 8 < fams.size() ? c0 + 8 : fams.size();
-    size_t depth = 0;
-    for (size_t f = c0; f < c1; ++f) depth = fams[f].size() > depth ? fams[f].size() : depth;
-    for (size_t k = 0; k < depth; ++k)
-      for (size_t f = c0; f < c0 + 8; ++f) {
-        const Item* it = (f < c1 && k < fams[f].size()) ? &fams[f][k] : nullptr;
-        if (it == nullptr && (depth == 1 || f >= c1)) continue;  // no sibling to align: skip the padding
-        if (emit(it)) return LSK_EWORKSPACE;
+  for (int c0 = 0; c0 < nf; c0 += 8) {
+    const int c1 = c0 + 8 < nf ? c0 + 8 : nf;
+    int depth = 0;
+    for (int f = c0; f < c1; ++f) depth = fsize(fam_order[f]) > depth ? fsize(fam_order[f]) : depth;
+    for (int k = 0; k < depth; ++k)
+      for (int f = c0; f < c0 + 8; ++f) {
+        const bool real = f < c1 && k < fsize(fam_order[f]);
+        if (!real && (depth == 1 || f >= c1)) continue;  // no sibling to align: skip the padding
+        emit(real ? &items[fam_off[fam_order[f]] + k] : nullptr);
       }
   }
+  *n_parts = np;
+  (void)ng;
+  return 0;
+}
+
+extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
+                             int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts) {
+  LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
+  thread_local std::vector<int32_t> w, g;
+  int np = 0;
+  const int rc = plan_into(blocks, nb, group, split, w, g, &np);
+  if (rc) return rc;
+  const int nw = (int)(w.size() / 8), ng = (int)(g.size() / 8);
+  LSK_REQUIRE(nw <= max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
+  LSK_REQUIRE(ng == 0 || (groups != nullptr && ng <= max_groups), LSK_EWORKSPACE,
+              "lsk_attn_plan: too many combine groups");
+  std::copy(w.begin(), w.end(), works);
+  if (ng) std::copy(g.begin(), g.end(), groups);
   *n_works = nw;
   *n_groups = ng;
   *n_parts = np;
@@ -498,14 +518,16 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
 // first to the least-loaded slot (ties: lowest slot; equal costs keep plan order).  Output: records
 // recs[slot][round][8] (the work record with nrows | kvh << 8 in field 2), each slot's items in processing
 // order from round 0, padded with nrows = 0 records up to n_rounds = the largest item count of a slot.
-// With recs == NULL only n_rounds is computed.  Which workgroup computes an item never changes its result.
-extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* recs,
-                                 int max_recs, int* n_rounds) {
-  LSK_REQUIRE(n_rounds && (works || n_works == 0), LSK_EARG, "lsk_attn_schedule: null pointer");
+// Which workgroup computes an item never changes its result.
+static int schedule_into(const int32_t* works, int n_works, int n_kv_heads, int n_slots, std::vector<int32_t>& recs,
+                         int* n_rounds) {
   LSK_REQUIRE(n_works >= 0 && n_kv_heads > 0 && n_kv_heads < (1 << 23) && n_slots > 0, LSK_ESHAPE,
               "lsk_attn_schedule: bad arguments");
   struct It { int id, cost; };
-  std::vector<It> items;
+  thread_local std::vector<It> items;
+  thread_local std::vector<std::pair<long, int>> heap;
+  thread_local std::vector<int> slot_of, count, rank;
+  items.clear();
   for (int w = 0; w < n_works; ++w) {
     const int32_t* wp = works + (long)w * 8;
     if (wp[2] <= 0) continue;
@@ -514,40 +536,121 @@ extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_hea
     for (int h = 0; h < n_kv_heads; ++h) items.push_back({w * n_kv_heads + h, steps + 2});
   }
   std::stable_sort(items.begin(), items.end(), [](const It& a, const It& b) { return a.cost > b.cost; });
-  // min-heap of (load, slot)
-  std::vector<std::pair<long, int>> heap;
-  heap.reserve(n_slots);
+  heap.clear();
   for (int sl = 0; sl < n_slots; ++sl) heap.push_back({0, sl});
   auto cmp = [](const std::pair<long, int>& a, const std::pair<long, int>& b) {
     return a.first > b.first || (a.first == b.first && a.second > b.second);
   };
   std::make_heap(heap.begin(), heap.end(), cmp);
-  std::vector<std::vector<int>> per(n_slots);
-  for (const It& it : items) {
+  const int n = (int)items.size();
+  slot_of.resize(n);
+  rank.resize(n);
+  count.assign(n_slots, 0);
+  int R = 0;
+  for (int i = 0; i < n; ++i) {
     std::pop_heap(heap.begin(), heap.end(), cmp);
     auto& top = heap.back();
-    per[top.second].push_back(it.id);
-    top.first += it.cost;
+    slot_of[i] = top.second;
+    rank[i] = count[top.second]++;
+    R = count[top.second] > R ? count[top.second] : R;
+    top.first += items[i].cost;
     std::push_heap(heap.begin(), heap.end(), cmp);
   }
+  recs.assign((size_t)n_slots * R * 8, 0);
+  for (int i = 0; i < n; ++i) {
+    const int id = items[i].id, w = id / n_kv_heads, h = id - w * n_kv_heads;
+    const int32_t* wp = works + (long)w * 8;
+    int32_t* rp = recs.data() + ((size_t)slot_of[i] * R + rank[i]) * 8;
+    rp[0] = wp[0]; rp[1] = wp[1]; rp[2] = wp[2] | (h << 8); rp[3] = wp[3];
+    rp[4] = wp[4]; rp[5] = wp[5]; rp[6] = wp[6]; rp[7] = wp[7];
+  }
+  *n_rounds = R;
+  return 0;
+}
+
+// With recs == NULL only n_rounds is computed.
+extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* recs,
+                                 int max_recs, int* n_rounds) {
+  LSK_REQUIRE(n_rounds && (works || n_works == 0), LSK_EARG, "lsk_attn_schedule: null pointer");
+  thread_local std::vector<int32_t> r;
   int R = 0;
-  for (int sl = 0; sl < n_slots; ++sl) R = (int)per[sl].size() > R ? (int)per[sl].size() : R;
+  const int rc = schedule_into(works, n_works, n_kv_heads, n_slots, r, &R);
+  if (rc) return rc;
   *n_rounds = R;
   if (recs == nullptr) return 0;
   LSK_REQUIRE((long)n_slots * R <= max_recs, LSK_EWORKSPACE, "lsk_attn_schedule: %ld records > %d",
               (long)n_slots * R, max_recs);
-  for (int sl = 0; sl < n_slots; ++sl)
-    for (int r = 0; r < R; ++r) {
-      int32_t* rp = recs + ((long)sl * R + r) * 8;
-      if (r < (int)per[sl].size()) {
-        const int id = per[sl][r], w = id / n_kv_heads, h = id - w * n_kv_heads;
-        const int32_t* wp = works + (long)w * 8;
-        rp[0] = wp[0]; rp[1] = wp[1]; rp[2] = wp[2] | (h << 8); rp[3] = wp[3];
-        rp[4] = wp[4]; rp[5] = wp[5]; rp[6] = wp[6]; rp[7] = wp[7];
-      } else {
-        for (int f = 0; f < 8; ++f) rp[f] = 0;
-      }
+  std::copy(r.begin(), r.end(), recs);
+  return 0;
+}
+
+// One packed segment's kernel metadata from its blocks in packed order (host only; see include/lsk.h).
+extern "C" int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const int64_t* T, int nb, int group,
+                                int split, int n_kv_heads, int n_slots, int bucketing, int max_batch, int max_seq,
+                                int rope_len, int32_t* meta, long meta_cap, long* counts) {
+  LSK_REQUIRE(counts && (nb == 0 || (rows && pos0 && T)), LSK_EARG, "lsk_pack_segment: null pointer");
+  LSK_REQUIRE(nb >= 0 && (bucketing == 0 || bucketing == 1), LSK_EARG, "lsk_pack_segment: bad arguments");
+  long N = 0;
+  for (int b = 0; b < nb; ++b) {
+    LSK_REQUIRE(rows[b] >= 0 && rows[b] < max_batch, LSK_ESHAPE, "block row %ld outside the cache's %d rows",
+                (long)rows[b], max_batch);
+    LSK_REQUIRE(T[b] >= 1 && pos0[b] >= 0 && pos0[b] + T[b] <= max_seq, LSK_ESHAPE,
+                "block positions [%ld, %ld) outside max_seq=%d", (long)pos0[b], (long)(pos0[b] + T[b]), max_seq);
+    LSK_REQUIRE(pos0[b] + T[b] <= rope_len, LSK_ESHAPE, "positions beyond the RoPE table");
+    N += T[b];
+  }
+  LSK_REQUIRE(N < (1L << 30), LSK_ESHAPE, "lsk_pack_segment: %ld tokens", N);
+  thread_local std::vector<int32_t> blk, works, groups, recs;
+  blk.resize((size_t)nb * 4);
+  long off = 0;
+  for (int b = 0; b < nb; ++b) {
+    blk[b * 4 + 0] = (int32_t)off;
+    blk[b * 4 + 1] = (int32_t)pos0[b];
+    blk[b * 4 + 2] = (int32_t)T[b];
+    blk[b * 4 + 3] = (int32_t)rows[b];
+    off += T[b];
+  }
+  int np = 0, R = 0;
+  int rc = plan_into(blk.data(), nb, group, split, works, groups, &np);
+  if (rc) return rc;
+  const int nw = (int)(works.size() / 8), ng = (int)(groups.size() / 8);
+  rc = schedule_into(works.data(), nw, n_kv_heads, n_slots, recs, &R);
+  if (rc) return rc;
+  const long len = 2 * N + 4L * nb + 8L * nw + 8L * ng + (long)recs.size();
+  // reference accounting (solutions/packed.py:109-138): buckets = runs of equal T ("exact") or all blocks ("pad")
+  long kv_read = 0, kv_padded = 0, kv_gathered = 0, pairs = 0;
+  for (int a = 0; a < nb;) {
+    int e = a + 1;
+    if (bucketing == 0)
+      while (e < nb && T[e] == T[a]) ++e;
+    else
+      e = nb;
+    long mx = 0;
+    bool contiguous = true;
+    for (int j = a; j < e; ++j) {
+      mx = pos0[j] + T[j] > mx ? pos0[j] + T[j] : mx;
+      kv_read += pos0[j] + T[j];
+      contiguous = contiguous && rows[j] == rows[a] + (j - a);
     }
+    const long L = std::min((mx + 63) / 64 * 64, (long)max_seq);
+    kv_padded += (long)(e - a) * L;
+    if (!contiguous) kv_gathered += (long)(e - a) * L;
+    a = e;
+  }
+  for (int b = 0; b < nb; ++b) pairs += T[b] * pos0[b] + T[b] * (T[b] + 1) / 2;
+  counts[0] = N; counts[1] = nw; counts[2] = ng; counts[3] = np; counts[4] = R; counts[5] = len;
+  counts[6] = kv_read; counts[7] = kv_padded; counts[8] = kv_gathered; counts[9] = pairs;
+  if (meta == nullptr) return 0;
+  LSK_REQUIRE(len <= meta_cap, LSK_EWORKSPACE, "lsk_pack_segment: %ld metadata words > %ld", len, meta_cap);
+  int32_t* o = meta;
+  for (int b = 0; b < nb; ++b)
+    for (long t = 0; t < T[b]; ++t) *o++ = (int32_t)rows[b];
+  for (int b = 0; b < nb; ++b)
+    for (long t = 0; t < T[b]; ++t) *o++ = (int32_t)(pos0[b] + t);
+  o = std::copy(blk.begin(), blk.end(), o);
+  o = std::copy(works.begin(), works.end(), o);
+  o = std::copy(groups.begin(), groups.end(), o);
+  std::copy(recs.begin(), recs.end(), o);
   return 0;
 }
 

@@ -72,6 +72,19 @@ int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* 
 int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_slots, int32_t* recs, int max_recs,
                       int* n_rounds);
 
+/* One packed segment's kernel metadata in one host call (no GPU work): blocks (rows, pos0, T; int64, nb of
+ * them) already in packed order -> meta int32 [rows N][pos N][blocks nb*4][works nw*8][groups ng*8]
+ * [recs n_slots*n_rounds*8], exactly what lsk_attn_plan(split) + lsk_attn_schedule give, plus the token
+ * row / position expansion.  counts[10] = {N, n_works, n_groups, n_parts, n_rounds, meta_len, kv_read,
+ * kv_read_padded, kv_gathered, attended (query, position) pairs}; the kv_* figures are the reference's
+ * bucket accounting (bucketing 0 = "exact": runs of equal T, 1 = "pad": one bucket).  Blocks outside
+ * [0, max_batch) x [0, min(max_seq, rope_len)) are rejected with LSK_ESHAPE.  meta == NULL: counts only;
+ * meta_cap too small: LSK_EWORKSPACE with counts written.  Replaces solutions/packed.py:81-139 (build_packed's
+ * ordering bookkeeping, metadata and accounting) for the native kernels. */
+int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const int64_t* T, int nb, int group, int split,
+                     int n_kv_heads, int n_slots, int bucketing, int max_batch, int max_seq, int rope_len,
+                     int32_t* meta, long meta_cap, long* counts);
+
 /* Workspace bytes for the split partials of a plan with n_parts partial slots. */
 size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
 

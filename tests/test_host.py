@@ -249,6 +249,38 @@ def test_build_packed_arrays_matches_block_path(bucketing):
                [(x.start, x.end, x.b, x.T, x.L, x.b0) for x in ref.buckets]
 
 
+@pytest.mark.parametrize("bucketing", ["exact", "pad"])
+def test_native_segment_packer_equals_plan_plus_schedule(bucketing):
+    """lsk_pack_segment (one host call) writes exactly the metadata of lsk_attn_plan + lsk_attn_schedule plus the
+    token expansion, and the reference's bucket accounting, that the step-by-step path (pack_blocks) builds."""
+    from thesis_amd.solutions.packed import Block, build_packed_arrays, pack_blocks
+
+    rng = np.random.default_rng(11)
+    for G, split in ((4, 1024), (1, 2048), (8, 512)):
+        stub = _stub_model(G=G)
+        stub.cache.attn_split = split
+        for trial in range(15):
+            n = int(rng.integers(1, 40))
+            rows = rng.integers(0, 8, n)
+            pos0 = rng.integers(0, 3500, n)
+            T = rng.integers(1, 60 if trial % 3 == 0 else 9, n)
+            got = build_packed_arrays(stub, rows, pos0, T, bucketing, upload_meta=False)
+            ordered = [Block(int(r), int(p), int(t)) for r, p, t in zip(got.blk_rows, got.blk_pos0, got.blk_T)]
+            if bucketing == "exact":
+                cut = np.flatnonzero(np.diff(got.blk_T)) + 1
+                groups = [list(g) for g in np.split(np.arange(len(ordered)), cut)]
+            else:
+                groups = [list(range(len(ordered)))]
+            ref = pack_blocks(stub, ordered, [[ordered[i] for i in g] for g in groups], bucketing)
+            assert np.array_equal(got.meta_host, ref.meta.numpy())
+            assert (got.n_works, got.n_groups, got.n_parts, got.n_rounds) == \
+                   (ref.n_works, ref.n_groups, ref.n_parts, ref.n_rounds)
+            assert (got.kv_read, got.kv_read_padded, got.kv_gathered) == \
+                   (ref.kv_read, ref.kv_read_padded, ref.kv_gathered)
+            assert (got.attn_bytes, got.attn_flops) == (ref.attn_bytes, ref.attn_flops)
+            assert np.array_equal(got.pos_h, ref.pos_h) and np.array_equal(got.rows_h, ref.rows_h)
+
+
 def test_build_packed_rejects_bad_input():
     from thesis_amd.solutions.packed import Block, build_packed
 

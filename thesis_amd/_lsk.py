@@ -33,6 +33,7 @@ _SIGS = {
     "lsk_kv_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
     "lsk_attn_schedule": (_I, [_P, _I, _I, _I, _P, _I, _P]),
+    "lsk_pack_segment": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
     "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z,
                              _P]),
@@ -315,6 +316,36 @@ def attn_schedule(works: np.ndarray, n_kv_heads: int, n_slots: int):
     _check(lib.lsk_attn_schedule(wp, len(works), n_kv_heads, n_slots, recs.ctypes.data, n_slots * R.value,
                                  ctypes.byref(R)), "lsk_attn_schedule")
     return recs[:n_slots * R.value * 8], R.value
+
+
+_PACK_BUF = [np.zeros(1 << 16, dtype=np.int32)]
+_PACK_COUNTS = np.zeros(10, dtype=np.int64)
+
+
+def pack_segment(rows: np.ndarray, pos0: np.ndarray, T: np.ndarray, group: int, split: int, n_kv_heads: int,
+                 n_slots: int, bucketing: int, max_batch: int, max_seq: int, rope_len: int):
+    """lsk_pack_segment over int64 block arrays in packed order -> (meta int32 [meta_len] (a fresh array),
+    counts (N, n_works, n_groups, n_parts, n_rounds, meta_len, kv_read, kv_read_padded, kv_gathered, pairs)).
+    Out-of-range blocks raise ValueError (the reference's build_packed behaviour)."""
+    lib = load()
+    nb = len(T)
+    r = rows if rows.dtype == np.int64 and rows.flags.c_contiguous else np.ascontiguousarray(rows, dtype=np.int64)
+    p = pos0 if pos0.dtype == np.int64 and pos0.flags.c_contiguous else np.ascontiguousarray(pos0, dtype=np.int64)
+    t = T if T.dtype == np.int64 and T.flags.c_contiguous else np.ascontiguousarray(T, dtype=np.int64)
+    cnt = _PACK_COUNTS
+    for _ in range(2):
+        buf = _PACK_BUF[0]
+        rc = lib.lsk_pack_segment(r.ctypes.data, p.ctypes.data, t.ctypes.data, nb, group, split, n_kv_heads, n_slots,
+                                  bucketing, max_batch, max_seq, rope_len, buf.ctypes.data, buf.size,
+                                  cnt.ctypes.data)
+        if rc == -4:                                   # LSK_EWORKSPACE: grow to the reported length and retry
+            _PACK_BUF[0] = np.zeros(int(cnt[5]) * 2, dtype=np.int32)
+            continue
+        if rc == -2:
+            raise ValueError(lib.lsk_last_error().decode())
+        _check(rc, "lsk_pack_segment")
+        return buf[:int(cnt[5])].copy(), tuple(int(c) for c in cnt)
+    raise LskError("lsk_pack_segment: metadata buffer")
 
 
 def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:

@@ -63,8 +63,12 @@ class _Base:
 
     def t_segment(self, n_layers: int, n, C, buckets: int = 1):
         n = np.asarray(n)
+        if not n_layers:
+            return np.zeros_like(n, dtype=np.float64)
         t = n_layers * (self.layer_gemm_ms(n) + self.kv_ms(C) + self.layer_ops_ms(buckets)) + self.segment_ops_ms()
-        return np.where(n > 0, t, 0.0) if n_layers else np.zeros_like(n, dtype=np.float64)
+        if n.ndim == 0:
+            return t if n > 0 else 0.0
+        return t if n.min() > 0 else np.where(n > 0, t, 0.0)
 
     def t_sh(self, B, k: int, C):
         return self.t_segment(k, B, C) + self.head_ms(B)
@@ -99,6 +103,12 @@ class RooflineCostModel(_Base):
 
     def _look(self, tab, n, w, p):
         n = np.asarray(n)
+        if n.dtype.kind in "iu":                     # the common cases: table entries (same values)
+            if n.ndim == 0:
+                v = int(n)
+                return tab[max(v, 0)] if v <= self._n_max else max(w / self.gpu.bw, 2.0 * p * v / self.F)
+            if n.size and n.min() >= 0 and n.max() <= self._n_max:
+                return tab[n]
         exact = np.maximum(w / self.gpu.bw, 2.0 * p * n / self.F)
         return np.where(n <= self._n_max, tab[np.clip(n, 0, self._n_max).astype(np.int64)], exact)
 
@@ -107,10 +117,14 @@ class RooflineCostModel(_Base):
 
     def head_ms(self, n):
         n = np.asarray(n)
-        return np.where(n > 0, self._look(self._head, n, self.dims.head_bytes, self.dims.head_params)
-                        + self.gpu.n_op_head * self.gpu.t_op, 0.0)
+        t = self._look(self._head, n, self.dims.head_bytes, self.dims.head_params) + self.gpu.n_op_head * self.gpu.t_op
+        if n.ndim == 0:
+            return t if n > 0 else 0.0
+        return t if n.size and n.min() > 0 else np.where(n > 0, t, 0.0)
 
     def kv_ms(self, C):
+        if isinstance(C, (int, float, np.integer, np.floating)):
+            return float(C) * self.dims.kv_bytes_per_pos / self.gpu.bw
         return np.asarray(C, dtype=np.float64) * self.dims.kv_bytes_per_pos / self.gpu.bw
 
     def layer_ops_ms(self, buckets: int = 1):

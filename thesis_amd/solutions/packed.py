@@ -94,7 +94,6 @@ class PackedBatch:
     blk_pos0: np.ndarray = None
     blk_T: np.ndarray = None
     order: np.ndarray = None
-    buckets: list = field(default_factory=list)
     n_tokens: int = 0
     kv_read: int = 0
     kv_read_padded: int = 0
@@ -114,6 +113,17 @@ class PackedBatch:
     _model: object = None
     _blocks: Optional[list] = None
     _tags: Optional[list] = None
+    _buckets: Optional[list] = None
+    _bounds: Optional[np.ndarray] = None
+    _bucketing: str = "exact"
+
+    @property
+    def buckets(self) -> list:
+        """The reference's bucket bookkeeping (solutions/packed.py:109-138), built on first access."""
+        if self._buckets is None:
+            self._buckets = _buckets(self.blk_rows, self.blk_pos0, self.blk_T, self.offsets, self._bounds,
+                                     self._bucketing, self._model.cache.max_seq)
+        return self._buckets
 
     @property
     def blocks(self) -> list:
@@ -181,20 +191,63 @@ def build_packed_arrays(model, rows, pos0, T, bucketing: str = "exact", tags: Op
     T = np.asarray(T, dtype=np.int64)
     order = packed_order(rows, pos0, T, bucketing)
     rws, p0, Ts = rows[order], pos0[order], T[order]
-    if bucketing == "exact" and len(Ts):
-        cut = np.flatnonzero(np.diff(Ts)) + 1
-        bounds = np.concatenate([[0], cut, [len(Ts)]])
+    cache = model.cache
+    if cache is None:
+        raise ValueError("allocate_cache() first")
+    n_slots = _lsk.cu_count(model.device)
+    meta, cnt = _lsk.pack_segment(rws, p0, Ts, model.group, cache.attn_split, model.cfg.n_kv_heads, n_slots,
+                                  0 if bucketing == "exact" else 1, cache.max_batch, cache.max_seq,
+                                  model.rope_cos.shape[0])
+    N, nw, ng, n_parts, n_rounds, _, kv_read, kv_padded, kv_gathered, pairs = cnt
+    nb = len(Ts)
+    offsets = qo_indptr(Ts)
+    pb = PackedBatch(offsets, meta[N:2 * N].astype(np.int64), meta[:N].astype(np.int64), rws, p0, Ts, n_tokens=N,
+                     nb=nb, n_works=nw, n_groups=ng, n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots,
+                     _model=model, meta_host=meta, kv_read=kv_read, kv_read_padded=kv_padded,
+                     kv_gathered=kv_gathered, _bucketing=bucketing)
+    if bucketing == "exact" and nb:
+        pb._bounds = np.concatenate([[0], np.flatnonzero(np.diff(Ts)) + 1, [nb]])
     else:
-        bounds = np.array([0, len(Ts)]) if len(Ts) else np.array([0])
-    otags = [tags[i] for i in order] if tags is not None else None
-    pb = _pack(model, rws, p0, Ts, bounds, bucketing, upload_meta)
+        pb._bounds = np.array([0, nb]) if nb else np.array([0])
+    _attn_work(pb, model, kv_read, pairs)
+    if upload_meta and N:
+        pb.meta = upload(meta, model.device, dtype=torch.int32)
     pb.order = order
-    pb._tags = otags
+    pb._tags = [tags[i] for i in order] if tags is not None else None
     return pb
+
+
+def _attn_work(pb: PackedBatch, model, kv_read: int, pairs: int) -> None:
+    """Algorithmic work of one attention launch (per layer): K+V of every attended position read once per
+    (block, KV head), Q read and O written once; flops = 4 Hq D per (query, attended position)."""
+    c = model.cfg
+    es = model.dtype.itemsize
+    pb.attn_bytes = float(kv_read) * c.n_kv_heads * c.head_dim * 2 * es + pb.n_tokens * c.n_heads * c.head_dim * 2 * es
+    pb.attn_flops = 4.0 * c.n_heads * c.head_dim * float(pairs)
+
+
+def _buckets(rws, pos0, Ts, offsets, bounds, bucketing: str, max_seq: int) -> list:
+    out = []
+    for gi in range(len(bounds) - 1):
+        a, b = int(bounds[gi]), int(bounds[gi + 1])
+        n = b - a
+        gr, gp, gt = rws[a:b], pos0[a:b], Ts[a:b]
+        start, end = int(offsets[a]), int(offsets[b])
+        Tm = int(gt.max())
+        L = min((int((gp + gt).max()) + 63) // 64 * 64, max_seq)
+        contiguous = bool((gr == np.arange(gr[0], gr[0] + n)).all())
+        pad = None
+        if bucketing == "pad" and (gt != Tm).any():
+            pad = torch.full((n, Tm), -1, dtype=torch.long)
+            for j in range(n):
+                pad[j, :int(gt[j])] = torch.arange(int(offsets[a + j]), int(offsets[a + j + 1]))
+        out.append(Bucket(start, end, n, Tm, L, None if contiguous else torch.as_tensor(gr), int(gr[0]), None, pad))
+    return out
 
 
 def _pack(model, rws: np.ndarray, pos0: np.ndarray, Ts: np.ndarray, bounds: np.ndarray, bucketing: str,
           upload_meta: bool) -> PackedBatch:
+    """Blocks already in packed order with a caller-given bucket partition (pack_blocks)."""
     _validate(model, rws, pos0, Ts)
     nb = len(Ts)
     offsets = qo_indptr(Ts)
@@ -211,36 +264,15 @@ def _pack(model, rws: np.ndarray, pos0: np.ndarray, Ts: np.ndarray, bounds: np.n
                            grps.ravel(), recs]).astype(np.int32)
     pb = PackedBatch(offsets, pos_h, rows_h, rws, pos0, Ts, n_tokens=N, nb=nb, n_works=len(works),
                      n_groups=len(grps), n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots, _model=model,
-                     meta_host=meta)
-    # algorithmic work of one attention launch (per layer): K+V of every attended position read once per
-    # (block, KV head), Q read and O written once; flops = 4 Hq D per (query, attended position)
-    c = model.cfg
-    es = model.dtype.itemsize
-    pb.attn_bytes = float((pos0 + Ts).sum()) * c.n_kv_heads * c.head_dim * 2 * es + N * c.n_heads * c.head_dim * 2 * es
-    pb.attn_flops = 4.0 * c.n_heads * c.head_dim * float((Ts * pos0 + Ts * (Ts + 1) // 2).sum())
+                     meta_host=meta, _bounds=bounds, _bucketing=bucketing)
+    _attn_work(pb, model, int((pos0 + Ts).sum()), int((Ts * pos0 + Ts * (Ts + 1) // 2).sum()))
     if upload_meta and N:
         pb.meta = upload(meta, model.device, dtype=torch.int32)
-    # ---- reference bucket bookkeeping (solutions/packed.py:109-138), host only
-    max_seq = model.cache.max_seq
-    for gi in range(len(bounds) - 1):
-        a, b = int(bounds[gi]), int(bounds[gi + 1])
-        n = b - a
-        gr, gp, gt = rws[a:b], pos0[a:b], Ts[a:b]
-        start, end = int(offsets[a]), int(offsets[b])
-        Tm = int(gt.max())
-        L = min((int((gp + gt).max()) + 63) // 64 * 64, max_seq)
-        contiguous = bool((gr == np.arange(gr[0], gr[0] + n)).all())
-        pad = None
-        if bucketing == "pad" and (gt != Tm).any():
-            pad = torch.full((n, Tm), -1, dtype=torch.long)
-            for j in range(n):
-                pad[j, :int(gt[j])] = torch.arange(int(offsets[a + j]), int(offsets[a + j + 1]))
-        pb.buckets.append(Bucket(start, end, n, Tm, L, None if contiguous else torch.as_tensor(gr), int(gr[0]), None,
-                                 pad))
-        pb.kv_read += int((gp + gt).sum())
-        pb.kv_read_padded += n * L
-        if not contiguous:
-            pb.kv_gathered += n * L
+    pb.kv_read = int((pos0 + Ts).sum())
+    for bk in pb.buckets:
+        pb.kv_read_padded += bk.b * bk.L
+        if bk.rows is not None:
+            pb.kv_gathered += bk.b * bk.L
     return pb
 
 

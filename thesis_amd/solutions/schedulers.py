@@ -24,19 +24,25 @@ def expected_tokens(alpha, d) -> np.ndarray:
     return (1 - a ** (np.asarray(d, dtype=np.float64) + 1)) / (1 - a)
 
 
+_G_COLS: dict = {}
+
+
 def expected_token_targets(alphas, cost_ratios, min_draft: int, max_draft: int) -> np.ndarray:
     """Largest gamma with a positive marginal gain of E[tokens]/E[time] = ((1 - a^(g+1)) / (1 - a)) / (1 + c g):
     a^g ((1 - a) c (g - 1) + c + (1 - a)) > c  (common/policies.py:54-68)."""
-    a = np.clip(np.asarray(alphas, dtype=np.float64), 0.0, 1.0)
-    c = np.broadcast_to(np.asarray(cost_ratios, dtype=np.float64), a.shape)
+    a = np.minimum(np.maximum(np.asarray(alphas, dtype=np.float64), 0.0), 1.0)
+    c = np.asarray(cost_ratios, dtype=np.float64)
     if max_draft < 1:
         return np.full(a.shape, min_draft, dtype=np.int64)
-    g = np.arange(1, max_draft + 1, dtype=np.int64)[:, None]
-    gain = a[None] ** g * ((1 - a)[None] * c[None] * (g - 1) + c[None] + (1 - a)[None]) > c[None]
+    g = _G_COLS.get(max_draft)
+    if g is None:
+        g = _G_COLS[max_draft] = np.arange(1, max_draft + 1, dtype=np.int64)[:, None]
+    om = 1 - a
+    gain = a ** g * (om * c * (g - 1) + c + om) > c
     last = (max_draft - 1) - np.argmax(gain[::-1], axis=0)
     t = np.where(gain.any(axis=0), last + 1, min_draft)
     t = np.where(a >= 1 - 1e-7, max_draft, t)
-    return np.clip(t, min_draft, max_draft).astype(np.int64)
+    return np.minimum(np.maximum(t, min_draft), max_draft).astype(np.int64)
 
 
 def best_gamma_expected(alpha: float, c: float, gmax: int) -> int:
@@ -116,7 +122,7 @@ class AspireScheduler(Scheduler):
         C = float(ctx[dec].sum())
         t_sh = float(self.cm.t_sh(n, self.k, C))
         t_v = self.cm.t_deep(n * (d + 1), self.k, C, n)
-        ratio = np.clip(t_sh / np.maximum(t_v, 1e-9), 1e-4, 1.0)
+        ratio = np.minimum(np.maximum(t_sh / np.maximum(t_v, 1e-9), 1e-4), 1.0)
         tgt = expected_token_targets(self.ema.alpha, ratio, self.min_draft, self.d_max)
         floor = np.where(self.ema.fresh, max(self.min_draft, self.initial_draft), self.min_draft)
         tgt = np.minimum(np.maximum(tgt, floor), self.d_max)
