@@ -86,7 +86,9 @@ struct Vec8<float> {
 
 #define NORM_MAX_PASSES 4  // dim <= 4 * 256 * 8 = 8192
 
-template <typename T>
+// KSC: the number of K-slice partials as a compile-time constant (all of a thread's partial loads are issued
+// before the first add; the adds keep slice order), or -1 for a run-time count.
+template <typename T, int KSC>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ x, long ldx, const float* __restrict__ P,
                                                           int KS, long pstride, const T* __restrict__ w,
                                                           T* __restrict__ x_out, long ldxo, T* __restrict__ out,
@@ -103,11 +105,23 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
       if (KS > 0) {
         float acc[8];
         const float* pr = P + (long)row * dim + j;
+        if constexpr (KSC > 0) {
+          float pv[KSC][8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = pr[i];
-        for (int s2 = 1; s2 < KS; ++s2)
+          for (int s2 = 0; s2 < KSC; ++s2) Vec8<float>::ld(pr + s2 * pstride, pv[s2]);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pr[s2 * pstride + i];
+          for (int i = 0; i < 8; ++i) acc[i] = pv[0][i];
+#pragma unroll
+          for (int s2 = 1; s2 < KSC; ++s2)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pv[s2][i];
+        } else {
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] = pr[i];
+          for (int s2 = 1; s2 < KS; ++s2)
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pr[s2 * pstride + i];
+        }
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[p][i] = Elem<T>::round(v[p][i] + Elem<T>::round(acc[i]));
         if (x_out != nullptr) Vec8<T>::st(x_out + (long)row * ldxo + j, v[p]);
@@ -142,8 +156,15 @@ template <typename T>
 static void launch_add_rmsnorm(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
                                void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim, float eps,
                                hipStream_t s) {
-  add_rmsnorm_kernel<T><<<n_rows, 256, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w, (T*)x_out, ldxo,
-                                               (T*)out, ldo, dim, eps);
+#define LSK_NORM_LAUNCH(KSC_)                                                                                    \
+  add_rmsnorm_kernel<T, KSC_><<<n_rows, 256, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w, (T*)x_out, \
+                                                     ldxo, (T*)out, ldo, dim, eps)
+  if (KS == 4) LSK_NORM_LAUNCH(4);
+  else if (KS == 2) LSK_NORM_LAUNCH(2);
+  else if (KS == 8) LSK_NORM_LAUNCH(8);
+  else if (KS == 1) LSK_NORM_LAUNCH(1);
+  else LSK_NORM_LAUNCH(-1);
+#undef LSK_NORM_LAUNCH
 }
 
 extern "C" int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w,
@@ -185,15 +206,26 @@ extern "C" int lsk_rmsnorm(int dtype, const void* x, const void* w, void* out, i
 // with c, s = the fp32 tables at pos_t stored to the model dtype first (solutions/packed.py:106-107)
 // and one dtype rounding after each multiply and after the add.
 // Grid: (token, head); a thread owns one rotation pair (j, j + D/2) or, for v heads, two elements.
-template <typename T>
+// KSC as for add_rmsnorm_kernel: a compile-time slice count issues every partial load before the first add.
+template <typename T, int KSC>
 __device__ __forceinline__ float qkv_val(const T* qkv, const float* P, int KS, long pstride, long idx) {
   if (P == nullptr) return Elem<T>::ld(qkv + idx);
-  float a = P[idx];
-  for (int s = 1; s < KS; ++s) a = a + P[s * pstride + idx];
-  return Elem<T>::round(a);
+  if constexpr (KSC > 0) {
+    float pv[KSC];
+#pragma unroll
+    for (int s = 0; s < KSC; ++s) pv[s] = P[s * pstride + idx];
+    float a = pv[0];
+#pragma unroll
+    for (int s = 1; s < KSC; ++s) a = a + pv[s];
+    return Elem<T>::round(a);
+  } else {
+    float a = P[idx];
+    for (int s = 1; s < KS; ++s) a = a + P[s * pstride + idx];
+    return Elem<T>::round(a);
+  }
 }
 
-template <typename T>
+template <typename T, int KSC>
 __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __restrict__ P, int KS, long pstride,
                                    T* __restrict__ q_out, T* __restrict__ kc, T* __restrict__ vc,
                                    const float* __restrict__ cos_tab, const float* __restrict__ sin_tab,
@@ -209,8 +241,8 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
     if (h < Hq + Hkv) {
       const float* ct = cos_tab + (long)p * D;
       const float* st = sin_tab + (long)p * D;
-      const float x1 = qkv_val(qkv, P, KS, pstride, base + j);
-      const float x2 = qkv_val(qkv, P, KS, pstride, base + j + half);
+      const float x1 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j);
+      const float x2 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j + half);
       const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
       const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
       const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
@@ -228,8 +260,8 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
     } else {
       // V cache: 32-position blocks, each transposed ([B, Hkv, S/32, D, 32])
       T* dst = vc + ((long)row * Hkv + (h - Hq - Hkv)) * (long)D * max_seq + (long)(p >> 5) * 32 * D + (p & 31);
-      Elem<T>::st(dst + (long)j * 32, qkv_val(qkv, P, KS, pstride, base + j));
-      Elem<T>::st(dst + (long)(j + half) * 32, qkv_val(qkv, P, KS, pstride, base + j + half));
+      Elem<T>::st(dst + (long)j * 32, qkv_val<T, KSC>(qkv, P, KS, pstride, base + j));
+      Elem<T>::st(dst + (long)(j + half) * 32, qkv_val<T, KSC>(qkv, P, KS, pstride, base + j + half));
     }
   }
 }
@@ -240,8 +272,14 @@ static void launch_rope(const void* qkv, const float* P, int KS, long pstride, v
                         int Hkv, int D, int B, int S, int tab_len, hipStream_t s) {
   dim3 grid(N, Hq + 2 * Hkv);
   const int threads = (D / 2 + 63) / 64 * 64;
-  rope_append_kernel<T><<<grid, threads, 0, s>>>((const T*)qkv, P, KS, pstride, (T*)q_out, (T*)kc, (T*)vc, ct, st,
-                                                  rows, pos, Hq, Hkv, D, B, S, tab_len);
+#define LSK_ROPE_LAUNCH(KSC_)                                                                                   \
+  rope_append_kernel<T, KSC_><<<grid, threads, 0, s>>>((const T*)qkv, P, KS, pstride, (T*)q_out, (T*)kc, (T*)vc, \
+                                                       ct, st, rows, pos, Hq, Hkv, D, B, S, tab_len)
+  if (P != nullptr && KS == 4) LSK_ROPE_LAUNCH(4);
+  else if (P != nullptr && KS == 2) LSK_ROPE_LAUNCH(2);
+  else if (P != nullptr && KS == 8) LSK_ROPE_LAUNCH(8);
+  else LSK_ROPE_LAUNCH(-1);
+#undef LSK_ROPE_LAUNCH
 }
 
 static int rope_common(int dtype, const void* qkv, const float* P, int KS, void* q_out, void* kcache, void* vcache,
