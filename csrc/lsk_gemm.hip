@@ -244,6 +244,188 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
   }
 }
 
+// ----------------------------------------------------------------------------- wide-M tier
+// For many token rows the decode kernel re-reads every weight tile once per 16*MS-token tile.  This kernel
+// reads it once per 16*MSW*NWV tokens: the NT x 4 weight fragments of a 128-k chunk are staged in LDS (through
+// PF chunks of register prefetch) and NWV waves multiply them with their own MSW token groups.
+//
+// Exactly the decode kernel's arithmetic: the decode kernel's wave c % 4 accumulates chunks c, c + 4, ... of
+// its K slice in order (then, for wave nfull % 4, the tail k-steps) and the four waves are summed in order.
+// Here the chunks are visited class by class (class 0: chunks 0, 4, 8, ...; then class 1; ...), each class into
+// a fresh accumulator `cur` that is folded into the running sum `tot` (tot = p0, tot + p1, tot + p2, tot + p3),
+// so every output sees the same MFMA sequence and the same three adds: results are bitwise those of the
+// decode kernel, which keeps the batch invariance of the GEMM.  Covered shapes (launch_wide): N % 64 == 0 and
+// K slices of whole 128-k chunks (no tail k-steps).
+template <int NS, int MSW, int EPI, int NWV, int PF>
+__global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* __restrict__ A, long lda,
+                                                                const uint16_t* __restrict__ W,
+                                                                uint16_t* __restrict__ C, long ldc,
+                                                                const uint16_t* __restrict__ R, long ldr,
+                                                                float* __restrict__ P, int M, int N, int K, int ffn,
+                                                                int kslice, int n_tiles, int m_blocks, int n_slices) {
+  constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
+  constexpr int NTH = 64 * NWV;
+  constexpr int CHUNK_E = NT * 4 * 512;  // bf16 elements of one staged chunk (NT row groups x 4 k-steps)
+  constexpr int LPT = CHUNK_E / (NTH * 8);
+  static_assert(LPT >= 1 && CHUNK_E % (NTH * 8) == 0, "staging split");
+  constexpr int TB = NWV * MSW * 16;    // tokens per workgroup
+  __shared__ __attribute__((aligned(16))) uint16_t wl[2][CHUNK_E];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l16 = lane & 15, lg = lane >> 4;
+  // id -> (row tile, K slice, token block): the token blocks of one (row tile, slice) take consecutive slots
+  // of one XCD, so they run side by side and share each weight chunk through that XCD's L2
+  const int xcd = blockIdx.x & 7, qid = blockIdx.x >> 3;
+  const int mb = qid % m_blocks, rest = qid / m_blocks;
+  const int s = rest % n_slices, tg = rest / n_slices;
+  const int tn = tg * 8 + xcd;
+  if (tn >= n_tiles) return;
+  const int n0 = tn * 16 * NS;
+  const int k0 = s * kslice, k1 = min(K, k0 + kslice);
+  const int nks = K >> 5;
+  const int nfull = (k1 - k0) / 128;
+  auto group_of = [&](int g) { return (g < NS) ? (n0 / 16 + g) : ((ffn + n0) / 16 + (g - NS)); };
+  // staging: piece p = tid + NTH j -> row group p / 256, k-step (p / 64) % 4, lane p % 64 of the chunk
+  const uint16_t* wsrc[LPT];
+  int wdst[LPT];
+#pragma unroll
+  for (int j = 0; j < LPT; ++j) {
+    const int pc = tid + NTH * j;
+    const int g = pc >> 8, ks = (pc >> 6) & 3, l = pc & 63;
+    wsrc[j] = W + ((long)group_of(g) * nks + (k0 >> 5) + ks) * 512 + 8 * l;
+    wdst[j] = (g * 4 + ks) * 512 + 8 * l;
+  }
+  const uint16_t* arow[MSW];
+  int mrow[MSW];
+#pragma unroll
+  for (int t = 0; t < MSW; ++t) {
+    const int m = mb * TB + (wave * MSW + t) * 16 + l16;
+    mrow[t] = m;
+    arow[t] = A + (long)(m < M - 1 ? m : M - 1) * lda + k0 + 8 * lg;
+  }
+  lsk_f32x4 cur[NT][MSW], tot[NT][MSW];
+#pragma unroll
+  for (int a = 0; a < NT; ++a)
+#pragma unroll
+    for (int t = 0; t < MSW; ++t) cur[a][t] = tot[a][t] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+  // visiting order: chunk class q = 0..3 holds chunks q, q + 4, ...; n_q of them; sequence index i -> chunk
+  int cum[5];
+  cum[0] = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) cum[q + 1] = cum[q] + (nfull > q ? (nfull - q + 3) / 4 : 0);
+  auto chunk_at = [&](int i) {
+    const int q = (i >= cum[1]) + (i >= cum[2]) + (i >= cum[3]);
+    return q + 4 * (i - cum[q]);
+  };
+  lsk_i32x4 stg[PF][LPT];
+  auto issue = [&](lsk_i32x4 (&r)[LPT], int c) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) r[j] = __builtin_nontemporal_load((const lsk_i32x4*)(wsrc[j] + (long)c * 4 * 512));
+  };
+  auto put = [&](lsk_i32x4 (&r)[LPT], int b) {
+#pragma unroll
+    for (int j = 0; j < LPT; ++j) *(lsk_i32x4*)(&wl[b][wdst[j]]) = r[j];
+  };
+  lsk_bf16x8 af[2][4][MSW];
+  auto load_a = [&](lsk_bf16x8 (&a)[4][MSW], int c) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int t = 0; t < MSW; ++t) a[ks][t] = *(const lsk_bf16x8*)(arow[t] + c * 128 + ks * 32);
+  };
+  auto comp = [&](const lsk_bf16x8 (&a)[4][MSW], int b) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      lsk_bf16x8 wf[NT];
+#pragma unroll
+      for (int g = 0; g < NT; ++g) wf[g] = *(const lsk_bf16x8*)(&wl[b][(g * 4 + ks) * 512 + 8 * lane]);
+#pragma unroll
+      for (int g = 0; g < NT; ++g)
+#pragma unroll
+        for (int t = 0; t < MSW; ++t)
+          cur[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g], a[ks][t], cur[g][t], 0, 0, 0);
+    }
+  };
+  int cls = 0;
+  auto fold = [&]() {  // close class cls, start the next one
+#pragma unroll
+    for (int g = 0; g < NT; ++g)
+#pragma unroll
+      for (int t = 0; t < MSW; ++t) {
+        if (cls == 0) {
+          tot[g][t] = cur[g][t];
+        } else {
+          tot[g][t][0] = tot[g][t][0] + cur[g][t][0];
+          tot[g][t][1] = tot[g][t][1] + cur[g][t][1];
+          tot[g][t][2] = tot[g][t][2] + cur[g][t][2];
+          tot[g][t][3] = tot[g][t][3] + cur[g][t][3];
+        }
+        cur[g][t] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+      }
+    ++cls;
+  };
+  // prologue: chunks 0 .. PF-1 of the sequence in flight, chunk 0 in LDS buffer 0
+#pragma unroll
+  for (int j = 0; j < PF; ++j)
+    if (j < nfull) issue(stg[j], chunk_at(j));
+  if (nfull > 0) {
+    load_a(af[0], chunk_at(0));
+    put(stg[0], 0);
+  }
+  __syncthreads();
+  // sequence index i (i0 a multiple of 2 PF, so i % 2 == u % 2 and i % PF == u % PF): fold the classes that
+  // ended before i, multiply chunk i from LDS buffer i % 2, refill register slot i % PF with chunk i + PF, move
+  // chunk i + 1 from its register slot into the other LDS buffer
+  for (int i0 = 0; i0 < nfull; i0 += 2 * PF) {
+#pragma unroll
+    for (int u = 0; u < 2 * PF; ++u) {
+      const int i = i0 + u;
+      if (i < nfull) {
+        while (cls < 3 && i >= cum[cls + 1]) fold();
+        if (i + 1 < nfull) load_a(af[(u + 1) & 1], chunk_at(i + 1));
+        comp(af[u & 1], u & 1);
+        if (i + PF < nfull) issue(stg[u % PF], chunk_at(i + PF));
+        if (i + 1 < nfull) put(stg[(u + 1) % PF], (u + 1) & 1);
+        __syncthreads();
+      }
+    }
+  }
+  while (cls < 4) fold();
+  // epilogue: lane holds rows 16 g + 4 lg + i of its token group t, token l16
+#pragma unroll
+  for (int t = 0; t < MSW; ++t) {
+    const int m = mrow[t];
+    if (m >= M) continue;
+#pragma unroll
+    for (int g = 0; g < NS; ++g) {
+      const int n = n0 + 16 * g + 4 * lg;
+      if (n >= N) continue;
+      if constexpr (EPI == EPI_PARTIAL) {
+        *(float4*)(P + ((long)s * M + m) * N + n) = make_float4(tot[g][t][0], tot[g][t][1], tot[g][t][2], tot[g][t][3]);
+      } else {
+        uint16_t o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float v = tot[g][t][i];
+          float outv;
+          if constexpr (EPI == LSK_EPI_SILU_MUL) {
+            outv = rbf(silu_f(rbf(v))) * rbf(tot[g + NS][t][i]);
+          } else if constexpr (EPI == LSK_EPI_RESIDUAL) {
+            outv = bf2f(R[(long)m * ldr + n + i]) + rbf(v);
+          } else {
+            outv = v;
+          }
+          o[i] = f2bf(outv);
+        }
+        uint2 pk;
+        pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
+        pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
+        *(uint2*)(C + (long)m * ldc + n) = pk;
+      }
+    }
+  }
+}
+
 // Final greedy pick over the per-tile maxima: larger value wins, ties keep the smaller index
 // (torch.argmax semantics over the bf16 logits).  out[dst ? dst[m] : m] = index.
 __global__ __launch_bounds__(256) void argmax_tiles_kernel(const float* __restrict__ v, const int* __restrict__ idx,
@@ -436,6 +618,42 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 #undef LSK_GEMM_CASE
 }
 
+// Wide-M tier selection (measured on MI355X at the 8B layer shapes, against the decode kernel's 64-token
+// tiles): a workgroup covers TB = 128 tokens (256 for silu-mul above 128), so the tier runs when M is above
+// 64, its last token block is at least 3/4 full (or the only one) and the launch has >= 192 workgroups;
+// otherwise the finer 64-token tiles of the decode kernel waste less.  Returns false when the decode kernel should run (also for shapes the tier
+// does not cover: N % 64 != 0 or K slices that are not whole 128-k chunks).
+static bool launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
+                        const uint16_t* R, long ldr, float* P, int M, int N, int K, int ffn, int ks) {
+  const bool silu = epi == LSK_EPI_SILU_MUL;
+  const int tb = (silu && M > 128) ? 256 : 128;
+  const int rem = M % tb;
+  if (M <= 64 || !(M <= tb || rem == 0 || 4 * rem >= 3 * tb)) return false;
+  if (N % 64 != 0 || (epi != EPI_PARTIAL && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0) return false;
+  const int n_tiles = N / 64;
+  const int m_blocks = (M + tb - 1) / tb;
+  if ((long)n_tiles * m_blocks * ks < 192) return false;  // too few workgroups to stream the weights
+  const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * m_blocks * ks));
+  const int kslice = K / ks;
+#define LSK_WIDE(MSW_, EPI_) \
+  gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, M, N, K, ffn, kslice, \
+                                                             n_tiles, m_blocks, ks)
+  if (silu) {
+    if (tb == 256) LSK_WIDE(2, LSK_EPI_SILU_MUL);
+    else LSK_WIDE(1, LSK_EPI_SILU_MUL);
+  } else if (epi == EPI_PARTIAL) {
+    LSK_WIDE(1, EPI_PARTIAL);
+  } else if (epi == LSK_EPI_RESIDUAL) {
+    LSK_WIDE(1, LSK_EPI_RESIDUAL);
+  } else if (epi == LSK_EPI_NONE) {
+    LSK_WIDE(1, LSK_EPI_NONE);
+  } else {
+    return false;
+  }
+#undef LSK_WIDE
+  return true;
+}
+
 extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc,
                         const void* R, long ldr, int M, int N, int K, int epilogue, int ffn, void* stream) {
   LSK_REQUIRE(A && W && C, LSK_EARG, "lsk_gemm: null pointer");
@@ -452,6 +670,9 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
                 "lsk_gemm: bf16 needs K %% 32 == 0, 16-byte aligned A rows and a packed W (ldw == K; K=%d ldw=%ld)", K,
                 ldw);
     LSK_REQUIRE(N % 16 == 0, LSK_ESHAPE, "lsk_gemm: bf16 needs N %% 16 == 0 (N=%d)", N);
+    if (launch_wide(epilogue, s, (const uint16_t*)A, lda, (const uint16_t*)W, (uint16_t*)C, ldc,
+                    (const uint16_t*)R, ldr, nullptr, M, N, K, ffn, 1))
+      return lsk_check_launch("lsk_gemm(bf16, wide)");
     // whole-K workgroups
     const int ns = tile_ns(N, M, epilogue);
     const int ms = ms_for(M);
@@ -484,6 +705,9 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
                   N % 16 == 0 && lda % 8 == 0,
               LSK_ESHAPE, "lsk_gemm_partial: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
+  if (launch_wide(EPI_PARTIAL, (hipStream_t)stream, (const uint16_t*)A, lda, (const uint16_t*)W, nullptr, 0, nullptr,
+                  0, P, M, N, K, 0, ks))
+    return lsk_check_launch("lsk_gemm_partial(wide)");
   const int ns = tile_ns(N, M, EPI_PARTIAL);
   const int ms = ms_for(M);
   dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,

@@ -57,24 +57,33 @@ def test_gemm_bf16_none_matches_fp32_reference(cuda, M, N, K):
     assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max()
 
 
-def test_gemm_bf16_is_batch_invariant(cuda):
+@pytest.mark.parametrize("K,N", [(1024, 384), (4096, 256)])
+def test_gemm_bf16_is_batch_invariant(cuda, K, N):
     """Every row's result is bitwise independent of M and of which rows share a tile (16- to 128-token tiles,
-    one or several token tiles, every epilogue)."""
+    one or several token tiles, the wide-M tier above 64 / 128 rows, every epilogue)."""
     lsk = _lsk()
     g = _gen(3)
-    K, N = 1024, 384
-    a = torch.randn(300, K, generator=g).to(BF16).to(cuda)
+    M = 300
+    a = torch.randn(M, K, generator=g).to(BF16).to(cuda)
     w = lsk.PackedWeight(torch.randn(N, K, generator=g).to(BF16).to(cuda))
     w13 = lsk.PackedWeight(torch.randn(2 * N, K, generator=g).to(BF16).to(cuda))
+    r = torch.randn(M, N, generator=g).to(BF16).to(cuda)
     full = lsk.gemm(a, w)
+    full_r = lsk.gemm(a, w, residual=r, epilogue=lsk.EPI_RESIDUAL)
     full_s = lsk.gemm(a, w13, epilogue=lsk.EPI_SILU_MUL)
     ns, ks = lsk.gemm_plan(N, K)
     full_p = lsk.gemm_partial(a, w, ks)
-    for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104), (10, 130), (0, 300)]:
+    for lo, hi in [(0, 1), (7, 8), (3, 19), (150, 200), (0, 33), (40, 104), (10, 130), (0, 65), (20, 149),
+                   (0, 300)]:
         sub = a[lo:hi].contiguous()
         assert torch.equal(lsk.gemm(sub, w), full[lo:hi]), (lo, hi)
+        assert torch.equal(lsk.gemm(sub, w, residual=r[lo:hi].contiguous(), epilogue=lsk.EPI_RESIDUAL),
+                           full_r[lo:hi]), (lo, hi)
         assert torch.equal(lsk.gemm(sub, w13, epilogue=lsk.EPI_SILU_MUL), full_s[lo:hi]), (lo, hi)
         assert torch.equal(lsk.gemm_partial(sub, w, ks), full_p[:, lo:hi]), (lo, hi)
+    # the wide tier against fp32 math (its own check, independent of the decode kernel)
+    ref = (a.float() @ w.unpack().float().t()).to(BF16)
+    assert ((full.float() - ref.float()).abs() <= 2.0 ** -7 * ref.float().abs() + 2e-2).all()
 
 
 @pytest.mark.parametrize("big", [0, 1])

@@ -9,8 +9,8 @@ Measured, each with HIP events on the stream liblsk launches on (median of repet
              (solutions/calibrate.py:59-62)
   flops      8192^3 bf16 matmul through torch (hipBLASLt): the device's dense rate as a library reaches
              it, kept only for the roofline-peak variant (solutions/calibrate.py:63-66)
-  flops_eff  highest flop rate of the model's own layer GEMMs (qkv, o, w13 + silu-mul, w2) through
-             lsk_gemm for n = 1..512 tokens (solutions/calibrate.py:126-140)
+  flops_eff  highest flop rate of the model's own layer GEMMs as the layer runs them (qkv, o, w2 as K-slice
+             partials, w13 + silu-mul) for n = 1..512 tokens (solutions/calibrate.py:126-140)
   knee       hinge fit t = a + b max(n - knee, 0) of one real packed layer timed for n = 1..512
              single-token requests (solutions/calibrate.py:143-172)
   t_op       back-to-back tiny liblsk launches (a one-row lsk_copy_rows) (solutions/calibrate.py:67-72)
@@ -116,10 +116,14 @@ def trace_ops(m) -> dict:
 
 
 def _layer_gemms(m) -> list:
-    """(weight, input width, epilogue) of the four projections of layer 0, as the layer runner calls them."""
+    """(weight, input width, K slices) of the four projections of layer 0 as the bf16 layer runner launches
+    them: qkv, o and w2 as K-slice partials (the plan's slice count), w13 with the silu-mul epilogue (0)."""
     lw, c = m.layers[0], m.cfg
-    return [(lw.wqkv, c.dim, _lsk.EPI_NONE), (lw.wo, m.q_size, _lsk.EPI_NONE),
-            (lw.w13, c.dim, _lsk.EPI_SILU_MUL), (lw.w2, c.intermediate_size, _lsk.EPI_NONE)]
+    out = []
+    for w, k in ((lw.wqkv, c.dim), (lw.wo, m.q_size), (lw.w13, c.dim), (lw.w2, c.intermediate_size)):
+        ks = 0 if w is lw.w13 else (_lsk.gemm_plan(w.shape[0], k)[1] if m.dtype == torch.bfloat16 else 1)
+        out.append((w, k, ks))
+    return out
 
 
 def measure_flops_eff(m, ns=N_GRID) -> dict:
@@ -131,12 +135,18 @@ def measure_flops_eff(m, ns=N_GRID) -> dict:
     with torch.inference_mode():
         for n in ns:
             xs = [torch.randn(n, k, device=m.device, dtype=m.dtype) for _, k, _ in shapes]
-            outs = [torch.empty(n, w.shape[0] // (2 if e == _lsk.EPI_SILU_MUL else 1), device=m.device,
-                                dtype=m.dtype) for w, _, e in shapes]
+            outs = [torch.empty(n, w.shape[0] // 2, device=m.device, dtype=m.dtype) if ks == 0 else
+                    (torch.empty(ks, n, w.shape[0], device=m.device) if m.dtype == torch.bfloat16 else
+                     torch.empty(n, w.shape[0], device=m.device, dtype=m.dtype)) for w, _, ks in shapes]
 
             def run():
-                for (w, _, e), x, o in zip(shapes, xs, outs):
-                    _lsk.gemm(x, w, out=o, epilogue=e)
+                for (w, _, ks), x, o in zip(shapes, xs, outs):
+                    if ks == 0:
+                        _lsk.gemm(x, w, out=o, epilogue=_lsk.EPI_SILU_MUL)
+                    elif m.dtype == torch.bfloat16:
+                        _lsk.gemm_partial(x, w, ks, out=o)
+                    else:
+                        _lsk.gemm(x, w, out=o)
             ms = timed_ms(run)
             rows.append({"n": n, "ms": ms, "flop_per_ms": 2.0 * params * n / ms})
     best = max(rows, key=lambda r: r["flop_per_ms"])
