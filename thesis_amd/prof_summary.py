@@ -60,6 +60,10 @@ def classify(short: str, grid_x_threads=None) -> str:
             n_rows = grid_x_threads // 256 * 16 * ns
             cls = "gemm_qkv" if n_rows == 6144 else "gemm_o_w2"
         return cls
+    m = re.match(r"gemm_wide_kernel<(\d+), (\d+), (\d+)(?:, \d+)*>", short)
+    if m:                                    # wide-M tier: same classes, qkv and o / w2 not told apart
+        cls = _EPI.get(m.group(3), "gemm")
+        return "gemm_qkv_o_w2" if cls == "gemm_partial" else cls
     for key, cls in (("attn_bf16_kernel", "attention"), ("attn_f32_kernel", "attention"),
                      ("attn_combine_kernel", "attention_combine"), ("add_rmsnorm_kernel", "rmsnorm"),
                      ("rope_append_kernel", "rope_append"), ("argmax_tiles_kernel", "head_pick"),
@@ -181,12 +185,14 @@ def cmd_pmc(a):
         fc[c].append(v)
     for _, c, v in write.values():
         wc[c].append(v)
-    print("# HBM traffic of the decode steps (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n")
+    print(f"# HBM traffic of {a.subject} (rocprofv3 --pmc FETCH_SIZE, then WRITE_SIZE)\n")
     if a.cmd:
         print("Commands:\n")
         for c in a.cmd.split(" ;; "):
             print(f"    {c}")
         print()
+    if a.title:
+        print(a.title + "\n")
     print(f"Calibration: a plain copy of {a.calib_mib} MiB read FETCH_SIZE = {fm:.0f} KiB and WRITE_SIZE = "
           f"{wm:.0f} KiB, so the scale factors are fetch x{f_scale:.3f} and write x{w_scale:.3f} "
           f"(counter KiB -> bytes moved).\n")
@@ -238,6 +244,8 @@ def main(argv=None):
     p.add_argument("--req-sizes", help="counter CSV of TCC_EA0_RDREQ_{32B,64B,128B}_sum")
     p.add_argument("--bench")
     p.add_argument("--cmd")
+    p.add_argument("--title")
+    p.add_argument("--subject", default="the decode steps")
     a = ap.parse_args(argv)
     (cmd_trace if a.mode == "trace" else cmd_pmc)(a)
 
