@@ -230,7 +230,9 @@ def run_attention_bench(args):
     v_new = torch.empty_like(k_new).normal_(generator=g)
     offs = np.concatenate([[0], np.cumsum(T)[:-1]])
     blocks = np.stack([offs, ctx, T, np.arange(B)], axis=1).astype(np.int32)
-    works, groups, n_parts = _lsk.attn_plan(blocks, Hq // Hkv, _lsk.ATTN_SPLIT)
+    n_slots = _lsk.cu_count(dev)
+    rows_cap = _lsk.attn_rows_cap(blocks, Hq // Hkv, _lsk.ATTN_SPLIT, Hkv, D, n_slots)
+    works, groups, n_parts = _lsk.attn_plan(blocks, Hq // Hkv, _lsk.ATTN_SPLIT, rows_cap)
     blk_d = torch.from_numpy(blocks).to(dev)
     wk_d = torch.from_numpy(works).to(dev)
     gr_d = torch.from_numpy(groups).to(dev) if len(groups) else None
@@ -242,13 +244,12 @@ def run_attention_bench(args):
     acc_d = torch.from_numpy(acc).to(dev)
     kv_len = torch.from_numpy(ctx.copy()).to(dev)
 
-    n_slots = _lsk.cu_count(dev)
     recs, n_rounds = _lsk.attn_schedule(works, Hkv, n_slots)
     recs_d = torch.from_numpy(recs).to(dev)
 
     def attn():
         _lsk.ragged_attn(q, kc, vc, blk_d, wk_d, len(works), gr_d, len(groups), n_parts, out, Hq,
-                         1.0 / math.sqrt(D), ws, recs_d, n_rounds, n_slots)
+                         1.0 / math.sqrt(D), ws, recs_d, n_rounds, n_slots, rows_cap)
 
     def timed(fn, iters):
         for _ in range(5):
@@ -273,7 +274,7 @@ def run_attention_bench(args):
         "workload": "verify attention: 256 requests, GQA 32/8, head_dim 128, bf16 KV, lognormal contexts "
                     "(median 1500, sigma 0.5, clip [64, 8192]), 1-9 query rows each",
         "contexts": {"sum": int(ctx.sum()), "median": float(np.median(ctx)), "max": int(ctx.max())},
-        "query_rows": N, "work_items": int(len(works)), "split_positions": _lsk.ATTN_SPLIT,
+        "query_rows": N, "work_items": int(len(works)), "rows_per_item": rows_cap, "split_positions": _lsk.ATTN_SPLIT,
         "attn_us": round(1e3 * t_attn, 2), "attn_bytes": attn_bytes,
         "attn_GBs": round(attn_bytes / (t_attn * 1e-3) / 1e9, 1),
         "attn_hbm_frac": round(attn_bytes / (t_attn * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),

@@ -20,7 +20,8 @@
 //                                 load depends on nothing but its own index
 //   groups int32 [n_group][8] = {blk, row0, nrows, part_first, n_split, 0, 0, 0}
 // The G query heads of a KV head are folded into query rows: row = t * G + g (t = token of the
-// block, g = head within the group); a workgroup serves 16 rows, so one KV read serves G*T <= 16 rows.
+// block, g = head within the group); a work item serves up to ATTN_ROWS = 48 rows, so one KV read serves
+// G*T <= 48 rows.
 //
 // Long contexts are split into fixed, position-aligned chunks of LSK_ATTN_SPLIT positions
 // (flash-decoding).  Split boundaries, tile boundaries, the wave that owns a tile and both merge
@@ -28,6 +29,7 @@
 // tokens share its block or batch (batch invariance: a T = 1 decode query and the same query inside a
 // T = 9 verify block give bitwise identical outputs).
 #include <algorithm>
+#include <functional>
 #include <vector>
 
 #include "lsk_common.h"
@@ -35,13 +37,31 @@
 
 #define ATTN_TILE 64   // work ranges are split at multiples of this (planner granularity)
 #define ATTN_STEP 32   // KV positions per step of a wave
-#define ATTN_QT 2      // 16-row MFMA column tiles per work item
-#define ATTN_ROWS (16 * ATTN_QT)  // query rows per work item
+#define ATTN_QT 3      // 16-row MFMA column tiles per work item
+#define ATTN_ROWS (16 * ATTN_QT)  // query rows per work item: a T <= 12 block of a 4-head group in one item
+#define ATTN_MERGE_TILES 2  // column tiles merged per LDS pass of the wave merge
 #define ATTN_MAX_SPLITS 128
 #define ATTN_WAVES 8   // waves per work item; fixed, because it fixes which wave accumulates which step
 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// max / sum over the four 16-lane rows of a wave, result in every lane (the xor-16 then xor-32 butterfly),
+// with gfx950's row swaps: v_permlane16_swap(x, x) yields rows {0,0,2,2} and {1,1,3,3},
+// v_permlane32_swap(x, x) the lower and the upper half in every lane.  Plain VALU, no LDS round trip;
+// a + b == b + a, so every lane ends with the same bits.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
 
 // bf16 path.  Cache layouts: K in fragment-major 32-position blocks (k_cache_offset), V in transposed
 // 32-position blocks (V^T per block), so both MFMA operands come straight from HBM as 16-byte vectors and
@@ -49,15 +69,18 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 //   S^T[pos][q] = K Q^T        v_mfma_f32_16x16x32_bf16, A = K rows (16 positions x 32 d), B = Q^T
 //   O^T[d][q]  += V^T P^T      v_mfma_f32_16x16x32_bf16, A = V^T (16 d x 32 positions), B = P^T
 // Each lane owns one query column (l16) of each column tile, so the running max / row sum are lane-local
-// up to xor shuffles over the four 16-lane groups.  A 32-position step uses two S^T sub-tiles whose MFMA
-// rows are mapped to positions so that lane group g holds positions 8g .. 8g+7 of the step: exactly the 8
-// consecutive positions its P^T fragment and its 16-byte V^T load need.
-// A work item carries up to 32 query rows (two column tiles sharing every K / V fragment), so the KV of a
-// (block, KV head) is read by one workgroup for blocks of up to 32 / G tokens.  The 8 waves take the
+// up to a butterfly over the four 16-lane rows (rows_max / rows_sum).  A 32-position step uses two S^T
+// sub-tiles whose MFMA rows are mapped to positions so that lane group g holds positions 8g .. 8g+7 of the
+// step: exactly the 8 consecutive positions its P^T fragment and its 16-byte V^T load need.
+// A work item carries up to 48 query rows (three column tiles sharing every K / V fragment), so the KV of a
+// (block, KV head) is read by one workgroup for blocks of up to 48 / G tokens (a 9-token verify block of a
+// 4-head group is 36 rows).  The item's Q sits in LDS (rows padded by 16 bytes: the 16-byte reads of 16
+// rows hit distinct banks), which keeps three tiles' accumulators within 256 VGPRs.  The 8 waves take the
 // 32-position steps of the item's KV range round robin (step index within the split mod 8), keep the next
-// step's K and V loads in flight while they compute, and are merged in wave order through LDS; 8 waves keep
-// the chain of dependent steps short when a decode batch has few (block, KV head) pairs.
-template <int D>
+// step's K and V loads in flight while they compute, and are merged in wave order through LDS, two column
+// tiles per pass; 8 waves keep the chain of dependent steps short when a decode batch has few
+// (block, KV head) pairs.
+template <int D, int QT>
 __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
     const int32_t* __restrict__ recs, int n_rounds, uint16_t* __restrict__ out, float* __restrict__ o_part,
@@ -65,8 +88,16 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   constexpr int KSTEPS = D / 32;
   constexpr int CT = D / 16;
   constexpr int NW = ATTN_WAVES;
-  __shared__ float s_ml[NW][2][ATTN_ROWS];
-  __shared__ __attribute__((aligned(16))) float s_o[NW][ATTN_ROWS][D + 4];
+  constexpr int ROWS = 16 * QT;                      // rows per item
+  constexpr bool QREG = QT == 1;                     // one tile: Q fragments in registers, no s_q
+  constexpr int MT = QT < ATTN_MERGE_TILES ? QT : ATTN_MERGE_TILES;
+  constexpr int MR = 16 * MT;                        // rows per merge pass
+  constexpr int QLD = D + 8;                         // s_q row stride in bf16 elements
+  constexpr int QCH = D / 8;                         // 16-byte chunks per Q row
+  constexpr int QPT = (ROWS * QCH + 64 * NW - 1) / (64 * NW);  // Q chunks staged per thread
+  __shared__ float s_ml[NW][2][ROWS];
+  __shared__ __attribute__((aligned(16))) float s_o[NW][MR][D + 4];
+  __shared__ __attribute__((aligned(16))) uint16_t s_q[QREG ? 1 : ROWS][QLD];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -92,19 +123,41 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   auto kbase_of = [&](const Item& it) { return kc + ((long)it.crow * Hkv + it.kvh) * (long)S * D; };
   auto vbase_of = [&](const Item& it) { return vt + ((long)it.crow * Hkv + it.kvh) * (long)D * S; };
 
-  lsk_bf16x8 qf[ATTN_QT][KSTEPS];
-  int qpos[ATTN_QT];
-  auto load_q = [&](const Item& it) {
-#pragma unroll
-    for (int qt = 0; qt < ATTN_QT; ++qt) {
-      const bool valid = 16 * qt + l16 < it.nrows;
-      const int r = it.row0 + 16 * qt + (valid ? l16 : 0);
+  // Q of an item: global -> registers (in flight during the previous item's merge) -> LDS; rows >= nrows are 0.
+  // One tile (QREG): each lane loads its own column's fragments straight into qreg.
+  lsk_bf16x8 qst[QPT];
+  lsk_bf16x8 qreg[KSTEPS];
+  auto q_load = [&](const Item& it) {
+    if constexpr (QREG) {
+      const bool valid = l16 < it.nrows;
+      const int r = it.row0 + (valid ? l16 : 0);
       const int t = r / G, g = r - t * G;
-      qpos[qt] = valid ? it.pos0 + t : -1;  // invalid rows: every score masked
       const uint16_t* qrow = q + ((long)(it.q_start + t) * Hq + it.kvh * G + g) * D;
 #pragma unroll
       for (int j = 0; j < KSTEPS; ++j)
-        qf[qt][j] = valid ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
+        qreg[j] = valid ? *(const lsk_bf16x8*)(qrow + 32 * j + 8 * lg) : (lsk_bf16x8){};
+      return;
+    }
+#pragma unroll
+    for (int i = 0; i < QPT; ++i) {
+      const int c = tid + i * 64 * NW;
+      const int r = c / QCH, c8 = c - r * QCH;
+      lsk_bf16x8 v = {};
+      if (r < it.nrows) {
+        const int rr = it.row0 + r, t = rr / G, g = rr - t * G;
+        v = *(const lsk_bf16x8*)(q + ((long)(it.q_start + t) * Hq + it.kvh * G + g) * D + 8 * c8);
+      }
+      qst[i] = v;
+    }
+  };
+  auto q_store = [&]() {
+    if constexpr (!QREG) {
+#pragma unroll
+      for (int i = 0; i < QPT; ++i) {
+        const int c = tid + i * 64 * NW;
+        const int r = c / QCH, c8 = c - r * QCH;
+        if (r < ROWS) *(lsk_bf16x8*)(&s_q[r][8 * c8]) = qst[i];
+      }
     }
   };
   auto ldkv = [&](const uint16_t* p) -> lsk_bf16x8 {
@@ -126,7 +179,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   // a wave's steps of an item: 32-position steps wave, wave + NW, ... of the item's range, in order
   auto first_step = [&](const Item& it) { return it.kv_lo + ATTN_STEP * wave; };
   auto issue_first = [&](const Item& it) {
-    load_q(it);
+    q_load(it);
     const int sb = first_step(it);
     if (sb < it.kv_hi) {
       load_k(kbase_of(it), sb);
@@ -138,17 +191,27 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   if (cur.nrows == 0) return;
   issue_first(cur);
   Item nxt = fetch(1);  // the next record is read while this item streams
+  if constexpr (!QREG) {
+    q_store();
+    __syncthreads();
+  }
   for (int r = 0; cur.nrows > 0; ++r) {
     const int nq = (cur.nrows + 15) >> 4;  // column tiles in use (wave-uniform)
     const int kv_hi = cur.kv_hi;
     const uint16_t* kb = kbase_of(cur);
     const uint16_t* vb = vbase_of(cur);
+    int qpos[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) {
+      const int rl = 16 * qt + l16;
+      qpos[qt] = rl < cur.nrows ? cur.pos0 + (cur.row0 + rl) / G : -1;  // invalid rows: every score masked
+    }
     // positions every valid row of the item may read without masking: <= the first row's position, < kv_hi
     const int full_lim = min(kv_hi - 1, cur.pos0 + cur.row0 / G);
-    lsk_f32x4 oacc[ATTN_QT][CT];
-    float m_run[ATTN_QT], l_run[ATTN_QT];
+    lsk_f32x4 oacc[QT][CT];
+    float m_run[QT], l_run[QT];
 #pragma unroll
-    for (int qt = 0; qt < ATTN_QT; ++qt) {
+    for (int qt = 0; qt < QT; ++qt) {
       m_run[qt] = -INFINITY;
       l_run[qt] = 0.f;
 #pragma unroll
@@ -157,34 +220,33 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     for (int sb = first_step(cur); sb < kv_hi; sb += ATTN_STEP * NW) {
       const int sn = sb + ATTN_STEP * NW;
       const bool more = sn < kv_hi;
-      lsk_f32x4 sacc[ATTN_QT][2];
+      const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
+      lsk_bf16x8 pb[QT];
+      float alpha[QT];
+      // per column tile: S^T = K Q^T, then the online-softmax update of its 16 query columns
 #pragma unroll
-      for (int qt = 0; qt < ATTN_QT; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         if (qt < nq) {
+          lsk_bf16x8 qf[KSTEPS];
+#pragma unroll
+          for (int j = 0; j < KSTEPS; ++j)
+            qf[j] = QREG ? qreg[j] : *(const lsk_bf16x8*)(&s_q[16 * qt + l16][32 * j + 8 * lg]);
+          lsk_f32x4 sacc[2];
 #pragma unroll
           for (int a = 0; a < 2; ++a) {
-            sacc[qt][a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
+            sacc[a] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int j = 0; j < KSTEPS; ++j)
-              sacc[qt][a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[qt][j], sacc[qt][a], 0, 0, 0);
+              sacc[a] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[a][j], qf[j], sacc[a], 0, 0, 0);
           }
-        }
-      }
-      if (more) load_k(kb, sn);  // the next step's K streams in during this step's softmax and P.V
-      const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
-      lsk_bf16x8 pb[ATTN_QT];
-      float alpha[ATTN_QT];
-#pragma unroll
-      for (int qt = 0; qt < ATTN_QT; ++qt) {
-        if (qt < nq) {
-          // sacc[qt][a][e] <-> position sb + 8 lg + 4 a + e, query column l16 of tile qt
+          // sacc[a][e] <-> position sb + 8 lg + 4 a + e, query column l16 of tile qt
           float sv[8];
           float mt = -INFINITY;
 #pragma unroll
           for (int a = 0; a < 2; ++a)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
-              float sc = sacc[qt][a][e] * scale_log2;
+              float sc = sacc[a][e] * scale_log2;
               if (!full) {
                 const int kp = sb + 8 * lg + 4 * a + e;
                 sc = (kp < kv_hi && kp <= qpos[qt]) ? sc : -INFINITY;
@@ -192,8 +254,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
               sv[4 * a + e] = sc;
               mt = fmaxf(mt, sc);
             }
-          mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-          mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+          mt = rows_max(mt);
           const float m_new = fmaxf(m_run[qt], mt);
           alpha[qt] = (m_new == m_run[qt]) ? 1.f : fast_exp2(m_run[qt] - m_new);
           float rs = 0.f;
@@ -203,14 +264,14 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
             rs += pe;
             pb[qt][e] = static_cast<__bf16>(pe);
           }
-          rs += __shfl_xor(rs, 16, 64);
-          rs += __shfl_xor(rs, 32, 64);
+          rs = rows_sum(rs);
           l_run[qt] = l_run[qt] * alpha[qt] + rs;
           m_run[qt] = m_new;
         }
       }
+      if (more) load_k(kb, sn);  // the next step's K streams in during this step's P.V
 #pragma unroll
-      for (int qt = 0; qt < ATTN_QT; ++qt) {
+      for (int qt = 0; qt < QT; ++qt) {
         if (qt < nq) {
 #pragma unroll
           for (int c = 0; c < CT; ++c) {
@@ -232,47 +293,67 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
       nxt = fetch(r + 2);
     }
     // ---- merge the waves in order: M = max m_w, e_w = exp2(m_w - M), L = sum e_w l_w, O = sum e_w O_w
+    //      (ATTN_MERGE_TILES column tiles per pass through s_o; the pass loop is unrolled, so a tile's
+    //      accumulators are dead after its pass)
 #pragma unroll
-    for (int qt = 0; qt < ATTN_QT; ++qt) {
-      if (qt < nq) {
-        if (lg == 0) {
-          s_ml[wave][0][16 * qt + l16] = m_run[qt];
-          s_ml[wave][1][16 * qt + l16] = l_run[qt];
-        }
+    for (int p0 = 0; p0 < QT; p0 += MT) {
+      if (p0 >= nq) break;
 #pragma unroll
-        for (int c = 0; c < CT; ++c)
-          *(float4*)(&s_o[wave][16 * qt + l16][16 * c + 4 * lg]) =
-              make_float4(oacc[qt][c][0], oacc[qt][c][1], oacc[qt][c][2], oacc[qt][c][3]);
-      }
-    }
-    __syncthreads();
-    for (int e = tid; e < done.nrows * D; e += 64 * NW) {
-      const int qr = e / D, d = e - qr * D;
-      float M = -INFINITY;
+      for (int qt = p0; qt < p0 + MT && qt < QT; ++qt) {
+        if (qt < nq) {
+          if (lg == 0) {
+            s_ml[wave][0][16 * qt + l16] = m_run[qt];
+            s_ml[wave][1][16 * qt + l16] = l_run[qt];
+          }
 #pragma unroll
-      for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][0][qr]);
-      float L = 0.f, O = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        const float mw = s_ml[w][0][qr];
-        const float ew = (mw == -INFINITY) ? 0.f : ((mw == M) ? 1.f : fast_exp2(mw - M));
-        L = L + ew * s_ml[w][1][qr];
-        O = O + ew * s_o[w][qr][d];
-      }
-      const int rr = done.row0 + qr;
-      const int tt = rr / G, gg = rr - tt * G;
-      if (done.part < 0) {
-        out[(long)(done.q_start + tt) * Hq * D + (long)(done.kvh * G + gg) * D + d] = f2bf(O / L);
-      } else {
-        const long slot = ((long)done.part * Hkv + done.kvh) * ATTN_ROWS + qr;
-        o_part[slot * D + d] = O;
-        if (d == 0) {
-          ml_part[slot * 2 + 0] = M;
-          ml_part[slot * 2 + 1] = L;
+          for (int c = 0; c < CT; ++c)
+            *(float4*)(&s_o[wave][16 * (qt - p0) + l16][16 * c + 4 * lg]) =
+                make_float4(oacc[qt][c][0], oacc[qt][c][1], oacc[qt][c][2], oacc[qt][c][3]);
         }
       }
+      __syncthreads();
+      // 4 consecutive d of one row per thread: the row's weights are formed once per 4 outputs, s_o is read as
+      // float4 (consecutive lanes, consecutive 16 bytes), each output keeps the order O = ((e_0 O_0 + e_1 O_1) + ...)
+      const int pr = min(done.nrows - 16 * p0, MR);
+      for (int e = tid; e < pr * (D / 4); e += 64 * NW) {
+        const int ql = e / (D / 4), d = 4 * (e - ql * (D / 4));
+        const int qr = 16 * p0 + ql;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, s_ml[w][0][qr]);
+        float L = 0.f;
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+          const float mw = s_ml[w][0][qr];
+          const float ew = (mw == -INFINITY) ? 0.f : ((mw == M) ? 1.f : fast_exp2(mw - M));
+          L = L + ew * s_ml[w][1][qr];
+          const float4 ow = *(const float4*)(&s_o[w][ql][d]);
+          O.x = O.x + ew * ow.x;
+          O.y = O.y + ew * ow.y;
+          O.z = O.z + ew * ow.z;
+          O.w = O.w + ew * ow.w;
+        }
+        const int rr = done.row0 + qr;
+        const int tt = rr / G, gg = rr - tt * G;
+        if (done.part < 0) {
+          uint2 pk;
+          pk.x = (uint32_t)f2bf(O.x / L) | ((uint32_t)f2bf(O.y / L) << 16);
+          pk.y = (uint32_t)f2bf(O.z / L) | ((uint32_t)f2bf(O.w / L) << 16);
+          *(uint2*)(out + (long)(done.q_start + tt) * Hq * D + (long)(done.kvh * G + gg) * D + d) = pk;
+        } else {
+          const long slot = ((long)done.part * Hkv + done.kvh) * ATTN_ROWS + qr;
+          *(float4*)(o_part + slot * D + d) = O;
+          if (d == 0) {
+            ml_part[slot * 2 + 0] = M;
+            ml_part[slot * 2 + 1] = L;
+          }
+        }
+      }
+      // every wave is past its steps, so s_q takes the next item's Q (its loads have landed during the merge)
+      if (p0 == 0 && cur.nrows > 0) q_store();
+      __syncthreads();  // the merge has read s_o / s_ml before they are written again; s_q is visible
     }
-    __syncthreads();  // the merge has read s_o / s_ml before the next item writes them
   }
 }
 
@@ -407,10 +488,13 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
 // Work order: a "family" is the set of query tiles of one (block, split); its tiles read the same K/V.
 // Families are sorted by size and dealt in chunks of 8 launch slots; slots of shorter families in a chunk are
 // padding items (nrows = 0), so sibling tiles sit 8 slots apart.  Output appended to `works` / `groups`.
-static int plan_into(const int32_t* blocks, int nb, int group, int split, std::vector<int32_t>& works,
+static int plan_into(const int32_t* blocks, int nb, int group, int split, int rows_cap, std::vector<int32_t>& works,
                      std::vector<int32_t>& groups, int* n_parts) {
   LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && split % ATTN_TILE == 0, LSK_ESHAPE,
               "lsk_attn_plan: bad arguments (split must be a positive multiple of %d)", ATTN_TILE);
+  LSK_REQUIRE(rows_cap > 0 && rows_cap % 16 == 0 && rows_cap <= ATTN_ROWS, LSK_ESHAPE,
+              "lsk_attn_plan: rows per item %d (a multiple of 16 up to %d)", rows_cap, ATTN_ROWS);
+  const int R = rows_cap;
   struct Item { int b, row0, nrows, lo, hi, part; };  // b: block index (its fields are copied into the record)
   thread_local std::vector<Item> items;               // families back to back
   thread_local std::vector<int> fam_off, fam_order, part_first, ns_of;
@@ -423,12 +507,12 @@ static int plan_into(const int32_t* blocks, int nb, int group, int split, std::v
     const int pos0 = blocks[b * 4 + 1], T = blocks[b * 4 + 2];
     LSK_REQUIRE(T >= 0 && pos0 >= 0, LSK_ESHAPE, "lsk_attn_plan: block %d has T=%d pos0=%d", b, T, pos0);
     const int rows = T * group;
-    const int nq = (rows + ATTN_ROWS - 1) / ATTN_ROWS;
+    const int nq = (rows + R - 1) / R;
     if (nq == 0) continue;
     // KV range of the family = the longest tile's range; each tile uses its own end
     int ns_max = 0;
     for (int qt = 0; qt < nq; ++qt) {
-      const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+      const int row0 = qt * R, nrows = rows - row0 < R ? rows - row0 : R;
       const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
       const int ns = (int)((kv_end + split - 1) / split);
       LSK_REQUIRE(ns <= ATTN_MAX_SPLITS || split >= (1 << 29), LSK_ESHAPE,
@@ -438,7 +522,7 @@ static int plan_into(const int32_t* blocks, int nb, int group, int split, std::v
     part_first.resize(nq);
     ns_of.resize(nq);
     for (int qt = 0; qt < nq; ++qt) {
-      const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+      const int row0 = qt * R, nrows = rows - row0 < R ? rows - row0 : R;
       const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
       ns_of[qt] = (int)((kv_end + split - 1) / split);
       if (ns_of[qt] > 1) {
@@ -455,7 +539,7 @@ static int plan_into(const int32_t* blocks, int nb, int group, int split, std::v
       fam_off.push_back((int)items.size());
       for (int qt = 0; qt < nq; ++qt) {
         if (sidx >= ns_of[qt]) continue;
-        const int row0 = qt * ATTN_ROWS, nrows = rows - row0 < ATTN_ROWS ? rows - row0 : ATTN_ROWS;
+        const int row0 = qt * R, nrows = rows - row0 < R ? rows - row0 : R;
         const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
         const long lo = (long)sidx * split;
         const long hi = (lo + split < kv_end) ? lo + split : kv_end;
@@ -494,12 +578,13 @@ static int plan_into(const int32_t* blocks, int nb, int group, int split, std::v
   return 0;
 }
 
-extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
-                             int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts) {
+extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int rows_cap, int32_t* works,
+                             int max_works, int32_t* groups, int max_groups, int* n_works, int* n_groups,
+                             int* n_parts) {
   LSK_REQUIRE(blocks && works && n_works && n_groups && n_parts, LSK_EARG, "lsk_attn_plan: null pointer");
   thread_local std::vector<int32_t> w, g;
   int np = 0;
-  const int rc = plan_into(blocks, nb, group, split, w, g, &np);
+  const int rc = plan_into(blocks, nb, group, split, rows_cap, w, g, &np);
   if (rc) return rc;
   const int nw = (int)(w.size() / 8), ng = (int)(g.size() / 8);
   LSK_REQUIRE(nw <= max_works, LSK_EWORKSPACE, "lsk_attn_plan: too many work items (max %d)", max_works);
@@ -511,6 +596,91 @@ extern "C" int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split
   *n_groups = ng;
   *n_parts = np;
   return 0;
+}
+
+// Rows per work item for one launch over n_slots persistent workgroups (one per CU).  The cap never changes a
+// result: a row's scores, softmax and P.V depend only on its own column, its position and the fixed splits.
+// It trades parallelism against KV re-reads: with few (block, KV head) pairs a launch is latency-bound and
+// splitting a block's rows over more workgroups shortens the longest item (16-row items run the one-tile
+// kernel, Q in registers; wider items the three-tile kernel, whose extra tiles cost every step and the merge);
+// once the items fill the chip, every extra item re-reads its block's KV and the launch is bandwidth-bound.
+// Estimate per cap = max(longest-first makespan of the items, KV bytes / sustained bandwidth) with item time
+//   one-tile kernel:   steps * c
+//   three-tile kernel: a + b (nq - 1) + steps (c + d [nq = 3])
+// (steps = 32-position steps per wave, 8 waves), constants fitted to graph-timed decode-shaped launches on
+// MI355X (contexts 300-1400, 1-9 query tokens of a 4-head group, 10-64 requests); equal estimates go to
+// the shorter makespan, then to the larger cap.
+#define ATTN_COST_ITEM_US 1.0
+#define ATTN_COST_TILE_US 3.5
+#define ATTN_COST_STEP_US 2.9
+#define ATTN_COST_STEP3_US 0.6
+#define ATTN_COST_BW_BYTES_PER_US 6.0e6
+static int rows_cap_for(const int32_t* blocks, int nb, int group, int split, int n_kv_heads, int head_dim,
+                        int n_slots) {
+  LSK_REQUIRE(nb >= 0 && group > 0 && split >= ATTN_TILE && n_kv_heads > 0 && head_dim > 0 && n_slots > 0,
+              LSK_ESHAPE, "lsk_attn_rows_cap: bad arguments");
+  auto items_at = [&](int R) {
+    long n = 0;
+    for (int b = 0; b < nb; ++b) {
+      const long rows = (long)blocks[b * 4 + 2] * group, end = (long)blocks[b * 4 + 1] + blocks[b * 4 + 2];
+      n += (rows + R - 1) / R * ((end + split - 1) / split);
+    }
+    return n * n_kv_heads;
+  };
+  if (items_at(ATTN_ROWS) >= 2L * n_slots) return ATTN_ROWS;  // several items per workgroup: fewest bytes wins
+  thread_local std::vector<double> cost;
+  thread_local std::vector<double> load;
+  const double pos_bytes = 4.0 * head_dim;  // K and V, bf16, one KV head
+  int best = ATTN_ROWS;
+  double best_t = 1e300, best_span = 1e300;
+  for (int R = ATTN_ROWS; R >= 16; R -= 16) {
+    cost.clear();
+    double bytes = 0.0;
+    for (int b = 0; b < nb; ++b) {
+      const int pos0 = blocks[b * 4 + 1], T = blocks[b * 4 + 2], rows = T * group;
+      for (int row0 = 0; row0 < rows; row0 += R) {
+        const int nrows = rows - row0 < R ? rows - row0 : R, nq = (nrows + 15) / 16;
+        const long kv_end = (long)pos0 + (row0 + nrows - 1) / group + 1;
+        for (long lo = 0; lo < kv_end; lo += split) {
+          const long len = (lo + split < kv_end ? lo + split : kv_end) - lo;
+          const long steps = (len + ATTN_STEP * ATTN_WAVES - 1) / (ATTN_STEP * ATTN_WAVES);
+          const double c = R == 16 ? steps * ATTN_COST_STEP_US
+                                   : ATTN_COST_ITEM_US + ATTN_COST_TILE_US * (nq - 1) +
+                                         steps * (ATTN_COST_STEP_US + (nq == 3 ? ATTN_COST_STEP3_US : 0.0));
+          for (int h = 0; h < n_kv_heads; ++h) cost.push_back(c);
+          bytes += (double)len * pos_bytes * n_kv_heads;
+        }
+      }
+    }
+    double span = 0.0;
+    if ((long)cost.size() <= n_slots) {
+      for (double c : cost) span = c > span ? c : span;
+    } else {
+      std::sort(cost.begin(), cost.end(), [](double a, double b) { return a > b; });
+      load.assign(n_slots, 0.0);  // min-heap of slot loads
+      for (double c : cost) {
+        std::pop_heap(load.begin(), load.end(), std::greater<double>());
+        load.back() += c;
+        std::push_heap(load.begin(), load.end(), std::greater<double>());
+      }
+      for (double l : load) span = l > span ? l : span;
+    }
+    const double bw = bytes / ATTN_COST_BW_BYTES_PER_US;
+    const double t = span > bw ? span : bw;
+    // equal estimates (bandwidth-bound, same bytes): the shorter makespan, i.e. the faster kernel
+    if (t < best_t * (1 - 1e-9) || (t <= best_t * (1 + 1e-9) && span < best_span)) {
+      best_t = t;
+      best_span = span;
+      best = R;
+    }
+  }
+  return best;
+}
+
+extern "C" int lsk_attn_rows_cap(const int32_t* blocks, int nb, int group, int split, int n_kv_heads, int head_dim,
+                                 int n_slots) {
+  LSK_REQUIRE(blocks || nb == 0, LSK_EARG, "lsk_attn_rows_cap: null pointer");
+  return rows_cap_for(blocks, nb, group, split, n_kv_heads, head_dim, n_slots);
 }
 
 // Static schedule of a plan over n_slots persistent workgroups (one per CU): items are (work, KV head) pairs
@@ -586,8 +756,8 @@ extern "C" int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_hea
 
 // One packed segment's kernel metadata from its blocks in packed order (host only; see include/lsk.h).
 extern "C" int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const int64_t* T, int nb, int group,
-                                int split, int n_kv_heads, int n_slots, int bucketing, int max_batch, int max_seq,
-                                int rope_len, int32_t* meta, long meta_cap, long* counts) {
+                                int split, int n_kv_heads, int head_dim, int n_slots, int bucketing, int max_batch,
+                                int max_seq, int rope_len, int32_t* meta, long meta_cap, long* counts) {
   LSK_REQUIRE(counts && (nb == 0 || (rows && pos0 && T)), LSK_EARG, "lsk_pack_segment: null pointer");
   LSK_REQUIRE(nb >= 0 && (bucketing == 0 || bucketing == 1), LSK_EARG, "lsk_pack_segment: bad arguments");
   long N = 0;
@@ -611,7 +781,9 @@ extern "C" int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const 
     off += T[b];
   }
   int np = 0, R = 0;
-  int rc = plan_into(blk.data(), nb, group, split, works, groups, &np);
+  const int cap = rows_cap_for(blk.data(), nb, group, split, n_kv_heads, head_dim, n_slots);
+  if (cap < 0) return cap;
+  int rc = plan_into(blk.data(), nb, group, split, cap, works, groups, &np);
   if (rc) return rc;
   const int nw = (int)(works.size() / 8), ng = (int)(groups.size() / 8);
   rc = schedule_into(works.data(), nw, n_kv_heads, n_slots, recs, &R);
@@ -639,7 +811,7 @@ extern "C" int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const 
   }
   for (int b = 0; b < nb; ++b) pairs += T[b] * pos0[b] + T[b] * (T[b] + 1) / 2;
   counts[0] = N; counts[1] = nw; counts[2] = ng; counts[3] = np; counts[4] = R; counts[5] = len;
-  counts[6] = kv_read; counts[7] = kv_padded; counts[8] = kv_gathered; counts[9] = pairs;
+  counts[6] = kv_read; counts[7] = kv_padded; counts[8] = kv_gathered; counts[9] = pairs; counts[10] = cap;
   if (meta == nullptr) return 0;
   LSK_REQUIRE(len <= meta_cap, LSK_EWORKSPACE, "lsk_pack_segment: %ld metadata words > %ld", len, meta_cap);
   int32_t* o = meta;
@@ -655,19 +827,22 @@ extern "C" int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const 
 }
 
 extern "C" size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim) {
-  // o_part [n_parts][Hkv][64][D] fp32, ml_part [n_parts][Hkv][64][2] fp32
+  // o_part [n_parts][Hkv][ATTN_ROWS][D] fp32, ml_part [n_parts][Hkv][ATTN_ROWS][2] fp32
   const size_t rows = (size_t)n_parts * n_kv_heads * ATTN_ROWS;
   return lsk_align_up(rows * head_dim * sizeof(float), 256) + lsk_align_up(rows * 2 * sizeof(float), 256);
 }
 
 extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache,
                                const int32_t* blocks, const int32_t* works, int n_works, const int32_t* groups,
-                               int n_groups, int n_parts, const int32_t* recs, int n_rounds, int n_slots, void* out,
+                               int n_groups, int n_parts, const int32_t* recs, int n_rounds, int n_slots,
+                               int rows_cap, void* out,
                                int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
                                size_t ws_bytes, void* stream) {
   LSK_REQUIRE(q && kcache && vcache && blocks && works && out, LSK_EARG, "lsk_ragged_attn: null pointer");
   LSK_REQUIRE(dtype != LSK_DTYPE_BF16 || n_works == 0 || (recs && n_rounds > 0 && n_slots > 0), LSK_EARG,
               "lsk_ragged_attn: the bf16 path needs a schedule (lsk_attn_schedule)");
+  LSK_REQUIRE(rows_cap > 0 && rows_cap % 16 == 0 && rows_cap <= ATTN_ROWS, LSK_EARG,
+              "lsk_ragged_attn: rows_cap %d (the plan's rows per item: 16, 32 or %d)", rows_cap, ATTN_ROWS);
   LSK_REQUIRE(n_heads > 0 && n_kv_heads > 0 && n_heads % n_kv_heads == 0 && max_seq > 0 && n_works >= 0,
               LSK_ESHAPE, "lsk_ragged_attn: bad shape");
   if (n_works == 0) return 0;
@@ -690,16 +865,18 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
     }
     const float scale_log2 = scale * 1.4426950408889634f;
     const dim3 pgrid(n_slots);
-    if (head_dim == 128)
-      attn_bf16_kernel<128><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                              (const uint16_t*)vcache, recs, n_rounds,
-                                                              (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
-                                                              max_seq, scale_log2);
-    else
-      attn_bf16_kernel<64><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,
-                                                             (const uint16_t*)vcache, recs, n_rounds,
-                                                             (uint16_t*)out, o_part, ml_part, G, n_kv_heads,
-                                                             max_seq, scale_log2);
+    // one column tile (items of <= 16 rows): Q in registers; otherwise three tiles with Q staged in LDS
+#define LSK_ATTN_LAUNCH(DD, QT)                                                                               \
+  attn_bf16_kernel<DD, QT><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,     \
+                                                              (const uint16_t*)vcache, recs, n_rounds,         \
+                                                              (uint16_t*)out, o_part, ml_part, G, n_kv_heads,  \
+                                                              max_seq, scale_log2)
+    if (head_dim == 128) {
+      if (rows_cap == 16) LSK_ATTN_LAUNCH(128, 1); else LSK_ATTN_LAUNCH(128, ATTN_QT);
+    } else {
+      if (rows_cap == 16) LSK_ATTN_LAUNCH(64, 1); else LSK_ATTN_LAUNCH(64, ATTN_QT);
+    }
+#undef LSK_ATTN_LAUNCH
     int rc = lsk_check_launch("lsk_ragged_attn");
     if (rc) return rc;
     if (n_groups > 0) {

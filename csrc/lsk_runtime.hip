@@ -185,12 +185,12 @@ extern "C" size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_p
 }
 
 // meta (device int32): [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8]
-// [recs n_slots*n_rounds*8] (lsk_attn_plan, lsk_attn_schedule)
+// [recs n_slots*n_rounds*8] (lsk_attn_plan with rows_cap, lsk_attn_schedule)
 // capture (host array of n_layers device pointers or NULL): capture[i] != NULL receives the output of
 // layer i (the hidden state entering exit layer i + 1; solutions/packed.py:190-195).
 extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
                                   const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, int n_rounds,
-                                  int n_slots, void* workspace, size_t ws_bytes, void* const* capture,
+                                  int n_slots, int rows_cap, void* workspace, size_t ws_bytes, void* const* capture,
                                   double attn_bytes, double attn_flops, void* stream) {
   Model* m = get(handle);
   LSK_REQUIRE(m != nullptr, LSK_EARG, "lsk_forward_layers: bad handle %ld", handle);
@@ -263,8 +263,8 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
                                         m->max_batch, m->max_seq, stream));
       LSK_PROF2(LSK_PROF_ATTN, attn_bytes, attn_flops,
                 lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts,
-                                recs, n_rounds, n_slots, attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes,
-                                stream));
+                                recs, n_rounds, n_slots, rows_cap, attn, m->n_heads, m->n_kv_heads, m->head_dim,
+                                m->max_seq, scale, part, part_bytes, stream));
       LSK_PROF2(LSK_PROF_GEMM_O, es_d * (dimd * qd + Nd * qd) + pbytes(m->ks_o, dimd), 2.0 * Nd * qd * dimd,
                 lsk_gemm_partial(attn, qd, m->wo[i], qd, P, N, m->dim, qd, m->ks_o, stream));
       const void* xi = (i == start) ? x_in : x_out;
@@ -309,7 +309,8 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
                              m->n_heads, m->n_kv_heads, m->head_dim, m->max_batch, m->max_seq, stream));
     LSK_PROF(LSK_PROF_ATTN, attn_bytes, attn_flops,
              lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts, recs,
-                             n_rounds, n_slots, attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes, stream));
+                             n_rounds, n_slots, rows_cap, attn, m->n_heads, m->n_kv_heads, m->head_dim, m->max_seq, scale,
+                             part, part_bytes, stream));
     LSK_PROF(LSK_PROF_GEMM_O, gemm_bytes(Nd, dimd, qd, dimd, true), 2.0 * Nd * qd * dimd,
              lsk_gemm(m->dtype, attn, qd, m->wo[i], qd, x_out, m->dim, xi, m->dim, N, m->dim, qd, LSK_EPI_RESIDUAL, 0,
                       stream));

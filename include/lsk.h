@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 4
+#define LSK_ABI_VERSION 5
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -56,12 +56,20 @@ int lsk_kv_append(int dtype, const void* k, const void* v, void* kcache, void* v
                   void* stream);
 
 /* Host-side planner for lsk_ragged_attn (host pointers, no GPU work).
- * blocks: int32 [nb][4] = {q_start, pos0, T, row}.  Writes work items int32 [n][8] and combine
- * groups int32 [n][8]; `split` = KV positions per split (LSK_ATTN_SPLIT for bf16; >= the longest
- * context, e.g. 1<<30, for the unsplit fp32 path).  Mirrors the per-bucket metadata of
- * solutions/packed.py:109-138 (build_packed) without the dense masks. */
-int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int32_t* works, int max_works,
+ * blocks: int32 [nb][4] = {q_start, pos0, T, row}.  Writes work items int32 [n][8] (each <= rows_cap of a
+ * block's T * group query rows over one KV split) and combine groups int32 [n][8]; `split` = KV positions per
+ * split (LSK_ATTN_SPLIT for bf16; >= the longest context, e.g. 1<<30, for the unsplit fp32 path);
+ * rows_cap = 16, 32 or 48 (lsk_attn_rows_cap; the outputs do not depend on it).  Mirrors the per-bucket
+ * metadata of solutions/packed.py:109-138 (build_packed) without the dense masks. */
+int lsk_attn_plan(const int32_t* blocks, int nb, int group, int split, int rows_cap, int32_t* works, int max_works,
                   int32_t* groups, int max_groups, int* n_works, int* n_groups, int* n_parts);
+
+/* Rows per work item for a launch of these blocks over n_slots persistent workgroups (host only): 16, 32 or
+ * 48, the cap with the smallest estimated time (latency-bound launches split a block's rows over more
+ * workgroups, bandwidth-bound ones keep them together so the KV is read once); negative on bad arguments.
+ * Has no reference counterpart (the reference runs one SDPA per bucket). */
+int lsk_attn_rows_cap(const int32_t* blocks, int nb, int group, int split, int n_kv_heads, int head_dim,
+                      int n_slots);
 
 /* Static schedule of a plan's (work, KV head) items over n_slots persistent workgroups (host pointers):
  * longest first to the least-loaded slot.  Writes recs int32 [n_slots][n_rounds][8]: slot s's items in
@@ -74,16 +82,16 @@ int lsk_attn_schedule(const int32_t* works, int n_works, int n_kv_heads, int n_s
 
 /* One packed segment's kernel metadata in one host call (no GPU work): blocks (rows, pos0, T; int64, nb of
  * them) already in packed order -> meta int32 [rows N][pos N][blocks nb*4][works nw*8][groups ng*8]
- * [recs n_slots*n_rounds*8], exactly what lsk_attn_plan(split) + lsk_attn_schedule give, plus the token
- * row / position expansion.  counts[10] = {N, n_works, n_groups, n_parts, n_rounds, meta_len, kv_read,
- * kv_read_padded, kv_gathered, attended (query, position) pairs}; the kv_* figures are the reference's
- * bucket accounting (bucketing 0 = "exact": runs of equal T, 1 = "pad": one bucket).  Blocks outside
- * [0, max_batch) x [0, min(max_seq, rope_len)) are rejected with LSK_ESHAPE.  meta == NULL: counts only;
- * meta_cap too small: LSK_EWORKSPACE with counts written.  Replaces solutions/packed.py:81-139 (build_packed's
- * ordering bookkeeping, metadata and accounting) for the native kernels. */
+ * [recs n_slots*n_rounds*8], exactly what lsk_attn_rows_cap + lsk_attn_plan(split, cap) + lsk_attn_schedule
+ * give, plus the token row / position expansion.  counts[11] = {N, n_works, n_groups, n_parts, n_rounds,
+ * meta_len, kv_read, kv_read_padded, kv_gathered, attended (query, position) pairs, rows_cap}; the kv_* figures
+ * are the reference's bucket accounting (bucketing 0 = "exact": runs of equal T, 1 = "pad": one bucket).
+ * Blocks outside [0, max_batch) x [0, min(max_seq, rope_len)) are rejected with LSK_ESHAPE.  meta == NULL:
+ * counts only; meta_cap too small: LSK_EWORKSPACE with counts written.  Replaces solutions/packed.py:81-139
+ * (build_packed's ordering bookkeeping, metadata and accounting) for the native kernels. */
 int lsk_pack_segment(const int64_t* rows, const int64_t* pos0, const int64_t* T, int nb, int group, int split,
-                     int n_kv_heads, int n_slots, int bucketing, int max_batch, int max_seq, int rope_len,
-                     int32_t* meta, long meta_cap, long* counts);
+                     int n_kv_heads, int head_dim, int n_slots, int bucketing, int max_batch, int max_seq,
+                     int rope_len, int32_t* meta, long meta_cap, long* counts);
 
 /* Workspace bytes for the split partials of a plan with n_parts partial slots. */
 size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
@@ -91,13 +99,16 @@ size_t lsk_attn_workspace_bytes(int n_parts, int n_kv_heads, int head_dim);
 /* Ragged verify/decode attention: a query at position p of row r attends cache[r, :, 0..p].
  * q [N, Hq, D], K: bf16 fragment-major [B, Hkv, S/32, D/16, 64, 8] / fp32 [B, Hkv, S, D],
  * V blocked-transposed [B, Hkv, S/32, D, 32], out [N, Hq*D].  scale = 1/sqrt(D) for the reference's SDPA default.
- * bf16 runs n_slots persistent workgroups over the schedule records (recs, n_rounds); fp32 reads works.
+ * bf16 runs n_slots persistent workgroups over the schedule records (recs, n_rounds); rows_cap is the cap the
+ * plan was made with (16: one-tile kernel, Q in registers; 32 / 48: three-tile kernel, Q in LDS); the two
+ * kernels give bitwise equal outputs.  fp32 reads works.
  * Replaces solutions/packed.py:142-166 (_attend: per-bucket gather + masked SDPA + scatter)
  * and common/model.py:352-364 (the padded path's masked SDPA). */
 int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
                     const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
-                    const int32_t* recs, int n_rounds, int n_slots, void* out, int n_heads, int n_kv_heads,
-                    int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes, void* stream);
+                    const int32_t* recs, int n_rounds, int n_slots, int rows_cap, void* out, int n_heads,
+                    int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes,
+                    void* stream);
 
 /* bf16 weight storage of the GEMMs: W [N, K] row-major (ldw) <-> fragment-major Wp (N*K elements, no
  * padding): fragment (g, j) = rows 16g..16g+15 x k 32j..32j+31 is 1 KiB, lane l's 8 elements being
@@ -197,13 +208,13 @@ size_t lsk_segment_workspace_bytes(long handle, int n_tokens, int n_parts);
 
 /* Layers [start, end) over n_tokens packed tokens: x_out = layers(x_in) (x_in is not modified).
  * meta: device int32 [rows N][pos N][blocks nb*4][works n_works*8][groups n_groups*8]
- * [recs n_slots*n_rounds*8] (see lsk_attn_plan, lsk_attn_schedule).
+ * [recs n_slots*n_rounds*8] (see lsk_attn_plan, lsk_attn_schedule); rows_cap as for lsk_ragged_attn.
  * capture: NULL or a host array of n_layers device pointers; capture[i] != NULL receives layer i's output
  * (solutions/packed.py:190-195).  Replaces packed_layers (solutions/packed.py:188-196). */
 int lsk_forward_layers(long handle, const void* x_in, void* x_out, int n_tokens, int start, int end,
                        const int32_t* meta, int nb, int n_works, int n_groups, int n_parts, int n_rounds, int n_slots,
-                       void* workspace, size_t ws_bytes, void* const* capture, double attn_bytes, double attn_flops,
-                       void* stream);
+                       int rows_cap, void* workspace, size_t ws_bytes, void* const* capture, double attn_bytes,
+                       double attn_flops, void* stream);
 
 /* ---- optional per-launch profiling (no reference counterpart: measurement support) ----
  * When enabled, the layer runner (and callers using lsk_prof_start/stop around their own launches)

@@ -59,9 +59,12 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_pack_weight(8, 64, 16, 40, 64, None) == -2                          # N % 16 != 0
     assert lib.lsk_unpack_weight(8, 16, 64, 64, 48, None) == -2                        # K % 32 != 0
     assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
-    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 8, 32, 8, 96, 64, 0.1, None, 0, None) == -3
-    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, 0, 0, 8, 32, 8, 128, 64, 0.1, None, 0,
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 48, 8, 32, 8, 96, 64, 0.1, None, 0,
+                               None) == -3                                            # head_dim 96
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, 0, 0, 48, 8, 32, 8, 128, 64, 0.1, None, 0,
                                None) == -1                                            # bf16 without a schedule
+    assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 24, 8, 32, 8, 128, 64, 0.1, None, 0,
+                               None) == -1                                            # rows per item not 16/32/48
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
 
 
@@ -158,6 +161,15 @@ def test_attention_schedule_covers_every_item_once_longest_first(n_slots):
     assert max(loads) <= sum(loads) / n_slots + max(cost(i) for i in flat)
     again, R2 = lsk.attn_schedule(works, Hkv, n_slots)
     assert R2 == R and np.array_equal(again.reshape(n_slots, R, 8), recs)   # deterministic
+
+
+def test_attention_rows_per_item_policy():
+    """Few (block, KV head) pairs: rows split over more workgroups; a full chip: 48-row items (KV read once)."""
+    lsk = _lsk()
+    few = np.array([(9 * i, 700, 9, i) for i in range(4)], dtype=np.int32)          # 4 verify blocks, 36 rows
+    assert lsk.attn_rows_cap(few, 4, lsk.ATTN_SPLIT, 8, 128, 256) == 16
+    many = np.array([(9 * i, 1500, 9, i) for i in range(256)], dtype=np.int32)      # 2048 pairs on 256 CUs
+    assert lsk.attn_rows_cap(many, 4, lsk.ATTN_SPLIT, 8, 128, 256) == 48
 
 
 def test_attention_plan_places_sibling_tiles_eight_slots_apart():

@@ -240,18 +240,21 @@ def _attn_case(seed, dtype, B, Hq, Hkv, D, S, blocks):
     return q, kc, vc, np.array(tab, dtype=np.int32), ref
 
 
-def _run_attn(lsk, cuda, q, kc, vc, tab, split):
+def _run_attn(lsk, cuda, q, kc, vc, tab, split, rows_cap=None):
+    """rows_cap None: the launch policy's choice (lsk_attn_rows_cap)."""
     Hq, D = q.shape[1], q.shape[2]
     Hkv = kc.shape[1]
-    works, groups, n_parts = lsk.attn_plan(tab, Hq // Hkv, split)
+    n_slots = lsk.cu_count(cuda)
+    if rows_cap is None:
+        rows_cap = lsk.attn_rows_cap(tab, Hq // Hkv, split, Hkv, D, n_slots)
+    works, groups, n_parts = lsk.attn_plan(tab, Hq // Hkv, split, rows_cap)
     out = torch.empty(q.shape[0], Hq * D, dtype=q.dtype, device=cuda)
     ws = torch.empty(max(lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=cuda)
     gdev = torch.from_numpy(groups).to(cuda) if len(groups) else None
-    n_slots = lsk.cu_count(cuda)
     recs, n_rounds = lsk.attn_schedule(works, Hkv, n_slots)
     lsk.ragged_attn(q.to(cuda), _kstore(lsk, kc).to(cuda), lsk.v_to_blocked(vc).to(cuda), torch.from_numpy(tab).to(cuda),
                     torch.from_numpy(works).to(cuda), len(works), gdev, len(groups), n_parts, out, Hq,
-                    1.0 / math.sqrt(D), ws, torch.from_numpy(recs).to(cuda), n_rounds, n_slots)
+                    1.0 / math.sqrt(D), ws, torch.from_numpy(recs).to(cuda), n_rounds, n_slots, rows_cap)
     return out.cpu()
 
 
@@ -276,6 +279,17 @@ def test_ragged_attention_bf16_matches_brute_force(cuda, case):
     err = (got - ref).abs()
     assert err.max() < 2e-2, err.max()
     assert err.mean() < 3e-3, err.mean()
+
+
+@pytest.mark.parametrize("case", range(len(ATTN_CASES)))
+def test_ragged_attention_rows_per_item_never_changes_the_output(cuda, case):
+    """16-row items (one-tile kernel, Q in registers), 32- and 48-row items (three-tile kernel, Q in LDS):
+    bitwise equal outputs, with splits, in every shape."""
+    lsk = _lsk()
+    B, Hq, Hkv, D, S, blocks = ATTN_CASES[case]
+    q, kc, vc, tab, _ = _attn_case(40 + case, BF16, B, Hq, Hkv, D, S, blocks)
+    outs = {cap: _run_attn(lsk, cuda, q, kc, vc, tab, ATTN_TEST_SPLIT, cap) for cap in (16, 32, 48)}
+    assert torch.equal(outs[16], outs[48]) and torch.equal(outs[32], outs[48])
 
 
 def test_ragged_attention_f32_matches_brute_force(cuda):

@@ -20,8 +20,8 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
-ATTN_ROWS = 32            # query rows per attention work item
-ABI_VERSION = 4
+ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
+ABI_VERSION = 5
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -31,12 +31,13 @@ _SIGS = {
     "lsk_rmsnorm": (_I, [_I, _P, _P, _P, _I, _I, _F, _L, _L, _P]),
     "lsk_rope_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lsk_kv_append": (_I, [_I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
-    "lsk_attn_plan": (_I, [_P, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
+    "lsk_attn_plan": (_I, [_P, _I, _I, _I, _I, _P, _I, _P, _I, _P, _P, _P]),
+    "lsk_attn_rows_cap": (_I, [_P, _I, _I, _I, _I, _I, _I]),
     "lsk_attn_schedule": (_I, [_P, _I, _I, _I, _P, _I, _P]),
-    "lsk_pack_segment": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
+    "lsk_pack_segment": (_I, [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _L, _P]),
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
-    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _P, _I, _I, _I, _I, _F, _P, _Z,
-                             _P]),
+    "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _P, _I, _I, _I, _I, _F, _P,
+                             _Z, _P]),
     "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
     "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
@@ -55,8 +56,8 @@ _SIGS = {
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
     "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
-    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _P, _Z, _P, ctypes.c_double,
-                                ctypes.c_double, _P]),
+    "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P,
+                                ctypes.c_double, ctypes.c_double, _P]),
     "lsk_prof_enable": (_I, [_I]),
     "lsk_prof_start": (_I, [_I, ctypes.c_double, ctypes.c_double, _P]),
     "lsk_prof_stop": (_I, [_P]),
@@ -271,21 +272,32 @@ def kv_append(k, v, kcache, vcache, rows_i32, pos_i32):
                                 _ptr(pos_i32), k.shape[0], Hkv, D, B, S, _stream()), "lsk_kv_append")
 
 
-def attn_plan(blocks: np.ndarray, group: int, split: int):
-    """blocks int32 [nb, 4] = (q_start, pos0, T, row) -> (works [n,8], groups [n,8], n_parts)."""
+def attn_plan(blocks: np.ndarray, group: int, split: int, rows_cap: int = ATTN_ROWS):
+    """blocks int32 [nb, 4] = (q_start, pos0, T, row) -> (works [n,8], groups [n,8], n_parts); work items of at
+    most rows_cap (16, 32 or 48) query rows."""
     blocks = np.ascontiguousarray(blocks, dtype=np.int32)
     nb = blocks.shape[0]
-    rows = int(((blocks[:, 2].astype(np.int64) * group + ATTN_ROWS - 1) // ATTN_ROWS).sum()) if nb else 0
+    rows = int(((blocks[:, 2].astype(np.int64) * group + rows_cap - 1) // max(rows_cap, 1)).sum()) if nb else 0
     max_ctx = int((blocks[:, 1].astype(np.int64) + blocks[:, 2]).max()) if nb else 0
     max_works = 8 * max(1, rows * max(1, (max_ctx + split - 1) // split)) + 64   # XCD-order padding
     max_groups = max(1, rows)
     works = np.zeros((max_works, 8), dtype=np.int32)
     groups = np.zeros((max_groups, 8), dtype=np.int32)
     nw, ng, npart = ctypes.c_int(0), ctypes.c_int(0), ctypes.c_int(0)
-    _check(load().lsk_attn_plan(blocks.ctypes.data, nb, group, split, works.ctypes.data, max_works,
+    _check(load().lsk_attn_plan(blocks.ctypes.data, nb, group, split, rows_cap, works.ctypes.data, max_works,
                                 groups.ctypes.data, max_groups, ctypes.byref(nw), ctypes.byref(ng),
                                 ctypes.byref(npart)), "lsk_attn_plan")
     return works[:nw.value], groups[:ng.value], npart.value
+
+
+def attn_rows_cap(blocks: np.ndarray, group: int, split: int, n_kv_heads: int, head_dim: int, n_slots: int) -> int:
+    """Rows per attention work item (16, 32 or 48) for a launch of these blocks over n_slots workgroups."""
+    blocks = np.ascontiguousarray(blocks, dtype=np.int32)
+    rc = load().lsk_attn_rows_cap(blocks.ctypes.data if len(blocks) else None, len(blocks), group, split,
+                                  n_kv_heads, head_dim, n_slots)
+    if rc < 0:
+        _check(rc, "lsk_attn_rows_cap")
+    return rc
 
 
 _CU_COUNT: dict = {}
@@ -319,13 +331,14 @@ def attn_schedule(works: np.ndarray, n_kv_heads: int, n_slots: int):
 
 
 _PACK_BUF = [np.zeros(1 << 16, dtype=np.int32)]
-_PACK_COUNTS = np.zeros(10, dtype=np.int64)
+_PACK_COUNTS = np.zeros(11, dtype=np.int64)
 
 
 def pack_segment(rows: np.ndarray, pos0: np.ndarray, T: np.ndarray, group: int, split: int, n_kv_heads: int,
-                 n_slots: int, bucketing: int, max_batch: int, max_seq: int, rope_len: int):
+                 head_dim: int, n_slots: int, bucketing: int, max_batch: int, max_seq: int, rope_len: int):
     """lsk_pack_segment over int64 block arrays in packed order -> (meta int32 [meta_len] (a fresh array),
-    counts (N, n_works, n_groups, n_parts, n_rounds, meta_len, kv_read, kv_read_padded, kv_gathered, pairs)).
+    counts (N, n_works, n_groups, n_parts, n_rounds, meta_len, kv_read, kv_read_padded, kv_gathered, pairs,
+    rows_cap)).
     Out-of-range blocks raise ValueError (the reference's build_packed behaviour)."""
     lib = load()
     nb = len(T)
@@ -335,9 +348,9 @@ def pack_segment(rows: np.ndarray, pos0: np.ndarray, T: np.ndarray, group: int, 
     cnt = _PACK_COUNTS
     for _ in range(2):
         buf = _PACK_BUF[0]
-        rc = lib.lsk_pack_segment(r.ctypes.data, p.ctypes.data, t.ctypes.data, nb, group, split, n_kv_heads, n_slots,
-                                  bucketing, max_batch, max_seq, rope_len, buf.ctypes.data, buf.size,
-                                  cnt.ctypes.data)
+        rc = lib.lsk_pack_segment(r.ctypes.data, p.ctypes.data, t.ctypes.data, nb, group, split, n_kv_heads,
+                                  head_dim, n_slots, bucketing, max_batch, max_seq, rope_len, buf.ctypes.data,
+                                  buf.size, cnt.ctypes.data)
         if rc == -4:                                   # LSK_EWORKSPACE: grow to the reported length and retry
             _PACK_BUF[0] = np.zeros(int(cnt[5]) * 2, dtype=np.int32)
             continue
@@ -353,8 +366,9 @@ def attn_workspace_bytes(n_parts: int, n_kv_heads: int, head_dim: int) -> int:
 
 
 def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out, n_heads,
-                scale, workspace=None, recs_dev=None, n_rounds=0, n_slots=0):
-    """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32]."""
+                scale, workspace=None, recs_dev=None, n_rounds=0, n_slots=0, rows_cap=ATTN_ROWS):
+    """kcache: K cache storage (k_dims); vcache: the blocked-transposed V storage [B, Hkv, S/32, D, 32];
+    rows_cap: the cap the plan was made with."""
     _dev(q, kcache, vcache, blocks_dev, works_dev, out)
     _check_kcache(q.dtype, kcache)
     B_, H_, S_, D_ = k_dims(kcache)
@@ -363,7 +377,7 @@ def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     _check(load().lsk_ragged_attn(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
                                   _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(recs_dev),
-                                  n_rounds, n_slots, _ptr(out), n_heads, Hkv, D, S, float(scale),
+                                  n_rounds, n_slots, rows_cap, _ptr(out), n_heads, Hkv, D, S, float(scale),
                                   _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
 
 
@@ -469,12 +483,13 @@ class NativeModel:
         return int(load().lsk_segment_workspace_bytes(self.handle, n_tokens, n_parts))
 
     def forward_layers(self, x_in, x_out, n_tokens, start, end, meta_dev, nb, n_works, n_groups, n_parts, n_rounds,
-                       n_slots, workspace, capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
+                       n_slots, rows_cap, workspace, capture_ptrs=None, attn_bytes=0.0, attn_flops=0.0):
         _dev(x_in, x_out, meta_dev, workspace)
         cap = _ptr_array(capture_ptrs) if capture_ptrs is not None else None
         ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
         _check(load().lsk_forward_layers(self.handle, _ptr(x_in), _ptr(x_out), n_tokens, start, end, _ptr(meta_dev),
-                                         nb, n_works, n_groups, n_parts, n_rounds, n_slots, _ptr(workspace), ws_bytes,
+                                         nb, n_works, n_groups, n_parts, n_rounds, n_slots, rows_cap, _ptr(workspace),
+                                         ws_bytes,
                                          cap,
                                          float(attn_bytes), float(attn_flops), _stream()),
                "lsk_forward_layers")

@@ -344,7 +344,7 @@ class EESDEngine:
             nd, nex = len(drf_src), N
             if not deep and self.graphs is not None and not _lsk.Profiler.enabled:
                 # shallow-only step of a fixed shape: staged at fixed addresses, replayed as a graph below
-                gkey = (N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_rounds, pb.n_slots, nd, k)
+                gkey = (N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_rounds, pb.n_slots, pb.rows_cap, nd, k)
                 (pb.meta, sel_t, drf_src_t, drf_dst_t), gentry = self.graphs.stage(
                     gkey, [pb.meta_host, sel, drf_src, drf_dst])
             else:

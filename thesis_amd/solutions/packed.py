@@ -108,6 +108,7 @@ class PackedBatch:
     n_parts: int = 0
     n_rounds: int = 0
     n_slots: int = 0
+    rows_cap: int = 48                     # query rows per attention work item (lsk_attn_rows_cap)
     attn_bytes: float = 0.0
     attn_flops: float = 0.0
     _model: object = None
@@ -195,15 +196,15 @@ def build_packed_arrays(model, rows, pos0, T, bucketing: str = "exact", tags: Op
     if cache is None:
         raise ValueError("allocate_cache() first")
     n_slots = _lsk.cu_count(model.device)
-    meta, cnt = _lsk.pack_segment(rws, p0, Ts, model.group, cache.attn_split, model.cfg.n_kv_heads, n_slots,
-                                  0 if bucketing == "exact" else 1, cache.max_batch, cache.max_seq,
-                                  model.rope_cos.shape[0])
-    N, nw, ng, n_parts, n_rounds, _, kv_read, kv_padded, kv_gathered, pairs = cnt
+    meta, cnt = _lsk.pack_segment(rws, p0, Ts, model.group, cache.attn_split, model.cfg.n_kv_heads,
+                                  model.cfg.head_dim, n_slots, 0 if bucketing == "exact" else 1, cache.max_batch,
+                                  cache.max_seq, model.rope_cos.shape[0])
+    N, nw, ng, n_parts, n_rounds, _, kv_read, kv_padded, kv_gathered, pairs, rows_cap = cnt
     nb = len(Ts)
     offsets = qo_indptr(Ts)
     pb = PackedBatch(offsets, meta[N:2 * N].astype(np.int64), meta[:N].astype(np.int64), rws, p0, Ts, n_tokens=N,
                      nb=nb, n_works=nw, n_groups=ng, n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots,
-                     _model=model, meta_host=meta, kv_read=kv_read, kv_read_padded=kv_padded,
+                     rows_cap=rows_cap, _model=model, meta_host=meta, kv_read=kv_read, kv_read_padded=kv_padded,
                      kv_gathered=kv_gathered, _bucketing=bucketing)
     if bucketing == "exact" and nb:
         pb._bounds = np.concatenate([[0], np.flatnonzero(np.diff(Ts)) + 1, [nb]])
@@ -257,13 +258,16 @@ def _pack(model, rws: np.ndarray, pos0: np.ndarray, Ts: np.ndarray, bounds: np.n
     rows_h = np.repeat(rws, Ts)
     blk = np.stack([offsets[:-1], pos0, Ts, rws], axis=1).astype(np.int32) if nb else np.zeros((0, 4), np.int32)
     split = model.cache.attn_split
-    works, grps, n_parts = _lsk.attn_plan(blk, model.group, split) if nb else (np.zeros((0, 8), np.int32),) * 2 + (0,)
     n_slots = _lsk.cu_count(model.device)
+    cap = _lsk.attn_rows_cap(blk, model.group, split, model.cfg.n_kv_heads, model.cfg.head_dim, n_slots)
+    works, grps, n_parts = (_lsk.attn_plan(blk, model.group, split, cap) if nb
+                            else (np.zeros((0, 8), np.int32),) * 2 + (0,))
     recs, n_rounds = _lsk.attn_schedule(works, model.cfg.n_kv_heads, n_slots)
     meta = np.concatenate([rows_h.astype(np.int32), pos_h.astype(np.int32), blk.ravel(), works.ravel(),
                            grps.ravel(), recs]).astype(np.int32)
     pb = PackedBatch(offsets, pos_h, rows_h, rws, pos0, Ts, n_tokens=N, nb=nb, n_works=len(works),
-                     n_groups=len(grps), n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots, _model=model,
+                     n_groups=len(grps), n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots, rows_cap=cap,
+                     _model=model,
                      meta_host=meta, _bounds=bounds, _bucketing=bucketing)
     _attn_work(pb, model, int((pos0 + Ts).sum()), int((Ts * pos0 + Ts * (Ts + 1) // 2).sum()))
     if upload_meta and N:
@@ -335,7 +339,7 @@ def packed_layers(model, x: torch.Tensor, pb: PackedBatch, start: int, end: int,
                     cap_ptrs[k - 1] = t.data_ptr()
     ws = model.workspace(model.native.workspace_bytes(N, pb.n_parts))
     model.native.forward_layers(x, out, N, start, end, pb.meta, pb.nb, pb.n_works, pb.n_groups, pb.n_parts,
-                                pb.n_rounds, pb.n_slots, ws, cap_ptrs, pb.attn_bytes, pb.attn_flops)
+                                pb.n_rounds, pb.n_slots, pb.rows_cap, ws, cap_ptrs, pb.attn_bytes, pb.attn_flops)
     return out
 
 
