@@ -160,30 +160,40 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
       }
     }
   };
-  auto ldkv = [&](const uint16_t* p) -> lsk_bf16x8 {
-    return __builtin_bit_cast(lsk_bf16x8, __builtin_nontemporal_load((const lsk_i32x4*)p));
+  // K / V fragments come through buffer loads over the item's (row, KV head) stripe of S * D elements: the
+  // descriptor and every uniform offset live in SGPRs, a lane adds one 32-bit offset, so no 64-bit per-lane
+  // addresses occupy VGPRs.  Non-temporal (aux 2): each byte is read once per launch.
+  auto stripe = [&](const uint16_t* base) {
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, S * D * 2, LSK_BUFFER_RSRC_WORD3);
   };
+  auto ldkv = [&](__amdgpu_buffer_rsrc_t rs, int vo, int so) -> lsk_bf16x8 {
+    return __builtin_bit_cast(lsk_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 2));
+  };
+  const int k_vo = 16 * lane;                       // bytes: lane l's 8 elements of a 1 KiB K fragment
+  const int v_vo = 2 * (32 * l16 + 8 * lg);         // bytes: column l16's positions 8 lg .. 8 lg + 7 of a V^T row
+  constexpr int STRIDE = ATTN_STEP * NW;  // positions between a wave's consecutive steps
   lsk_bf16x8 kf[2][KSTEPS];
   lsk_bf16x8 vf[CT];
   // fragment-major K cache: fragment (a, j) of the step's 32-position block is 1 KiB in lane order
-  auto load_k = [&](const uint16_t* kb, int sb) {
+  auto load_k = [&](__amdgpu_buffer_rsrc_t kr, int sb) {
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(kb + (long)sb * D + (a * KSTEPS + j) * 512 + 8 * lane);
+      for (int j = 0; j < KSTEPS; ++j) kf[a][j] = ldkv(kr, k_vo, 2 * (sb * D + (a * KSTEPS + j) * 512));
   };
-  auto load_v = [&](const uint16_t* vb, int sb) {
+  auto load_v = [&](__amdgpu_buffer_rsrc_t vr, int sb) {
 #pragma unroll
-    for (int c = 0; c < CT; ++c) vf[c] = ldkv(vb + (long)sb * D + (16 * c + l16) * 32 + 8 * lg);
+    for (int c = 0; c < CT; ++c) vf[c] = ldkv(vr, v_vo, 2 * (sb * D + 16 * c * 32));
   };
   // a wave's steps of an item: 32-position steps wave, wave + NW, ... of the item's range, in order
   auto first_step = [&](const Item& it) { return it.kv_lo + ATTN_STEP * wave; };
   auto issue_first = [&](const Item& it) {
     q_load(it);
     const int sb = first_step(it);
+    const auto kr = stripe(kbase_of(it)), vr = stripe(vbase_of(it));
     if (sb < it.kv_hi) {
-      load_k(kbase_of(it), sb);
-      load_v(vbase_of(it), sb);
+      load_k(kr, sb);
+      load_v(vr, sb);
     }
   };
 
@@ -198,8 +208,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   for (int r = 0; cur.nrows > 0; ++r) {
     const int nq = (cur.nrows + 15) >> 4;  // column tiles in use (wave-uniform)
     const int kv_hi = cur.kv_hi;
-    const uint16_t* kb = kbase_of(cur);
-    const uint16_t* vb = vbase_of(cur);
+    const auto kb = stripe(kbase_of(cur)), vb = stripe(vbase_of(cur));
     int qpos[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -217,8 +226,8 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
 #pragma unroll
       for (int c = 0; c < CT; ++c) oacc[qt][c] = (lsk_f32x4){0.f, 0.f, 0.f, 0.f};
     }
-    for (int sb = first_step(cur); sb < kv_hi; sb += ATTN_STEP * NW) {
-      const int sn = sb + ATTN_STEP * NW;
+    for (int sb = first_step(cur); sb < kv_hi; sb += STRIDE) {
+      const int sn = sb + STRIDE;
       const bool more = sn < kv_hi;
       const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
       lsk_bf16x8 pb[QT];

@@ -18,6 +18,10 @@ typedef short lsk_s16x4 __attribute__((ext_vector_type(4)));
 typedef float lsk_f32x4 __attribute__((ext_vector_type(4)));
 typedef int lsk_i32x4 __attribute__((ext_vector_type(4)));
 
+// Word 3 of a raw buffer descriptor on gfx9-family parts (gfx950): 32-bit data format, no swizzle, no stride;
+// loads of 16 bytes at byte offsets read the memory as is.
+#define LSK_BUFFER_RSRC_WORD3 0x00020000
+
 __device__ __forceinline__ float bf2f(uint16_t b) { return __uint_as_float(((uint32_t)b) << 16); }
 
 __device__ __forceinline__ uint16_t f2bf(float f) {
