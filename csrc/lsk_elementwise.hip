@@ -95,12 +95,13 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
                                                           long ldo, int dim, float eps) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[NORM_MAX_PASSES][8];
+  float v[NORM_MAX_PASSES][8], wv[NORM_MAX_PASSES][8];
   float ss = 0.f;
 #pragma unroll
   for (int p = 0; p < NORM_MAX_PASSES; ++p) {
     const int j = (p * 256 + tid) * 8;
     if (j < dim) {
+      if (out != nullptr) Vec8<T>::ld(w + j, wv[p]);  // issued with the row's loads: no second round trip
       Vec8<T>::ld(x + (long)row * ldx + j, v[p]);
       if (KS > 0) {
         float acc[8];
@@ -143,10 +144,9 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
   for (int p = 0; p < NORM_MAX_PASSES; ++p) {
     const int j = (p * 256 + tid) * 8;
     if (j < dim) {
-      float wv[8], o[8];
-      Vec8<T>::ld(w + j, wv);
+      float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = wv[i] * Elem<T>::round(v[p][i] * r);
+      for (int i = 0; i < 8; ++i) o[i] = wv[p][i] * Elem<T>::round(v[p][i] * r);
       Vec8<T>::st(out + (long)row * ldo + j, o);
     }
   }
@@ -232,17 +232,19 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
                                    const int32_t* __restrict__ rows, const int32_t* __restrict__ pos, int Hq, int Hkv,
                                    int D, int max_batch, int max_seq, int tab_len) {
   const int t = blockIdx.x, h = blockIdx.y;
-  const int row = rows[t], p = pos[t];
-  if (row < 0 || row >= max_batch || p < 0 || p >= max_seq || p >= tab_len) return;  // host validates too
   const int half = D >> 1;
   const long width = (long)(Hq + 2 * Hkv) * D;
   const long base = (long)t * width + (long)h * D;
   for (int j = threadIdx.x; j < half; j += blockDim.x) {
+    // the token's values do not depend on its row / position: their loads go out with the row / position
+    // loads instead of after them
+    const float x1 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j);
+    const float x2 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j + half);
+    const int row = rows[t], p = pos[t];
+    if (row < 0 || row >= max_batch || p < 0 || p >= max_seq || p >= tab_len) return;  // host validates too
     if (h < Hq + Hkv) {
       const float* ct = cos_tab + (long)p * D;
       const float* st = sin_tab + (long)p * D;
-      const float x1 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j);
-      const float x2 = qkv_val<T, KSC>(qkv, P, KS, pstride, base + j + half);
       const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
       const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
       const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
@@ -260,8 +262,8 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
     } else {
       // V cache: 32-position blocks, each transposed ([B, Hkv, S/32, D, 32])
       T* dst = vc + ((long)row * Hkv + (h - Hq - Hkv)) * (long)D * max_seq + (long)(p >> 5) * 32 * D + (p & 31);
-      Elem<T>::st(dst + (long)j * 32, qkv_val<T, KSC>(qkv, P, KS, pstride, base + j));
-      Elem<T>::st(dst + (long)(j + half) * 32, qkv_val<T, KSC>(qkv, P, KS, pstride, base + j + half));
+      Elem<T>::st(dst + (long)j * 32, x1);
+      Elem<T>::st(dst + (long)(j + half) * 32, x2);
     }
   }
 }
