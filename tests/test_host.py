@@ -170,6 +170,37 @@ def test_attention_rows_per_item_policy():
     assert lsk.attn_rows_cap(few, 4, lsk.ATTN_SPLIT, 8, 128, 256) == 16
     many = np.array([(9 * i, 1500, 9, i) for i in range(256)], dtype=np.int32)      # 2048 pairs on 256 CUs
     assert lsk.attn_rows_cap(many, 4, lsk.ATTN_SPLIT, 8, 128, 256) == 48
+    # every block fits 16 rows: all caps give the same items, so the one-tile kernel (no per-item overhead) wins
+    decode = np.array([(i, 700, 1, i) for i in range(32)], dtype=np.int32)
+    assert lsk.attn_rows_cap(decode, 4, lsk.ATTN_SPLIT, 8, 128, 256) == 16
+    # the cap is one of the kernel's tile multiples, whatever the shape
+    rng = np.random.default_rng(1)
+    for _ in range(20):
+        nb = int(rng.integers(1, 80))
+        T = rng.integers(1, 13, nb)
+        blk = np.stack([np.concatenate([[0], np.cumsum(T)[:-1]]), rng.integers(0, 6000, nb), T, np.arange(nb)], 1)
+        cap = lsk.attn_rows_cap(blk.astype(np.int32), int(rng.choice([1, 4, 8])), lsk.ATTN_SPLIT, 8, 128, 256)
+        assert cap in (16, 32, 48)
+    assert lsk.attn_rows_cap(np.zeros((0, 4), np.int32), 4, lsk.ATTN_SPLIT, 8, 128, 256) in (16, 32, 48)
+    with pytest.raises(lsk.LskError):
+        lsk.attn_rows_cap(decode, 4, lsk.ATTN_SPLIT, 8, 128, 0)                   # no workgroups
+
+
+@pytest.mark.parametrize("cap", [16, 32, 48])
+def test_attention_plan_items_respect_the_rows_cap(cap):
+    """Every work item holds <= cap rows of one block, and the items of a block cover its rows once."""
+    lsk = _lsk()
+    blocks = np.array([(0, 100, 9, 0), (9, 5000, 12, 1), (21, 30, 1, 2)], dtype=np.int32)
+    works, _, _ = lsk.attn_plan(blocks, 4, 4096, cap)
+    for b, (qs, p0, T, row) in enumerate(blocks):
+        mine = [w for w in works if w[2] > 0 and w[0] == qs]
+        assert all(w[2] <= cap for w in mine)
+        per_split = {}
+        for w in mine:
+            per_split.setdefault(int(w[3]), []).extend(range(int(w[1]), int(w[1]) + int(w[2])))
+        assert all(sorted(r) == list(range(4 * T)) for r in per_split.values()), (cap, b)
+    with pytest.raises(lsk.LskError):
+        lsk.attn_plan(blocks, 4, 4096, 24)
 
 
 def test_attention_plan_places_sibling_tiles_eight_slots_apart():
