@@ -711,8 +711,12 @@ static int schedule_into(const int32_t* works, int n_works, int n_kv_heads, int 
     const int32_t* wp = works + (long)w * 8;
     if (wp[2] <= 0) continue;
     LSK_REQUIRE(wp[2] <= ATTN_ROWS, LSK_ESHAPE, "lsk_attn_schedule: work %d has %d rows", w, wp[2]);
+    // cost in tenths of a wave step: the steps (a three-tile item's 1.2x as long), plus the per-item overhead and
+    // 1.2 steps per extra column tile (the per-item terms of the rows-per-item estimate, in step units)
     const int steps = (wp[4] - wp[3] + ATTN_STEP * ATTN_WAVES - 1) / (ATTN_STEP * ATTN_WAVES);
-    for (int h = 0; h < n_kv_heads; ++h) items.push_back({w * n_kv_heads + h, steps + 2});
+    const int nq = (wp[2] + 15) / 16;
+    const int cost = steps * (nq == 3 ? 12 : 10) + 20 + 12 * (nq - 1);
+    for (int h = 0; h < n_kv_heads; ++h) items.push_back({w * n_kv_heads + h, cost});
   }
   std::stable_sort(items.begin(), items.end(), [](const It& a, const It& b) { return a.cost > b.cost; });
   heap.clear();

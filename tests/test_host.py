@@ -155,7 +155,11 @@ def test_attention_schedule_covers_every_item_once_longest_first(n_slots):
     assert max(len(x) for x in per_slot) == R
     flat = [i for x in per_slot for i in x]
     assert sorted(flat) == sorted(w * Hkv + h for w in real for h in range(Hkv))
-    cost = lambda i: -(-(works[i // Hkv][4] - works[i // Hkv][3]) // 256) + 2  # noqa: E731
+
+    def cost(i):
+        w = works[i // Hkv]
+        steps, nq = -(-(w[4] - w[3]) // 256), (w[2] + 15) // 16
+        return steps * (12 if nq == 3 else 10) + 20 + 12 * (nq - 1)
     loads = [sum(cost(i) for i in x) for x in per_slot]
     # greedy longest-first bound: no slot exceeds the mean by more than the largest item
     assert max(loads) <= sum(loads) / n_slots + max(cost(i) for i in flat)
