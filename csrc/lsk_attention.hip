@@ -425,7 +425,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
 // ----------------------------------------------------------------------------- fp32 path
 // Straightforward per-query kernel for fp32 models (parity runs; V cache in the same blocked transposed
 // layout as the bf16 path): one wave per query row, the
-// row's positions 0..qpos in 64-position chunks (lane = position), online softmax with exact expf,
+// row's positions 0..qpos in 64-position chunks (lane = position), online softmax with lsk_exp,
 // O[d] accumulated over the chunk's positions in order.  Fixed order per query -> batch invariant.
 template <int D>
 __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__ q, const float* __restrict__ kc,
@@ -462,8 +462,8 @@ __global__ __launch_bounds__(256) void attn_f32_kernel(const float* __restrict__
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) mt = fmaxf(mt, __shfl_xor(mt, off, 64));
       const float m_new = fmaxf(m_run, mt);
-      const float alpha = (m_new == m_run) ? 1.f : expf(m_run - m_new);
-      const float p = (s == -INFINITY) ? 0.f : expf(s - m_new);
+      const float alpha = (m_new == m_run) ? 1.f : lsk_exp(m_run - m_new);
+      const float p = (s == -INFINITY) ? 0.f : lsk_exp(s - m_new);
       float rs = p;
 #pragma unroll
       for (int off = 32; off >= 1; off >>= 1) rs += __shfl_xor(rs, off, 64);

@@ -34,6 +34,29 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
 // Round a float through bf16 and back (value of the float once stored in a bf16 tensor).
 __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }
 
+// exp(x) in fp32 (Cody and Waite's range reduction): x = n ln2 + r with n = rint(x log2(e)) and ln2 split into
+// a 16-bit head (n * head is exact for the |n| <= 128 reached here) and a tail; exp(r) = sum_{k<=7} r^k / k!
+// by Horner on |r| <= ln2 / 2 (truncation below 6e-9 relative); then 2^n by ldexp.  Results below 2^-124
+// (x < -86) are flushed to 0 so no subnormal is ever produced; x > 89 gives +inf.  Each step is one IEEE fp32
+// operation and the build contracts nothing into FMAs, so a host restatement of the same steps (the fp32
+// oracle's) produces the same bits.  Used by the fp32 attention softmax and by SiLU.
+__device__ __forceinline__ float lsk_exp(float x) {
+  if (x != x) return x;
+  if (x < -86.0f) return 0.0f;
+  if (x > 89.0f) return __builtin_huge_valf();
+  const float n = __builtin_rintf(x * 1.4426950216293335f);
+  const float r = (x - n * 0.693145751953125f) - n * 1.428606765330187e-06f;
+  float p = 0.00019841270113829523f;
+  p = p * r + 0.0013888889225199819f;
+  p = p * r + 0.008333333767950535f;
+  p = p * r + 0.0416666679084301f;
+  p = p * r + 0.1666666716337204f;
+  p = p * r + 0.5f;
+  p = p * r + 1.0f;
+  p = p * r + 1.0f;
+  return __builtin_ldexpf(p, (int)n);
+}
+
 // Offset of K cache element (position p, dim d) within one (row, KV head) stripe of S positions x D.
 // bf16: fragment-major 32-position blocks of 32 D elements, each block 2 (D / 32) MFMA fragments of 1 KiB:
 //   fragment (a, j), lane l = 16 lg + l16 holds positions 8 (l16 / 4) + 4 a + l16 % 4 of the block and

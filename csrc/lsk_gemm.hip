@@ -38,7 +38,7 @@
 #define EPI_PARTIAL 3
 #define EPI_ARGMAX 4
 
-__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + lsk_exp(-x)); }
 
 // One lane's 16 bytes of a weight fragment, non-temporal (streamed once per launch).
 __device__ __forceinline__ lsk_bf16x8 ld_w(const uint16_t* p) {

@@ -17,6 +17,9 @@ points of its eager ops kept in place (so a bf16 oracle rounds where the referen
   packed_layer(s)  solutions/packed.py:169-196
   qo_indptr        solutions/packed.py:199-201
 
+OracleLlama(ordered=True) (fp32) evaluates the reductions in the fixed order of oracle/ordered.py, the
+fp32 kernels' order, so the fp32 engine is compared with it bit for bit.
+
 Pinned by (tests/test_oracle.py): HF transformers LlamaForCausalLM golden logits / hidden states
 (tests/golden/hf_tiny.npz), fp64 brute-force per-token attention, packed == per-block forward,
 and the reference's own hand-written build_packed cases (tests/test_eesd.py:99-117, 534-546).
@@ -33,6 +36,8 @@ from typing import Optional
 import numpy as np
 import torch
 import torch.nn.functional as F
+
+from oracle import ordered as O
 
 
 # ----------------------------------------------------------------------------- config
@@ -174,8 +179,13 @@ def load_hf_weights(path) -> dict:
 class OracleLlama:
     """CPU LayerSkip-Llama; same attributes as the reference model object where the packed path reads them."""
 
-    def __init__(self, cfg: OracleConfig, weights: dict, dtype=torch.float32, max_seq: int = 512):
+    def __init__(self, cfg: OracleConfig, weights: dict, dtype=torch.float32, max_seq: int = 512,
+                 ordered: bool = False):
+        """ordered=True (fp32 only): the reductions run in the fixed order of oracle/ordered.py."""
+        if ordered and dtype != torch.float32:
+            raise ValueError("the ordered oracle is fp32 only")
         self.cfg, self.dtype, self.device = cfg, dtype, torch.device("cpu")
+        self.ordered = ordered
         self.group = cfg.n_heads // cfg.n_kv_heads
         self.q_size = cfg.n_heads * cfg.head_dim
         self.kv_size = cfg.n_kv_heads * cfg.head_dim
@@ -249,6 +259,8 @@ class OracleLlama:
         return F.embedding(ids, self.embed_w)
 
     def head(self, h: torch.Tensor) -> torch.Tensor:
+        if getattr(self, "ordered", False):
+            return O.n2t(O.linear(O.rms_norm(O.t2n(h), O.t2n(self.norm_w), self.cfg.norm_eps), O.t2n(self.lm_head_w)))
         return F.linear(rms_norm(h, self.norm_w, self.cfg.norm_eps), self.lm_head_w)
 
     # ---- whole-sequence forward of one request (used against HF and as the AR reference)
@@ -361,6 +373,9 @@ def build_packed(model, blocks: list, bucketing: str = "exact") -> OPacked:
 
 def attend(model, i: int, q: torch.Tensor, pb: OPacked) -> torch.Tensor:
     """Per-bucket masked SDPA over the cache rows of layer i; q [N, Hq, D] -> [N, Hq*D]."""
+    if getattr(model, "ordered", False):
+        o = O.attend(O.t2n(q), O.t2n(model.cache.k[i]), O.t2n(model.cache.v[i]), pb.rows, pb.pos, model.group)
+        return O.n2t(o.reshape(q.shape[0], model.q_size))
     G, Hkv, D = model.group, model.cfg.n_kv_heads, model.cfg.head_dim
     ck, cv = model.cache.k[i], model.cache.v[i]
     out = torch.empty(q.shape[0], model.q_size, dtype=q.dtype)
@@ -382,10 +397,20 @@ def attend(model, i: int, q: torch.Tensor, pb: OPacked) -> torch.Tensor:
     return out
 
 
+def _ordered_ops(model):
+    """(norm, linear, act) of the layer: oracle/ordered.py's fixed-order fp32 forms, or torch's."""
+    if not getattr(model, "ordered", False):
+        return (lambda x, w: rms_norm(x, w, model.cfg.norm_eps)), F.linear, F.silu
+    return (lambda x, w: O.n2t(O.rms_norm(O.t2n(x), O.t2n(w), model.cfg.norm_eps)),
+            lambda x, w: O.n2t(O.linear(O.t2n(x), O.t2n(w))),
+            lambda x: O.n2t(O.silu_f32(O.t2n(x))))
+
+
 def packed_layer(model, i: int, x: torch.Tensor, pb: OPacked) -> torch.Tensor:
     cfg, lw = model.cfg, model.layers[i]
     N = x.shape[0]
-    qkv = F.linear(rms_norm(x, lw.attn_norm, cfg.norm_eps), lw.wqkv)
+    norm, linear, act = _ordered_ops(model)
+    qkv = linear(norm(x, lw.attn_norm), lw.wqkv)
     q = qkv[:, :model.q_size].reshape(N, cfg.n_heads, cfg.head_dim)
     k = qkv[:, model.q_size:model.q_size + model.kv_size].reshape(N, cfg.n_kv_heads, cfg.head_dim)
     v = qkv[:, model.q_size + model.kv_size:].reshape(N, cfg.n_kv_heads, cfg.head_dim)
@@ -393,9 +418,9 @@ def packed_layer(model, i: int, x: torch.Tensor, pb: OPacked) -> torch.Tensor:
     k = rope(k, pb.cos, pb.sin)
     model.cache.k[i][pb.rows, :, pb.pos] = k
     model.cache.v[i][pb.rows, :, pb.pos] = v
-    x = x + F.linear(attend(model, i, q, pb), lw.wo)
-    g, u = F.linear(rms_norm(x, lw.ffn_norm, cfg.norm_eps), lw.w13).chunk(2, dim=-1)
-    return x + F.linear(F.silu(g) * u, lw.w2)
+    x = x + linear(attend(model, i, q, pb), lw.wo)
+    g, u = linear(norm(x, lw.ffn_norm), lw.w13).chunk(2, dim=-1)
+    return x + linear(act(g) * u, lw.w2)
 
 
 def packed_layers(model, x, pb, start: int, end: int, capture: Optional[dict] = None, capture_layers: tuple = ()):

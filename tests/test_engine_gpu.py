@@ -19,12 +19,12 @@ pytestmark = pytest.mark.gpu
 F32, BF16 = torch.float32, torch.bfloat16
 
 
-def _pair(ocfg, dtype, seed=0, std=0.05, max_seq=1024):
+def _pair(ocfg, dtype, seed=0, std=0.05, max_seq=1024, ordered=False):
     from oracle.model import OracleLlama, random_weights
     from thesis_amd.common.model import LayerSkipLlama
 
     w = random_weights(ocfg, seed=seed, std=std)
-    o = OracleLlama(ocfg, w, dtype=dtype, max_seq=max_seq)
+    o = OracleLlama(ocfg, w, dtype=dtype, max_seq=max_seq, ordered=ordered)
     g = LayerSkipLlama.from_weights(to_model_config(ocfg), w, device="cuda", dtype=dtype, max_seq=max_seq)
     return o, g
 
@@ -74,6 +74,28 @@ def test_packed_forward_fp32_matches_oracle(cuda, which):
     for i in range(o.n_layers):
         assert torch.allclose(g.cache.k[i].cpu(), o.cache.k[i], atol=1e-4, rtol=1e-4)
         assert torch.allclose(g.cache.v[i].cpu(), o.cache.v[i], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("which", ["tiny", "small"])
+def test_packed_forward_fp32_is_bit_exact_against_the_ordered_oracle(cuda, which):
+    """fp32, bit for bit: with the reductions in one fixed order on both sides (oracle/ordered.py restates the
+    fp32 kernels' orders; both use the same Cody-Waite exp), every layer's appended K / V, every exit hidden
+    state, the final hidden state and the logits are identical to the oracle's."""
+    o, g = _pair(tiny_cfg() if which == "tiny" else small_cfg(), F32, ordered=True)
+    o.allocate_cache(4, 128)
+    g.allocate_cache(4, 128)
+    blocks = [(0, 24, 1), (1, 24, 4), (2, 24, 2), (3, 24, 9)]
+    xo, xg, lo, lg, oc, gc = _ragged_forward(o, g, blocks, capture_layers=(1, 2, 3))
+    diffs = {"hidden": (xg - xo).abs().max().item(), "logits": (lg - lo).abs().max().item()}
+    for i in range(o.n_layers):
+        diffs[f"k{i}"] = (g.cache.k[i].cpu() - o.cache.k[i]).abs().max().item()
+        diffs[f"v{i}"] = (g.cache.v[i].cpu() - o.cache.v[i]).abs().max().item()
+    print("max |gpu - ordered oracle|:", diffs)
+    assert torch.equal(xg, xo) and torch.equal(lg, lo)
+    for k in (1, 2, 3):
+        assert torch.equal(gc[k].cpu(), oc[k])
+    for i in range(o.n_layers):
+        assert torch.equal(g.cache.k[i].cpu(), o.cache.k[i]) and torch.equal(g.cache.v[i].cpu(), o.cache.v[i])
 
 
 def test_packed_forward_bf16_logits_within_tolerance(cuda):
@@ -184,6 +206,30 @@ def test_engine_forced_acceptance_matches_oracle(cuda):
                              forced_seed=7)
     assert got == ref
     assert res["metrics"]["acceptance_rate"] > 0.2           # forcing really accepts drafts
+
+
+def test_engine_fp32_kv_and_rollback_state_are_bit_exact(cuda):
+    """After a whole speculative run with forced rejections (drafts rolled back), every slot's committed KV
+    prefix [0, pos) in every layer is bitwise the ordered oracle engine's, and so are the rollback pointers
+    (the committed lengths) and the tokens."""
+    from oracle.engine import ForcedAcceptance, OracleEngine
+
+    ocfg = small_cfg()
+    o, g = _pair(ocfg, F32, std=0.1, ordered=True)
+    prompts = _prompts(5, ocfg.vocab_size, seed=21)
+    oe = OracleEngine(o, 5, 24, 25, mode="spec", k=2, gamma=4, d_max=6, forced=ForcedAcceptance(0.3, seed=5))
+    ref = oe.run_static([(p.pid, p.tokens) for p in prompts])
+    got, eng, res = _run_gpu(g, prompts, 5, 25, sched="fixed", k=2, gamma=4, d_max=6, forced_accept_p=0.3,
+                             forced_seed=5)
+    assert got == ref
+    assert res["metrics"]["acceptance_rate"] < 1.0                # drafts were rejected and rolled back
+    assert np.array_equal(eng.pos, oe.pos)                      # rollback state: committed KV lengths
+    for s, pr in enumerate(prompts):                              # 5 prompts in 5 slots: prompt s in slot s
+        L = int(oe.pos[s])
+        assert L >= len(pr.tokens) + len(ref[pr.pid]) - 1
+        for i in range(o.n_layers):
+            assert torch.equal(g.cache.k[i][s, :, :L].cpu(), o.cache.k[i][s, :, :L]), (s, i)
+            assert torch.equal(g.cache.v[i][s, :, :L].cpu(), o.cache.v[i][s, :, :L]), (s, i)
 
 
 @pytest.mark.parametrize("dtype", [BF16, F32])

@@ -9,6 +9,8 @@
   * packed forward == per-block forward (tests/test_eesd.py:120-142 of the reference)
   * build_packed against the reference's hand-written cases (tests/test_eesd.py:99-117, 534-546)
   * losslessness of the oracle engine (spec == AR) and the acceptance closed form
+  * the ordered fp32 mode (oracle/ordered.py): the same golden vectors, the default oracle, exp against
+    float64 exp, and planted order / term mistakes that change the bits the bitwise GPU checks compare
 """
 
 from __future__ import annotations
@@ -26,7 +28,7 @@ from oracle.engine import ForcedAcceptance, OracleEngine
 GOLDEN = Path(__file__).resolve().parent / "golden" / "hf_tiny.npz"
 
 
-def _golden_model(name):
+def _golden_model(name, ordered=False):
     import importlib.util
 
     spec = importlib.util.spec_from_file_location("mkg", GOLDEN.with_name("make_hf_golden.py"))
@@ -35,14 +37,14 @@ def _golden_model(name):
     v = mkg.VARIANTS[name]
     cfg = mkg.oracle_cfg(v)
     w = om.random_weights(cfg, seed=mkg.SEED, std=mkg.STD)
-    m = om.OracleLlama(cfg, w, dtype=torch.float32, max_seq=512)
+    m = om.OracleLlama(cfg, w, dtype=torch.float32, max_seq=512, ordered=ordered)
     m.allocate_cache(2, 256)
     return m
 
 
-def _check_golden(name, atol=1e-4):
+def _check_golden(name, atol=1e-4, ordered=False):
     g = np.load(GOLDEN)
-    m = _golden_model(name)
+    m = _golden_model(name, ordered)
     ids = g["ids"].tolist()
     with torch.inference_mode():
         logits, hidden = m.prefill(ids, slot=1, capture=True)
@@ -237,3 +239,72 @@ def test_acceptance_closed_form_in_oracle_engine():
     out = eng.run_static(prompts)
     ar = OracleEngine(m, 2, 24, 30, mode="ar").run_static(prompts)
     assert out == ar and eng.n_deep > 0
+
+
+# ----------------------------------------------------------------------------- ordered fp32 mode
+
+@pytest.mark.parametrize("name", ["default", "tied", "llama3_rope"])
+def test_ordered_oracle_matches_hf_golden(name):
+    assert _check_golden(name, ordered=True)
+
+
+def test_ordered_oracle_matches_the_default_oracle():
+    import oracle.ordered as O
+    from conftest import small_cfg
+
+    cfg = small_cfg()
+    w = om.random_weights(cfg, seed=4, std=0.05)
+    a = om.OracleLlama(cfg, w, dtype=torch.float32, max_seq=256)
+    b = om.OracleLlama(cfg, w, dtype=torch.float32, max_seq=256, ordered=True)
+    for m in (a, b):
+        m.allocate_cache(3, 128)
+    blocks = [om.OBlock(0, 0, 40), om.OBlock(1, 0, 7), om.OBlock(2, 0, 70)]
+    ids = torch.randint(0, cfg.vocab_size, (117,), generator=torch.Generator().manual_seed(0))
+    ya = om.packed_layers(a, a.embed(ids), om.build_packed(a, blocks), 0, a.n_layers)
+    yb = om.packed_layers(b, b.embed(ids), om.build_packed(b, blocks), 0, b.n_layers)
+    assert torch.allclose(ya, yb, atol=1e-5, rtol=1e-5)
+    assert torch.allclose(a.head(ya), b.head(yb), atol=1e-5, rtol=1e-5)
+    assert not torch.equal(ya, yb)          # the orders differ, so the bits do: the bitwise checks can tell
+    assert O.exp_f32(np.float32(0)) == 1
+
+
+def test_exp_f32_is_within_two_ulp_of_exp():
+    import oracle.ordered as O
+
+    x = np.concatenate([np.linspace(-85.9, 88.5, 200001, dtype=np.float32),
+                        np.random.default_rng(0).normal(0, 4, 100000).astype(np.float32)])
+    got = O.exp_f32(x).astype(np.float64)
+    ref = np.exp(x.astype(np.float64))
+    ulp = np.spacing(ref.astype(np.float32)).astype(np.float64)
+    assert (np.abs(got - ref) / ulp).max() <= 2.0
+    assert O.exp_f32(np.float32(-np.inf)) == 0 and O.exp_f32(np.float32(-87)) == 0
+    assert np.isinf(O.exp_f32(np.float32(90))) and np.isnan(O.exp_f32(np.float32(np.nan)))
+    sil = O.silu_f32(np.float32([-100, -3, 0, 2.5, 100]))
+    assert np.allclose(sil, np.array([-100, -3, 0, 2.5, 100]) / (1 + np.exp(-np.array([-100, -3, 0, 2.5, 100.]))),
+                       rtol=1e-6, atol=1e-30)                     # silu(-100) = -0: exp(100) is inf in fp32
+
+
+def test_ordered_checks_catch_planted_mistakes(monkeypatch):
+    """A dropped Taylor term breaks the exp bound; a plain left-to-right sum instead of the lane / butterfly
+    order gives different bits for the same products (what the GPU's bitwise comparison would flag)."""
+    import oracle.ordered as O
+
+    x = np.linspace(-20, 20, 10001, dtype=np.float32)
+    ref = np.exp(x.astype(np.float64))
+    bad = list(O._TAYLOR)
+    bad[2] = np.float32(0.0)                                     # drop the r^5 / 5! term
+    monkeypatch.setattr(O, "_TAYLOR", bad)
+    got = O.exp_f32(x).astype(np.float64)
+    monkeypatch.undo()
+    assert (np.abs(got - ref) / np.spacing(ref.astype(np.float32))).max() > 2.0
+    rng = np.random.default_rng(1)
+    a = rng.normal(size=(8, 700)).astype(np.float32)
+    w = rng.normal(size=(16, 700)).astype(np.float32)
+    ordered = O.linear(a, w)
+    plain = np.zeros((8, 16), np.float32)
+    for k in range(700):
+        plain = plain + a[:, k:k + 1] * w[None, :, k]
+    assert np.allclose(ordered, plain, atol=1e-3) and not np.array_equal(ordered, plain)
+    nrm = O.rms_norm(a, np.ones(700, np.float32), 1e-5)
+    plain_ms = np.float32(1) / np.sqrt((a * a).sum(axis=1, dtype=np.float32) / np.float32(700) + np.float32(1e-5))
+    assert np.allclose(nrm, a * plain_ms[:, None], rtol=1e-5) and not np.array_equal(nrm, a * plain_ms[:, None])
