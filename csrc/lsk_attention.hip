@@ -72,10 +72,12 @@ __device__ __forceinline__ float rows_sum(float x) {
 // up to a butterfly over the four 16-lane rows (rows_max / rows_sum).  A 32-position step uses two S^T
 // sub-tiles whose MFMA rows are mapped to positions so that lane group g holds positions 8g .. 8g+7 of the
 // step: exactly the 8 consecutive positions its P^T fragment and its 16-byte V^T load need.
-// A work item carries up to 48 query rows (three column tiles sharing every K / V fragment), so the KV of a
-// (block, KV head) is read by one workgroup for blocks of up to 48 / G tokens (a 9-token verify block of a
-// 4-head group is 36 rows).  The item's Q sits in LDS (rows padded by 16 bytes: the 16-byte reads of 16
-// rows hit distinct banks), which keeps three tiles' accumulators within 256 VGPRs.  The 8 waves take the
+// QT column tiles of 16 query rows share every K / V fragment of a work item.  QT = 3 (items of up to 48 rows):
+// the KV of a (block, KV head) is read by one workgroup for blocks of up to 48 / G tokens (a 9-token verify
+// block of a 4-head group is 36 rows); the item's Q sits in LDS (rows padded by 16 bytes: the 16-byte reads of
+// 16 rows hit distinct banks), which keeps three tiles' accumulators within 256 VGPRs.  QT = 1 (items of up to
+// 16 rows, for launches whose rows-per-item cap is 16): Q stays in registers.  A row's arithmetic is the same
+// in both, so they give bitwise equal outputs.  The 8 waves take the
 // 32-position steps of the item's KV range round robin (step index within the split mod 8), keep the next
 // step's K and V loads in flight while they compute, and are merged in wave order through LDS, two column
 // tiles per pass; 8 waves keep the chain of dependent steps short when a decode batch has few
