@@ -143,16 +143,18 @@ def run_main(args):
             engine_step(eng)
         prof = _lsk.Profiler.collect()
         _lsk.Profiler.enable(False)
-    replay = replay_w13(model, trace, eng.k, args.replay_steps) if args.replay_steps > 0 else {}
+    replay = replay_gemms(model, trace, eng.k, args.replay_steps) if args.replay_steps > 0 else {}
     return cfg, model, eng, committed, elapsed, trace, prof, replay
 
 
-def replay_w13(model, trace: list, k: int, n_steps: int) -> dict:
-    """Average launch duration of the FFN up-projection GEMM (w13 = [gate; up], silu-mul epilogue, the
-    largest kernel class of the step) over the launches the first `n_steps` timed steps made: the same
-    token counts (shallow segment through layers [0, k), deep segment through [k, L)) and each layer's
-    own weights, issued back to back on the engine's stream between one pair of HIP events.  Events
-    around every single launch would add their own dispatch overhead (a few microseconds) to each."""
+def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
+    """Average launch duration of each projection GEMM class (qkv, o and w2 as split-K partial launches, w13 =
+    [gate; up] with the silu-mul epilogue) over the launches the first `n_steps` timed steps made: the same
+    token counts (shallow segment through layers [0, k), deep segment through [k, L)) and each layer's own
+    weights, a class's launches issued back to back on the engine's stream between one pair of HIP events.
+    Events around every single launch would add their own dispatch overhead (a few microseconds) to each.
+    Per class: algorithmic bytes (weights + activations + outputs, fp32 partials for the split-K classes) and
+    flops per launch, and t_roof = max(bytes / HBM peak, flops / bf16 MFMA peak)."""
     from thesis_amd import _lsk
 
     c = model.cfg
@@ -163,28 +165,57 @@ def replay_w13(model, trace: list, k: int, n_steps: int) -> dict:
             seq += [(sum(b[2] for b in st["dp"]), i) for i in range(k, c.n_layers)]
     if not seq:
         return {}
+    es = model.dtype.itemsize
     m_max = max(m for m, _ in seq)
+    dim, ffn = c.dim, c.intermediate_size
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+    qkvd = qd + 2 * kvd
     g = torch.Generator(device=model.device).manual_seed(1)
-    a = torch.empty(m_max, c.dim, dtype=model.dtype, device=model.device).normal_(generator=g)
-    h = torch.empty(m_max, c.intermediate_size, dtype=model.dtype, device=model.device)
+    x = torch.empty(m_max, max(dim, qd, ffn), dtype=model.dtype, device=model.device).normal_(generator=g)
+    h = torch.empty(m_max, ffn, dtype=model.dtype, device=model.device)
+    ks = {"qkv": _lsk.gemm_plan(qkvd, dim)[1], "o": _lsk.gemm_plan(dim, qd)[1], "w2": _lsk.gemm_plan(dim, ffn)[1]}
+    part = torch.empty(max(ks["qkv"] * qkvd, ks["o"] * dim, ks["w2"] * dim) * m_max, dtype=torch.float32,
+                       device=model.device)
 
-    def run():
+    def pv(n, m, kk):
+        return part[:kk * m * n].view(kk, m, n)
+
+    classes = {
+        # name: (launch(m, layer), bytes(m), flops(m))
+        "gemm_qkv": (lambda m, i: _lsk.gemm_partial(x[:m, :dim], model.layers[i].wqkv, ks["qkv"],
+                                                    out=pv(qkvd, m, ks["qkv"])),
+                     lambda m: es * (qkvd * dim + m * dim) + 4.0 * ks["qkv"] * m * qkvd,
+                     lambda m: 2.0 * m * dim * qkvd),
+        "gemm_o": (lambda m, i: _lsk.gemm_partial(x[:m, :qd], model.layers[i].wo, ks["o"], out=pv(dim, m, ks["o"])),
+                   lambda m: es * (dim * qd + m * qd) + 4.0 * ks["o"] * m * dim,
+                   lambda m: 2.0 * m * qd * dim),
+        "gemm_w13": (lambda m, i: _lsk.gemm(x[:m, :dim], model.layers[i].w13, h[:m], epilogue=_lsk.EPI_SILU_MUL),
+                     lambda m: es * (2.0 * ffn * dim + m * dim + m * ffn),
+                     lambda m: 4.0 * m * dim * ffn),
+        "gemm_w2": (lambda m, i: _lsk.gemm_partial(x[:m, :ffn], model.layers[i].w2, ks["w2"], out=pv(dim, m, ks["w2"])),
+                    lambda m: es * (dim * ffn + m * ffn) + 4.0 * ks["w2"] * m * dim,
+                    lambda m: 2.0 * m * ffn * dim),
+    }
+    out = {}
+    for name, (launch, nbytes, nflops) in classes.items():
+        for m, i in seq:                       # warm-up pass
+            launch(m, i)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
         for m, i in seq:
-            _lsk.gemm(a[:m], model.layers[i].w13, h[:m], epilogue=_lsk.EPI_SILU_MUL)
-
-    run()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    e0.record()
-    run()
-    e1.record()
-    torch.cuda.synchronize()
-    us = 1e3 * e0.elapsed_time(e1) / len(seq)
-    es = model.dtype.itemsize if hasattr(model.dtype, "itemsize") else 2
-    alg = float(np.mean([es * (2.0 * c.intermediate_size * c.dim + m * c.dim + m * c.intermediate_size)
-                         for m, _ in seq]))
-    return {"launches": len(seq), "avg_us": round(us, 2), "bytes_per_launch": alg,
-            "token_counts": sorted(set(m for m, _ in seq))}
+            launch(m, i)
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1e3 * e0.elapsed_time(e1) / len(seq)
+        b = float(np.mean([nbytes(m) for m, _ in seq]))
+        f = float(np.mean([nflops(m) for m, _ in seq]))
+        t_roof = float(np.mean([max(nbytes(m) / (HBM_PEAK_GBS * 1e3), nflops(m) / (BF16_PEAK_TFLOPS * 1e6))
+                                for m, _ in seq]))     # us
+        out[name] = {"launches": len(seq), "avg_us": round(us, 2), "bytes_per_launch": b, "flops_per_launch": f,
+                     "t_roof_us": round(t_roof, 2), "frac": round(t_roof / us, 4)}
+    out["token_counts"] = sorted(set(m for m, _ in seq))
+    return out
 
 
 def summarize_kernels(prof: dict) -> dict:
@@ -363,7 +394,7 @@ def main():
     ap.add_argument("--profile-steps", type=int, default=40)
     ap.add_argument("--attn-iters", type=int, default=50)
     ap.add_argument("--replay-steps", type=int, default=20,
-                    help="timed steps whose w13 GEMM launches are replayed for the roofline figure")
+                    help="timed steps whose projection GEMM launches are replayed for the roofline figures")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-attn", action="store_true")
@@ -403,20 +434,30 @@ def main():
 
     # roofline of the largest kernel class of the decode step: the w13 GEMM (weight stream, HBM-bound at
     # these token counts); its average launch duration comes from the back-to-back replay above
-    roofline = None
+    roofline = gemm_roofline = None
     if replay:
         from thesis_amd.prof_summary import read_traffic
 
-        b, us = replay["bytes_per_launch"], replay["avg_us"]
+        w13 = replay["gemm_w13"]
+        b, us = w13["bytes_per_launch"], w13["avg_us"]
         ach = b / (us * 1e-6) / 1e9
         traffic = read_traffic(TRAFFIC_SUMMARY, "gemm_w13")
         roofline = {"kernel": "gemm_w13 (gemm_bf16_kernel, silu-mul epilogue)", "bound": "hbm",
                     "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_launch_us": us,
-                    "bytes_per_launch": b, "launches_timed": replay["launches"],
+                    "bytes_per_launch": b, "launches_timed": w13["launches"],
                     "token_counts": replay["token_counts"]}
         if traffic is not None:
             roofline["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
+        # all four projection GEMM classes of the step: roofline time over measured time (the MFMA-utilisation
+        # figure where a GEMM is compute-bound; these token counts make every one of them HBM-bound)
+        names = ("gemm_qkv", "gemm_o", "gemm_w13", "gemm_w2")
+        gemm_roofline = {
+            "frac": round(sum(replay[n]["t_roof_us"] for n in names) / sum(replay[n]["avg_us"] for n in names), 4),
+            "definition": "sum of t_roof over sum of measured launch time, t_roof = max(bytes / 8 TB/s, "
+                          "flops / 2.5166 PFLOP/s) per launch",
+            "classes": {n: {k: replay[n][k] for k in ("avg_us", "t_roof_us", "frac", "bytes_per_launch",
+                                                       "flops_per_launch")} for n in names}}
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
 
     line = {
@@ -428,7 +469,8 @@ def main():
                    "scheduler": "aspire (latency-aware)", "acceptance": "forced geometric p=0.3",
                    "cost_model": cost_model_source, "weights": "random init bf16",
                    "parallelism": "single GPU"},
-        "roofline": roofline, "cpu_baseline": cpu, "verify_attn": attn, "kernels": kernels,
+        "roofline": roofline, "gemm_roofline": gemm_roofline, "cpu_baseline": cpu, "verify_attn": attn,
+        "kernels": kernels,
         "steps_detail": {"committed_tokens": committed, "deep_steps": sum(1 for s in trace if s["dp"]),
                          "mean_shallow_rows": float(np.mean([len(s["sh"]) for s in trace])) if trace else None,
                          "mean_deep_rows": float(np.mean([sum(b[2] for b in s["dp"]) for s in trace if s["dp"]]))

@@ -568,15 +568,16 @@ static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : 4); }
 
 // Tile width of a launch (16 * NS weight rows per workgroup; n = output columns, ffn for silu-mul).
 // Every row tile reads the whole M x K-slice activation block, so wide tiles cut those re-reads;
-// measured on MI355X at the 8B shapes (M = 32 .. 64), 64-row tiles beat 32-row ones for qkv, o, w2 and
-// the head, and 4 + 4 row groups (gate, up) for w13.  The reduction order of an output does not depend
-// on NS or MS (only on K and the plan's KS), so the tile could follow M without breaking batch
-// invariance.
-static int tile_ns(int n, int M, int epi) {
-  (void)M;
-  (void)epi;
+// measured on MI355X at the 8B shapes, 64-row tiles win for w2, w13 (4 + 4 row groups, gate and up) and
+// the head at every M, and for qkv / o from 33 tokens on.  A split-K launch with short slices (<= 1024 k)
+// and fewer than two 64-row workgroups per CU is latency-bound per workgroup: up to 32 tokens, 32-row
+// tiles (twice the workgroups) measured faster for qkv (13.2 vs 14.7 us at 32 tokens).  The reduction
+// order of an output does not depend on NS or MS (only on K and the plan's KS), so the tile follows M
+// without breaking batch invariance.
+static int tile_ns(int n, int M, int epi, int kslice = 0, int ks = 1) {
   int ns = 4;
   while (ns > 1 && n % (16 * ns) != 0) ns >>= 1;
+  if (ns == 4 && epi == EPI_PARTIAL && M <= 32 && kslice <= 1024 && (long)(n / 64) * ks < 512) ns = 2;
   return ns;
 }
 
@@ -708,7 +709,7 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
   if (launch_wide(EPI_PARTIAL, (hipStream_t)stream, (const uint16_t*)A, lda, (const uint16_t*)W, nullptr, 0, nullptr,
                   0, P, M, N, K, 0, ks))
     return lsk_check_launch("lsk_gemm_partial(wide)");
-  const int ns = tile_ns(N, M, EPI_PARTIAL);
+  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks);
   const int ms = ms_for(M);
   dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,
                 ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, K / ks);
