@@ -180,8 +180,24 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     def pv(n, m, kk):
         return part[:kk * m * n].view(kk, m, n)
 
+    # LM-head calls of the same steps: one call for the drafts and the verify tokens when they fit one GEMM
+    # token tile (the engine merges them), else one each
+    head_seq = []
+    for st in trace[:n_steps]:
+        nd, nv = int(st.get("n_draft", len(st["sh"]))), sum(b[2] for b in st["dp"])
+        if nv and nd + nv <= _lsk.GEMM_TOKEN_TILE:
+            head_seq.append((nd + nv, None))
+        else:
+            head_seq += [(mm, None) for mm in (nd, nv) if mm]
+    V = c.vocab_size
+    m_max = max(m_max, max((m for m, _ in head_seq), default=1))
+    if x.shape[0] < m_max:
+        x = torch.empty(m_max, x.shape[1], dtype=model.dtype, device=model.device).normal_(generator=g)
+    ids = torch.empty(m_max, dtype=torch.long, device=model.device)
+    head_ws = torch.empty(int(_lsk.load().lsk_head_workspace_bytes(m_max, c.vocab_size)), dtype=torch.uint8,
+                          device=model.device)
     classes = {
-        # name: (launch(m, layer), bytes(m), flops(m))
+        # name: (launch(m, layer), bytes(m), flops(m), launch list)
         "gemm_qkv": (lambda m, i: _lsk.gemm_partial(x[:m, :dim], model.layers[i].wqkv, ks["qkv"],
                                                     out=pv(qkvd, m, ks["qkv"])),
                      lambda m: es * (qkvd * dim + m * dim) + 4.0 * ks["qkv"] * m * qkvd,
@@ -195,25 +211,34 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
         "gemm_w2": (lambda m, i: _lsk.gemm_partial(x[:m, :ffn], model.layers[i].w2, ks["w2"], out=pv(dim, m, ks["w2"])),
                     lambda m: es * (dim * ffn + m * ffn) + 4.0 * ks["w2"] * m * dim,
                     lambda m: 2.0 * m * ffn * dim),
+        # the final norm's output is the head's input; the launch is the LM-head GEMM with its fused per-tile
+        # argmax plus the pick over tiles (lsk_head_argmax)
+        "gemm_lm_head": (lambda m, i: _lsk.head_argmax(x[:m, :dim], model.lm_head_w, ids[:m], workspace=head_ws),
+                         lambda m: es * (V * dim + m * dim),
+                         lambda m: 2.0 * m * dim * V, head_seq),
     }
     out = {}
-    for name, (launch, nbytes, nflops) in classes.items():
-        for m, i in seq:                       # warm-up pass
+    for name, spec in classes.items():
+        launch, nbytes, nflops = spec[:3]
+        launches = spec[3] if len(spec) > 3 else seq
+        if not launches:
+            continue
+        for m, i in launches:                  # warm-up pass
             launch(m, i)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         e0.record()
-        for m, i in seq:
+        for m, i in launches:
             launch(m, i)
         e1.record()
         torch.cuda.synchronize()
-        us = 1e3 * e0.elapsed_time(e1) / len(seq)
-        b = float(np.mean([nbytes(m) for m, _ in seq]))
-        f = float(np.mean([nflops(m) for m, _ in seq]))
+        us = 1e3 * e0.elapsed_time(e1) / len(launches)
+        b = float(np.mean([nbytes(m) for m, _ in launches]))
+        f = float(np.mean([nflops(m) for m, _ in launches]))
         t_roof = float(np.mean([max(nbytes(m) / (HBM_PEAK_GBS * 1e3), nflops(m) / (BF16_PEAK_TFLOPS * 1e6))
-                                for m, _ in seq]))     # us
-        out[name] = {"launches": len(seq), "avg_us": round(us, 2), "bytes_per_launch": b, "flops_per_launch": f,
-                     "t_roof_us": round(t_roof, 2), "frac": round(t_roof / us, 4)}
+                                for m, _ in launches]))     # us
+        out[name] = {"launches": len(launches), "avg_us": round(us, 2), "bytes_per_launch": b,
+                     "flops_per_launch": f, "t_roof_us": round(t_roof, 2), "frac": round(t_roof / us, 4)}
     out["token_counts"] = sorted(set(m for m, _ in seq))
     return out
 
@@ -451,12 +476,18 @@ def main():
             roofline["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
         # all four projection GEMM classes of the step: roofline time over measured time (the MFMA-utilisation
         # figure where a GEMM is compute-bound; these token counts make every one of them HBM-bound)
-        names = ("gemm_qkv", "gemm_o", "gemm_w13", "gemm_w2")
+        names = [n for n in ("gemm_qkv", "gemm_o", "gemm_w13", "gemm_w2", "gemm_lm_head") if n in replay]
+
+        def agg(ns):
+            t_roof = sum(replay[n]["t_roof_us"] * replay[n]["launches"] for n in ns)
+            t_meas = sum(replay[n]["avg_us"] * replay[n]["launches"] for n in ns)
+            return round(t_roof / t_meas, 4)
+
         gemm_roofline = {
-            "frac": round(sum(replay[n]["t_roof_us"] for n in names) / sum(replay[n]["avg_us"] for n in names), 4),
-            "definition": "sum of t_roof over sum of measured launch time, t_roof = max(bytes / 8 TB/s, "
-                          "flops / 2.5166 PFLOP/s) per launch",
-            "classes": {n: {k: replay[n][k] for k in ("avg_us", "t_roof_us", "frac", "bytes_per_launch",
+            "frac": agg(names), "frac_layer_gemms": agg([n for n in names if n != "gemm_lm_head"]),
+            "definition": "over the QKV / O / MLP / LM-head launches of the replayed steps: sum of t_roof over sum "
+                          "of measured launch time, t_roof = max(bytes / 8 TB/s, flops / 2.5166 PFLOP/s) per launch",
+            "classes": {n: {k: replay[n][k] for k in ("launches", "avg_us", "t_roof_us", "frac", "bytes_per_launch",
                                                        "flops_per_launch")} for n in names}}
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
 
