@@ -111,3 +111,23 @@ int lsk_check_launch(const char* what);
   } while (0)
 
 static inline size_t lsk_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// ----------------------------------------------------------------------------- fragment-major activations
+// The layer loop keeps the GEMM inputs of launches of up to LSK_AF_MAX_TOKENS tokens in the packed weights'
+// fragment-major order: 16-token groups, each 16 x 32 block one 1 KiB fragment in MFMA lane order, so a wave's
+// activation load is one contiguous 1 KiB (8 full cache lines) instead of 16 half lines of 16 token rows.
+// Used where it measured faster: the qkv input (the attention RMSNorm output, 6 % faster qkv launches in the 8B
+// decode steps).  w13 and w2 read row-major inputs: fragment-major stores of their producers cost more than the
+// loads saved.
+// Element (token r, column c) of a matrix of nks = columns / 32 k-steps sits at lsk_frag_off(r, c, nks).
+// Buffers hold whole 16-token groups; the padding tokens' values only reach discarded output columns.
+// Both layouts hold the same values, so every result is bitwise the same as with row-major activations.
+#define LSK_AF_MAX_TOKENS 64
+__host__ __device__ __forceinline__ long lsk_frag_off(int r, int c, int nks) {
+  return ((long)((r >> 4) * nks + (c >> 5)) * 64 + (r & 15) + 16 * ((c & 31) >> 3)) * 8 + (c & 7);
+}
+// Internal to liblsk (used by lsk_forward_layers; same arguments and errors as the exported entry points,
+// with the fragment-major operands described above).
+int lsk_add_rmsnorm_impl(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w, float eps,
+                         void* x_out, long ldxo, void* out, long ldo, int out_frag, int n_rows, int dim, void* stream);
+int lsk_gemm_partial_af(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream);

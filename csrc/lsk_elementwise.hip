@@ -92,7 +92,7 @@ template <typename T, int KSC>
 __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ x, long ldx, const float* __restrict__ P,
                                                           int KS, long pstride, const T* __restrict__ w,
                                                           T* __restrict__ x_out, long ldxo, T* __restrict__ out,
-                                                          long ldo, int dim, float eps) {
+                                                          long ldo, int out_nks, int dim, float eps) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   float v[NORM_MAX_PASSES][8], wv[NORM_MAX_PASSES][8];
@@ -147,18 +147,19 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
       float o[8];
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = wv[p][i] * Elem<T>::round(v[p][i] * r);
-      Vec8<T>::st(out + (long)row * ldo + j, o);
+      // out_nks > 0: fragment-major output (the 8 elements at j stay one 16-byte slice)
+      Vec8<T>::st(out + (out_nks > 0 ? lsk_frag_off(row, j, out_nks) : (long)row * ldo + j), o);
     }
   }
 }
 
 template <typename T>
 static void launch_add_rmsnorm(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
-                               void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim, float eps,
-                               hipStream_t s) {
+                               void* x_out, long ldxo, void* out, long ldo, int out_nks, int n_rows, int dim,
+                               float eps, hipStream_t s) {
 #define LSK_NORM_LAUNCH(KSC_)                                                                                    \
   add_rmsnorm_kernel<T, KSC_><<<n_rows, 256, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w, (T*)x_out, \
-                                                     ldxo, (T*)out, ldo, dim, eps)
+                                                     ldxo, (T*)out, ldo, out_nks, dim, eps)
   if (KS == 4) LSK_NORM_LAUNCH(4);
   else if (KS == 2) LSK_NORM_LAUNCH(2);
   else if (KS == 8) LSK_NORM_LAUNCH(8);
@@ -170,19 +171,29 @@ static void launch_add_rmsnorm(const void* x, long ldx, const float* P, int KS, 
 extern "C" int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w,
                                float eps, void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim,
                                void* stream) {
+  return lsk_add_rmsnorm_impl(dtype, x, ldx, partials, ks, w, eps, x_out, ldxo, out, ldo, 0, n_rows, dim, stream);
+}
+
+int lsk_add_rmsnorm_impl(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w, float eps,
+                         void* x_out, long ldxo, void* out, long ldo, int out_frag, int n_rows, int dim,
+                         void* stream) {
   LSK_REQUIRE(x != nullptr && (ks == 0 || partials != nullptr) && (out == nullptr || w != nullptr), LSK_EARG,
               "lsk_add_rmsnorm: null pointer");
   LSK_REQUIRE(n_rows >= 0 && dim > 0 && dim % 8 == 0 && dim <= NORM_MAX_PASSES * 256 * 8 && ldx >= dim && ks >= 0 &&
                   ldx % 8 == 0 && (out == nullptr || (ldo >= dim && ldo % 8 == 0)) &&
                   (x_out == nullptr || (ldxo >= dim && ldxo % 8 == 0)),
               LSK_ESHAPE, "lsk_add_rmsnorm: bad shape n_rows=%d dim=%d", n_rows, dim);
+  LSK_REQUIRE(!out_frag || (dtype == LSK_DTYPE_BF16 && out != nullptr && dim % 32 == 0), LSK_EARG,
+              "lsk_add_rmsnorm: a fragment-major output needs bf16, an output and dim %% 32 == 0");
   if (n_rows == 0) return 0;
   const long pstride = (long)n_rows * dim;
+  const int out_nks = out_frag ? dim / 32 : 0;
   hipStream_t s = (hipStream_t)stream;
   if (dtype == LSK_DTYPE_BF16)
-    launch_add_rmsnorm<uint16_t>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, n_rows, dim, eps, s);
+    launch_add_rmsnorm<uint16_t>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, out_nks, n_rows, dim, eps,
+                                 s);
   else if (dtype == LSK_DTYPE_F32)
-    launch_add_rmsnorm<float>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, n_rows, dim, eps, s);
+    launch_add_rmsnorm<float>(x, ldx, partials, ks, pstride, w, x_out, ldxo, out, ldo, 0, n_rows, dim, eps, s);
   else
     LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_add_rmsnorm: dtype %d", dtype);
   return lsk_check_launch("lsk_add_rmsnorm");

@@ -63,7 +63,8 @@ constexpr int gemm_occupancy() {
   return 8 * CK * (NT + MS) + 4 * NT * MS <= 240 ? 2 : 1;
 }
 
-template <int NS, int MS, int EPI, int CK = gemm_unit<NS, MS, EPI>()>
+// AF: A is fragment-major (lsk_frag_off, whole 16-token groups).
+template <int NS, int MS, int EPI, int CK = gemm_unit<NS, MS, EPI>(), bool AF = false>
 __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm_bf16_kernel(const uint16_t* __restrict__ A, long lda,
                                                         const uint16_t* __restrict__ W, long ldw,
                                                         uint16_t* __restrict__ C, long ldc,
@@ -72,6 +73,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                         int kslice, int n_tiles, int m_tiles) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
+  static_assert(!AF || EPI == EPI_PARTIAL, "fragment-major A: split-K partial launches");
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
 
@@ -107,10 +109,15 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
   const uint16_t* arow[MS];
 #pragma unroll
   for (int t = 0; t < MS; ++t) {
-    int m = m0 + 16 * t + l16;
-    m = m < M - 1 ? m : M - 1;
-    arow[t] = A + (long)m * lda + k0 + 8 * lg;
+    if constexpr (AF) {
+      arow[t] = A + ((long)(m0 / 16 + t) * nks + (k0 >> 5)) * 512 + 8 * lane;  // k-step j at + j * 512
+    } else {
+      int m = m0 + 16 * t + l16;
+      m = m < M - 1 ? m : M - 1;
+      arow[t] = A + (long)m * lda + k0 + 8 * lg;
+    }
   }
+  constexpr long AK = AF ? 16 : 1;  // A elements per k (fragment-major: 512 per 32-k step)
 
   lsk_f32x4 acc[NT][MS];
 #pragma unroll
@@ -133,7 +140,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
 #pragma unroll
       for (int a = 0; a < NT; ++a) wf[ks][a] = ld_w(wrow[a] + (long)k * 16);
 #pragma unroll
-      for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + k);
+      for (int t = 0; t < MS; ++t) af[ks][t] = *(const lsk_bf16x8*)(arow[t] + AK * k);
     }
   };
   auto comp = [&](lsk_bf16x8 (&wf)[CK][NT], lsk_bf16x8 (&af)[CK][MS]) {
@@ -163,7 +170,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
 #pragma unroll
       for (int a = 0; a < NT; ++a) w1[a] = ld_w(wrow[a] + (long)k * 16);
 #pragma unroll
-      for (int t = 0; t < MS; ++t) a1[t] = *(const lsk_bf16x8*)(arow[t] + k);
+      for (int t = 0; t < MS; ++t) a1[t] = *(const lsk_bf16x8*)(arow[t] + AK * k);
 #pragma unroll
       for (int a = 0; a < NT; ++a)
 #pragma unroll
@@ -220,6 +227,25 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
       }
     }
     return;
+  } else if (EPI == LSK_EPI_SILU_MUL && NS >= 2 && N % 8 == 0 && ldc % 8 == 0) {
+    // 8 outputs per lane, one 16-byte store: a wave covers 16 tokens x 32 columns per pass (lane l: token
+    // 16 g + l % 16, columns 32 c + 8 (l / 16) .. +7), 8x fewer stores than one element per lane
+    constexpr int FC = TN / 32;
+    const int wv = tid >> 6;
+    for (int f = wv; f < MS * FC; f += 4) {
+      const int ml = 16 * (f / FC) + l16, nl0 = 32 * (f % FC) + 8 * lg;
+      const int m = m0 + ml, n = n0 + nl0;
+      if (m >= M || n >= N) continue;  // N % 8 == 0: the 8 columns are all in range or all out
+      uint32_t pk[4];
+#pragma unroll
+      for (int i = 0; i < 8; i += 2) {
+        const int a0 = (nl0 + i) >> 4, w0 = (nl0 + i) & 15;
+        const float o0 = rbf(silu_f(rbf(reduced(a0, ml, w0)))) * rbf(reduced(a0 + NS, ml, w0));
+        const float o1 = rbf(silu_f(rbf(reduced(a0, ml, w0 + 1)))) * rbf(reduced(a0 + NS, ml, w0 + 1));
+        pk[i >> 1] = (uint32_t)f2bf(o0) | ((uint32_t)f2bf(o1) << 16);
+      }
+      *(uint4*)(C + (long)m * ldc + n) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+    }
   } else {
     for (int o = tid; o < TN * TM; o += 256) {
       const int ml = o / TN, nl = o - ml * TN;
@@ -606,17 +632,31 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
                                                                 ffn, kslice, nt, mt);
 }
 
-// Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).
+// Fragment-major activations: split-K partial launches only.
+template <int NS, int MS>
+static void launch_bf16_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, float* P, int M,
+                           int N, int K, int kslice, int nt, int mt) {
+  gemm_bf16_kernel<NS, MS, EPI_PARTIAL, gemm_unit<NS, MS, EPI_PARTIAL>(), true><<<grid, 256, 0, s>>>(
+      A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt);
+}
+
+// Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).  af: a split-K
+// partial launch with a fragment-major A.
 static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipStream_t s, const void* A, long lda,
                           const void* W, long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av,
-                          int* ai, int M, int N, int K, int ffn, int kslice) {
+                          int* ai, int M, int N, int K, int ffn, int kslice, bool af = false) {
   const dim3 grid(mt > 1 ? (unsigned)(((nt + 7) / 8) * 8 * mt) : (unsigned)nt, 1, (unsigned)ks);
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)W;
   uint16_t* c = (uint16_t*)C;
   const uint16_t* r = (const uint16_t*)R;
-#define LSK_GEMM_CASE(NS_, MS_) \
-  if (ns == NS_ && ms == MS_) launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt);
+#define LSK_GEMM_CASE(NS_, MS_)                                                                                  \
+  if (ns == NS_ && ms == MS_) {                                                                                  \
+    if (af)                                                                                                      \
+      launch_bf16_af<NS_, MS_>(grid, s, a, w, ldw, P, M, N, K, kslice, nt, mt);                                  \
+    else                                                                                                         \
+      launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt); \
+  }
   LSK_GEMM_CASE(1, 1) LSK_GEMM_CASE(1, 2) LSK_GEMM_CASE(1, 3) LSK_GEMM_CASE(1, 4)
   LSK_GEMM_CASE(2, 1) LSK_GEMM_CASE(2, 2) LSK_GEMM_CASE(2, 3) LSK_GEMM_CASE(2, 4)
   LSK_GEMM_CASE(4, 1) LSK_GEMM_CASE(4, 2) LSK_GEMM_CASE(4, 3) LSK_GEMM_CASE(4, 4)
@@ -718,6 +758,19 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
   dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,
                 ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, K / ks);
   return lsk_check_launch("lsk_gemm_partial");
+}
+
+int lsk_gemm_partial_af(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream) {
+  LSK_REQUIRE(A && W && P, LSK_EARG, "lsk_gemm_partial_af: null pointer");
+  LSK_REQUIRE(M >= 0 && M <= LSK_AF_MAX_TOKENS && N > 0 && N % 16 == 0 && K > 0 && ks >= 1 && K % ks == 0 &&
+                  (K / ks) % 32 == 0,
+              LSK_ESHAPE, "lsk_gemm_partial_af: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
+  if (M == 0) return 0;
+  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks);
+  const int ms = ms_for(M);
+  dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), 1, ks, (hipStream_t)stream, A, 0, W, K, nullptr, 0, nullptr, 0, P,
+                nullptr, nullptr, M, N, K, 0, K / ks, true);
+  return lsk_check_launch("lsk_gemm_partial_af");
 }
 
 extern "C" size_t lsk_head_workspace_bytes(int M, int N) {

@@ -79,7 +79,8 @@ Layout layout(const Model& m, int N, int n_parts) {
     off += lsk_align_up(bytes, 256);
     return o;
   };
-  L.xn = take((size_t)N * m.dim * es);
+  const size_t n16 = (size_t)(N + 15) / 16 * 16;  // xn: whole 16-token groups (fragment-major use)
+  L.xn = take(n16 * m.dim * es);
   L.qkv = take((size_t)N * (qd + 2 * kvd) * es);
   L.q = take((size_t)N * qd * es);
   L.attn = take((size_t)N * qd * es);
@@ -233,6 +234,8 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
     // kernel reduces in slice order (RoPE + append; add + RMSNorm, which also materialises the residual
     // stream x).  Same rounding points as the unfused sequence.
     float* P = (float*)(ws + L.gpart);
+    // up to LSK_AF_MAX_TOKENS tokens, the qkv input (attention RMSNorm output) is kept fragment-major
+    const int af = N <= LSK_AF_MAX_TOKENS && m->dim % 32 == 0;
     const double norm_bytes_b = es_d * (2.0 * Nd * dimd + dimd);
     auto pbytes = [&](int ks, double width) { return 4.0 * ks * Nd * width; };
 #define LSK_PROF2(cls, b, f, call)                               \
@@ -244,19 +247,20 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
     for (int i = start; i < end; ++i) {
       if (i == start) {
         LSK_PROF2(LSK_PROF_NORM, norm_bytes_b, 4.0 * Nd * dimd,
-                  lsk_add_rmsnorm(m->dtype, x_in, m->dim, nullptr, 0, m->attn_norm[i], m->eps, nullptr, 0, xn, m->dim,
-                                  N, m->dim, stream));
+                  lsk_add_rmsnorm_impl(m->dtype, x_in, m->dim, nullptr, 0, m->attn_norm[i], m->eps, nullptr, 0, xn,
+                                       m->dim, af, N, m->dim, stream));
       } else {
         LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_w2, dimd), 4.0 * Nd * dimd,
-                  lsk_add_rmsnorm(m->dtype, x_out, m->dim, P, m->ks_w2, m->attn_norm[i], m->eps, x_out, m->dim, xn,
-                                  m->dim, N, m->dim, stream));
+                  lsk_add_rmsnorm_impl(m->dtype, x_out, m->dim, P, m->ks_w2, m->attn_norm[i], m->eps, x_out, m->dim,
+                                       xn, m->dim, af, N, m->dim, stream));
         if (capture && capture[i - 1]) {
           hipError_t e = hipMemcpyAsync(capture[i - 1], x_out, (size_t)N * m->dim * es, hipMemcpyDeviceToDevice, s);
           if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }
         }
       }
       LSK_PROF2(LSK_PROF_GEMM_QKV, es_d * (qkvd * dimd + Nd * dimd) + pbytes(m->ks_qkv, qkvd), 2.0 * Nd * dimd * qkvd,
-                lsk_gemm_partial(xn, m->dim, m->wqkv[i], m->dim, P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream));
+                af ? lsk_gemm_partial_af(xn, m->wqkv[i], P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream)
+                   : lsk_gemm_partial(xn, m->dim, m->wqkv[i], m->dim, P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream));
       LSK_PROF2(LSK_PROF_ROPE, pbytes(m->ks_qkv, qkvd) + es_d * Nd * qkvd, 6.0 * Nd * (qd + kvd),
                 lsk_rope_append_partial(m->dtype, P, m->ks_qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab,
                                         m->tab_len, rows, pos, N, m->n_heads, m->n_kv_heads, m->head_dim,
@@ -269,8 +273,8 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
                 lsk_gemm_partial(attn, qd, m->wo[i], qd, P, N, m->dim, qd, m->ks_o, stream));
       const void* xi = (i == start) ? x_in : x_out;
       LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_o, dimd), 4.0 * Nd * dimd,
-                lsk_add_rmsnorm(m->dtype, xi, m->dim, P, m->ks_o, m->ffn_norm[i], m->eps, x_out, m->dim, xn, m->dim,
-                                N, m->dim, stream));
+                lsk_add_rmsnorm_impl(m->dtype, xi, m->dim, P, m->ks_o, m->ffn_norm[i], m->eps, x_out, m->dim, xn,
+                                     m->dim, 0, N, m->dim, stream));
       LSK_PROF2(LSK_PROF_GEMM_W13, es_d * (2.0 * ffd * dimd + Nd * dimd + Nd * ffd), 4.0 * Nd * dimd * ffd,
                 lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
                          LSK_EPI_SILU_MUL, m->ffn, stream));

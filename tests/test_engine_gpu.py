@@ -111,6 +111,45 @@ def test_packed_forward_bf16_logits_within_tolerance(cuda):
     assert rel.max() < 2e-2
 
 
+def test_packed_forward_bf16_small_segments_equal_a_large_segment(cuda):
+    """Segments of up to 64 tokens keep the qkv GEMM's input fragment-major, larger ones row-major: the same
+    blocks give bitwise the same hidden states and KV either way."""
+    from thesis_amd.solutions.packed import Block, build_packed, packed_layers
+
+    _, g = _pair(small_cfg(), BF16)
+    B, P0 = 24, 24
+    g.allocate_cache(B, 128)
+    gen = torch.Generator().manual_seed(5)
+    for row in range(B):
+        ids = torch.randint(0, 512, (P0,), generator=gen)
+        packed_layers(g, g.embed(ids.to("cuda")), build_packed(g, [Block(row, 0, P0)]), 0, g.n_layers)
+    Ts = [1, 4, 2, 9, 3, 1, 5, 7, 2, 1, 6, 3, 8, 1, 2, 4, 9, 1, 3, 2, 5, 1, 7, 2]
+    ids = {row: torch.randint(0, 512, (T,), generator=gen) for row, T in enumerate(Ts)}
+
+    def run(rows):
+        pb = build_packed(g, [Block(r, P0, Ts[r]) for r in rows])
+        x = g.embed(torch.cat([ids[b.row] for b in pb.blocks]).to("cuda"))
+        h = packed_layers(g, x, pb, 0, g.n_layers)
+        out, off = {}, 0
+        for b in pb.blocks:
+            out[b.row] = h[off:off + b.T].cpu()
+            off += b.T
+        return out, pb.n_tokens
+
+    big, n_big = run(range(B))
+    kv_big = [(g.cache.k[i].clone(), g.cache.v[i].clone()) for i in range(g.n_layers)]
+    small, sizes = {}, []
+    for part in (range(0, 8), range(8, 16), range(16, 24)):
+        o, n = run(part)
+        small.update(o)
+        sizes.append(n)
+    assert n_big > 64 and max(sizes) <= 64, (n_big, sizes)
+    for row in range(B):
+        assert torch.equal(small[row], big[row]), f"row {row}"
+    for i in range(g.n_layers):
+        assert torch.equal(g.cache.k[i], kv_big[i][0]) and torch.equal(g.cache.v[i], kv_big[i][1]), f"layer {i}"
+
+
 def _oracle_ragged(o, blocks, seed=0):
     """The oracle half of _ragged_forward: the same id draws, prefixes and blocks -> logits."""
     from oracle.model import OBlock, build_packed as obuild, packed_layers as olayers
