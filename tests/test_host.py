@@ -583,6 +583,9 @@ def test_rocprof_summary_counts_after_the_calibration_copy(tmp_path, capsys):
     assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 192 * 256) == "gemm_qkv"
     assert ps.classify("gemm_bf16_kernel<2, 2, 3>", 128 * 256) == "gemm_o_w2"
     assert ps.classify("attn_bf16_kernel<128>") == "attention"
+    # the fragment-major-activation flag is a bool template argument
+    assert ps.classify("gemm_bf16_kernel<2, 2, 3, 4, true>", 192 * 256) == "gemm_qkv"
+    assert ps.classify("gemm_bf16_kernel<4, 3, 2, 2, false>") == "gemm_w13"
 
 
 def test_method_registry():

@@ -50,7 +50,7 @@ def short_name(name: str) -> str:
 def classify(short: str, grid_x_threads=None) -> str:
     """Kernel class; the split-K GEMMs of qkv and of o / w2 are told apart by their grid's x extent
     (weight row tiles), which the counter CSV does not carry (it reports the total grid)."""
-    m = re.match(r"gemm_bf16_kernel<(\d+), (\d+), (\d+)(?:, \d+)*>", short)
+    m = re.match(r"gemm_bf16_kernel<(\d+), (\d+), (\d+)(?:, (?:\d+|true|false))*>", short)
     if m:
         cls = _EPI.get(m.group(3), "gemm")
         if cls == "gemm_partial":
@@ -60,7 +60,7 @@ def classify(short: str, grid_x_threads=None) -> str:
             n_rows = grid_x_threads // 256 * 16 * ns
             cls = "gemm_qkv" if n_rows == 6144 else "gemm_o_w2"
         return cls
-    m = re.match(r"gemm_wide_kernel<(\d+), (\d+), (\d+)(?:, \d+)*>", short)
+    m = re.match(r"gemm_wide_kernel<(\d+), (\d+), (\d+)(?:, (?:\d+|true|false))*>", short)
     if m:                                    # wide-M tier: same classes, qkv and o / w2 not told apart
         cls = _EPI.get(m.group(3), "gemm")
         return "gemm_qkv_o_w2" if cls == "gemm_partial" else cls
