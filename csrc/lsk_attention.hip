@@ -86,7 +86,7 @@ template <int D, int QT>
 __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vt,
     const int32_t* __restrict__ recs, int n_rounds, uint16_t* __restrict__ out, float* __restrict__ o_part,
-    float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2) {
+    float* __restrict__ ml_part, int G, int Hkv, int S, float scale_log2, int out_nks) {
   constexpr int KSTEPS = D / 32;
   constexpr int CT = D / 16;
   constexpr int NW = ATTN_WAVES;
@@ -351,7 +351,9 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
           uint2 pk;
           pk.x = (uint32_t)f2bf(O.x / L) | ((uint32_t)f2bf(O.y / L) << 16);
           pk.y = (uint32_t)f2bf(O.z / L) | ((uint32_t)f2bf(O.w / L) << 16);
-          *(uint2*)(out + (long)(done.q_start + tt) * Hq * D + (long)(done.kvh * G + gg) * D + d) = pk;
+          // out_nks > 0: fragment-major output (the o projection's input); 4 columns stay one 8-byte piece
+          const int ot = done.q_start + tt, oc = (done.kvh * G + gg) * D + d;
+          *(uint2*)(out + (out_nks > 0 ? lsk_frag_off(ot, oc, out_nks) : (long)ot * Hq * D + oc)) = pk;
         } else {
           const long slot = ((long)done.part * Hkv + done.kvh) * ATTN_ROWS + qr;
           *(float4*)(o_part + slot * D + d) = O;
@@ -378,7 +380,7 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
                                                            const int32_t* __restrict__ groups,
                                                            const float* __restrict__ o_part,
                                                            const float* __restrict__ ml_part, T* __restrict__ out,
-                                                           int G, int Hkv) {
+                                                           int G, int Hkv, int out_nks) {
   __shared__ float s_w[ATTN_ROWS][ATTN_MAX_SPLITS];
   __shared__ float s_L[ATTN_ROWS];
   const int32_t* gp = groups + (long)blockIdx.x * 8;
@@ -416,7 +418,8 @@ __global__ __launch_bounds__(256) void attn_combine_kernel(const int32_t* __rest
     const float L = s_L[rl];
     const int r = row0 + rl;
     const int t = r / G, g = r - t * G;
-    T* o = out + (long)(q_start + t) * Hq * D + (long)(kvh * G + g) * D + 4 * d4;
+    const int ot = q_start + t, oc = (kvh * G + g) * D + 4 * d4;
+    T* o = out + (out_nks > 0 ? lsk_frag_off(ot, oc, out_nks) : (long)ot * Hq * D + oc);
     Elem<T>::st(o + 0, O.x / L);
     Elem<T>::st(o + 1, O.y / L);
     Elem<T>::st(o + 2, O.z / L);
@@ -853,7 +856,20 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
                                int rows_cap, void* out,
                                int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
                                size_t ws_bytes, void* stream) {
+  return lsk_ragged_attn_impl(dtype, q, kcache, vcache, blocks, works, n_works, groups, n_groups, n_parts, recs,
+                              n_rounds, n_slots, rows_cap, out, 0, n_heads, n_kv_heads, head_dim, max_seq, scale,
+                              workspace, ws_bytes, stream);
+}
+
+int lsk_ragged_attn_impl(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
+                         const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
+                         const int32_t* recs, int n_rounds, int n_slots, int rows_cap, void* out, int out_frag,
+                         int n_heads, int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace,
+                         size_t ws_bytes, void* stream) {
   LSK_REQUIRE(q && kcache && vcache && blocks && works && out, LSK_EARG, "lsk_ragged_attn: null pointer");
+  LSK_REQUIRE(!out_frag || (dtype == LSK_DTYPE_BF16 && (n_heads * head_dim) % 32 == 0), LSK_EARG,
+              "lsk_ragged_attn: a fragment-major output needs bf16 and n_heads * head_dim %% 32 == 0");
+  const int out_nks = out_frag ? n_heads * head_dim / 32 : 0;
   LSK_REQUIRE(dtype != LSK_DTYPE_BF16 || n_works == 0 || (recs && n_rounds > 0 && n_slots > 0), LSK_EARG,
               "lsk_ragged_attn: the bf16 path needs a schedule (lsk_attn_schedule)");
   LSK_REQUIRE(rows_cap > 0 && rows_cap % 16 == 0 && rows_cap <= ATTN_ROWS, LSK_EARG,
@@ -885,7 +901,7 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
   attn_bf16_kernel<DD, QT><<<pgrid, 64 * ATTN_WAVES, 0, s>>>((const uint16_t*)q, (const uint16_t*)kcache,     \
                                                               (const uint16_t*)vcache, recs, n_rounds,         \
                                                               (uint16_t*)out, o_part, ml_part, G, n_kv_heads,  \
-                                                              max_seq, scale_log2)
+                                                              max_seq, scale_log2, out_nks)
     if (head_dim == 128) {
       if (rows_cap == 16) LSK_ATTN_LAUNCH(128, 1); else LSK_ATTN_LAUNCH(128, ATTN_QT);
     } else {
@@ -898,10 +914,10 @@ extern "C" int lsk_ragged_attn(int dtype, const void* q, const void* kcache, con
       dim3 cg(n_groups, n_kv_heads);
       if (head_dim == 128)
         attn_combine_kernel<uint16_t, 128><<<cg, 256, 0, s>>>(blocks, groups, o_part, ml_part, (uint16_t*)out, G,
-                                                               n_kv_heads);
+                                                               n_kv_heads, out_nks);
       else
         attn_combine_kernel<uint16_t, 64><<<cg, 256, 0, s>>>(blocks, groups, o_part, ml_part, (uint16_t*)out, G,
-                                                              n_kv_heads);
+                                                              n_kv_heads, out_nks);
       return lsk_check_launch("lsk_ragged_attn(combine)");
     }
     return 0;

@@ -79,11 +79,11 @@ Layout layout(const Model& m, int N, int n_parts) {
     off += lsk_align_up(bytes, 256);
     return o;
   };
-  const size_t n16 = (size_t)(N + 15) / 16 * 16;  // xn: whole 16-token groups (fragment-major use)
+  const size_t n16 = (size_t)(N + 15) / 16 * 16;  // xn, attn: whole 16-token groups (fragment-major use)
   L.xn = take(n16 * m.dim * es);
   L.qkv = take((size_t)N * (qd + 2 * kvd) * es);
   L.q = take((size_t)N * qd * es);
-  L.attn = take((size_t)N * qd * es);
+  L.attn = take(n16 * qd * es);
   L.h = take((size_t)N * m.ffn * es);
   L.part = take(n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, m.n_kv_heads, m.head_dim) : 0);
   size_t gp = 0;
@@ -234,8 +234,10 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
     // kernel reduces in slice order (RoPE + append; add + RMSNorm, which also materialises the residual
     // stream x).  Same rounding points as the unfused sequence.
     float* P = (float*)(ws + L.gpart);
-    // up to LSK_AF_MAX_TOKENS tokens, the qkv input (attention RMSNorm output) is kept fragment-major
+    // up to LSK_AF_MAX_TOKENS tokens, the qkv input (attention RMSNorm output) and the o input (attention
+    // output) are kept fragment-major
     const int af = N <= LSK_AF_MAX_TOKENS && m->dim % 32 == 0;
+    const int af_o = N <= LSK_AF_MAX_TOKENS && qd % 32 == 0;
     const double norm_bytes_b = es_d * (2.0 * Nd * dimd + dimd);
     auto pbytes = [&](int ks, double width) { return 4.0 * ks * Nd * width; };
 #define LSK_PROF2(cls, b, f, call)                               \
@@ -266,11 +268,12 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
                                         m->tab_len, rows, pos, N, m->n_heads, m->n_kv_heads, m->head_dim,
                                         m->max_batch, m->max_seq, stream));
       LSK_PROF2(LSK_PROF_ATTN, attn_bytes, attn_flops,
-                lsk_ragged_attn(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups, n_parts,
-                                recs, n_rounds, n_slots, rows_cap, attn, m->n_heads, m->n_kv_heads, m->head_dim,
-                                m->max_seq, scale, part, part_bytes, stream));
+                lsk_ragged_attn_impl(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups,
+                                     n_parts, recs, n_rounds, n_slots, rows_cap, attn, af_o, m->n_heads,
+                                     m->n_kv_heads, m->head_dim, m->max_seq, scale, part, part_bytes, stream));
       LSK_PROF2(LSK_PROF_GEMM_O, es_d * (dimd * qd + Nd * qd) + pbytes(m->ks_o, dimd), 2.0 * Nd * qd * dimd,
-                lsk_gemm_partial(attn, qd, m->wo[i], qd, P, N, m->dim, qd, m->ks_o, stream));
+                af_o ? lsk_gemm_partial_af(attn, m->wo[i], P, N, m->dim, qd, m->ks_o, stream)
+                     : lsk_gemm_partial(attn, qd, m->wo[i], qd, P, N, m->dim, qd, m->ks_o, stream));
       const void* xi = (i == start) ? x_in : x_out;
       LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_o, dimd), 4.0 * Nd * dimd,
                 lsk_add_rmsnorm_impl(m->dtype, xi, m->dim, P, m->ks_o, m->ffn_norm[i], m->eps, x_out, m->dim, xn,

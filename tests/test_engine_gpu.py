@@ -112,8 +112,8 @@ def test_packed_forward_bf16_logits_within_tolerance(cuda):
 
 
 def test_packed_forward_bf16_small_segments_equal_a_large_segment(cuda):
-    """Segments of up to 64 tokens keep the qkv GEMM's input fragment-major, larger ones row-major: the same
-    blocks give bitwise the same hidden states and KV either way."""
+    """Segments of up to 64 tokens keep the qkv and o GEMMs' inputs fragment-major, larger ones row-major: the
+    same blocks give bitwise the same hidden states and KV either way."""
     from thesis_amd.solutions.packed import Block, build_packed, packed_layers
 
     _, g = _pair(small_cfg(), BF16)
