@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                         int kslice, int n_tiles, int m_tiles) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
-  static_assert(!AF || EPI == EPI_PARTIAL, "fragment-major A: split-K partial launches");
+  static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX, "fragment-major A: split-K partial and LM head");
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
 
@@ -802,6 +802,61 @@ extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W
   if (rc) return rc;
   argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
   return lsk_check_launch("lsk_head_argmax(pick)");
+}
+
+extern "C" size_t lsk_head_norm_workspace_bytes(int M, int N, int K) {
+  const size_t m16 = (size_t)(M + 15) / 16 * 16;
+  return lsk_align_up(m16 * (size_t)K * 2, 256) + lsk_head_workspace_bytes(M, N);
+}
+
+template <int MS>
+static void launch_head_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, uint16_t* C,
+                           long ldc, float* av, int* ai, int M, int N, int K, int nt) {
+  gemm_bf16_kernel<4, MS, EPI_ARGMAX, gemm_unit<4, MS, EPI_ARGMAX>(), true><<<grid, 256, 0, s>>>(
+      A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, K, nt, 1);
+}
+
+// Final norm into the workspace (fragment-major up to LSK_AF_MAX_TOKENS rows), then the head GEMM with its
+// per-tile argmax and the pick, as lsk_head_argmax.
+extern "C" int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const void* norm_w, float eps, const void* W,
+                                    long ldw, int M, int N, int K, void* logits, long ldl, int64_t* out,
+                                    const int64_t* dst_idx, void* workspace, size_t ws_bytes, void* stream) {
+  LSK_REQUIRE(h && norm_w && W && out, LSK_EARG, "lsk_head_norm_argmax: null pointer");
+  LSK_REQUIRE(dtype == LSK_DTYPE_BF16, LSK_EUNSUPPORTED, "lsk_head_norm_argmax: bf16 only");
+  LSK_REQUIRE(M >= 0 && N > 0 && K > 0 && ldh >= K && ldw == K && K % 32 == 0 && N % 64 == 0 &&
+                  (logits == nullptr || ldl >= N),
+              LSK_ESHAPE, "lsk_head_norm_argmax: bad shape M=%d N=%d K=%d (packed W, N %% 64 == 0, K %% 32 == 0)", M,
+              N, K);
+  if (M == 0) return 0;
+  const size_t need = lsk_head_norm_workspace_bytes(M, N, K);
+  LSK_REQUIRE(workspace != nullptr && ws_bytes >= need, LSK_EWORKSPACE,
+              "lsk_head_norm_argmax: workspace %zu < %zu", ws_bytes, need);
+  const size_t xn_bytes = lsk_align_up((size_t)(M + 15) / 16 * 16 * (size_t)K * 2, 256);
+  uint16_t* xn = (uint16_t*)workspace;
+  char* hw = (char*)workspace + xn_bytes;
+  const bool af = M <= LSK_AF_MAX_TOKENS;
+  int rc = lsk_add_rmsnorm_impl(dtype, h, ldh, nullptr, 0, norm_w, eps, nullptr, 0, xn, K, af ? 1 : 0, M, K, stream);
+  if (rc) return rc;
+  if (!af)
+    return lsk_head_argmax(dtype, xn, K, W, ldw, M, N, K, logits, ldl, out, dst_idx, hw, ws_bytes - xn_bytes, stream);
+  hipStream_t s = (hipStream_t)stream;
+  const int nt = N / 64;
+  const size_t half = lsk_align_up((size_t)M * nt * 4, 256);
+  float* av = (float*)hw;
+  int* ai = (int*)(hw + half);
+  const dim3 grid((unsigned)nt);
+  const uint16_t* w = (const uint16_t*)W;
+  uint16_t* c = (uint16_t*)logits;
+  switch (ms_for(M)) {  // one token tile: 16 * MS >= M
+    case 1: launch_head_af<1>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
+    case 2: launch_head_af<2>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
+    case 3: launch_head_af<3>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
+    default: launch_head_af<4>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
+  }
+  rc = lsk_check_launch("lsk_head_norm_argmax(gemm)");
+  if (rc) return rc;
+  argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
+  return lsk_check_launch("lsk_head_norm_argmax(pick)");
 }
 
 static int pack_common(bool pack, const void* src, void* dst, long ld, int N, int K, void* stream) {

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 5
+#define LSK_ABI_VERSION 6
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -144,6 +144,17 @@ int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P,
 size_t lsk_head_workspace_bytes(int M, int N);
 int lsk_head_argmax(int dtype, const void* A, long lda, const void* W, long ldw, int M, int N, int K, void* logits,
                     long ldl, int64_t* out, const int64_t* dst_idx, void* workspace, size_t ws_bytes, void* stream);
+
+/* Final norm + LM head + greedy pick in one call (bf16; W packed, ldw == K): out[dst_idx ? dst_idx[m] : m] =
+ * argmax_n rnd(rmsnorm(h[m], norm_w, eps) . W[n]) (first index on ties), optionally storing the bf16 logits
+ * [M, ldl].  Bitwise the same as lsk_rmsnorm followed by lsk_head_argmax; up to 64 rows the normalised rows
+ * stay in the workspace in the GEMM's fragment order.  workspace >= lsk_head_norm_workspace_bytes(M, N, K).
+ * Replaces LayerSkipLlama.head + .argmax(-1): F.linear(rms_norm(h, norm_w), lm_head_w) (common/model.py:329-330;
+ * solutions/engine.py:255,352,463). */
+size_t lsk_head_norm_workspace_bytes(int M, int N, int K);
+int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const void* norm_w, float eps, const void* W, long ldw,
+                         int M, int N, int K, void* logits, long ldl, int64_t* out, const int64_t* dst_idx,
+                         void* workspace, size_t ws_bytes, void* stream);
 
 /* Residual add + RMSNorm: x_new = rnd(x + rnd(sum_{s<ks} P[s])) (ks = 0: x_new = x), stored to x_out when
  * non-NULL; out = rmsnorm(x_new, w) when out != NULL.  P: fp32 [ks][n_rows][dim].

@@ -488,3 +488,30 @@ def test_head_argmax_matches_logits_argmax(cuda, M):
     big = torch.full((2 * M,), -1, dtype=torch.long, device=cuda)
     lsk.head_argmax(a, wd, big, dst_idx=dst)
     assert torch.equal(big[::2], ref) and (big[1::2] == -1).all()
+
+
+@pytest.mark.parametrize("M", [1, 17, 40, 64, 100])
+def test_head_norm_argmax_equals_norm_then_head(cuda, M):
+    """One-call final norm + head + pick (fragment-major normalised rows up to 64, row-major above) is bitwise
+    the RMSNorm followed by the fused head: ids, logits, and the scatter through dst_idx."""
+    lsk = _lsk()
+    g = _gen(13)
+    V, K = 4096 + 64, 512
+    h = (torch.randn(M, K, generator=g) * 3).to(BF16).to(cuda)
+    nw = (1 + 0.1 * torch.randn(K, generator=g)).to(BF16).to(cuda)
+    w = torch.randn(V, K, generator=g).to(BF16)
+    w[3000] = w[100]
+    wd = lsk.PackedWeight(w.to(cuda))
+    xn = torch.empty(M, K, dtype=BF16, device=cuda)
+    lsk.rmsnorm(h, nw, 1e-5, out=xn)
+    ref_ids = torch.empty(M, dtype=torch.long, device=cuda)
+    ref_lo = torch.empty(M, V, dtype=BF16, device=cuda)
+    lsk.head_argmax(xn, wd, ref_ids, logits=ref_lo)
+    ids = torch.empty(M, dtype=torch.long, device=cuda)
+    lo = torch.empty(M, V, dtype=BF16, device=cuda)
+    lsk.head_norm_argmax(h, nw, 1e-5, wd, ids, logits=lo)
+    assert torch.equal(ids, ref_ids) and torch.equal(lo, ref_lo)
+    dst = torch.arange(M, device=cuda) * 2
+    big = torch.full((2 * M,), -1, dtype=torch.long, device=cuda)
+    lsk.head_norm_argmax(h, nw, 1e-5, wd, big, dst_idx=dst)
+    assert torch.equal(big[::2], ref_ids) and (big[1::2] == -1).all()

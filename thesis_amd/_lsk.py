@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -45,6 +45,8 @@ _SIGS = {
     "lsk_gemm_partial": (_I, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _P]),
     "lsk_head_workspace_bytes": (_Z, [_I, _I]),
     "lsk_head_argmax": (_I, [_I, _P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _P, _P, _Z, _P]),
+    "lsk_head_norm_workspace_bytes": (_Z, [_I, _I, _I]),
+    "lsk_head_norm_argmax": (_I, [_I, _P, _L, _P, _F, _P, _L, _I, _I, _I, _P, _L, _P, _P, _P, _Z, _P]),
     "lsk_add_rmsnorm": (_I, [_I, _P, _L, _P, _I, _P, _F, _P, _L, _P, _L, _I, _I, _P]),
     "lsk_rope_append_partial": (_I, [_I, _P, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "lsk_embed": (_I, [_P, _L, _L, _P, _L, _P, _P, _P, _I, _P]),
@@ -566,6 +568,25 @@ def head_argmax(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor, dst_idx: to
                                   _ptr(logits), logits.stride(0) if logits is not None else 0, _ptr(out),
                                   _ptr(dst_idx), _ptr(workspace), workspace.numel() * workspace.element_size(),
                                   _stream()), "lsk_head_argmax")
+    return out
+
+
+def head_norm_argmax(h: torch.Tensor, norm_w: torch.Tensor, eps: float, w, out: torch.Tensor,
+                     dst_idx: torch.Tensor | None = None, logits: torch.Tensor | None = None,
+                     workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """argmax(lm_head(rmsnorm(h))) per row in one native call (bf16), bitwise equal to rmsnorm + head_argmax."""
+    _dev(h, norm_w, out, dst_idx, logits, workspace)
+    _check_weight(h, w)
+    M, K = h.shape
+    N = w.shape[0]
+    need = int(load().lsk_head_norm_workspace_bytes(M, N, K))
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=h.device)
+    _check(load().lsk_head_norm_argmax(dtype_code(h.dtype), _ptr(h), h.stride(0), _ptr(norm_w), float(eps), _ptr(w),
+                                       w.stride(0), M, N, K, _ptr(logits), logits.stride(0) if logits is not None else 0,
+                                       _ptr(out), _ptr(dst_idx), _ptr(workspace),
+                                       workspace.numel() * workspace.element_size(), _stream()),
+           "lsk_head_norm_argmax")
     return out
 
 

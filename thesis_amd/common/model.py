@@ -405,18 +405,19 @@ class LayerSkipLlama:
         if n == 0:
             return out
         es, dim, V = self.dtype.itemsize, self.cfg.dim, self.cfg.vocab_size
-        xn = self.buffer("head_xn", (n, dim), self.dtype)
         P = _lsk.Profiler
+        if self.dtype == torch.bfloat16:
+            # final norm + LM head with a per-tile argmax + the pick over tiles, one native call (no logits
+            # materialised; up to 64 rows the normalised rows stay in the GEMM's fragment order)
+            ws = self.buffer("head_ws", (int(_lsk.load().lsk_head_norm_workspace_bytes(n, V, dim)),), torch.uint8)
+            P.start(7, es * (float(V) * dim + 3.0 * n * dim + dim), 2.0 * n * dim * V)
+            _lsk.head_norm_argmax(x, self.norm_w, self.cfg.norm_eps, self.lm_head_w, out, dst_idx, workspace=ws)
+            P.stop()
+            return out
+        xn = self.buffer("head_xn", (n, dim), self.dtype)
         P.start(0, es * (2.0 * n * dim + dim), 4.0 * n * dim)
         _lsk.rmsnorm(x, self.norm_w, self.cfg.norm_eps, out=xn)
         P.stop()
-        if self.dtype == torch.bfloat16:
-            # fused LM head + per-tile argmax, then the pick over tiles (no logits materialised)
-            ws = self.buffer("head_ws", (int(_lsk.load().lsk_head_workspace_bytes(n, V)),), torch.uint8)
-            P.start(7, es * (float(V) * dim + n * dim), 2.0 * n * dim * V)
-            _lsk.head_argmax(xn, self.lm_head_w, out, dst_idx, workspace=ws)
-            P.stop()
-            return out
         logits = self.buffer("head_logits", (n, V), self.dtype)
         P.start(7, es * (float(V) * dim + n * dim + n * V), 2.0 * n * dim * V)
         _lsk.gemm(xn, self.lm_head_w, out=logits)
