@@ -601,13 +601,14 @@ static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 48 ? 3 : 4)
 // measured on MI355X at the 8B shapes, 64-row tiles win for w2, w13 (4 + 4 row groups, gate and up) and
 // the head at every M, and for qkv / o from 33 tokens on.  A split-K launch with short slices (<= 1024 k)
 // and fewer than two 64-row workgroups per CU is latency-bound per workgroup: up to 32 tokens, 32-row
-// tiles (twice the workgroups) measured faster for qkv (13.2 vs 14.7 us at 32 tokens).  The reduction
+// tiles (twice the workgroups) measured faster for qkv (13.2 vs 14.7 us at 32 tokens); with fragment-major
+// activations (cheaper activation loads per workgroup) up to 48 tokens (qkv -0.35 us, o -0.24 us per launch).  The reduction
 // order of an output does not depend on NS or MS (only on K and the plan's KS), so the tile follows M
 // without breaking batch invariance.
-static int tile_ns(int n, int M, int epi, int kslice = 0, int ks = 1) {
+static int tile_ns(int n, int M, int epi, int kslice = 0, int ks = 1, int short_max = 32) {
   int ns = 4;
   while (ns > 1 && n % (16 * ns) != 0) ns >>= 1;
-  if (ns == 4 && epi == EPI_PARTIAL && M <= 32 && kslice <= 1024 && (long)(n / 64) * ks < 512) ns = 2;
+  if (ns == 4 && epi == EPI_PARTIAL && M <= short_max && kslice <= 1024 && (long)(n / 64) * ks < 512) ns = 2;
   return ns;
 }
 
@@ -766,7 +767,7 @@ int lsk_gemm_partial_af(const void* A, const void* W, float* P, int M, int N, in
                   (K / ks) % 32 == 0,
               LSK_ESHAPE, "lsk_gemm_partial_af: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
-  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks);
+  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks, 48);
   const int ms = ms_for(M);
   dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), 1, ks, (hipStream_t)stream, A, 0, W, K, nullptr, 0, nullptr, 0, P,
                 nullptr, nullptr, M, N, K, 0, K / ks, true);
