@@ -66,6 +66,16 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 24, 8, 32, 8, 128, 64, 0.1, None, 0,
                                None) == -1                                            # rows per item not 16/32/48
     assert lib.lsk_model_create(1, 0, 64, 4, 2, 16, 128, 64, 1e-5, *([None] * 8), 1, 64, None, None, 1) < 0
+    # one-call final norm + head: pointers, dtype, shape and workspace are checked before any launch
+    hn = lib.lsk_head_norm_argmax
+    assert hn(1, None, 64, 8, 1e-5, 8, 64, 4, 128, 64, None, 0, 8, None, 8, 1 << 20, None) == -1     # null h
+    assert hn(5, 8, 64, 8, 1e-5, 8, 64, 4, 128, 64, None, 0, 8, None, 8, 1 << 20, None) == -3        # not bf16
+    assert hn(1, 8, 64, 8, 1e-5, 8, 64, 4, 100, 64, None, 0, 8, None, 8, 1 << 20, None) == -2        # N % 64
+    assert hn(1, 8, 64, 8, 1e-5, 8, 128, 4, 128, 64, None, 0, 8, None, 8, 1 << 20, None) == -2       # W not packed
+    need = lib.lsk_head_norm_workspace_bytes(4, 128, 64)
+    assert need == 2048 + lib.lsk_head_workspace_bytes(4, 128)     # 16 rows x 64 x bf16, then the head's
+    assert hn(1, 8, 64, 8, 1e-5, 8, 64, 4, 128, 64, None, 0, 8, None, 8, need - 1, None) == -4       # workspace
+    assert hn(1, 8, 64, 8, 1e-5, 8, 64, 0, 128, 64, None, 0, 8, None, 8, 0, None) == 0               # M = 0
 
 
 @pytest.mark.parametrize("D", [64, 128])
