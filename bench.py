@@ -269,43 +269,70 @@ def attention_case(seed: int = 0, n_req: int = 256, median: float = 1500.0, sigm
     return ctx, T, acc
 
 
-def run_attention_bench(args):
-    from thesis_amd import _lsk
+class AttentionInputs:
+    """The verify-attention microbenchmark's device state: 256 requests (attention_case) with Hq 32 / Hkv 8,
+    head_dim 128, a bf16 cache of N(0, 1) K (fragment-major) and V (blocked V^T), N(0, 1) queries, new K / V
+    rows for the append, the attention plan at the production split, its schedule and workspace."""
 
-    dev = torch.device("cuda:0")
     Hq, Hkv, D = 32, 8, 128
-    ctx, T, acc = attention_case(args.seed)
-    B = len(ctx)
-    S = int(math.ceil((ctx + T).max() / 64) * 64)
-    N = int(T.sum())
-    g = torch.Generator(device=dev).manual_seed(args.seed)
-    kc = torch.empty(B, Hkv, S // 32, D // 16, 64, 8, dtype=torch.bfloat16, device=dev).normal_(generator=g)  # frag K
-    vc = torch.empty(B, Hkv, S // 32, D, 32, dtype=torch.bfloat16, device=dev).normal_(generator=g)  # blocked V^T
-    q = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
-    k_new = torch.empty(N, Hkv, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
-    v_new = torch.empty_like(k_new).normal_(generator=g)
-    offs = np.concatenate([[0], np.cumsum(T)[:-1]])
-    blocks = np.stack([offs, ctx, T, np.arange(B)], axis=1).astype(np.int32)
-    n_slots = _lsk.cu_count(dev)
-    rows_cap = _lsk.attn_rows_cap(blocks, Hq // Hkv, _lsk.ATTN_SPLIT, Hkv, D, n_slots)
-    works, groups, n_parts = _lsk.attn_plan(blocks, Hq // Hkv, _lsk.ATTN_SPLIT, rows_cap)
-    blk_d = torch.from_numpy(blocks).to(dev)
-    wk_d = torch.from_numpy(works).to(dev)
-    gr_d = torch.from_numpy(groups).to(dev) if len(groups) else None
-    ws = torch.empty(max(_lsk.attn_workspace_bytes(n_parts, Hkv, D), 1), dtype=torch.uint8, device=dev)
-    out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
-    rows = torch.from_numpy(np.repeat(np.arange(B), T).astype(np.int32)).to(dev)
-    pos = torch.from_numpy((np.repeat(ctx, T) + (np.arange(N) - np.repeat(offs, T))).astype(np.int32)).to(dev)
-    slots = torch.arange(B, dtype=torch.int32, device=dev)
-    acc_d = torch.from_numpy(acc).to(dev)
-    kv_len = torch.from_numpy(ctx.copy()).to(dev)
 
-    recs, n_rounds = _lsk.attn_schedule(works, Hkv, n_slots)
-    recs_d = torch.from_numpy(recs).to(dev)
+    def __init__(self, seed: int, dev):
+        from thesis_amd import _lsk
 
-    def attn():
-        _lsk.ragged_attn(q, kc, vc, blk_d, wk_d, len(works), gr_d, len(groups), n_parts, out, Hq,
-                         1.0 / math.sqrt(D), ws, recs_d, n_rounds, n_slots, rows_cap)
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        self.ctx, self.T, self.acc = ctx, T, acc = attention_case(seed)
+        self.B = B = len(ctx)
+        self.S = S = int(math.ceil((ctx + T).max() / 64) * 64)
+        self.N = N = int(T.sum())
+        g = torch.Generator(device=dev).manual_seed(seed)
+        self.kc = torch.empty(B, Hkv, S // 32, D // 16, 64, 8, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        self.vc = torch.empty(B, Hkv, S // 32, D, 32, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        self.q = torch.empty(N, Hq, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        self.k_new = torch.empty(N, Hkv, D, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+        self.v_new = torch.empty_like(self.k_new).normal_(generator=g)
+        self.offs = offs = np.concatenate([[0], np.cumsum(T)[:-1]])
+        self.blocks = np.stack([offs, ctx, T, np.arange(B)], axis=1).astype(np.int32)
+        self.split = _lsk.ATTN_SPLIT        # what KVCache uses for a cache of >= 1024 (row, KV head) stripes
+        self.n_slots = _lsk.cu_count(dev)
+        self.rows_cap = _lsk.attn_rows_cap(self.blocks, Hq // Hkv, self.split, Hkv, D, self.n_slots)
+        self.works, self.groups, self.n_parts = _lsk.attn_plan(self.blocks, Hq // Hkv, self.split, self.rows_cap)
+        self.blk_d = torch.from_numpy(self.blocks).to(dev)
+        self.wk_d = torch.from_numpy(self.works).to(dev)
+        self.gr_d = torch.from_numpy(self.groups).to(dev) if len(self.groups) else None
+        self.ws = torch.empty(max(_lsk.attn_workspace_bytes(self.n_parts, Hkv, D), 1), dtype=torch.uint8, device=dev)
+        self.out = torch.empty(N, Hq * D, dtype=torch.bfloat16, device=dev)
+        self.rows = torch.from_numpy(np.repeat(np.arange(B), T).astype(np.int32)).to(dev)
+        self.pos = torch.from_numpy((np.repeat(ctx, T) + (np.arange(N) - np.repeat(offs, T))).astype(np.int32)).to(dev)
+        self.slots = torch.arange(B, dtype=torch.int32, device=dev)
+        self.acc_d = torch.from_numpy(acc).to(dev)
+        self.kv_len = torch.from_numpy(ctx.copy()).to(dev)
+        recs, self.n_rounds = _lsk.attn_schedule(self.works, Hkv, self.n_slots)
+        self.recs_d = torch.from_numpy(recs).to(dev)
+
+    def attn(self):
+        from thesis_amd import _lsk
+
+        _lsk.ragged_attn(self.q, self.kc, self.vc, self.blk_d, self.wk_d, len(self.works), self.gr_d,
+                         len(self.groups), self.n_parts, self.out, self.Hq, 1.0 / math.sqrt(self.D), self.ws,
+                         self.recs_d, self.n_rounds, self.n_slots, self.rows_cap)
+
+    def append(self):
+        from thesis_amd import _lsk
+
+        _lsk.kv_append(self.k_new, self.v_new, self.kc, self.vc, self.rows, self.pos)
+
+    def rollback(self):
+        from thesis_amd import _lsk
+
+        _lsk.kv_rollback(self.kv_len, self.slots, self.acc_d, self.B)
+
+
+def run_attention_bench(args):
+    dev = torch.device("cuda:0")
+    a = AttentionInputs(args.seed, dev)
+    Hq, Hkv, D = a.Hq, a.Hkv, a.D
+    ctx, T, B, N, offs = a.ctx, a.T, a.B, a.N, a.offs
+    works = a.works
 
     def timed(fn, iters):
         for _ in range(5):
@@ -318,9 +345,9 @@ def run_attention_bench(args):
         torch.cuda.synchronize()
         return float(np.mean([e0.elapsed_time(e1) for e0, e1 in ev]))
 
-    t_attn = timed(attn, args.attn_iters)
-    t_append = timed(lambda: _lsk.kv_append(k_new, v_new, kc, vc, rows, pos), args.attn_iters)
-    t_rb = timed(lambda: _lsk.kv_rollback(kv_len, slots, acc_d, B), args.attn_iters)
+    t_attn = timed(a.attn, args.attn_iters)
+    t_append = timed(a.append, args.attn_iters)
+    t_rb = timed(a.rollback, args.attn_iters)
     kv_bytes = float((ctx + T).sum()) * Hkv * D * 2 * 2
     qo_bytes = float(N) * Hq * D * 2 * 2
     attn_bytes = kv_bytes + qo_bytes
@@ -330,7 +357,7 @@ def run_attention_bench(args):
         "workload": "verify attention: 256 requests, GQA 32/8, head_dim 128, bf16 KV, lognormal contexts "
                     "(median 1500, sigma 0.5, clip [64, 8192]), 1-9 query rows each",
         "contexts": {"sum": int(ctx.sum()), "median": float(np.median(ctx)), "max": int(ctx.max())},
-        "query_rows": N, "work_items": int(len(works)), "rows_per_item": rows_cap, "split_positions": _lsk.ATTN_SPLIT,
+        "query_rows": N, "work_items": int(len(works)), "rows_per_item": a.rows_cap, "split_positions": a.split,
         "attn_us": round(1e3 * t_attn, 2), "attn_bytes": attn_bytes,
         "attn_GBs": round(attn_bytes / (t_attn * 1e-3) / 1e9, 1),
         "attn_hbm_frac": round(attn_bytes / (t_attn * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
@@ -347,21 +374,38 @@ def run_attention_bench(args):
     # size-independent property at full size: a sample of requests against the fp64 brute force
     if args.check_attn:
         from oracle.model import brute_attention
+        from thesis_amd import _lsk
 
-        got = out.float().cpu()
-        kh, vh, qh = _lsk.k_from_frag(kc.cpu()), _lsk.v_from_blocked(vc.cpu()), q.cpu()
+        a.attn()
+        got = a.out.float().cpu()
         worst = 0.0
         for r in (0, B // 2, B - 1):
             sl = slice(int(offs[r]), int(offs[r] + T[r]))
-            ref = brute_attention(qh[sl], kh, vh, [r] * int(T[r]), list(range(ctx[r], ctx[r] + T[r])), Hq // Hkv)
+            kh, vh = _lsk.k_from_frag(a.kc[r:r + 1].cpu()), _lsk.v_from_blocked(a.vc[r:r + 1].cpu())
+            ref = brute_attention(a.q[sl].cpu(), kh, vh, [0] * int(T[r]), list(range(ctx[r], ctx[r] + T[r])),
+                                  Hq // Hkv)
             worst = max(worst, float((got[sl].double() - ref).abs().max()))
         res["check_max_abs_err_vs_fp64"] = worst
-    del kc, vc
+    del a
     torch.cuda.empty_cache()
     return res
 
 
 # ----------------------------------------------------------------------------- CPU baseline
+
+def host_cores() -> tuple:
+    """(threads to use, CPUs in the affinity mask, cgroup CPU quota or None): the host cores this process may
+    actually run on, i.e. the affinity mask capped by the container's CPU quota (/sys/fs/cgroup/cpu.max)."""
+    affinity = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return (min(affinity, quota) if quota else affinity), affinity, quota
+
 
 def run_cpu_baseline(args, trace: list, k: int):
     """The CPU oracle replays the GPU run's first timed steps (same segment shapes, bf16) on the host
@@ -372,7 +416,9 @@ def run_cpu_baseline(args, trace: list, k: int):
     c = PRESETS["llama3-8b"]
     ocfg = OracleConfig(c.vocab_size, c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate_size,
                         c.norm_eps, c.rope_theta, c.max_position_embeddings)
-    threads = torch.get_num_threads()
+    threads, affinity, quota = host_cores()
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     t0 = time.time()
     m = OracleLlama.synthetic(ocfg, dtype=torch.bfloat16, seed=args.seed, max_seq=2048)
     m.allocate_cache(args.batch, 1024 + args.max_new + 8 + 40)
@@ -399,11 +445,13 @@ def run_cpu_baseline(args, trace: list, k: int):
             if spent >= args.cpu_seconds and tokens > 0:
                 break
     del m
+    torch.set_num_threads(prev_threads)
     return {"value": round(tokens / spent, 2) if spent > 0 else None, "unit": "tokens/s", "cores": threads,
             "kind": "port",
-            "sample": f"CPU oracle (torch-CPU restatement, bf16) replaying the first {steps} timed engine steps "
-                      f"({n_deep} deep) of this run with the same packed segment shapes; {tokens} committed "
-                      f"tokens in {spent:.1f}s"}
+            "sample": f"CPU oracle (torch-CPU restatement, bf16) on {threads} threads (CPUs in this process's "
+                      f"affinity mask: {affinity}; cgroup CPU quota: {quota if quota else 'none'}) replaying the "
+                      f"first {steps} timed engine steps ({n_deep} deep) of this run with the same packed segment "
+                      f"shapes; {tokens} committed tokens in {spent:.1f}s"}
 
 
 # ----------------------------------------------------------------------------- main

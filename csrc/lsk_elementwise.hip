@@ -89,9 +89,11 @@ struct Vec8<float> {
 // KSC: the number of K-slice partials as a compile-time constant (all of a thread's partial loads are issued
 // before the first add; the adds keep slice order), or -1 for a run-time count.
 template <typename T, int KSC>
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ x, long ldx, const float* __restrict__ P,
+// x and x_out may be the same rows (the layer runner updates the residual stream in place), so neither is
+// declared __restrict__; every thread reads its 8 elements of a row before it writes them.
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* x, long ldx, const float* __restrict__ P,
                                                           int KS, long pstride, const T* __restrict__ w,
-                                                          T* __restrict__ x_out, long ldxo, T* __restrict__ out,
+                                                          T* x_out, long ldxo, T* __restrict__ out,
                                                           long ldo, int out_nks, int dim, float eps) {
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -125,8 +127,8 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* __restrict__ 
         }
 #pragma unroll
         for (int i = 0; i < 8; ++i) v[p][i] = Elem<T>::round(v[p][i] + Elem<T>::round(acc[i]));
-        if (x_out != nullptr) Vec8<T>::st(x_out + (long)row * ldxo + j, v[p]);
       }
+      if (x_out != nullptr) Vec8<T>::st(x_out + (long)row * ldxo + j, v[p]);  // x_new (= x when KS == 0)
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss += v[p][i] * v[p][i];
     }

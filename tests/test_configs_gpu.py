@@ -5,8 +5,12 @@ is lossless token for token against autoregressive decoding of the same model, i
   config 3  Llama3.2-1B shape, bf16, B = 64, prompts of 512, exit 6, draft 6 (32 new tokens here; the forced
             geometric acceptance run checks the rollback bookkeeping)
   config 4  Llama3-8B shape, bf16, B = 32, prompts U[128, 1024], exit 8, aspire drafts in [2, 8] (24 new tokens)
+  config 2  isolated verify attention + KV append + rollback at the microbenchmark's exact inputs: 256
+            requests, GQA 32/8, head_dim 128, bf16 cache, lognormal contexts (median 1500, sigma 0.5, clipped to
+            [64, 8192]), 1-9 query rows each, the production 4096-position splits (bench.AttentionInputs)
   config 5  Llama2-7B shape (MHA, vocab 32000), bf16, exit 8, draft 4, 256-token prefill chunks piggybacked on
-            the decode steps (M3); 16 slots and 24 requests of U[256, 1024] prompt tokens, 16 new tokens each
+            the decode steps (M3); 16 slots and 24 requests of U[256, 1024] prompt tokens, 16 new tokens each,
+            and the open-loop driver at B = 128 with Poisson arrivals at 8 requests/s
 The reference's own check for these paths is spec == AR (tests/test_eesd.py:55-97); the oracle comparisons of
 the same code paths run at small shapes in the other test files.
 """
@@ -14,7 +18,9 @@ the same code paths run at small shapes in the other test files.
 from __future__ import annotations
 
 import gc
+import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -97,3 +103,82 @@ def test_config5_llama2_7b_bf16_m3_chunks(cuda):
                       m3_chunk_cap=256, prefill_chunk=256, max_wait=100)
     assert sp == ar
     assert eng.stats["piggyback_tokens"] > 0
+
+
+def test_config5_llama2_7b_poisson_b128_spec_equals_ar(cuda):
+    """Open loop (solutions/engine.py:625-673): Poisson arrivals at 8 requests/s into B = 128 slots, 256-token
+    prompt chunks piggybacked on the decode steps.  Whatever packing the arrival times produce, every request's
+    tokens equal its autoregressive tokens, and the M3 chunks wrote the KV the deep segments read."""
+    from thesis_amd.solutions.cost_model import GPUParams, ModelDims, RooflineCostModel
+    from thesis_amd.solutions.engine import EESDEngine, EngineConfig
+
+    m = _model("llama2-7b", torch.bfloat16, 1152)
+    prompts = _prompts(24, m.cfg.vocab_size, 256, 1024, seed=15)
+    gpu = GPUParams(bw=6.6e9, flops=1.2e12, t_op=0.007, n_op_layer=9, n_op_bucket=0, n_op_head=3, n_op_segment=1,
+                    flops_eff=4.2e11, knee_measured=600.0)
+    cm = RooflineCostModel(gpu, ModelDims.from_config(m.cfg))
+    ar, _, _ = _run(m, prompts, 24, 1024, 32, cost_model=cm, mode="ar", k=8)
+    eng = EESDEngine(m, 128, 1024, 32, (), EngineConfig(sched="fixed", k=8, gamma=4, d_max=4, prefill="m3",
+                                                        m3_chunk_cap=256, prefill_chunk=256, max_wait=100), cm)
+    res = eng.run_poisson(prompts, 8.0, len(prompts), warm_requests=0, seed=4, keep_outputs=True)
+    sp = {c["pid"]: c["tokens"] for c in res["completions"]}
+    assert sp == ar
+    assert res["metrics"]["poisson_rate_per_s"] == 8.0 and res["metrics"]["evaluated_completions"] == len(prompts)
+    assert eng.stats["piggyback_tokens"] > 0, "arrivals during decoding must ride the decode steps"
+    assert res["metrics"]["wall_throughput_tok_s"] > 0
+
+
+# ----------------------------------------------------------------------------- config 2: the microbenchmark
+
+def _ubench_sample(a) -> list:
+    """Requests checked against the fp64 brute force: the longest context, the shortest, every one whose
+    block crosses a split boundary (up to 4), the largest and smallest query blocks, and a seeded spread."""
+    ctx, T, split = a.ctx, a.T, a.split
+    end = ctx + T
+    crossing = [int(r) for r in np.flatnonzero((ctx // split) != ((end - 1) // split))][:4]
+    multi = [int(r) for r in np.flatnonzero(end > split)][:3]
+    picks = [int(np.argmax(ctx)), int(np.argmin(ctx)), int(np.argmax(T)), int(np.argmin(T))] + crossing + multi
+    picks += [int(r) for r in np.random.default_rng(7).choice(a.B, 6, replace=False)]
+    return sorted(set(picks))
+
+
+def test_config2_verify_attention_microbench_matches_brute_force(cuda):
+    """The microbenchmark's attention launch (256 requests, 4096-position splits, contexts up to 8192, the rows
+    cap and schedule the benchmark uses) after its KV append: the appended rows equal the inputs bitwise, the
+    cached prefix [0, ctx) is untouched, sampled requests (longest, multi-split, split-crossing, ragged) match
+    the fp64 brute force at the kernel tests' bounds, and the rollback gives kv_len = ctx + accepted + 1."""
+    import bench
+    from oracle.model import brute_attention
+    from thesis_amd import _lsk
+
+    a = bench.AttentionInputs(0, cuda)
+    Hq, Hkv, D = a.Hq, a.Hkv, a.D
+    assert a.ctx.max() > a.split and a.n_parts > 0              # two-split requests, combine groups in the plan
+    sample = _ubench_sample(a)
+    assert len(sample) >= 8
+    before = {r: (a.kc[r:r + 1].clone(), a.vc[r:r + 1].clone()) for r in sample[:4]}
+    a.append()
+    a.attn()
+    torch.cuda.synchronize()
+    got = a.out.float().cpu()
+    k_new, v_new = a.k_new.cpu(), a.v_new.cpu()
+    worst_max, worst_mean = 0.0, 0.0
+    for r in sample:
+        c, t, o = int(a.ctx[r]), int(a.T[r]), int(a.offs[r])
+        kh = _lsk.k_from_frag(a.kc[r:r + 1].cpu())
+        vh = _lsk.v_from_blocked(a.vc[r:r + 1].cpu())
+        assert torch.equal(kh[0, :, c:c + t].transpose(0, 1), k_new[o:o + t]), f"request {r}: appended K"
+        assert torch.equal(vh[0, :, c:c + t].transpose(0, 1), v_new[o:o + t]), f"request {r}: appended V"
+        if r in before:
+            k0 = _lsk.k_from_frag(before[r][0].cpu())
+            v0 = _lsk.v_from_blocked(before[r][1].cpu())
+            assert torch.equal(kh[..., :c, :], k0[..., :c, :]) and torch.equal(vh[..., :c, :], v0[..., :c, :])
+        ref = brute_attention(a.q[o:o + t].cpu(), kh, vh, [0] * t, list(range(c, c + t)), Hq // Hkv)
+        err = (got[o:o + t].double() - ref).abs()
+        worst_max, worst_mean = max(worst_max, float(err.max())), max(worst_mean, float(err.mean()))
+        assert err.max() < 2e-2 and err.mean() < 3e-3, (r, c, t, float(err.max()), float(err.mean()))
+    print(f"config 2: {len(sample)} requests (contexts {sorted(int(a.ctx[r]) for r in sample)}), split {a.split}, "
+          f"rows cap {a.rows_cap}: max |err| {worst_max:.3e}, worst mean {worst_mean:.3e}")
+    a.rollback()
+    assert torch.equal(a.kv_len.cpu(), torch.from_numpy(a.ctx + a.acc + 1))
+    assert (a.acc <= a.T - 1).all() and (a.acc >= 0).all()

@@ -187,6 +187,148 @@ def test_bf16_logits_are_as_close_to_fp32_as_the_oracles_bf16(cuda):
     print(f"relative L2 to fp32: oracle bf16 max {d_ref.max():.3e} mean {d_ref.mean():.3e}; "
           f"this build bf16 max {d_ours.max():.3e} mean {d_ours.mean():.3e}")
     assert d_ours.mean() <= 1.25 * d_ref.mean() and d_ours.max() <= 1.5 * d_ref.max()
+    # two-sided: a kernel that skipped one of the reference's bf16 rounding points would sit closer to fp32
+    assert d_ours.mean() >= 0.75 * d_ref.mean()
+
+
+ONE_LAYER_CFGS = {
+    "small": dict(n_layers=1),
+    "d128": dict(n_layers=1, dim=1024, n_heads=8, n_kv_heads=2, head_dim=128, intermediate_size=2816),
+}
+
+
+def _one_layer_state(ocfg, seed, n_prefix=40):
+    """The same bf16 state on both sides: bf16 weights, a cached prefix of random bf16 K / V (written into the
+    oracle's [B, Hkv, S, D] cache and copied into the kernels' layouts), bf16 input rows of ragged blocks."""
+    from oracle.model import OBlock, OracleLlama, build_packed as obuild, random_weights
+    from thesis_amd import _lsk
+    from thesis_amd.common.model import LayerSkipLlama
+    from thesis_amd.solutions.packed import Block, build_packed
+
+    w = random_weights(ocfg, seed=seed, std=0.05)
+    o = OracleLlama(ocfg, w, dtype=BF16, max_seq=1024)
+    g = LayerSkipLlama.from_weights(to_model_config(ocfg), w, device="cuda", dtype=BF16, max_seq=1024)
+    B = 6
+    o.allocate_cache(B, 128)
+    g.allocate_cache(B, 128)
+    gen = torch.Generator().manual_seed(seed + 1)
+    for i in range(ocfg.n_layers):
+        shape = o.cache.k[i][:, :, :n_prefix].shape
+        o.cache.k[i][:, :, :n_prefix] = torch.randn(shape, generator=gen).to(BF16)
+        o.cache.v[i][:, :, :n_prefix] = torch.randn(shape, generator=gen).to(BF16)
+        g.cache.kstore[i].copy_(_lsk.k_to_frag(o.cache.k[i]).cuda())
+        g.cache.vb[i].copy_(_lsk.v_to_blocked(o.cache.v[i]).cuda())
+    blocks = [(0, n_prefix, 1), (1, n_prefix, 4), (2, n_prefix, 2), (3, n_prefix, 9), (4, n_prefix, 1),
+              (5, n_prefix, 6)]
+    opb = obuild(o, [OBlock(*b) for b in blocks])
+    gpb = build_packed(g, [Block(*b) for b in blocks])
+    assert [(b.row, b.pos0, b.T) for b in gpb.blocks] == [(b.row, b.pos0, b.T) for b in opb.blocks]
+    x = torch.randn(opb.n_tokens, ocfg.dim, generator=gen).to(BF16)
+    return o, g, opb, gpb, x
+
+
+def _rel(a, b):
+    a, b = a.float().cpu(), b.float().cpu()
+    return float((a - b).norm() / b.norm()), float((a != b).float().mean())
+
+
+@pytest.mark.parametrize("which", list(ONE_LAYER_CFGS))
+def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
+    """bf16 parity of one layer, stage by stage (solutions/packed.py:169-185, common/model.py:143-156): every GPU
+    stage is fed the bf16 oracle's input of that stage (the reference's eager bf16 ops and rounding points).
+      * RMSNorm, qkv GEMM + RoPE + KV append, o GEMM + residual, w13 GEMM + silu-mul, w2 GEMM + residual:
+        relative L2 <= 1e-4 (a tenth of the 1e-3 bar) and at most 2e-3 of the elements one rounding apart
+        (fp32 summation order only);
+      * attention: both sides round the softmax weights to bf16 for the P.V product, at different running
+        maxima, so each is ~2e-3 from the exact result.  Bar: this build's distance to the fp64 brute force lies
+        within [0.75, 1.25] x the oracle's own (a dropped term or a missing rescale lands far outside), and the
+        two differ by at most 3e-3."""
+    import math
+    import torch.nn.functional as F
+
+    from oracle.model import attend, brute_attention, rms_norm, rope
+    from thesis_amd import _lsk
+
+    ocfg = small_cfg(**ONE_LAYER_CFGS[which])
+    o, g, opb, gpb, x = _one_layer_state(ocfg, seed=3)
+    lw, glw, cfg = o.layers[0], g.layers[0], ocfg
+    N, qs, kvs = x.shape[0], o.q_size, o.kv_size
+    with torch.inference_mode():                              # the oracle's stages (the reference's ops)
+        xn1 = rms_norm(x, lw.attn_norm, cfg.norm_eps)
+        qkv = F.linear(xn1, lw.wqkv)
+        q = rope(qkv[:, :qs].reshape(N, cfg.n_heads, cfg.head_dim), opb.cos, opb.sin)
+        k = rope(qkv[:, qs:qs + kvs].reshape(N, cfg.n_kv_heads, cfg.head_dim), opb.cos, opb.sin)
+        v = qkv[:, qs + kvs:].reshape(N, cfg.n_kv_heads, cfg.head_dim)
+        o.cache.k[0][opb.rows, :, opb.pos] = k
+        o.cache.v[0][opb.rows, :, opb.pos] = v
+        att = attend(o, 0, q, opb)
+        x1 = x + F.linear(att, lw.wo)
+        xn2 = rms_norm(x1, lw.ffn_norm, cfg.norm_eps)
+        gg, uu = F.linear(xn2, lw.w13).chunk(2, dim=-1)
+        hh = F.silu(gg) * uu
+        out = x1 + F.linear(hh, lw.w2)
+    c = lambda t: t.contiguous().cuda()  # noqa: E731
+    rows, pos = opb.rows.to(torch.int32), opb.pos.to(torch.int32)
+    q_gpu = torch.empty(N, cfg.n_heads, cfg.head_dim, dtype=BF16, device="cuda")
+    _lsk.rope_append(_lsk.gemm(c(xn1), glw.wqkv), q_gpu, g.cache.kstore[0], g.cache.vb[0], g.rope_cos, g.rope_sin,
+                     c(rows), c(pos), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)
+    kv_same = (float((g.cache.k[0].cpu() == o.cache.k[0]).float().mean()),
+               float((g.cache.v[0].cpu() == o.cache.v[0]).float().mean()))
+    stages = {
+        "norm1": _rel(_lsk.rmsnorm(c(x), c(lw.attn_norm), cfg.norm_eps), xn1),
+        "qkv+rope": _rel(q_gpu, q),
+        "o+residual": _rel(_lsk.gemm(c(att), glw.wo, residual=c(x), epilogue=_lsk.EPI_RESIDUAL), x1),
+        "norm2": _rel(_lsk.rmsnorm(c(x1), c(lw.ffn_norm), cfg.norm_eps), xn2),
+        "w13+silu*mul": _rel(_lsk.gemm(c(xn2), glw.w13, epilogue=_lsk.EPI_SILU_MUL), hh),
+        "w2+residual": _rel(_lsk.gemm(c(hh), glw.w2, residual=c(x1), epilogue=_lsk.EPI_RESIDUAL), out),
+    }
+    # attention on the oracle's q and (appended) cache, through the kernel's own plan
+    g.cache.kstore[0].copy_(_lsk.k_to_frag(o.cache.k[0]).cuda())
+    g.cache.vb[0].copy_(_lsk.v_to_blocked(o.cache.v[0]).cuda())
+    tab = np.stack([gpb.offsets[:-1], gpb.blk_pos0, gpb.blk_T, gpb.blk_rows], axis=1).astype(np.int32)
+    n_slots = _lsk.cu_count(cuda)
+    cap = _lsk.attn_rows_cap(tab, o.group, g.cache.attn_split, cfg.n_kv_heads, cfg.head_dim, n_slots)
+    works, groups, n_parts = _lsk.attn_plan(tab, o.group, g.cache.attn_split, cap)
+    recs, n_rounds = _lsk.attn_schedule(works, cfg.n_kv_heads, n_slots)
+    att_gpu = torch.empty(N, qs, dtype=BF16, device="cuda")
+    ws = torch.empty(max(_lsk.attn_workspace_bytes(n_parts, cfg.n_kv_heads, cfg.head_dim), 1), dtype=torch.uint8,
+                     device="cuda")
+    dv = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()  # noqa: E731
+    _lsk.ragged_attn(c(q), g.cache.kstore[0], g.cache.vb[0], dv(tab), dv(works), len(works),
+                     dv(groups) if len(groups) else None, len(groups), n_parts, att_gpu, cfg.n_heads,
+                     1.0 / math.sqrt(cfg.head_dim), ws, dv(recs), n_rounds, n_slots, cap)
+    exact = brute_attention(q, o.cache.k[0], o.cache.v[0], opb.rows.tolist(), opb.pos.tolist(), o.group)
+    d_ours, d_oracle, d_pair = _rel(att_gpu, exact)[0], _rel(att, exact)[0], _rel(att_gpu, att)[0]
+    print(f"[{which}] " + "; ".join(f"{k} relL2 {r:.2e} differ {f:.1e}" for k, (r, f) in stages.items())
+          + f"; K/V equal {kv_same[0]:.5f}/{kv_same[1]:.5f}; attention relL2 to exact: this build {d_ours:.3e}, "
+            f"oracle {d_oracle:.3e}, between them {d_pair:.3e}")
+    for name, (r, f) in stages.items():
+        assert r <= 1e-4 and f <= 2e-3, (name, r, f)
+    assert min(kv_same) >= 0.999
+    assert 0.75 * d_oracle <= d_ours <= 1.25 * d_oracle
+    assert d_pair <= 3e-3
+
+
+@pytest.mark.parametrize("which", list(ONE_LAYER_CFGS))
+def test_one_layer_bf16_logits_against_the_bf16_oracle(cuda, which):
+    """The whole layer end to end (packed_layers, then the final norm + LM head) against the bf16 oracle from the
+    same state.  Every stage but attention agrees to ~1e-5 (test above); the attention's bf16 softmax weights
+    differ in rounding on the two sides (each ~2e-3 from exact), which carries into the logits: measured
+    4.6e-3 (head_dim 64) and 6.6e-3 (head_dim 128) per-row relative L2.  Bar: 1e-2, and the greedy tokens agree
+    on every row whose top-2 logit margin exceeds that noise."""
+    from oracle.model import packed_layer as olayer
+    from thesis_amd.solutions.packed import packed_layers
+
+    o, g, opb, gpb, x = _one_layer_state(small_cfg(**ONE_LAYER_CFGS[which]), seed=3)
+    with torch.inference_mode():
+        lo = o.head(olayer(o, 0, x, opb)).float()
+    lg = g.head(packed_layers(g, x.cuda(), gpb, 0, 1)).cpu().float()
+    rel = (lg - lo).norm(dim=-1) / lo.norm(dim=-1)
+    print(f"[{which}] one bf16 layer, logits per-row relative L2: max {rel.max():.3e} mean {rel.mean():.3e}")
+    assert rel.max() <= 1e-2
+    top2 = lo.topk(2, dim=-1).values
+    clear = (top2[:, 0] - top2[:, 1]) > 4 * (lg - lo).abs().max(dim=-1).values
+    assert torch.equal(lg.argmax(-1)[clear], lo.argmax(-1)[clear])
 
 
 def test_prefill_matches_oracle(cuda):

@@ -710,3 +710,31 @@ def test_exit_controller_probe_cadence_ema_and_switch():
     cyc.after_deep_step()
     cyc.observe_probe([1, 1, 1], 2)
     assert cyc.maybe_switch(8, 800.0, True) == 6 and cyc.timeline == [(0, 4), (1, 6)]
+
+
+def test_decoded_cache_views_refuse_writes():
+    """cache.k[i] / cache.v[i] (and k_all / v_all) of the bf16 cache are decoded copies of the kernels' storage;
+    a reference-style write into them (solutions/packed.py:180-181) raises instead of being lost, reads and
+    out-of-place results stay ordinary tensors, and the fp32 K cache (stored in the reference layout) stays a
+    writable view of the storage."""
+    from thesis_amd import _lsk
+    from thesis_amd.common.model import KVCache, ModelConfig
+
+    cfg = ModelConfig(vocab_size=64, dim=64, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=32, intermediate_size=128)
+    c = KVCache(cfg, 3, 64, torch.bfloat16, "cpu")
+    k = torch.randn(2, 2, 32).to(torch.bfloat16)
+    rows, pos = torch.tensor([0, 2]), torch.tensor([5, 9])
+    for view in (c.k[1], c.v[0], c.k_all, c.v_all[1]):
+        with pytest.raises(_lsk.LskError, match="decoded KV-cache view"):
+            view[rows, :, pos] = k
+        with pytest.raises(_lsk.LskError):
+            view[0].zero_()
+        with pytest.raises(_lsk.LskError):
+            view.index_put_((rows[:1],), torch.zeros_like(view[rows[:1]]))
+        assert type(view.clone()) is torch.Tensor and float((view + 1).sum()) == view.numel()
+    assert (c.kf_all == 0).all() and (c.vb_all == 0).all()
+    c32 = KVCache(cfg, 3, 64, torch.float32, "cpu")
+    c32.k[1][rows, :, pos] = k.float()
+    assert torch.equal(c32.kstore[1][rows, :, pos], k.float())
+    with pytest.raises(_lsk.LskError):
+        c32.v[1][rows, :, pos] = k.float()

@@ -515,3 +515,53 @@ def test_head_norm_argmax_equals_norm_then_head(cuda, M):
     big = torch.full((2 * M,), -1, dtype=torch.long, device=cuda)
     lsk.head_norm_argmax(h, nw, 1e-5, wd, big, dst_idx=dst)
     assert torch.equal(big[::2], ref_ids) and (big[1::2] == -1).all()
+
+
+def test_add_rmsnorm_without_partials_stores_x_out(cuda):
+    """ks = 0: x_new = x is stored to x_out whenever x_out is given (also in place, x_out == x), and the norm
+    of x is the plain RMSNorm's."""
+    lsk = _lsk()
+    g = _gen(9)
+    n, dim = 7, 1024
+    x = torch.randn(n, dim, generator=g).to(BF16).to(cuda)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(BF16).to(cuda)
+    xo = torch.full((n, dim), 7.0, dtype=BF16, device=cuda)
+    xn = torch.empty(n, dim, dtype=BF16, device=cuda)
+    lsk.add_rmsnorm(x, None, w, 1e-5, x_out=xo, out=xn)
+    assert torch.equal(xo, x)
+    assert torch.equal(xn, lsk.rmsnorm(x, w, 1e-5))
+    xi = x.clone()
+    lsk.add_rmsnorm(xi, None, None, 1e-5, x_out=xi)              # in place, no norm output
+    assert torch.equal(xi, x)
+
+
+@pytest.mark.parametrize("nc,nblk", [(1, 3), (5, 40), (7, 64)])
+def test_probe_matches_equal_the_closed_form(cuda, nc, nblk):
+    """M2 agreement counts (solutions/engine.py:491-514): out[c] = #{t : pred[c, t] == Y[t] and jl[t] <= acc[blk[t]]},
+    out[nc] = #{t : jl[t] <= acc[blk[t]]}, computed here by a plain loop over the tokens.  Verify blocks of 1-9
+    tokens (several hundred tokens in the larger cases, more than one pass of the 256-thread count), predictions
+    that agree with Y often, and accepted counts at both ends (0 and T - 1) so the boundary jl == acc is hit."""
+    lsk = _lsk()
+    rng = np.random.default_rng(nc * 100 + nblk)
+    T = rng.integers(1, 10, size=nblk)
+    T[-1] = max(T[-1], 3)                               # its tokens 1.. lie beyond acc = 0: some are not counted
+    acc = np.array([rng.integers(0, t) if t > 1 else 0 for t in T], dtype=np.int64)
+    acc[0] = T[0] - 1
+    acc[-1] = 0
+    nvt = int(T.sum())
+    blk = np.repeat(np.arange(nblk), T)
+    jl = np.concatenate([np.arange(t) for t in T])
+    Y = rng.integers(0, 50, size=nvt)
+    pred = np.where(rng.random((nc, nvt)) < 0.6, Y[None, :], rng.integers(0, 50, size=(nc, nvt)))
+    want = [0] * (nc + 1)
+    for t in range(nvt):
+        if jl[t] <= acc[blk[t]]:
+            want[nc] += 1
+            for c in range(nc):
+                want[c] += int(pred[c, t] == Y[t])
+    dev = lambda a, dt: torch.as_tensor(np.ascontiguousarray(a), dtype=dt).to(cuda)  # noqa: E731
+    out = torch.full((nc + 1,), -1, dtype=torch.long, device=cuda)
+    lsk.probe_matches(dev(pred.reshape(-1), torch.long), dev(Y, torch.long), dev(acc, torch.long),
+                      dev(blk, torch.int32), dev(jl, torch.int32), nc, nvt, out)
+    assert out.cpu().tolist() == want
+    assert 0 < want[nc] < nvt

@@ -153,15 +153,55 @@ class LayerWeights:
         return cls(g(wqkv), g(wo), g(w13), g(w2), attn_norm, ffn_norm)
 
 
+_INPLACE_DUNDERS = {"__setitem__", "__iadd__", "__isub__", "__imul__", "__itruediv__", "__ifloordiv__",
+                    "__imod__", "__ipow__", "__iand__", "__ior__", "__ixor__", "__ilshift__", "__irshift__"}
+
+
+class DecodedCacheView(Tensor):
+    """A decoded copy of one layer's K or V cache in the reference's [max_batch, Hkv, max_seq, D] layout.  The
+    kernels keep their own storage (fragment-major K, blocked V^T), so a write into this copy would never reach
+    the cache: every in-place operation on it or on a view of it (`view[rows, :, pos] = k`, `index_put_`,
+    `copy_`, `out=` ...) raises instead of being lost.  Out-of-place results (clone, .cpu(), arithmetic) are
+    ordinary tensors."""
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        kwargs = kwargs or {}
+        name = getattr(func, "__name__", "")
+        inplace = name in _INPLACE_DUNDERS or (name.endswith("_") and not name.startswith("_"))
+        target = args[0] if args else None
+        if (inplace and isinstance(target, DecodedCacheView)) or any(
+                isinstance(o, DecodedCacheView) for o in _as_list(kwargs.get("out"))):
+            raise _lsk.LskError(
+                f"{name} on a decoded KV-cache view: cache.k[i] / cache.v[i] are copies of the kernels' storage "
+                "(fragment-major K, blocked V^T), so the write would be lost; append with "
+                "thesis_amd._lsk.kv_append (lsk_kv_append) or write cache.kstore[i] / cache.vb[i] through "
+                "_lsk.k_to_frag / _lsk.v_to_blocked")
+        with torch._C.DisableTorchFunctionSubclass():
+            out = func(*args, **kwargs)
+        src = target if isinstance(target, Tensor) else None
+        if (isinstance(out, Tensor) and src is not None and out.device == src.device and out.numel()
+                and out.untyped_storage().data_ptr() == src.untyped_storage().data_ptr()):
+            return out.as_subclass(DecodedCacheView)            # a view of the copy stays guarded
+        return out
+
+
+def _as_list(o):
+    if o is None:
+        return []
+    return list(o) if isinstance(o, (list, tuple)) else [o]
+
+
 class _Decoded:
     """cache.k[i] / cache.v[i] of a layout the kernels store differently: layer i in the reference's
-    [max_batch, Hkv, max_seq, D] layout, as a copy (for inspection; the kernels write the storage)."""
+    [max_batch, Hkv, max_seq, D] layout, as a copy for inspection whose in-place writes raise
+    (DecodedCacheView); the kernels write the storage."""
 
     def __init__(self, store: Tensor, decode):
         self.store, self.decode = store, decode
 
     def __getitem__(self, i):
-        return self.decode(self.store[i])
+        return self.decode(self.store[i]).as_subclass(DecodedCacheView)
 
     def __len__(self):
         return self.store.shape[0]
@@ -208,11 +248,11 @@ class KVCache:
 
     @property
     def k_all(self) -> Tensor:
-        return _lsk.k_from_frag(self.kf_all) if self.frag_k else self._k_rows
+        return _lsk.k_from_frag(self.kf_all).as_subclass(DecodedCacheView) if self.frag_k else self._k_rows
 
     @property
     def v_all(self) -> Tensor:
-        return _lsk.v_from_blocked(self.vb_all)
+        return _lsk.v_from_blocked(self.vb_all).as_subclass(DecodedCacheView)
 
     @staticmethod
     def bytes_needed(cfg: ModelConfig, max_batch: int, max_seq: int, dtype_bytes: int = 2) -> int:
