@@ -30,6 +30,7 @@
 // T = 9 verify block give bitwise identical outputs).
 #include <algorithm>
 #include <functional>
+#include <mutex>
 #include <vector>
 
 #include "lsk_common.h"
@@ -935,4 +936,67 @@ int lsk_ragged_attn_impl(int dtype, const void* q, const void* kcache, const voi
   }
   LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_ragged_attn: dtype %d", dtype);
   return LSK_EUNSUPPORTED;
+}
+
+// ----------------------------------------------------------------------------- allocation-free entry point
+// lsk_ragged_attn_static keeps the split partials in this file-scope device array instead of a caller workspace,
+// for callers that cannot allocate device memory.  Each GPU the library runs on holds its own copy (at its own
+// address) until the process ends.  In host code `scratch` names the symbol only: its device address comes from
+// hipGetSymbolAddress with the device current, looked up once per device and kept in scratch_dev; kernels are
+// always given that address, never the array's name.  Every call on a GPU shares that GPU's array: calls that
+// overlap on one GPU (other streams, other host threads) race on it.  The partial slots need no clearing: every
+// slot a combine group reads is written by its work item in the same call before the combine launch reads it.
+static __device__ __align__(256) unsigned char scratch[LSK_ATTN_SCRATCH_BYTES];
+
+#define LSK_MAX_DEVICES 64
+static std::mutex scratch_mu;
+static void* scratch_dev[LSK_MAX_DEVICES];
+
+// Device address of the current device's scratch array (looked up on the first call per device).
+static int attn_scratch_address(void** out, hipStream_t stream) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  LSK_REQUIRE(e == hipSuccess, (int)e, "lsk_ragged_attn_static: hipGetDevice: %s", hipGetErrorString(e));
+  LSK_REQUIRE(dev >= 0 && dev < LSK_MAX_DEVICES, LSK_EUNSUPPORTED, "lsk_ragged_attn_static: device %d", dev);
+  if (stream != nullptr) {
+    int sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    LSK_REQUIRE(e == hipSuccess, (int)e, "lsk_ragged_attn_static: hipStreamGetDevice: %s", hipGetErrorString(e));
+    LSK_REQUIRE(sdev == dev, LSK_EARG,
+                "lsk_ragged_attn_static: the stream belongs to device %d but device %d is current (the scratch "
+                "array used is the current device's)", sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_dev[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    LSK_REQUIRE(e == hipSuccess && ptr != nullptr, e != hipSuccess ? (int)e : LSK_EUNSUPPORTED,
+                "lsk_ragged_attn_static: hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(e));
+    scratch_dev[dev] = ptr;
+  }
+  *out = scratch_dev[dev];
+  return 0;
+}
+
+extern "C" size_t lsk_ragged_attn_static_scratch_bytes(void) { return LSK_ATTN_SCRATCH_BYTES; }
+
+extern "C" int lsk_ragged_attn_static(int dtype, const void* q, const void* kcache, const void* vcache,
+                                      const int32_t* blocks, const int32_t* works, int n_works,
+                                      const int32_t* groups, int n_groups, int n_parts, const int32_t* recs,
+                                      int n_rounds, int n_slots, int rows_cap, void* out, int n_heads,
+                                      int n_kv_heads, int head_dim, int max_seq, float scale, void* stream) {
+  LSK_REQUIRE(n_parts >= 0 && n_kv_heads > 0 && head_dim > 0, LSK_ESHAPE, "lsk_ragged_attn_static: bad shape");
+  const size_t need = n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, n_kv_heads, head_dim) : 0;
+  LSK_REQUIRE(need <= LSK_ATTN_SCRATCH_BYTES, LSK_EWORKSPACE,
+              "lsk_ragged_attn_static: %d split partial slots x %d KV heads need %zu bytes of scratch, more than the "
+              "%u-byte static array; use lsk_ragged_attn with a workspace", n_parts, n_kv_heads, need,
+              (unsigned)LSK_ATTN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = attn_scratch_address(&ws, (hipStream_t)stream);
+    if (rc) return rc;
+  }
+  return lsk_ragged_attn_impl(dtype, q, kcache, vcache, blocks, works, n_works, groups, n_groups, n_parts, recs,
+                              n_rounds, n_slots, rows_cap, out, 0, n_heads, n_kv_heads, head_dim, max_seq, scale, ws,
+                              need, stream);
 }

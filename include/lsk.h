@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 6
+#define LSK_ABI_VERSION 7
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -109,6 +109,21 @@ int lsk_ragged_attn(int dtype, const void* q, const void* kcache, const void* vc
                     const int32_t* recs, int n_rounds, int n_slots, int rows_cap, void* out, int n_heads,
                     int n_kv_heads, int head_dim, int max_seq, float scale, void* workspace, size_t ws_bytes,
                     void* stream);
+
+/* Allocation-free lsk_ragged_attn: the same arguments and outputs without the workspace.  The split partials live
+ * in a static device array of LSK_ATTN_SCRATCH_BYTES per GPU (held until the process ends), so plans whose
+ * partials need more (lsk_attn_workspace_bytes(n_parts, n_kv_heads, head_dim) > LSK_ATTN_SCRATCH_BYTES, about 170
+ * partial slots at 8 KV heads x head_dim 128) are rejected with LSK_EWORKSPACE.  The current device must be the
+ * stream's.  All calls on one GPU share its array: calls that overlap on one GPU (several streams or host
+ * threads) race.  No hipMalloc / hipFree or other allocation happens inside.
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid allocation). */
+#define LSK_ATTN_SCRATCH_BYTES (32u << 20)
+size_t lsk_ragged_attn_static_scratch_bytes(void);
+int lsk_ragged_attn_static(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
+                           const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
+                           const int32_t* recs, int n_rounds, int n_slots, int rows_cap, void* out, int n_heads,
+                           int n_kv_heads, int head_dim, int max_seq, float scale, void* stream);
 
 /* bf16 weight storage of the GEMMs: W [N, K] row-major (ldw) <-> fragment-major Wp (N*K elements, no
  * padding): fragment (g, j) = rows 16g..16g+15 x k 32j..32j+31 is 1 KiB, lane l's 8 elements being

@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -38,6 +38,9 @@ _SIGS = {
     "lsk_attn_workspace_bytes": (_Z, [_I, _I, _I]),
     "lsk_ragged_attn": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _P, _I, _I, _I, _I, _F, _P,
                              _Z, _P]),
+    "lsk_ragged_attn_static_scratch_bytes": (_Z, []),
+    "lsk_ragged_attn_static": (_I, [_I, _P, _P, _P, _P, _P, _I, _P, _I, _I, _P, _I, _I, _I, _P, _I, _I, _I, _I, _F,
+                                    _P]),
     "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
     "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
@@ -381,6 +384,20 @@ def ragged_attn(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n
                                   _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts, _ptr(recs_dev),
                                   n_rounds, n_slots, rows_cap, _ptr(out), n_heads, Hkv, D, S, float(scale),
                                   _ptr(workspace), ws_bytes, _stream()), "lsk_ragged_attn")
+
+
+def ragged_attn_static(q, kcache, vcache, blocks_dev, works_dev, n_works, groups_dev, n_groups, n_parts, out,
+                       n_heads, scale, recs_dev=None, n_rounds=0, n_slots=0, rows_cap=ATTN_ROWS):
+    """ragged_attn without a workspace: the split partials live in the library's static per-GPU scratch array
+    (lsk_ragged_attn_static; plans needing more than lsk_ragged_attn_static_scratch_bytes() raise)."""
+    _dev(q, kcache, vcache, blocks_dev, works_dev, out)
+    _check_kcache(q.dtype, kcache)
+    B, Hkv, S, D = k_dims(kcache)
+    assert vcache.shape == (B, Hkv, S // 32, D, 32) and S % 64 == 0
+    _check(load().lsk_ragged_attn_static(dtype_code(q.dtype), _ptr(q), _ptr(kcache), _ptr(vcache), _ptr(blocks_dev),
+                                         _ptr(works_dev), n_works, _ptr(groups_dev), n_groups, n_parts,
+                                         _ptr(recs_dev), n_rounds, n_slots, rows_cap, _ptr(out), n_heads, Hkv, D, S,
+                                         float(scale), _stream()), "lsk_ragged_attn_static")
 
 
 def gemm(a: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None, residual: torch.Tensor | None = None,
