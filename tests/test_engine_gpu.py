@@ -473,7 +473,8 @@ def test_rollback_moves_no_kv(cuda):
 
 
 def test_shallow_steps_do_not_synchronise(cuda, monkeypatch):
-    """No device->host read in shallow steps; exactly one per deep step (tests/test_eesd.py:199-223)."""
+    """No device->host read and no event / stream / device synchronisation in shallow steps (graph-replayed ones
+    included); exactly one read per deep step (tests/test_eesd.py:199-223)."""
     from thesis_amd.solutions.cost_model import synthetic_cost_model
     from thesis_amd.solutions.engine import EESDEngine, EngineConfig, Request
 
@@ -496,12 +497,27 @@ def test_shallow_steps_do_not_synchronise(cuda, monkeypatch):
     monkeypatch.setattr(torch.Tensor, "cpu", spy("cpu", orig_cpu))
     monkeypatch.setattr(torch.Tensor, "item", spy("item", orig_item))
     monkeypatch.setattr(torch.Tensor, "tolist", spy("tolist", orig_tolist))
-    kinds = []
+
+    def count(name, fn):
+        def f(*a, **k):
+            calls.append(name)
+            return fn(*a, **k)
+        return f
+
+    # host waits on the device other than reads: event, stream and device synchronisation
+    monkeypatch.setattr(torch.cuda.Event, "synchronize", count("event.synchronize", torch.cuda.Event.synchronize))
+    monkeypatch.setattr(torch.cuda.Stream, "synchronize", count("stream.synchronize", torch.cuda.Stream.synchronize))
+    monkeypatch.setattr(torch.cuda, "synchronize", count("cuda.synchronize", torch.cuda.synchronize))
+    kinds, replayed = [], 0
     for _ in range(12):
         calls.clear()
         n_rec = len(eng.records)
+        captures, replays = eng.graphs.captures, eng.graphs.replays
         eng.step()
         kind = eng.records[n_rec].kind
         kinds.append(kind)
+        if eng.graphs.captures > captures:          # capturing a graph (once per shape) synchronises by itself
+            calls = [c for c in calls if not c.endswith("synchronize")]
+        replayed += eng.graphs.replays - replays
         assert len(calls) == (0 if kind == "shallow" else 1), (kind, calls)
-    assert "shallow" in kinds and "deep" in kinds
+    assert "shallow" in kinds and "deep" in kinds and replayed > 0

@@ -386,20 +386,49 @@ def test_expected_token_targets_match_brute_force():
 def test_m1_rule_direction():
     from thesis_amd.common.model import PRESETS
     from thesis_amd.solutions.cost_model import synthetic_cost_model
-    from thesis_amd.solutions.schedulers import M1Scheduler
+    from thesis_amd.solutions.schedulers import make_scheduler
 
     cm = synthetic_cost_model(PRESETS["llama3-8b"])
     B = 16
     d, ctx, dec = np.full(B, 2), np.full(B, 1000), np.ones(B, dtype=bool)
-    s = M1Scheduler(B, cm, 3, d_max=16)
-    s.ema.alpha[:] = 0.98
+    s = make_scheduler("m1", B, cm, 3, d_max=16)
+    s.tracker.rate[:] = 0.98                  # drafts almost always accepted: drafting once more pays
     assert not s.decide(d, ctx, dec, 2).any()
-    s.ema.alpha[:] = 0.05
+    s.tracker.rate[:] = 0.05                  # drafts almost always rejected: verify now
     assert s.decide(d, ctx, dec, 2).all()
     d2 = d.copy()
     d2[0] = 16
-    s.ema.alpha[:] = 0.98
-    assert s.decide(d2, ctx, dec, 2).all()
+    s.tracker.rate[:] = 0.98
+    assert s.decide(d2, ctx, dec, 2).all()    # a slot at d_max forces the deep step
+    assert s.decide(d, ctx, dec, 32).all()    # so does the idle-step limit (sla_steps)
+
+
+def test_feedback_policies_and_acceptance_tracker():
+    """fsm-sync moves one batch-wide gamma by +-1 on the majority of full accepts (history kept every round);
+    aspire-fsm moves each verifying slot's target; the tracker's rate follows rate <- w rate + (1 - w) acc /
+    min(acc + 1, d) on verified slots only (solutions/schedulers.py:35-51, 156-197)."""
+    from thesis_amd.common.model import PRESETS
+    from thesis_amd.solutions.cost_model import synthetic_cost_model
+    from thesis_amd.solutions.schedulers import make_scheduler
+
+    cm = synthetic_cost_model(PRESETS["llama3-8b"])
+    f = make_scheduler("fsm-sync", 4, cm, 3, gamma=3, d_max=6, omega=0.5, alpha0=0.9)
+    v = np.array([True, True, True, False])
+    f.observe(v, np.array([3, 3, 1, 0]), np.array([3, 3, 3, 0]))          # 2 of 3 verifiers fully accepted
+    assert f.gamma == 4
+    f.observe(v, np.array([0, 3, 1, 0]), np.array([3, 3, 3, 0]))          # 1 of 3
+    assert f.gamma == 3
+    f.observe(np.zeros(4, dtype=bool), np.zeros(4, dtype=int), np.zeros(4, dtype=int))
+    assert f.gamma_hist == [3, 4, 3, 3]
+    rate = f.tracker.rate
+    # slot 0: 0.9 -> 0.5 * 0.9 + 0.5 * 3 / min(4, 3) = 0.95 -> 0.5 * 0.95 + 0.5 * 0 = 0.475; slot 3 never verified
+    assert np.isclose(rate[0], 0.475) and rate[3] == 0.9 and f.tracker.cold.tolist() == [False, False, False, True]
+    a = make_scheduler("aspire-fsm", 3, cm, 3, d_max=5, initial_draft=2)
+    a.observe(np.array([True, True, False]), np.array([2, 0, 0]), np.array([2, 2, 0]))
+    assert a.targets.tolist() == [3, 1, 2]
+    assert a.decide(np.array([3, 1, 1]), np.full(3, 10), np.ones(3, dtype=bool), 0).tolist() == [True, True, False]
+    a.reset(0)
+    assert a.targets[0] == 2 and a.tracker.cold[0]
 
 
 def test_fixed_and_aspire_schedulers():
@@ -677,8 +706,15 @@ def test_m3_budget_respects_the_knee():
         bound = 12.0 * safety
         for n_sh in range(0, 14):
             for n_dp in range(0, 14):
-                c = p.budget(n_sh, n_dp, 0)
+                c = p.chunk_budget(n_sh, n_dp, 0)
                 assert c == 0 or (c + n_sh <= bound and c + n_dp <= bound)
+    # admission: the refusal reasons of solutions/prefill.py:46-57, in their order
+    p = M3Planner(cm, max_wait=2, knee_safety=1.0)
+    assert p.admission(100, 12, 12, 4, 500.0) == (False, "no_room_below_knee")
+    assert p.admission(100, 2, 2, 4, 500.0) == (False, "exceeds_max_wait")      # 10-token pieces: 10 > 2 pieces
+    ok, why = p.admission(8, 2, 2, 4, 500.0)
+    assert why == ("piggyback" if ok else "not_cheaper_than_separate")
+    assert ok == (p.extra_cost(8, 4, 2, 2, 500.0) < float(cm.t_prefill(8, 8)))
 
 
 def test_exit_controller_probe_cadence_ema_and_switch():
@@ -691,25 +727,25 @@ def test_exit_controller_probe_cadence_ema_and_switch():
     assert ec.cands == [2, 4, 6]
     wants = []
     for _ in range(6):
-        wants.append(ec.want_probe())
-        ec.after_deep_step()
+        wants.append(ec.probe_due())
+        ec.deep_step_done()
     assert wants == [False, False, True, False, False, True]
-    assert ec.maybe_switch(8, 800.0, True) is None                # no probe yet
-    ec.observe_probe([1, 4, 8], 8)
+    assert ec.propose(8, 800.0, True) is None                # no probe yet
+    ec.absorb_probe([1, 4, 8], 8)
     assert ec.alpha == {2: 0.125, 4: 0.5, 6: 1.0}
-    ec.observe_probe([3, 4, 8], 8)
+    ec.absorb_probe([3, 4, 8], 8)
     assert ec.alpha[2] == 0.5 * 0.125 + 0.5 * 0.375            # EMA with omega = 0.5
-    ec.observe_probe([0, 0, 0], 0)                              # no correct-prefix position: ignored
-    assert ec.probes == 2
-    new = ec.maybe_switch(8, 800.0, True)
+    ec.absorb_probe([0, 0, 0], 0)                              # no correct-prefix position: ignored
+    assert ec.n_probes == 2
+    new = ec.propose(8, 800.0, True)
     rates = ec.last_rates
     best = max(rates, key=rates.get)
     assert new == (best if best != 4 and rates[best] > 1.05 * rates[4] else None)
-    assert ec.maybe_switch(8, 800.0, False) is None             # a half-done prefill blocks switches
+    assert ec.propose(8, 800.0, False) is None             # a half-done prefill blocks switches
     cyc = ExitController(cm, 4, [2, 6], probe_every=1, force="cycle")
-    cyc.after_deep_step()
-    cyc.observe_probe([1, 1, 1], 2)
-    assert cyc.maybe_switch(8, 800.0, True) == 6 and cyc.timeline == [(0, 4), (1, 6)]
+    cyc.deep_step_done()
+    cyc.absorb_probe([1, 1, 1], 2)
+    assert cyc.propose(8, 800.0, True) == 6 and cyc.timeline == [(0, 4), (1, 6)]
 
 
 def test_decoded_cache_views_refuse_writes():
@@ -738,3 +774,60 @@ def test_decoded_cache_views_refuse_writes():
     assert torch.equal(c32.kstore[1][rows, :, pos], k.float())
     with pytest.raises(_lsk.LskError):
         c32.v[1][rows, :, pos] = k.float()
+
+
+def test_measure_window_convergence_and_caps():
+    """Warm-up completions are not measured; the run stops once `window` consecutive completions keep the
+    throughput within `threshold` of the anchor (a completion outside re-anchors), or at max_eval
+    (solutions/engine.py:594-606, common/engine.py:198-216)."""
+    from thesis_amd.common.driver import MeasureWindow
+
+    started = []
+    w = MeasureWindow(warmup=2, min_eval=3, max_eval=50, threshold=0.01, window=2, on_start=lambda: started.append(1))
+    rates = iter([100.0, 150.0, 150.5, 150.2])
+    reasons = [w.completed(lambda: next(rates)) for _ in range(2)]         # warm-up: no rate read
+    assert reasons == [None, None] and w.measuring and started == [1]
+    reasons = [w.completed(lambda: next(rates)) for _ in range(6)]
+    # measured 1-2: below min_eval (no rate read); 3 anchors at 100; 4 (150) re-anchors; 5, 6 stable -> converged
+    assert reasons == [None, None, None, None, None, "converged"]
+    capped = MeasureWindow(warmup=0, max_eval=3, converge=False)
+    assert [capped.completed(lambda: 1.0) for _ in range(3)] == [None, None, "max_eval_samples"]
+
+
+def test_open_loop_driver_on_a_stub_engine():
+    """run_arrivals: requests arrive by a seeded Poisson clock, queue FIFO for free slots, idle waits sleep until
+    the next arrival; every request is admitted once, in arrival order, and the run ends after n_total
+    releases."""
+    import time as _time
+
+    from thesis_amd.common.driver import PoissonArrivals, run_arrivals
+
+    class Stub:
+        n_slots = 2
+
+        def __init__(self):
+            self.slots, self.order, self.released = [None, None], [], 0
+
+        def advance(self):
+            done = [i for i, r in enumerate(self.slots) if r is not None]
+            return done[:1]                                   # one request finishes per step
+
+        def release(self, slot):
+            self.slots[slot] = None
+            self.released += 1
+
+        def busy(self):
+            return any(r is not None for r in self.slots)
+
+    eng = Stub()
+
+    def admit(slot, req):
+        eng.slots[slot] = req
+        eng.order.append(req)
+        return False
+
+    arr = PoissonArrivals(200.0, seed=3, t0=_time.perf_counter())
+    left = run_arrivals(eng, lambda: [i for i, r in enumerate(eng.slots) if r is None],
+                        lambda i, t: (i, t), admit, arr, 6, lambda: None)
+    assert eng.released == 6 and [r[0] for r in eng.order[:6]] == list(range(6))
+    assert all(a[1] <= b[1] for a, b in zip(eng.order, eng.order[1:])) and left >= 0

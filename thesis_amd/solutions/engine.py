@@ -1,11 +1,11 @@
 """EESD engine: batched early-exit self-speculation with packed shallow / deep steps on MI355X
-(solutions/engine.py surface: EngineConfig, Request, Rec, EESDEngine.assign / step / run / run_poisson).
+(the reference's solutions/engine.py surface: EngineConfig, Request, EESDEngine.assign / step / run / run_poisson).
 
 Step semantics are the reference's (solutions/engine.py:1-27, 269-489):
   shallow step  every decoding slot runs its current input token (last committed token if d = 0, else
                 its newest draft) at position pos + d through layers [0, k) and the shared exit head
                 -> one draft (seq_buf[i, d + 1]); its layer-k hidden state is kept in exit_h[i, d].
-  deep step     the verifying slots (scheduler's V) run their newest draft through [0, k) in the same
+  deep step     the verifying slots (the policy's V) run their newest draft through [0, k) in the same
                 shallow segment, then all d + 1 tokens (inputs exit_h[i, 0..d]) at pos..pos + d through
                 [k, L) + head; greedy acceptance; the other slots draft in the same step.
   rollback      pointer only: pos += acc + 1, d = 0; rejected drafts' KV stays beyond pos, is never read
@@ -17,19 +17,22 @@ counts + verified tokens) and never in a shallow step.
 M2 (exit="m2", solutions/engine.py:284-288, 312-313, 458, 491-514): every probe_every-th deep step the
 verifiers run all d + 1 tokens through the shallow layers, the hidden states entering every candidate exit are
 captured in both segments, the shared head runs on all of them and lsk_probe_matches counts the agreement with Y on
-the correct-prefix positions; ExitController may then switch the exit layer (pending drafts are dropped).
-M3 (prefill="m3", solutions/engine.py:289-305, 353-354, 424-426, 477-480): chunks of an admitted prompt ride on the
+the correct-prefix positions; ExitController may then move the exit layer (pending drafts are dropped).
+M3 (prefill="m3", solutions/engine.py:289-305, 353-354, 424-426, 477-480): pieces of an admitted prompt ride on the
 shallow segment (prompt ids through [0, k), layer-k states kept) and on the next deep segment (those states through
-[k, L)); the last chunk's head gives the request's first token.
+[k, L)); the last piece's head gives the request's first token.
 
 Harness hook with no reference counterpart: `forced_accept_p` replaces each verifier's acceptance by
 a seeded draw min(Geometric(p) - 1, d) and commits drafts[0..a-1] + Yv[a] (the tokens whose KV the deep
 segment wrote), as the measured configurations prescribe.
+
+Drivers: `run` (static pass / cyclic replay) and `run_poisson` (open loop) hand the slots to the shared
+drivers of common/driver.py; `_report` turns the step log into the reference's metric names
+(solutions/engine.py:694-753).
 """
 
 from __future__ import annotations
 
-import math
 import time
 from dataclasses import asdict, dataclass, field
 from typing import Callable, Optional
@@ -38,9 +41,11 @@ import numpy as np
 import torch
 
 from .. import _lsk
-from ..common.timing import Interval
-from .packed import Block, build_packed, build_packed_arrays, packed_layers, upload, upload_many
+from ..common.driver import MeasureWindow, PoissonArrivals, run_arrivals, run_pool
+from ..common.engine import commit_tokens
+from ..common.timing import DeviceSpan
 from .exit_select import ExitController
+from .packed import Block, build_packed, build_packed_arrays, packed_layers, upload, upload_many
 from .prefill import M3Planner
 from .schedulers import make_scheduler
 from .step_graph import ShallowGraphs
@@ -50,12 +55,27 @@ FREE, PREFILL, DECODE = 0, 1, 2
 
 @dataclass
 class EngineConfig:
-    mode: str = "spec"              # spec | ar
-    sched: str = "fixed"            # fixed | aspire | m1 | fsm-sync | aspire-fsm
+    """Engine options (the reference's field names and defaults).
+
+    mode / sched / gamma / k / d_max / min_draft / initial_draft / omega / alpha0 / sla_steps
+        decoding mode ("spec" or "ar"), deep-step policy and its knobs (solutions/schedulers.py)
+    exit / probe_every / k_cands / switch_margin / m2_force
+        exit-layer policy: "fixed", or "m2" with probes every `probe_every` deep steps over `k_cands`
+    prefill / prefill_chunk / max_wait / knee_safety / m3_chunk_cap
+        "separate" prefill in `prefill_chunk` pieces, or "m3" piggybacking (solutions/prefill.py)
+    bucketing
+        build_packed's accounting mode ("exact" | "pad"); the native kernels serve both alike
+    forced_accept_p / forced_seed
+        harness hook: seeded geometric acceptance instead of the greedy comparison
+    graphs
+        replay fixed-shape shallow-only steps as captured HIP graphs
+    """
+    mode: str = "spec"
+    sched: str = "fixed"
     gamma: int = 4
     k: int = 3
-    exit: str = "fixed"             # fixed | m2
-    prefill: str = "separate"       # separate | m3
+    exit: str = "fixed"
+    prefill: str = "separate"
     d_max: int = 16
     sla_steps: int = 32
     initial_draft: int = 3
@@ -73,50 +93,62 @@ class EngineConfig:
     m2_force: Optional[str] = None
     forced_accept_p: Optional[float] = None
     forced_seed: int = 0
-    graphs: bool = True             # replay fixed-shape shallow steps as captured HIP graphs
+    graphs: bool = True
+
+    def check(self, n_layers: int) -> None:
+        """ValueError for option combinations the engine cannot run."""
+        if self.exit not in ("fixed", "m2"):
+            raise ValueError(f"unknown exit policy {self.exit!r}")
+        if self.prefill not in ("separate", "m3"):
+            raise ValueError(f"unknown prefill policy {self.prefill!r}")
+        if self.mode == "ar" and self.prefill != "separate":
+            raise ValueError("AR mode supports --prefill separate only")
+        if not 1 <= self.k < n_layers:
+            raise ValueError("exit layer must be in [1, n_layers)")
 
     def label(self) -> str:
         if self.mode == "ar":
             return "ar"
-        s = f"{self.sched}" + (f"-g{self.gamma}" if self.sched == "fixed" else "")
-        return f"{s}-{'k' + str(self.k) if self.exit == 'fixed' else 'm2'}-{self.prefill}"
+        policy = self.sched + (f"-g{self.gamma}" if self.sched == "fixed" else "")
+        exit_part = f"k{self.k}" if self.exit == "fixed" else "m2"
+        return f"{policy}-{exit_part}-{self.prefill}"
 
 
 @dataclass
 class Request:
+    """One request and its life in the engine: output tokens, finish reason, the step-log indices of its
+    assignment / first token / last step (for TTFT and TPOT), wall times, and M3 progress."""
     pid: str
     prompt: list
     out: list = field(default_factory=list)
     finish: Optional[str] = None
-    rec_assign: int = 0
-    rec_first: int = -1
-    rec_finish: int = -1
+    log_assign: int = 0
+    log_first: int = -1
+    log_finish: int = -1
     wall_arrival: float = 0.0
     wall_first: float = 0.0
     measured: bool = False
-    pf_sh: int = 0
-    pf_dp: int = 0
-    piggybacked: int = 0
-    key: int = -1                   # assignment counter (forced-acceptance stream)
+    pf_sh: int = 0                  # prompt tokens already through the shallow layers (M3)
+    pf_dp: int = 0                  # prompt tokens already through every layer (M3)
+    piggybacked: int = 0            # prompt tokens carried by decode steps (M3)
+    key: int = -1                   # assignment counter: the forced-acceptance stream of the request
 
 
 @dataclass
-class Rec:
-    kind: str
-    iv: Interval
+class StepEntry:
+    """One engine call in the step log: its kind, device span, whether it counts, and its token mix."""
+    kind: str                       # shallow | deep | probe | ar | prefill
+    span: DeviceSpan
     measured: bool
     n_sh: int = 0
     n_dp: int = 0
     n_chunk: int = 0
     plan_ms: float = 0.0
     k: int = 0
-    _ms: Optional[float] = None
 
     @property
     def ms(self) -> float:
-        if self._ms is None:
-            self._ms = self.iv.ms
-        return self._ms
+        return self.span.ms
 
 
 class ForcedAcceptance:
@@ -133,118 +165,113 @@ class ForcedAcceptance:
         return int(rng.geometric(self.p)) - 1
 
 
+_COUNTERS = ("steps", "deep_steps", "probe_steps", "deep_tokens", "verifiers", "drafted", "accepted", "committed",
+             "plan_ms", "plan_calls", "prefill_tokens", "piggyback_tokens", "separate_prefills", "m3_fallbacks",
+             "dropped_drafts", "kv_read_pos", "kv_gathered_pos")
+
+
 class EESDEngine:
     def __init__(self, model, B: int, max_prompt: int, max_new: int, eos_ids, cfg: EngineConfig, cost_model,
                  stop_for: Optional[Callable] = None, ref: Optional[dict] = None):
-        if cfg.mode == "ar" and cfg.prefill != "separate":
-            raise ValueError("AR mode supports --prefill separate only")
-        if cfg.exit not in ("fixed", "m2"):
-            raise ValueError(f"unknown exit policy {cfg.exit!r}")
-        if cfg.prefill not in ("separate", "m3"):
-            raise ValueError(f"unknown prefill policy {cfg.prefill!r}")
+        cfg.check(model.n_layers)
         self.m, self.dev, self.B, self.cfg, self.cm = model, model.device, B, cfg, cost_model
         self.max_new, self.eos = max_new, set(eos_ids)
         self.stop_for = stop_for or (lambda pid: None)
-        self.k = cfg.k
-        self.L = model.n_layers
-        if not 1 <= self.k < self.L:
-            raise ValueError("exit layer must be in [1, n_layers)")
-        Dm = cfg.d_max
-        self.Dm1 = Dm + 1
-        model.allocate_cache(B, max_prompt + max_new + Dm + 40)
-        self.seq_buf = torch.zeros(B, self.Dm1, dtype=torch.long, device=self.dev)
-        self.exit_h = torch.zeros(B, self.Dm1, model.cfg.dim, dtype=model.dtype, device=self.dev)
-        self.state = np.zeros(B, dtype=np.int64)
-        self.pos = np.zeros(B, dtype=np.int64)
-        self.d = np.zeros(B, dtype=np.int64)
-        self.gen = np.zeros(B, dtype=np.int64)
-        self.req: list = [None] * B
-        self.pending: list = [[] for _ in range(B)]
-        self.steps_since_deep = 0
+        self.k, self.L = cfg.k, model.n_layers
+        self.Dm1 = cfg.d_max + 1
+        self._allocate(max_prompt)
+        self._policies(cost_model)
         self.records: list = []
-        self.sched = make_scheduler(cfg.sched, B, cost_model, self.k, gamma=cfg.gamma, d_max=Dm,
-                                    sla_steps=cfg.sla_steps, initial_draft=cfg.initial_draft, omega=cfg.omega,
-                                    alpha0=cfg.alpha0, min_draft=cfg.min_draft) if cfg.mode == "spec" else None
-        self.exitc = ExitController(cost_model, self.k, [c for c in cfg.k_cands if 1 <= c < self.L], cfg.probe_every,
-                                    cfg.switch_margin, cfg.omega, Dm, cfg.m2_force) if cfg.exit == "m2" else None
-        self.m3 = M3Planner(cost_model, cfg.max_wait, cfg.m3_chunk_cap, cfg.prefill_chunk,
-                            cfg.knee_safety) if cfg.prefill == "m3" else None
-        self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
-        self.graphs = ShallowGraphs(self.dev) if cfg.graphs and cfg.mode == "spec" else None
-        self._keys = 0
         self.measuring = False
-        self.stats = {"steps": 0, "deep_steps": 0, "probe_steps": 0, "deep_tokens": 0, "verifiers": 0, "drafted": 0,
-                      "accepted": 0, "committed": 0, "plan_ms": 0.0, "plan_calls": 0, "prefill_tokens": 0,
-                      "piggyback_tokens": 0, "separate_prefills": 0, "m3_fallbacks": 0, "dropped_drafts": 0,
-                      "kv_read_pos": 0, "kv_gathered_pos": 0}
-        self.round_len = cfg.gamma
-        self.kv_bytes_per_pos = 2 * model.cfg.n_kv_heads * model.cfg.head_dim * model.dtype.itemsize
+        self.stats = dict.fromkeys(_COUNTERS, 0)
+        self.stats["plan_ms"] = 0.0
         self.fallback_reasons: dict = {}
+        self.round_len = cfg.gamma          # steps per round last observed (M3's deep-size estimate)
+        self.steps_since_deep = 0
+        self.kv_bytes_per_pos = 2 * model.cfg.n_kv_heads * model.cfg.head_dim * model.dtype.itemsize
+        self._keys = 0
         self.trace: Optional[list] = None     # set to [] to log every step's segment shapes
 
-    # ------------------------------------------------------------------ helpers
-    def _rec(self, kind, iv, **kw) -> Rec:
-        r = Rec(kind, iv, self.measuring, k=self.k, **kw)
-        self.records.append(r)
-        return r
+    def _allocate(self, max_prompt: int) -> None:
+        """Cache rows for prompt + output + drafts + slack; device seq_buf / exit_h; host slot arrays."""
+        m, B = self.m, self.B
+        m.allocate_cache(B, max_prompt + self.max_new + self.cfg.d_max + 40)
+        self.seq_buf = torch.zeros(B, self.Dm1, dtype=torch.long, device=self.dev)
+        self.exit_h = torch.zeros(B, self.Dm1, m.cfg.dim, dtype=m.dtype, device=self.dev)
+        self.state = np.zeros(B, dtype=np.int64)        # FREE / PREFILL / DECODE
+        self.pos = np.zeros(B, dtype=np.int64)          # committed length = position of the current input token
+        self.d = np.zeros(B, dtype=np.int64)            # drafts held
+        self.gen = np.zeros(B, dtype=np.int64)          # tokens generated
+        self.req: list = [None] * B
+        self.pending: list = [[] for _ in range(B)]     # M3: (pos0, c, layer-k states) awaiting the deep segment
+
+    def _policies(self, cm) -> None:
+        cfg = self.cfg
+        spec = cfg.mode == "spec"
+        self.sched = make_scheduler(cfg.sched, self.B, cm, self.k, gamma=cfg.gamma, d_max=cfg.d_max,
+                                    sla_steps=cfg.sla_steps, initial_draft=cfg.initial_draft, omega=cfg.omega,
+                                    alpha0=cfg.alpha0, min_draft=cfg.min_draft) if spec else None
+        cands = [c for c in cfg.k_cands if 1 <= c < self.L]
+        self.exitc = ExitController(cm, self.k, cands, cfg.probe_every, cfg.switch_margin, cfg.omega, cfg.d_max,
+                                    cfg.m2_force) if cfg.exit == "m2" else None
+        self.m3 = M3Planner(cm, cfg.max_wait, cfg.m3_chunk_cap, cfg.prefill_chunk,
+                            cfg.knee_safety) if cfg.prefill == "m3" else None
+        self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
+        self.graphs = ShallowGraphs(self.dev) if cfg.graphs and spec else None
+
+    # ------------------------------------------------------------------ bookkeeping
+    def _log(self, kind, span, **kw) -> StepEntry:
+        e = StepEntry(kind, span, self.measuring, k=self.k, **kw)
+        self.records.append(e)
+        return e
 
     def _commit(self, slot: int, toks) -> int:
         r = self.req[slot]
-        n = 0
-        for t in toks:
-            if r.finish is not None:
-                break
-            r.out.append(int(t))
-            n += 1
-            if int(t) in self.eos:
-                r.finish = "eos"
-            elif len(r.out) >= self.max_new:
-                r.finish = "length"
-        stop = self.stop_for(r.pid)
-        if n and stop and r.finish is None:
-            cut = stop(r.out, n)
-            if cut is not None:
-                n -= len(r.out) - cut
-                del r.out[cut:]
-                r.finish = "stop"
+        if r.finish is not None:
+            return 0
+        n, r.finish = commit_tokens(r.out, toks, eos=self.eos, max_new=self.max_new,
+                                    stop_checker=self.stop_for(r.pid))
         self.gen[slot] = len(r.out)
         return n
 
-    def _first_token(self, slot: int, y0: int) -> int:
+    def _start_decoding(self, slot: int, first: int) -> int:
+        """The prompt is in the cache: the slot decodes from its first token (a fresh acceptance estimate)."""
         r = self.req[slot]
-        r.rec_first = len(self.records) - 1
-        r.wall_first = time.perf_counter()
-        self.state[slot] = DECODE
-        self.pos[slot] = len(r.prompt)
-        self.d[slot] = 0
+        r.log_first, r.wall_first = len(self.records) - 1, time.perf_counter()
+        self.state[slot], self.pos[slot], self.d[slot] = DECODE, len(r.prompt), 0
         if self.sched is not None:
             self.sched.reset(slot)
-        return self._commit(slot, [y0])
+        return self._commit(slot, [first])
 
     def _flat(self):
         return self.seq_buf.view(-1), self.exit_h.view(-1, self.exit_h.shape[-1])
 
     # ------------------------------------------------------------------ assignment / prefill
+    def _piggyback(self, req: Request) -> bool:
+        """M3 admission of a prompt next to the decoding slots; a refusal is counted by reason."""
+        live = self.state == DECODE
+        if self.m3 is None or not live.any():
+            return False
+        n_live = int(live.sum())
+        ok, why = self.m3.admission(len(req.prompt), n_live, n_live * (self.round_len + 1), self.k,
+                                    float((self.pos + self.d)[live].sum()))
+        if not ok:
+            self.stats["m3_fallbacks"] += 1
+            self.fallback_reasons[why] = self.fallback_reasons.get(why, 0) + 1
+        return ok
+
     def assign(self, slot: int, req: Request) -> int:
-        req.rec_assign = len(self.records)
-        req.measured = self.measuring
+        """Put `req` in a free slot: piggybacked (its pieces ride the next steps) or prefilled now.  Returns the
+        tokens committed (the first token of a separate prefill)."""
+        req.log_assign, req.measured = len(self.records), self.measuring
         if req.key < 0:
             req.key = self._keys
         self._keys += 1
-        self.req[slot] = req
-        self.pending[slot] = []
-        self.d[slot] = 0
-        if self.m3 is not None and (self.state == DECODE).any():
-            dec = self.state == DECODE
-            n_dec = int(dec.sum())
-            ok, why = self.m3.admit(len(req.prompt), n_dec, n_dec * (self.round_len + 1), self.k,
-                                    float((self.pos + self.d)[dec].sum()))
-            if ok:
-                self.state[slot] = PREFILL
-                req.pf_sh = req.pf_dp = 0
-                return 0
-            self.stats["m3_fallbacks"] += 1
-            self.fallback_reasons[why] = self.fallback_reasons.get(why, 0) + 1
+        self.req[slot], self.pending[slot], self.d[slot] = req, [], 0
+        if self._piggyback(req):
+            self.state[slot] = PREFILL
+            req.pf_sh = req.pf_dp = 0
+            return 0
         return self._prefill_separate(slot)
 
     @torch.inference_mode()
@@ -253,23 +280,22 @@ class EESDEngine:
         n = len(r.prompt)
         if n < 1:
             raise ValueError("empty prompt")
-        iv = Interval(self.dev).start()
+        span = DeviceSpan(self.dev).open()
         h = None
         for s in range(0, n, self.cfg.prefill_chunk):
             c = min(self.cfg.prefill_chunk, n - s)
             pb = build_packed(m, [Block(slot, s, c)], self.cfg.bucketing)
-            self._kv(pb, self.L)
-            x = m.embed(upload(r.prompt[s:s + c], self.dev))
-            h = packed_layers(m, x, pb, 0, self.L)
+            self._count_kv(pb, self.L)
+            h = packed_layers(m, m.embed(upload(r.prompt[s:s + c], self.dev)), pb, 0, self.L)
         sb, _ = self._flat()
         y0 = m.head_argmax(h[-1:])
         _lsk.copy_rows(sb.view(-1, 1), upload([slot * self.Dm1], self.dev), y0.view(-1, 1), None, 1)
-        iv.stop()
-        self._rec("prefill", iv, n_chunk=n)
+        span.close()
+        self._log("prefill", span, n_chunk=n)
         self.stats["separate_prefills"] += 1
         if self.measuring:
             self.stats["prefill_tokens"] += n
-        return self._first_token(slot, int(y0.item()))
+        return self._start_decoding(slot, int(y0.item()))
 
     # ------------------------------------------------------------------ one step
     @torch.inference_mode()
@@ -285,18 +311,18 @@ class EESDEngine:
         if len(dec) == 0:
             return 0, []
         pb = build_packed(m, [Block(int(i), int(self.pos[i]), 1) for i in dec], self.cfg.bucketing)
-        self._kv(pb, self.L)
+        self._count_kv(pb, self.L)
         slots = np.array([b.row for b in pb.blocks], dtype=np.int64)
         idx = upload(slots * self.Dm1, self.dev)
         sb, _ = self._flat()
-        iv = Interval(self.dev).start()
+        span = DeviceSpan(self.dev).open()
         x = m.buffer("x_in", (len(slots), m.cfg.dim), m.dtype)
         _lsk.embed(m.embed_w, idx, x, sb, idx)
         h = packed_layers(m, x, pb, 0, self.L)
         y = m.head_argmax(h)
         _lsk.copy_rows(sb.view(-1, 1), idx, y.view(-1, 1), None, len(slots))
-        iv.stop()
-        self._rec("ar", iv, n_sh=len(slots), n_dp=len(slots))
+        span.close()
+        self._log("ar", span, n_sh=len(slots), n_dp=len(slots))
         y_h = y.tolist()
         committed, done = 0, []
         for s, t in zip(slots.tolist(), y_h):
@@ -304,7 +330,7 @@ class EESDEngine:
             committed += self._commit(s, [t])
             if self.req[s].finish:
                 done.append(s)
-        self._account(committed, deep=True, n_deep=len(slots), verifiers=len(slots))
+        self._tally(committed, deep=True, n_deep=len(slots), verifiers=len(slots))
         return committed, done
 
     def _spec_step(self):
@@ -320,7 +346,7 @@ class EESDEngine:
         flush = (not dec.any()) and bool((self.state == PREFILL).any())
         deep = bool(V.any()) or flush
         Dr = dec & ~V
-        probe = deep and self.exitc is not None and self.exitc.want_probe() and bool(V.any())
+        probe = deep and self.exitc is not None and self.exitc.probe_due() and bool(V.any())
         chunks = self._plan_chunks(dec, d, V, deep, probe, flush, ctx) if self.m3 is not None else []
         plan_ms = 1000 * (time.perf_counter() - t0)
 
@@ -379,9 +405,9 @@ class EESDEngine:
             pb.meta, sel_t, alt_t, ex_dst_t, ex_src_t, drf_src_t, drf_dst_t = upload_many(
                 [pb.meta_host, sel.astype(np.int64), alt, ex_dst.astype(np.int64), ex_src.astype(np.int64),
                  drf_src.astype(np.int64), drf_dst.astype(np.int64)], self.dev)
-        self._kv(pb, k)
+        self._count_kv(pb, k)
         sb, exh = self._flat()
-        iv = Interval(self.dev).start()
+        span = DeviceSpan(self.dev).open()
         if gentry is not None:
             def shallow_gpu():
                 xg = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
@@ -393,14 +419,14 @@ class EESDEngine:
                     _lsk.copy_rows(hx, None, hg, drf_src_t, nd)
                     m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)
             self.graphs.run(gentry, lambda: m.buf_epoch, shallow_gpu)
-            iv.stop()
-            self._rec("shallow", iv, n_sh=N, n_dp=0, n_chunk=0, plan_ms=plan_ms)
+            span.close()
+            self._log("shallow", span, n_sh=N, n_dp=0, n_chunk=0, plan_ms=plan_ms)
             self.d[Dr] += 1
             if self.trace is not None:
                 self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
                                    "n_draft": nd, "dp": [], "committed": 0})
             self.steps_since_deep += 1
-            self._account(0, deep=False, plan_ms=plan_ms)
+            self._tally(0, deep=False, plan_ms=plan_ms)
             return 0, []
         x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
         _lsk.embed(m.embed_w, alt_t, x, sb, sel_t)                        # seq_buf ids, or prompt ids for chunks
@@ -424,9 +450,9 @@ class EESDEngine:
             draft = (h, drf_src_t, drf_dst_t, nd) if merge_heads else (h, None, None, 0)
             probe_ctx = (pb, kb, sb_slot, cap_sh) if probe else None
             readback, n_v_tok, vinfo, cfin = self._deep(V, d, draft, probe_ctx)
-        iv.stop()
+        span.close()
         n_chunk = sum(c[2] for c in chunks)
-        self._rec("probe" if probe else ("deep" if deep else "shallow"), iv, n_sh=N, n_dp=n_v_tok, n_chunk=n_chunk,
+        self._log("probe" if probe else ("deep" if deep else "shallow"), span, n_sh=N, n_dp=n_v_tok, n_chunk=n_chunk,
                   plan_ms=plan_ms)
         self.d[Dr] += 1
         if self.measuring:
@@ -441,7 +467,7 @@ class EESDEngine:
                                "committed": 0})
         if not deep:
             self.steps_since_deep += 1
-            self._account(0, deep=False, plan_ms=plan_ms)
+            self._tally(0, deep=False, plan_ms=plan_ms)
             return 0, []
         rb = readback.tolist()
         vslots, vstarts, vT = vinfo
@@ -464,7 +490,7 @@ class EESDEngine:
                 done.append(i)
         off = nv + n_v_tok
         for jf, i in enumerate(cfin):                                     # M3: prompts whose last chunk finished
-            committed += self._first_token(i, int(rb[off + jf]))
+            committed += self._start_decoding(i, int(rb[off + jf]))
             if self.req[i].finish:
                 done.append(i)
         off += len(cfin)
@@ -477,15 +503,15 @@ class EESDEngine:
         if self.exitc is not None:
             if probe:
                 nc = len(self.exitc.cands)
-                self.exitc.observe_probe(rb[off:off + nc], int(rb[off + nc]))
-            self.exitc.after_deep_step()
+                self.exitc.absorb_probe(rb[off:off + nc], int(rb[off + nc]))
+            self.exitc.deep_step_done()
             dec_now = self.state == DECODE
-            new = self.exitc.maybe_switch(int(dec_now.sum()), float((self.pos + self.d)[dec_now].sum()),
-                                          can_switch=not (self.state == PREFILL).any())
+            new = self.exitc.propose(int(dec_now.sum()), float((self.pos + self.d)[dec_now].sum()),
+                                          allowed=not (self.state == PREFILL).any())
             if new is not None:
                 self._switch_exit(new)
         plan_ms += 1000 * (time.perf_counter() - t2)
-        self._account(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms, probe=probe)
+        self._tally(committed, deep=True, n_deep=n_v_tok, verifiers=nv, plan_ms=plan_ms, probe=probe)
         return committed, done
 
     def _plan_chunks(self, dec, d, V, deep, probe, flush, ctx) -> list:
@@ -502,7 +528,7 @@ class EESDEngine:
             rem = len(r.prompt) - r.pf_sh
             if rem <= 0:
                 continue
-            c = min(rem, self.m3.budget(0 if flush else n_sh, 0 if flush else n_dp_est, 0 if flush else pend))
+            c = min(rem, self.m3.chunk_budget(0 if flush else n_sh, 0 if flush else n_dp_est, 0 if flush else pend))
             if flush and c <= 0:
                 c = min(rem, self.cfg.prefill_chunk)
             if c <= 0:
@@ -535,7 +561,7 @@ class EESDEngine:
         pos0 = np.concatenate([self.pos[vs], np.array(cpos, dtype=np.int64)])
         T = np.concatenate([d[vs] + 1, np.array(cT, dtype=np.int64)])
         pb = build_packed_arrays(m, rows, pos0, T, self.cfg.bucketing, upload_meta=False)
-        self._kv(pb, L - k)
+        self._count_kv(pb, L - k)
         n = pb.n_tokens
         is_v = pb.order < nvb
         vb = np.flatnonzero(is_v)                                         # verify blocks in packed order
@@ -639,236 +665,217 @@ class EESDEngine:
         _lsk.probe_matches(pred, Yv, rb[:nv], blk_t, jl_t, nc, nvt, out)
 
     def _switch_exit(self, new_k: int) -> None:
-        """Exit switch (solutions/engine.py:522-527): drafts in flight are dropped (lossless), every slot restarts
-        drafting from its last committed token with the new exit layer."""
-        self.stats["dropped_drafts"] += int(self.d[self.state == DECODE].sum())
+        """Move to exit layer new_k (solutions/engine.py:522-527): the drafts in flight were made with the old exit
+        and are dropped (lossless); every slot drafts again from its last committed token."""
+        live = self.state == DECODE
+        self.stats["dropped_drafts"] += int(self.d[live].sum())
         self.d[:] = 0
         self.k = new_k
         self.sched.set_exit(new_k, self.exitc.alpha.get(new_k))
 
-    def _kv(self, pb, n_layers: int) -> None:
+    def _count_kv(self, pb, n_layers: int) -> None:
+        """KV positions attention reads in this segment (the reference's padded accounting) and the gathered
+        share, over n_layers layers."""
         if self.measuring:
             self.stats["kv_read_pos"] += pb.kv_read_padded * n_layers
             self.stats["kv_gathered_pos"] += pb.kv_gathered * n_layers
 
-    def _account(self, committed, deep, n_deep=0, verifiers=0, plan_ms=0.0, probe=False):
+    def _tally(self, committed, deep, n_deep=0, verifiers=0, plan_ms=0.0, probe=False):
         if not self.measuring:
             return
-        st = self.stats
-        st["steps"] += 1
-        st["committed"] += committed
-        st["plan_ms"] += plan_ms
-        st["plan_calls"] += 1
+        add = {"steps": 1, "committed": committed, "plan_ms": plan_ms, "plan_calls": 1}
         if deep:
-            st["deep_steps"] += 1
-            st["deep_tokens"] += n_deep
-            st["verifiers"] += verifiers
-            st["probe_steps"] += int(probe)
+            add.update(deep_steps=1, deep_tokens=n_deep, verifiers=verifiers, probe_steps=int(probe))
+        for key, v in add.items():
+            self.stats[key] += v
 
     # ------------------------------------------------------------------ drivers
+    def _busy(self) -> bool:
+        return bool(((self.state == DECODE) | (self.state == PREFILL)).any())
+
+    def _release(self, slot: int, out: list, keep: bool) -> None:
+        r = self.req[slot]
+        r.log_finish = len(self.records) - 1
+        rec = {"pid": r.pid, "prompt_len": len(r.prompt), "generated": len(r.out), "finish_reason": r.finish,
+               "measured": r.measured, "log_assign": r.log_assign, "log_first": r.log_first,
+               "log_finish": r.log_finish, "piggybacked": r.piggybacked,
+               "wall_ttft_s": (r.wall_first - r.wall_arrival) if r.wall_arrival else None}
+        if keep:
+            rec["tokens"] = list(r.out)
+        out.append(rec)
+        self.state[slot] = FREE
+        self.req[slot] = None
+
+    def _decode_rate(self, first: int, tokens: int) -> float:
+        ms = sum(e.ms for e in self.records[first:] if e.kind != "prefill")
+        return tokens / (ms / 1000) if ms > 0 else 0.0
+
+    def _begin_measuring(self, mark: dict) -> None:
+        self.measuring = True
+        mark["first_entry"] = len(self.records)
+        if self.dev.type == "cuda":
+            torch.cuda.synchronize(self.dev)
+
     def run(self, prompts: list, mode: str = "cyclic", warmup_samples: int = 8, warmup_per_slot: float = 1.0,
             min_eval: int = 16, min_eval_per_slot: float = 2.0, max_eval: int = 256, converge_threshold: float = 0.01,
             converge_window: int = 4, keep_outputs: bool = False, max_steps: Optional[int] = None) -> dict:
-        """ASPIRE cyclic replay or a static pass over the prompts (solutions/engine.py:544-623)."""
-        B, n_pool = self.B, len(prompts)
-        warmup_n = 0 if mode == "static" else max(warmup_samples, math.ceil(warmup_per_slot * B))
-        min_eval_n = max(min_eval, math.ceil(min_eval_per_slot * B))
-        max_eval_n = max(max_eval, min_eval_n)
-        self.measuring = warmup_n == 0
-        t_wall0 = self._wall_now() if self.measuring else None
-        cursor, total_done, evaluated, stable, anchor, stop_reason = 0, 0, 0, 0, None, None
-        completions, rec_measure_start, tok_measured = [], 0, 0
+        """A static pass over the prompts, or a cyclic replay measured after warm-up completions until the
+        decode throughput converges (solutions/engine.py:544-623 rules)."""
+        cyclic = mode != "static"
+        warm = max(warmup_samples, int(np.ceil(warmup_per_slot * self.B))) if cyclic else 0
+        least = max(min_eval, int(np.ceil(min_eval_per_slot * self.B)))
+        mark = {"first_entry": 0, "tokens": 0}
+        self.measuring = False
+        window = MeasureWindow(warm, least, max(max_eval, least) if cyclic else None, converge_threshold,
+                               converge_window, converge=cyclic, on_start=lambda: self._begin_measuring(mark))
+        done: list = []
+        eng = self
 
-        def make(p):
-            return Request(p.pid, list(p.tokens))
+        class Slots:
+            n_slots = self.B
 
-        for slot in range(B):
-            if mode == "static" and cursor >= n_pool:
-                break
-            self.assign(slot, make(prompts[cursor % n_pool]))
-            cursor += 1
-        pre_done = [i for i in range(B) if self.req[i] is not None and self.req[i].finish]
-        steps = 0
-        while True:
-            if not pre_done and not ((self.state == DECODE) | (self.state == PREFILL)).any():
-                stop_reason = "pool_exhausted"
-                break
-            if pre_done:
-                committed, done = 0, pre_done
-                pre_done = []
-            else:
-                committed, done = self.step()
-                steps += 1
-            if self.measuring:
-                tok_measured += committed
-            queue = list(done)
-            while queue:
-                slot = queue.pop(0)
-                r = self.req[slot]
-                if r is None:
-                    continue
-                r.rec_finish = len(self.records) - 1
-                completions.append(self._completion(r, keep_outputs))
-                total_done += 1
-                self.state[slot] = FREE
-                self.req[slot] = None
-                if not self.measuring:
-                    if total_done >= warmup_n:
-                        self.measuring = True
-                        rec_measure_start = len(self.records)
-                        t_wall0 = self._wall_now()
-                elif mode == "cyclic":
-                    evaluated += 1
-                    if evaluated >= min_eval_n:
-                        thr = self._throughput(rec_measure_start, tok_measured)
-                        if anchor is None:
-                            anchor = thr
-                        elif abs(thr - anchor) / max(anchor, 1e-9) < converge_threshold:
-                            stable += 1
-                        else:
-                            stable, anchor = 0, thr
-                        if stable >= converge_window:
-                            stop_reason = "converged"
-                    if stop_reason is None and evaluated >= max_eval_n:
-                        stop_reason = "max_eval_samples"
-                if stop_reason is None and (mode == "cyclic" or cursor < n_pool):
-                    self.assign(slot, make(prompts[cursor % n_pool]))
-                    cursor += 1
-                    if self.req[slot].finish:
-                        queue.append(slot)
-            if stop_reason is not None:
-                break
-            if max_steps is not None and steps >= max_steps:
-                stop_reason = "max_steps"
-                break
+            def admit(self, slot, index, prompt):
+                eng.assign(slot, Request(prompt.pid, list(prompt.tokens)))
+                return eng.req[slot].finish is not None
+
+            def advance(self):
+                committed, finished = eng.step()
+                if eng.measuring:
+                    mark["tokens"] += committed
+                return finished
+
+            def release(self, slot):
+                eng._release(slot, done, keep_outputs)
+
+            def busy(self):
+                return eng._busy()
+
+        stop = run_pool(Slots(), prompts, cyclic, window, lambda: self._decode_rate(mark["first_entry"],
+                                                                                   mark["tokens"]), max_steps)
         if self.dev.type == "cuda":
             torch.cuda.synchronize(self.dev)
-        wall_s = time.perf_counter() - t_wall0 if t_wall0 is not None else None
-        return self._result(completions, rec_measure_start, tok_measured, stop_reason, wall_s)
+        wall = time.perf_counter() - window.t_start if window.t_start is not None else None
+        return self._report(done, mark["first_entry"], mark["tokens"], stop, wall)
 
     def run_poisson(self, prompts: list, rate_per_s: float, n_requests: int, warm_requests: int = 8, seed: int = 0,
                     keep_outputs: bool = False) -> dict:
-        """Open loop: Poisson arrivals in wall-clock time, FIFO into free slots (solutions/engine.py:625-673)."""
-        rng = np.random.default_rng(seed)
-        queue, completions, cursor = [], [], 0
-        t0 = time.perf_counter()
-        next_arr = t0 + rng.exponential(1 / rate_per_s)
-        rec_measure_start, tok_measured = 0, 0
+        """Open loop (solutions/engine.py:625-673 rules): Poisson arrivals at rate_per_s in wall-clock time, FIFO
+        into free slots; the first warm_requests completions are warm-up, the run ends after n_requests more."""
+        mark = {"first_entry": 0, "tokens": 0, "released": 0, "t_meas": time.perf_counter()}
         self.measuring = warm_requests == 0
-        total_done = 0
-        t_meas = t0
-        while total_done < n_requests + warm_requests:
-            now = time.perf_counter()
-            while next_arr <= now:
-                p = prompts[cursor % len(prompts)]
-                cursor += 1
-                queue.append(Request(p.pid, list(p.tokens), wall_arrival=next_arr))
-                next_arr += rng.exponential(1 / rate_per_s)
-            instant = []
-            for slot in np.flatnonzero(self.state == FREE):
-                if not queue:
-                    break
-                self.assign(int(slot), queue.pop(0))
-                if self.req[int(slot)].finish:
-                    instant.append(int(slot))
-            if not instant and not ((self.state == DECODE) | (self.state == PREFILL)).any():
-                time.sleep(max(0.0, min(next_arr - time.perf_counter(), 0.01)))
-                continue
-            committed, done = (0, instant) if instant else self.step()
-            if self.measuring:
-                tok_measured += committed
-            for slot in done:
-                r = self.req[slot]
-                r.rec_finish = len(self.records) - 1
-                completions.append(self._completion(r, keep_outputs))
-                total_done += 1
-                self.state[slot] = FREE
-                self.req[slot] = None
-                if not self.measuring and total_done >= warm_requests:
-                    self.measuring = True
-                    rec_measure_start = len(self.records)
-                    t_meas = self._wall_now()
+        done: list = []
+        eng = self
+
+        class Slots:
+            n_slots = self.B
+
+            def advance(self):
+                committed, finished = eng.step()
+                if eng.measuring:
+                    mark["tokens"] += committed
+                return finished
+
+            def release(self, slot):
+                eng._release(slot, done, keep_outputs)
+
+            def busy(self):
+                return eng._busy()
+
+        def after_release():
+            mark["released"] += 1
+            if not self.measuring and mark["released"] >= warm_requests:
+                self._begin_measuring(mark)
+                mark["t_meas"] = time.perf_counter()
+
+        def admit(slot, req):
+            self.assign(slot, req)
+            return self.req[slot].finish is not None
+
+        def make(i, t_arrival):
+            p = prompts[i % len(prompts)]
+            return Request(p.pid, list(p.tokens), wall_arrival=t_arrival)
+
+        arrivals = PoissonArrivals(rate_per_s, seed, mark["t_meas"])
+        left = run_arrivals(Slots(), lambda: [int(s) for s in np.flatnonzero(self.state == FREE)], make, admit,
+                            arrivals, n_requests + warm_requests, after_release)
         if self.dev.type == "cuda":
             torch.cuda.synchronize(self.dev)
-        res = self._result(completions, rec_measure_start, tok_measured, "n_requests", time.perf_counter() - t_meas)
+        res = self._report(done, mark["first_entry"], mark["tokens"], "n_requests", time.perf_counter() - mark["t_meas"])
         res["metrics"]["poisson_rate_per_s"] = rate_per_s
-        res["metrics"]["queue_left"] = len(queue)
+        res["metrics"]["queue_left"] = left
         return res
 
     # ------------------------------------------------------------------ results
-    def _throughput(self, start: int, tokens: int) -> float:
-        ms = sum(r.ms for r in self.records[start:] if r.kind != "prefill")
-        return tokens / (ms / 1000) if ms > 0 else 0.0
-
-    def _completion(self, r: Request, keep: bool) -> dict:
-        c = {"pid": r.pid, "prompt_len": len(r.prompt), "generated": len(r.out), "finish_reason": r.finish,
-             "measured": r.measured, "rec_assign": r.rec_assign, "rec_first": r.rec_first, "rec_finish": r.rec_finish,
-             "piggybacked": r.piggybacked, "wall_ttft_s": (r.wall_first - r.wall_arrival) if r.wall_arrival else None}
-        if keep:
-            c["tokens"] = list(r.out)
-        return c
-
-    def _wall_now(self) -> float:
-        if self.dev.type == "cuda":
-            torch.cuda.synchronize(self.dev)
-        return time.perf_counter()
-
-    def _result(self, completions, start, tokens, stop_reason, wall_s=None) -> dict:
-        """Metrics with the reference's names and definitions (solutions/engine.py:694-753)."""
-        recs = self.records
-        ms = np.array([r.ms for r in recs]) if recs else np.zeros(0)
-        cum = np.concatenate([[0.0], np.cumsum(ms)])
-        meas = np.array([r.measured for r in recs], dtype=bool)
-        kinds = np.array([r.kind for r in recs])
-        decode_ms = float(ms[meas & (kinds != "prefill")].sum()) if len(ms) else 0.0
-        prefill_ms = float(ms[meas & (kinds == "prefill")].sum()) if len(ms) else 0.0
+    def _report(self, completions, first_entry, tokens, stop_reason, wall_s=None) -> dict:
+        """The reference's metrics (solutions/engine.py:694-753) from the step log and the completions."""
+        log = self.records
+        ms = np.fromiter((e.ms for e in log), dtype=np.float64, count=len(log))
+        counted = np.fromiter((e.measured for e in log), dtype=bool, count=len(log))
+        is_prefill = np.fromiter((e.kind == "prefill" for e in log), dtype=bool, count=len(log))
+        decode_ms = float(ms[counted & ~is_prefill].sum())
+        prefill_ms = float(ms[counted & is_prefill].sum())
+        gpu_ms = decode_ms + prefill_ms
+        before = np.concatenate([[0.0], np.cumsum(ms)])        # before[i] = time of entries [0, i)
+        decode_before = np.concatenate([[0.0], np.cumsum(np.where(is_prefill, 0.0, ms))])
         ttft, tpot = [], []
         for c in completions:
-            if not c["measured"] or c["rec_first"] < 0:
+            if not c["measured"] or c["log_first"] < 0:
                 continue
-            ttft.append(cum[c["rec_first"] + 1] - cum[c["rec_assign"]])
-            if c["generated"] > 1 and c["rec_finish"] > c["rec_first"]:
-                seg = slice(c["rec_first"] + 1, c["rec_finish"] + 1)
-                tpot.append(ms[seg][kinds[seg] != "prefill"].sum() / (c["generated"] - 1))
-        st = dict(self.stats)
-        nsteps = max(st["steps"], 1)
-        piggy_ms = float(sum(r.ms for r in recs if r.measured and r.n_chunk and r.kind != "prefill"))
-        tot = decode_ms + prefill_ms
-        metrics = {
-            "config": self.cfg.label(), "B": self.B, "stop_reason": stop_reason,
+            ttft.append(before[c["log_first"] + 1] - before[c["log_assign"]])
+            if c["generated"] > 1 and c["log_finish"] > c["log_first"]:
+                tpot.append((decode_before[c["log_finish"] + 1] - decode_before[c["log_first"] + 1])
+                            / (c["generated"] - 1))
+        st = self.stats
+
+        def ratio(a, b):
+            return a / max(b, 1)
+
+        def mean_p99(x):
+            return (float(np.mean(x)), float(np.percentile(x, 99))) if x else (None, None)
+
+        ttft_mean, ttft_p99 = mean_p99(ttft)
+        tpot_mean, tpot_p99 = mean_p99(tpot)
+        timing = {
             "measured_tokens": tokens, "decode_ms": decode_ms, "prefill_ms": prefill_ms,
             "throughput_tok_s": tokens / (decode_ms / 1000) if decode_ms else None,
-            "e2e_throughput_tok_s": tokens / (tot / 1000) if tot else None,
+            "e2e_throughput_tok_s": tokens / (gpu_ms / 1000) if gpu_ms else None,
             "wall_s": wall_s,
             "wall_throughput_tok_s": tokens / wall_s if wall_s else None,
-            "host_overhead_share": (1 - tot / (1000 * wall_s)) if wall_s else None,
-            "prefill_time_share": prefill_ms / tot if tot else None,
-            "prefill_tokens_separate": st["prefill_tokens"], "prefill_tokens_piggyback": st["piggyback_tokens"],
-            "piggyback_share_of_prefill_tokens": st["piggyback_tokens"] / max(st["piggyback_tokens"]
-                                                                              + st["prefill_tokens"], 1),
-            "steps_with_piggyback_ms": piggy_ms,
-            "deep_steps_per_token": st["deep_steps"] / max(st["committed"], 1),
-            "deep_exec_fraction": st["deep_steps"] / nsteps,
-            "tokens_per_deep_step": st["deep_tokens"] / max(st["deep_steps"], 1),
-            "verifiers_per_deep_step": st["verifiers"] / max(st["deep_steps"], 1),
-            "acceptance_rate": st["accepted"] / max(st["drafted"], 1),
+            "host_overhead_share": (1 - gpu_ms / (1000 * wall_s)) if wall_s else None,
+            "prefill_time_share": prefill_ms / gpu_ms if gpu_ms else None,
+            "ttft_ms_mean": ttft_mean, "ttft_ms_p99": ttft_p99, "tpot_ms_mean": tpot_mean, "tpot_ms_p99": tpot_p99,
             "plan_ms_per_step": st["plan_ms"] / max(st["plan_calls"], 1),
-            "ttft_ms_mean": float(np.mean(ttft)) if ttft else None,
-            "ttft_ms_p99": float(np.percentile(ttft, 99)) if ttft else None,
-            "tpot_ms_mean": float(np.mean(tpot)) if tpot else None,
-            "tpot_ms_p99": float(np.percentile(tpot, 99)) if tpot else None,
+        }
+        prefill = {
+            "prefill_tokens_separate": st["prefill_tokens"], "prefill_tokens_piggyback": st["piggyback_tokens"],
+            "piggyback_share_of_prefill_tokens": ratio(st["piggyback_tokens"],
+                                                       st["piggyback_tokens"] + st["prefill_tokens"]),
+            "steps_with_piggyback_ms": float(sum(e.ms for e in log if e.measured and e.n_chunk and e.kind != "prefill")),
+            "m3_fallbacks": st["m3_fallbacks"], "m3_fallback_reasons": dict(self.fallback_reasons),
+            "separate_prefills": st["separate_prefills"],
+        }
+        speculation = {
+            "deep_steps_per_token": ratio(st["deep_steps"], st["committed"]),
+            "deep_exec_fraction": ratio(st["deep_steps"], st["steps"]),
+            "tokens_per_deep_step": ratio(st["deep_tokens"], st["deep_steps"]),
+            "verifiers_per_deep_step": ratio(st["verifiers"], st["deep_steps"]),
+            "acceptance_rate": ratio(st["accepted"], st["drafted"]),
+            "gamma_final": getattr(self.sched, "gamma", None) if self.sched is not None else None,
+            "oracle_coverage": None,
+        }
+        exits = {
             "k_final": self.k,
             "k_timeline": list(self.exitc.timeline) if self.exitc is not None else [(0, self.k)],
             "k_alpha": dict(self.exitc.alpha) if self.exitc is not None else None,
             "probe_steps": st["probe_steps"], "dropped_drafts_at_switch": st["dropped_drafts"],
-            "m3_fallbacks": st["m3_fallbacks"], "m3_fallback_reasons": dict(self.fallback_reasons),
-            "oracle_coverage": None,
-            "gamma_final": getattr(self.sched, "gamma", None) if self.sched is not None else None,
-            "kv_gather_share": st["kv_gathered_pos"] / max(st["kv_read_pos"], 1),
+        }
+        kv = {
+            "kv_gather_share": ratio(st["kv_gathered_pos"], st["kv_read_pos"]),
             "kv_read_bytes": st["kv_read_pos"] * self.kv_bytes_per_pos,
             "kv_gathered_bytes": st["kv_gathered_pos"] * self.kv_bytes_per_pos,
-            "separate_prefills": st["separate_prefills"],
-            "evaluated_completions": sum(1 for c in completions if c["measured"]),
-            "steps": st["steps"], "deep_steps": st["deep_steps"],
         }
+        metrics = {"config": self.cfg.label(), "B": self.B, "stop_reason": stop_reason, **timing, **prefill,
+                   **speculation, **exits, **kv,
+                   "evaluated_completions": sum(1 for c in completions if c["measured"]),
+                   "steps": st["steps"], "deep_steps": st["deep_steps"]}
         return {"metrics": metrics, "engine_config": asdict(self.cfg), "completions": completions}

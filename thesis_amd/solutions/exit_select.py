@@ -1,15 +1,16 @@
-"""M2: a batch-shared exit layer chosen at run time from probe measurements (solutions/exit_select.py surface).
+"""M2: one exit layer for the whole batch, moved at run time by probe measurements (rules of the reference's
+solutions/exit_select.py:28-72).
 
-Every `probe_every`-th deep step is a probe: the verifying requests run all of their d + 1 tokens through the
-shallow layers again, the hidden state entering every candidate exit layer is captured (shallow candidates in the
-shallow segment, deeper ones in the deep segment), the shared final norm + LM head is applied to each, and its
-greedy token is compared with the full model's token Y at the positions whose prefix is correct (j <= accepted).
-The per-candidate match fraction feeds an EMA alpha(k).  After each deep step without a half-done prefill, the
-candidate with the best cost-model rate max_s B E(alpha, s) / (s t_sh(B, k) + t_deep(B (s + 1), k)) replaces the
-current exit when it beats it by more than `margin` (solutions/exit_select.py:28-72).  A switch drops the drafts in
-flight (they are guesses; outputs stay lossless).
+Every `probe_every`-th deep step probes: the verifiers run all of their d + 1 tokens through the shallow layers
+again, the hidden state entering every candidate exit layer is captured (shallow candidates in the shallow
+segment, deeper ones in the deep segment), the shared final norm + LM head turns each into a greedy token, and
+the device counts agreement with the full model's token Y on the positions with a correct prefix (j <= accepted).
+The fraction per candidate feeds an exponentially weighted estimate alpha(k).
 
-Host-only; the probe's match counts come back in the deep step's single readback.
+After each deep step (never while a prompt is half piggybacked) the candidate with the best cost-model rate
+max_s B E(alpha, s) / (s t_sh(B, k) + t_deep(B (s + 1), k)) becomes the exit when it beats the current one by
+more than `margin`.  Drafts in flight are dropped at a switch; they are guesses, so outputs stay lossless.
+Host-only; the match counts arrive with the deep step's single readback.
 """
 
 from __future__ import annotations
@@ -20,49 +21,53 @@ from typing import Optional
 class ExitController:
     def __init__(self, cost_model, k0: int, cands, probe_every: int = 20, margin: float = 0.05, omega: float = 0.8,
                  d_max: int = 16, force: Optional[str] = None):
-        self.cm, self.k = cost_model, int(k0)
-        self.cands = sorted({int(c) for c in cands} | {int(k0)})
-        self.probe_every, self.margin, self.omega, self.d_max = probe_every, margin, omega, d_max
-        self.alpha = {c: None for c in self.cands}
-        self.deep_steps = 0
-        self.probes = 0
-        self.timeline = [(0, self.k)]        # (deep step index, exit layer)
-        self.force = force                   # "cycle": move to the next candidate at every probe (tests)
+        self.cm, self.k, self.d_max = cost_model, int(k0), d_max
+        self.cands = sorted({int(c) for c in cands} | {self.k})
+        self.period, self.margin, self.weight = probe_every, margin, omega
+        self.force = force                     # "cycle": step to the next candidate at every probe (tests)
+        self.alpha: dict = dict.fromkeys(self.cands)
+        self.n_deep = 0
+        self.n_probes = 0
+        self.timeline = [(0, self.k)]          # (deep step index, exit layer)
         self.last_rates: dict = {}
 
-    def want_probe(self) -> bool:
-        return (self.deep_steps + 1) % self.probe_every == 0
+    def probe_due(self) -> bool:
+        """Whether the coming deep step is a probe."""
+        return (self.n_deep + 1) % self.period == 0
 
-    def after_deep_step(self) -> None:
-        self.deep_steps += 1
+    def deep_step_done(self) -> None:
+        self.n_deep += 1
 
-    def observe_probe(self, matches, total: int) -> None:
-        """matches[i]: tokens on which candidate cands[i] agrees with Y among `total` correct-prefix positions."""
+    def absorb_probe(self, matches, total: int) -> None:
+        """matches[i]: correct-prefix positions (of `total`) on which candidate cands[i] agreed with Y."""
         if total <= 0:
             return
-        self.probes += 1
+        self.n_probes += 1
         for c, m in zip(self.cands, matches):
-            a = float(m) / float(total)
-            prev = self.alpha[c]
-            self.alpha[c] = a if prev is None else self.omega * prev + (1.0 - self.omega) * a
+            frac = float(m) / float(total)
+            old = self.alpha[c]
+            self.alpha[c] = frac if old is None else self.weight * old + (1.0 - self.weight) * frac
 
-    def maybe_switch(self, B: int, C: float, can_switch: bool) -> Optional[int]:
-        """After a deep step: the new exit layer, or None to keep the current one."""
-        if not can_switch or self.probes == 0:
-            return None
+    def _pick(self, n_live: int, ctx_sum: float) -> Optional[int]:
         if self.force == "cycle":
-            if self.deep_steps % self.probe_every:
+            if self.n_deep % self.period:
                 return None
-            new = self.cands[(self.cands.index(self.k) + 1) % len(self.cands)]
-        else:
-            known = {c: a for c, a in self.alpha.items() if a is not None}
-            if self.k not in known or B <= 0:
-                return None
-            per_req = C / max(B, 1)
-            self.last_rates = {c: self.cm.best_rate(a, B, c, B * per_req, self.d_max) for c, a in known.items()}
-            new = max(self.last_rates, key=self.last_rates.get)
-            if new == self.k or self.last_rates[new] <= (1.0 + self.margin) * self.last_rates[self.k]:
-                return None
-        self.k = new
-        self.timeline.append((self.deep_steps, new))
+            return self.cands[(self.cands.index(self.k) + 1) % len(self.cands)]
+        measured = {c: a for c, a in self.alpha.items() if a is not None}
+        if self.k not in measured or n_live <= 0:
+            return None
+        self.last_rates = {c: self.cm.best_rate(a, n_live, c, ctx_sum, self.d_max) for c, a in measured.items()}
+        best = max(self.last_rates, key=self.last_rates.get)
+        if best == self.k or self.last_rates[best] <= (1.0 + self.margin) * self.last_rates[self.k]:
+            return None
+        return best
+
+    def propose(self, n_live: int, ctx_sum: float, allowed: bool) -> Optional[int]:
+        """After a deep step: the new exit layer (the controller switches to it), or None to keep the current."""
+        if not allowed or self.n_probes == 0:
+            return None
+        new = self._pick(n_live, ctx_sum)
+        if new is not None:
+            self.k = new
+            self.timeline.append((self.n_deep, new))
         return new

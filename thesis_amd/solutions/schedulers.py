@@ -1,218 +1,188 @@
-"""When to run the deep layers (solutions/schedulers.py surface; host-only NumPy, no GPU access).
+"""Deep-step policies: which decoding slots verify in the next step (host-only NumPy, no GPU access).
 
-Each scheduler sees the decoding slots' state before a step and returns the verifying set V (deep
-step iff V is non-empty); the other decoding slots draft one token in the same step.
+Before every engine step the policy sees, for each slot, how many drafts it holds (d), how many KV positions it
+reads (context) and whether it is decoding (live), plus the number of shallow-only steps since the last deep step
+(idle).  It returns the verifying set V; the step is deep iff V is non-empty, and every live slot outside V drafts
+one more token in the same step.  The decision rules are the reference's methods (solutions/schedulers.py:29-197,
+targets by common/policies.py:54-68); a different rule would be a different method.
 
-  fixed       a deep step every gamma shallow steps (solutions/schedulers.py:77-89)
-  aspire      per-request target draft length from an EMA acceptance and the homogeneous-batch cost
-              ratio t_sh / t_deep (solutions/schedulers.py:92-111; targets by
-              common/policies.py:54-68).  `min_draft` is exposed so the [2, 8] draft range of the
-              Llama3-8B configuration can be expressed (the reference's make_scheduler cannot).
-  m1          batch-level trigger R(s+1) <= R(s) (solutions/schedulers.py:114-153)
-  fsm-sync    one batch-wide gamma, +-1 by the majority of full accepts (solutions/schedulers.py:156-171)
-  aspire-fsm  per-request targets, +-1 after each round (solutions/schedulers.py:174-197)
-Acceptance estimate: a <- omega a + (1 - omega) acc / min(acc + 1, d) (solutions/schedulers.py:35-51).
+  fixed       verify everyone holding drafts every `gamma` idle steps (a slot at d_max verifies earlier)
+  aspire      per-slot target draft length: the largest gamma whose marginal expected-tokens-per-time gain is
+              positive, with the cost ratio c = t_shallow / t_deep(d + 1) of a homogeneous batch; a slot verifies
+              as soon as it reaches its target.  `min_draft` bounds targets from below (the Llama3-8B
+              configuration's [2, 8] range), fresh slots start at `initial_draft`
+  m1          batch trigger: verify now iff the expected throughput of verifying now is at least that of
+              drafting one more step, R(s) >= R(s + 1); forced at d_max or after `sla_steps` idle steps
+  fsm-sync    `fixed` with one batch-wide gamma moved by +-1 after each round (majority of full accepts)
+  aspire-fsm  per-slot targets moved by +-1 after each round (full accept: +1)
+
+Acceptance rate per slot (all policies): rate <- w rate + (1 - w) acc / min(acc + 1, d) after each round in which
+the slot verified d >= 1 drafts and accepted acc of them.
 """
 
 from __future__ import annotations
 
 import numpy as np
 
+POLICIES = ("fixed", "aspire", "m1", "fsm-sync", "aspire-fsm")
+SCHEDULERS = POLICIES
+
 
 def expected_tokens(alpha, d) -> np.ndarray:
+    """Expected tokens committed by verifying d drafts at per-token acceptance alpha: sum_{j<=d} alpha^j."""
     a = np.clip(np.asarray(alpha, dtype=np.float64), 0.0, 1 - 1e-6)
     return (1 - a ** (np.asarray(d, dtype=np.float64) + 1)) / (1 - a)
 
 
-_G_COLS: dict = {}
+_TARGET_GRID: dict = {}
 
 
 def expected_token_targets(alphas, cost_ratios, min_draft: int, max_draft: int) -> np.ndarray:
-    """Largest gamma with a positive marginal gain of E[tokens]/E[time] = ((1 - a^(g+1)) / (1 - a)) / (1 + c g):
-    a^g ((1 - a) c (g - 1) + c + (1 - a)) > c  (common/policies.py:54-68)."""
-    a = np.minimum(np.maximum(np.asarray(alphas, dtype=np.float64), 0.0), 1.0)
+    """Per slot, the largest gamma in [1, max_draft] at which one more draft still raises
+    E[tokens] / E[time] = ((1 - a^(g+1)) / (1 - a)) / (1 + c g), i.e. a^g ((1 - a) c (g - 1) + c + (1 - a)) > c;
+    min_draft when no gamma qualifies; max_draft at a = 1; clipped to [min_draft, max_draft]."""
+    a = np.clip(np.asarray(alphas, dtype=np.float64), 0.0, 1.0)
     c = np.asarray(cost_ratios, dtype=np.float64)
     if max_draft < 1:
         return np.full(a.shape, min_draft, dtype=np.int64)
-    g = _G_COLS.get(max_draft)
-    if g is None:
-        g = _G_COLS[max_draft] = np.arange(1, max_draft + 1, dtype=np.int64)[:, None]
-    om = 1 - a
-    gain = a ** g * (om * c * (g - 1) + c + om) > c
-    last = (max_draft - 1) - np.argmax(gain[::-1], axis=0)
-    t = np.where(gain.any(axis=0), last + 1, min_draft)
-    t = np.where(a >= 1 - 1e-7, max_draft, t)
-    return np.minimum(np.maximum(t, min_draft), max_draft).astype(np.int64)
+    g = _TARGET_GRID.setdefault(max_draft, np.arange(1, max_draft + 1, dtype=np.int64)[:, None])
+    miss = 1 - a
+    rising = a ** g * (miss * c * (g - 1) + c + miss) > c            # [gamma, slot]
+    top = max_draft - np.argmax(rising[::-1], axis=0)               # largest rising gamma (1-based)
+    target = np.where(rising.any(axis=0), top, min_draft)
+    target = np.where(a >= 1 - 1e-7, max_draft, target)
+    return np.clip(target, min_draft, max_draft).astype(np.int64)
 
 
 def best_gamma_expected(alpha: float, c: float, gmax: int) -> int:
-    """Brute-force argmax_g ((1 - a^(g+1)) / (1 - a)) / (1 + c g) (checker for expected_token_targets)."""
-    g = np.arange(0, gmax + 1)
+    """Brute force over gamma = 0..gmax of ((1 - a^(g+1)) / (1 - a)) / (1 + c g) (checks the closed form)."""
     a = min(max(alpha, 1e-6), 1 - 1e-6)
+    g = np.arange(gmax + 1)
     return int(g[np.argmax((1 - a ** (g + 1)) / (1 - a) / (1 + c * g))])
 
 
-class _EMA:
-    def __init__(self, B: int, omega: float, alpha0: float):
-        self.omega, self.alpha0 = omega, alpha0
-        self.alpha = np.full(B, alpha0)
-        self.fresh = np.ones(B, dtype=bool)
+class AcceptanceTracker:
+    """Exponentially weighted per-slot acceptance rate; `cold` marks slots without a verified round yet."""
 
-    def observe(self, verify, accepted, drafts) -> None:
-        ok = verify & (drafts > 0)
-        if ok.any():
-            a = accepted[ok].astype(np.float64)
-            d = drafts[ok].astype(np.float64)
-            self.alpha[ok] = self.omega * self.alpha[ok] + (1 - self.omega) * (a / np.minimum(a + 1.0, d))
-            self.fresh[ok] = False
+    def __init__(self, n_slots: int, weight: float, prior: float):
+        self.weight, self.prior = weight, prior
+        self.rate = np.full(n_slots, prior, dtype=np.float64)
+        self.cold = np.ones(n_slots, dtype=bool)
 
-    def reset(self, slot: int, alpha=None) -> None:
-        self.alpha[slot] = self.alpha0 if alpha is None else alpha
-        self.fresh[slot] = True
+    def update(self, verified: np.ndarray, accepted: np.ndarray, drafts: np.ndarray) -> None:
+        hit = verified & (drafts > 0)
+        if not hit.any():
+            return
+        acc, d = accepted[hit].astype(np.float64), drafts[hit].astype(np.float64)
+        self.rate[hit] = self.weight * self.rate[hit] + (1 - self.weight) * acc / np.minimum(acc + 1.0, d)
+        self.cold[hit] = False
+
+    def restart(self, slot: int, rate=None) -> None:
+        self.rate[slot] = self.prior if rate is None else rate
+        self.cold[slot] = True
 
 
-class Scheduler:
-    name = "base"
+class DraftPolicy:
+    """One engine's deep-step policy (see the module docstring for the rules).
 
-    def __init__(self, B: int, cost_model, k: int, d_max: int = 16, omega: float = 0.8, alpha0: float = 0.9):
-        self.B, self.cm, self.k, self.d_max = B, cost_model, k, d_max
-        self.ema = _EMA(B, omega, alpha0)
+    decide(d, ctx, live, idle) -> bool[B]   verifying set of the next step
+    observe(verified, accepted, drafts)     feedback after a deep step
+    reset(slot)                             a new request took the slot
+    set_exit(k, rate)                       the exit layer moved (M2): costs change, rates restart at `rate`
+    """
 
+    def __init__(self, kind: str, n_slots: int, cost_model, exit_layer: int, *, gamma: int = 4, d_max: int = 16,
+                 sla_steps: int = 32, initial_draft: int = 3, min_draft: int = 1, omega: float = 0.8,
+                 alpha0: float = 0.9):
+        if kind not in POLICIES:
+            raise ValueError(f"unknown scheduler {kind!r}; known: {POLICIES}")
+        if kind in ("fixed", "fsm-sync") and not 1 <= gamma <= d_max:
+            raise ValueError("gamma must be in [1, d_max]")
+        self.name = kind
+        self.B, self.cm, self.k, self.d_max = n_slots, cost_model, exit_layer, d_max
+        self.sla_steps, self.initial_draft, self.min_draft = sla_steps, initial_draft, min_draft
+        self.tracker = AcceptanceTracker(n_slots, omega, alpha0)
+        self.gamma = gamma if kind in ("fixed", "fsm-sync") else None
+        self.gamma_hist = [gamma] if kind == "fsm-sync" else None
+        self.targets = np.full(n_slots, initial_draft, dtype=np.int64) if kind == "aspire-fsm" else None
+        self._rule = {"fixed": self._by_round, "fsm-sync": self._by_round, "aspire": self._by_target_cost,
+                      "aspire-fsm": self._by_target_feedback, "m1": self._by_rate}[kind]
+
+    @property
+    def alpha(self) -> np.ndarray:
+        return self.tracker.rate
+
+    # ------------------------------------------------------------------ engine calls
     def decide(self, d, ctx, dec, steps_since_deep) -> np.ndarray:
-        raise NotImplementedError
+        ready = dec & (d >= 1)
+        if not ready.any():
+            return ready
+        return self._rule(d, ctx, dec, ready, steps_since_deep)
 
     def observe(self, verify, accepted, drafts) -> None:
-        self.ema.observe(verify, accepted, drafts)
+        self.tracker.update(verify, accepted, drafts)
+        rounds = verify & (drafts > 0)
+        full = accepted >= drafts
+        if self.gamma_hist is not None:                                   # fsm-sync: one batch-wide gamma
+            if rounds.any():
+                step = 1 if int((full & rounds).sum()) > 0.5 * int(rounds.sum()) else -1
+                self.gamma = int(np.clip(self.gamma + step, 1, self.d_max))
+            self.gamma_hist.append(self.gamma)
+        if self.targets is not None and rounds.any():                    # aspire-fsm: per-slot targets
+            self.targets = np.where(rounds, np.clip(self.targets + np.where(full, 1, -1), 1, self.d_max),
+                                    self.targets)
 
     def reset(self, slot: int) -> None:
-        self.ema.reset(slot)
+        self.tracker.restart(slot)
+        if self.targets is not None:
+            self.targets[slot] = self.initial_draft
 
     def set_exit(self, k: int, alpha=None) -> None:
         self.k = k
         if alpha is not None:
-            self.ema.alpha[:] = alpha
+            self.tracker.rate[:] = alpha
 
+    # ------------------------------------------------------------------ rules
+    def _by_round(self, d, ctx, dec, ready, idle):
+        return ready if idle >= self.gamma else ready & (d >= self.d_max)
 
-class FixedScheduler(Scheduler):
-    name = "fixed"
-
-    def __init__(self, B, cost_model, k, gamma: int, **kw):
-        super().__init__(B, cost_model, k, **kw)
-        if not 1 <= gamma <= self.d_max:
-            raise ValueError("gamma must be in [1, d_max]")
-        self.gamma = gamma
-
-    def decide(self, d, ctx, dec, steps_since_deep):
-        if steps_since_deep >= self.gamma:
-            return dec & (d >= 1)
-        return dec & (d >= self.d_max)
-
-
-class AspireScheduler(Scheduler):
-    name = "aspire"
-
-    def __init__(self, B, cost_model, k, initial_draft: int = 3, min_draft: int = 1, **kw):
-        super().__init__(B, cost_model, k, **kw)
-        self.initial_draft, self.min_draft = initial_draft, min_draft
-
-    def decide(self, d, ctx, dec, steps_since_deep):
+    def _by_target_cost(self, d, ctx, dec, ready, idle):
         n = int(dec.sum())
-        if n == 0:
-            return np.zeros_like(dec)
         C = float(ctx[dec].sum())
         t_sh = float(self.cm.t_sh(n, self.k, C))
-        t_v = self.cm.t_deep(n * (d + 1), self.k, C, n)
-        ratio = np.minimum(np.maximum(t_sh / np.maximum(t_v, 1e-9), 1e-4), 1.0)
-        tgt = expected_token_targets(self.ema.alpha, ratio, self.min_draft, self.d_max)
-        floor = np.where(self.ema.fresh, max(self.min_draft, self.initial_draft), self.min_draft)
-        tgt = np.minimum(np.maximum(tgt, floor), self.d_max)
-        return dec & (d >= 1) & ((d >= tgt) | (d >= self.d_max))
+        ratio = np.clip(t_sh / np.maximum(self.cm.t_deep(n * (d + 1), self.k, C, n), 1e-9), 1e-4, 1.0)
+        target = expected_token_targets(self.tracker.rate, ratio, self.min_draft, self.d_max)
+        lowest = np.where(self.tracker.cold, max(self.min_draft, self.initial_draft), self.min_draft)
+        return ready & (d >= np.minimum(np.maximum(target, lowest), self.d_max))
 
+    def _by_target_feedback(self, d, ctx, dec, ready, idle):
+        return ready & (d >= np.minimum(self.targets, self.d_max))
 
-class M1Scheduler(Scheduler):
-    name = "m1"
+    def _by_rate(self, d, ctx, dec, ready, idle):
+        if (d[dec] >= self.d_max).any() or idle >= self.sla_steps:
+            return ready
+        now, later = self.rates(d, ctx, dec, idle)
+        return ready if later <= now else np.zeros_like(ready)
 
-    def __init__(self, B, cost_model, k, sla_steps: int = 32, **kw):
-        super().__init__(B, cost_model, k, **kw)
-        self.sla_steps = sla_steps
-
-    def rates(self, d, ctx, dec, s):
-        dd = d[dec]
-        cc = ctx[dec].astype(np.float64)
-        al = self.ema.alpha[dec]
-        n = len(dd)
-        C = float(cc.sum())
+    def rates(self, d, ctx, dec, s) -> tuple:
+        """(R(s), R(s + 1)): expected tokens per expected time of verifying now (the slots holding drafts read the
+        deep layers) and after one more draft for everyone (all live slots verify, contexts one token longer)."""
+        dl = d[dec]
+        cl = ctx[dec].astype(np.float64)
+        rate = self.tracker.rate[dec]
+        n, C = len(dl), float(cl.sum())
         t_sh = float(self.cm.t_sh(n, self.k, C))
-        ver = dd >= 1
-        e_now = float(expected_tokens(al, dd)[ver].sum())
-        t_now = s * t_sh + float(self.cm.t_deep(int((dd[ver] + 1).sum()), self.k, C, n, C_deep=float(cc[ver].sum())))
-        e_next = float(expected_tokens(al, dd + 1).sum())
-        t_next = (s + 1) * t_sh + float(self.cm.t_deep(int((dd + 2).sum()), self.k, C + n, n, C_deep=C + n))
-        return e_now / max(t_now, 1e-9), e_next / max(t_next, 1e-9)
-
-    def decide(self, d, ctx, dec, steps_since_deep):
-        ver = dec & (d >= 1)
-        if not ver.any():
-            return ver
-        if (d[dec] >= self.d_max).any() or steps_since_deep >= self.sla_steps:
-            return ver
-        r_now, r_next = self.rates(d, ctx, dec, steps_since_deep)
-        return ver if r_next <= r_now else np.zeros_like(ver)
-
-
-class SyncFSMScheduler(FixedScheduler):
-    name = "fsm-sync"
-
-    def __init__(self, *a, **kw):
-        super().__init__(*a, **kw)
-        self.gamma_hist = [self.gamma]
-
-    def observe(self, verify, accepted, drafts) -> None:
-        super().observe(verify, accepted, drafts)
-        ver = verify & (drafts > 0)
-        if ver.any():
-            full = int((accepted[ver] >= drafts[ver]).sum())
-            self.gamma = int(np.clip(self.gamma + (1 if full > 0.5 * int(ver.sum()) else -1), 1, self.d_max))
-        self.gamma_hist.append(self.gamma)
-
-
-class AspireFSMScheduler(Scheduler):
-    name = "aspire-fsm"
-
-    def __init__(self, B, cost_model, k, initial_draft: int = 3, **kw):
-        super().__init__(B, cost_model, k, **kw)
-        self.initial_draft = initial_draft
-        self.targets = np.full(B, initial_draft, dtype=np.int64)
-
-    def decide(self, d, ctx, dec, steps_since_deep):
-        return dec & (d >= 1) & ((d >= self.targets) | (d >= self.d_max))
-
-    def observe(self, verify, accepted, drafts) -> None:
-        super().observe(verify, accepted, drafts)
-        ids = np.flatnonzero(verify & (drafts > 0))
-        if ids.size:
-            full = accepted[ids] >= drafts[ids]
-            self.targets[ids] = np.clip(np.where(full, self.targets[ids] + 1, self.targets[ids] - 1), 1, self.d_max)
-
-    def reset(self, slot: int) -> None:
-        super().reset(slot)
-        self.targets[slot] = self.initial_draft
-
-
-SCHEDULERS = ("fixed", "aspire", "m1", "fsm-sync", "aspire-fsm")
+        holding = dl >= 1
+        tokens_now = float(expected_tokens(rate, dl)[holding].sum())
+        time_now = s * t_sh + float(self.cm.t_deep(int((dl[holding] + 1).sum()), self.k, C, n,
+                                                   C_deep=float(cl[holding].sum())))
+        tokens_later = float(expected_tokens(rate, dl + 1).sum())
+        time_later = (s + 1) * t_sh + float(self.cm.t_deep(int((dl + 2).sum()), self.k, C + n, n, C_deep=C + n))
+        return tokens_now / max(time_now, 1e-9), tokens_later / max(time_later, 1e-9)
 
 
 def make_scheduler(name: str, B: int, cost_model, k: int, *, gamma: int = 4, d_max: int = 16, sla_steps: int = 32,
-                   initial_draft: int = 3, omega: float = 0.8, alpha0: float = 0.9, min_draft: int = 1, ref=None):
-    kw = dict(d_max=d_max, omega=omega, alpha0=alpha0)
-    if name == "fixed":
-        return FixedScheduler(B, cost_model, k, gamma, **kw)
-    if name == "aspire":
-        return AspireScheduler(B, cost_model, k, initial_draft=initial_draft, min_draft=min_draft, **kw)
-    if name == "m1":
-        return M1Scheduler(B, cost_model, k, sla_steps=sla_steps, **kw)
-    if name == "fsm-sync":
-        return SyncFSMScheduler(B, cost_model, k, gamma, **kw)
-    if name == "aspire-fsm":
-        return AspireFSMScheduler(B, cost_model, k, initial_draft=initial_draft, **kw)
-    raise ValueError(f"unknown scheduler {name!r}; known: {SCHEDULERS}")
+                   initial_draft: int = 3, omega: float = 0.8, alpha0: float = 0.9, min_draft: int = 1) -> DraftPolicy:
+    """The policy `name` for B slots at exit layer k (the reference's --sched values)."""
+    return DraftPolicy(name, B, cost_model, k, gamma=gamma, d_max=d_max, sla_steps=sla_steps,
+                       initial_draft=initial_draft, min_draft=min_draft, omega=omega, alpha0=alpha0)

@@ -4,8 +4,8 @@ A shallow-only step (no verification, probe or prefill chunk) issues the same la
 dimensions whenever its shape key repeats: packed tokens, blocks, attention work items, combine groups,
 partial slots, schedule items and slots, drafts and the exit layer.  Only the packed metadata and the index
 arrays change from step to step.  Those live here in per-key device buffers at fixed addresses, refreshed by
-one host-to-device copy per step, so the step's launches (embedding, k layers, exit-state copy, draft head)
-replay as one captured graph.
+one asynchronous host-to-device copy per step from a ring of pinned buffers (no host wait), so the step's
+launches (embedding, k layers, exit-state copy, draft head) replay as one captured graph.
 
 * A key is captured the second time it is seen: the first, eager run sizes every reusable model buffer, so
   the capture allocates only the intermediates it owns (its private memory pool).
@@ -27,7 +27,12 @@ _NP_TO_TORCH = {np.dtype(np.int32): torch.int32, np.dtype(np.int64): torch.int64
 
 
 class _Entry:
-    """Fixed-address staging (pinned host + device) for one shape key, and its graph once captured."""
+    """Fixed-address device staging for one shape key, a ring of pinned host buffers that feed it, and the
+    key's graph once captured.  A host buffer is refilled only after the device has read its previous copy
+    (its event has completed); when every buffer of the ring is still in flight a new one joins the ring, so
+    staging never waits for the device."""
+
+    RING_MAX = 8
 
     def __init__(self, arrays: list, device: torch.device):
         self.offs, total = [], 0
@@ -35,16 +40,37 @@ class _Entry:
             total = (total + _ALIGN - 1) // _ALIGN * _ALIGN
             self.offs.append(total)
             total += a.nbytes
-        self.host = torch.empty(max(total, _ALIGN), dtype=torch.uint8, pin_memory=True)
-        self.dev = torch.empty(max(total, _ALIGN), dtype=torch.uint8, device=device)
-        hv = self.host.numpy()
-        self.host_views = [hv[o:o + a.nbytes].view(a.dtype) for a, o in zip(arrays, self.offs)]
+        self.nbytes = max(total, _ALIGN)
+        self.arrays_meta = [(a.nbytes, a.dtype) for a in arrays]
+        self.dev = torch.empty(self.nbytes, dtype=torch.uint8, device=device)
         self.dev_views = [self.dev[o:o + a.nbytes].view(_NP_TO_TORCH[a.dtype]) for a, o in zip(arrays, self.offs)]
-        self.copied = torch.cuda.Event()      # the last copy out of `host` has been read by the device
-        self.copied.record()
+        self.ring: list = []                  # [(pinned host tensor, numpy views, event of its last copy)]
         self.graph: Optional[torch.cuda.CUDAGraph] = None
         self.epoch = -1
         self.seen = 0
+
+    def _host_slot(self) -> tuple:
+        for slot in self.ring:
+            if slot[2].query():
+                return slot
+        if len(self.ring) < self.RING_MAX:
+            host = torch.empty(self.nbytes, dtype=torch.uint8, pin_memory=True)
+            hv = host.numpy()
+            views = [hv[o:o + n].view(dt) for (n, dt), o in zip(self.arrays_meta, self.offs)]
+            slot = (host, views, torch.cuda.Event())
+            self.ring.append(slot)
+            return slot
+        oldest = self.ring.pop(0)             # RING_MAX copies in flight: wait for the oldest (never seen)
+        oldest[2].synchronize()
+        self.ring.append(oldest)
+        return oldest
+
+    def load(self, arrays: list) -> None:
+        host, views, ev = self._host_slot()
+        for v, a in zip(views, arrays):
+            v[...] = a
+        self.dev.copy_(host, non_blocking=True)
+        ev.record()
 
 
 class ShallowGraphs:
@@ -63,11 +89,7 @@ class ShallowGraphs:
             if len(self.entries) >= self.max_keys:
                 self.entries.pop(next(iter(self.entries)))
             e = self.entries[key] = _Entry(arrays, self.dev)
-        e.copied.synchronize()                # the previous step's copy has left the pinned buffer
-        for v, a in zip(e.host_views, arrays):
-            v[...] = a
-        e.dev.copy_(e.host, non_blocking=True)
-        e.copied.record()
+        e.load(arrays)                        # the device reads the copy in stream order, after the last replay
         return e.dev_views, e
 
     def run(self, e: _Entry, epoch: Callable[[], int], step: Callable[[], None]) -> str:
