@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
                                                         const uint16_t* __restrict__ R, long ldr,
                                                         float* __restrict__ P, float* __restrict__ amax_v,
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
-                                                        int kslice, int n_tiles, int m_tiles) {
+                                                        int kslice, int n_tiles, int m_tiles, int m_lo) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX, "fragment-major A: split-K partial and LM head");
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
     if (tn >= n_tiles) return;  // padding slot of the last group of 8
   }
   const int n0 = tn * 16 * NS;
-  const int m0 = tm * 16 * MS;
+  const int m0 = m_lo + tm * 16 * MS;  // the launch covers rows [m_lo, M) (m_lo: rows a wide-tier launch covered)
   const int s = blockIdx.z;
   const int k0 = s * kslice;
   const int k1 = min(K, k0 + kslice);
@@ -287,7 +287,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
                                                                 const uint16_t* __restrict__ W,
                                                                 uint16_t* __restrict__ C, long ldc,
                                                                 const uint16_t* __restrict__ R, long ldr,
-                                                                float* __restrict__ P, int M, int N, int K, int ffn,
+                                                                float* __restrict__ P, float* __restrict__ amax_v,
+                                                                int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                                 int kslice, int n_tiles, int m_blocks, int n_slices) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int NTH = 64 * NWV;
@@ -418,6 +419,52 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
   }
   while (cls < 4) fold();
   // epilogue: lane holds rows 16 g + 4 lg + i of its token group t, token l16
+  if constexpr (EPI == EPI_ARGMAX) {
+    // per token, the largest bf16-rounded logit of the tile's 64 rows and its first index: each lane scans its 16
+    // rows in increasing order, then the four lanes of the token (lg = 0..3) combine, larger value first and the
+    // smaller index on ties -- the decode kernel's in-order scan over the same rounded values
+#pragma unroll
+    for (int t = 0; t < MSW; ++t) {
+      const int m = mrow[t];
+      float best = -INFINITY;
+      int bi = -1;
+#pragma unroll
+      for (int g = 0; g < NS; ++g) {
+        const int n = n0 + 16 * g + 4 * lg;
+        float v[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = rbf(tot[g][t][i]);
+        if (n < N) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (bi < 0 || v[i] > best) {
+              best = v[i];
+              bi = n + i;
+            }
+          if (C != nullptr && m < M) {
+            uint2 pk;
+            pk.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
+            pk.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
+            *(uint2*)(C + (long)m * ldc + n) = pk;
+          }
+        }
+      }
+#pragma unroll
+      for (int o = 16; o <= 32; o <<= 1) {
+        const float ov = __shfl_xor(best, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        if (oi >= 0 && (bi < 0 || ov > best || (ov == best && oi < bi))) {
+          best = ov;
+          bi = oi;
+        }
+      }
+      if (lg == 0 && m < M) {
+        amax_v[(long)m * n_tiles + tn] = best;
+        amax_i[(long)m * n_tiles + tn] = bi;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < MSW; ++t) {
     const int m = mrow[t];
@@ -615,22 +662,22 @@ static int tile_ns(int n, int M, int epi, int kslice = 0, int ks = 1, int short_
 template <int NS, int MS>
 static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, long ldw,
                         uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
-                        int N, int K, int ffn, int kslice, int nt, int mt) {
+                        int N, int K, int ffn, int kslice, int nt, int mt, int m_lo) {
   if (epi == LSK_EPI_RESIDUAL)
     gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                    ffn, kslice, nt, mt);
+                                                                    ffn, kslice, nt, mt, m_lo);
   else if (epi == LSK_EPI_SILU_MUL) {
     gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
-                                                                      K, ffn, kslice, nt, mt);
+                                                                      K, ffn, kslice, nt, mt, m_lo);
   } else if (epi == EPI_PARTIAL)
     gemm_bf16_kernel<NS, MS, EPI_PARTIAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                               kslice, nt, mt);
+                                                               kslice, nt, mt, m_lo);
   else if (epi == EPI_ARGMAX)
     gemm_bf16_kernel<NS, MS, EPI_ARGMAX><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                              kslice, nt, mt);
+                                                              kslice, nt, mt, m_lo);
   else
     gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                ffn, kslice, nt, mt);
+                                                                ffn, kslice, nt, mt, m_lo);
 }
 
 // Fragment-major activations: split-K partial launches only.
@@ -638,14 +685,14 @@ template <int NS, int MS>
 static void launch_bf16_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, float* P, int M,
                            int N, int K, int kslice, int nt, int mt) {
   gemm_bf16_kernel<NS, MS, EPI_PARTIAL, gemm_unit<NS, MS, EPI_PARTIAL>(), true><<<grid, 256, 0, s>>>(
-      A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt);
+      A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, 0);
 }
 
 // Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).  af: a split-K
 // partial launch with a fragment-major A.
 static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipStream_t s, const void* A, long lda,
                           const void* W, long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av,
-                          int* ai, int M, int N, int K, int ffn, int kslice, bool af = false) {
+                          int* ai, int M, int N, int K, int ffn, int kslice, bool af = false, int m_lo = 0) {
   const dim3 grid(mt > 1 ? (unsigned)(((nt + 7) / 8) * 8 * mt) : (unsigned)nt, 1, (unsigned)ks);
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)W;
@@ -656,7 +703,8 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
     if (af)                                                                                                      \
       launch_bf16_af<NS_, MS_>(grid, s, a, w, ldw, P, M, N, K, kslice, nt, mt);                                  \
     else                                                                                                         \
-      launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt); \
+      launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt, \
+                            m_lo);                                                                               \
   }
   LSK_GEMM_CASE(1, 1) LSK_GEMM_CASE(1, 2) LSK_GEMM_CASE(1, 3) LSK_GEMM_CASE(1, 4)
   LSK_GEMM_CASE(2, 1) LSK_GEMM_CASE(2, 2) LSK_GEMM_CASE(2, 3) LSK_GEMM_CASE(2, 4)
@@ -665,25 +713,34 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 }
 
 // Wide-M tier selection (measured on MI355X at the 8B layer shapes, against the decode kernel's 64-token
-// tiles): a workgroup covers TB = 128 tokens (256 for silu-mul above 128), so the tier runs when M is above
-// 64, its last token block is at least 3/4 full (or the only one) and the launch has >= 192 workgroups;
-// otherwise the finer 64-token tiles of the decode kernel waste less.  Returns false when the decode kernel should run (also for shapes the tier
-// does not cover: N % 64 != 0 or K slices that are not whole 128-k chunks).
-static bool launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
-                        const uint16_t* R, long ldr, float* P, int M, int N, int K, int ffn, int ks) {
+// tiles).  A workgroup covers TB = 128 tokens (256 for silu-mul above 128).  Above 64 tokens the tier covers the
+// full TB-token blocks and the decode kernel the remaining rows when they fit one of its token tiles (<= 64 rows:
+// one more pass over the weights, where another wide block would cost a full block's MFMA work); larger
+// remainders, and M <= TB, go in one partly filled wide block.  The LM head (argmax epilogue) always takes whole
+// blocks: a decode pass over its 1 GB of weights costs more than the empty rows of a block.  The launch needs
+// >= 192 workgroups to stream the weights.  Returns the rows [0, covered) the tier took (0: none; also for shapes
+// it does not cover: N % 64 != 0 or K slices that are not whole 128-k chunks).  Both tiers give bitwise the same
+// sums, so how rows are split between them never changes a result.
+static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
+                       const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks) {
+  if (M <= 64) return 0;
+  if (N % 64 != 0 || (epi != EPI_PARTIAL && C != nullptr && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0)
+    return 0;
   const bool silu = epi == LSK_EPI_SILU_MUL;
   const int tb = (silu && M > 128) ? 256 : 128;
   const int rem = M % tb;
-  if (M <= 64 || !(M <= tb || rem == 0 || 4 * rem >= 3 * tb)) return false;
-  if (N % 64 != 0 || (epi != EPI_PARTIAL && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0) return false;
+  int m_blocks = (M + tb - 1) / tb, covered = M;
+  if (epi != EPI_ARGMAX && M > tb && rem != 0 && rem <= 64) {
+    m_blocks = M / tb;
+    covered = m_blocks * tb;
+  }
   const int n_tiles = N / 64;
-  const int m_blocks = (M + tb - 1) / tb;
-  if ((long)n_tiles * m_blocks * ks < 192) return false;  // too few workgroups to stream the weights
+  if ((long)n_tiles * m_blocks * ks < 192) return 0;
   const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * m_blocks * ks));
   const int kslice = K / ks;
 #define LSK_WIDE(MSW_, EPI_) \
-  gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, M, N, K, ffn, kslice, \
-                                                             n_tiles, m_blocks, ks)
+  gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, \
+                                                             kslice, n_tiles, m_blocks, ks)
   if (silu) {
     if (tb == 256) LSK_WIDE(2, LSK_EPI_SILU_MUL);
     else LSK_WIDE(1, LSK_EPI_SILU_MUL);
@@ -693,11 +750,13 @@ static bool launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, con
     LSK_WIDE(1, LSK_EPI_RESIDUAL);
   } else if (epi == LSK_EPI_NONE) {
     LSK_WIDE(1, LSK_EPI_NONE);
+  } else if (epi == EPI_ARGMAX) {
+    LSK_WIDE(1, EPI_ARGMAX);
   } else {
-    return false;
+    return 0;
   }
 #undef LSK_WIDE
-  return true;
+  return covered;
 }
 
 extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc,
@@ -716,14 +775,18 @@ extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long 
                 "lsk_gemm: bf16 needs K %% 32 == 0, 16-byte aligned A rows and a packed W (ldw == K; K=%d ldw=%ld)", K,
                 ldw);
     LSK_REQUIRE(N % 16 == 0, LSK_ESHAPE, "lsk_gemm: bf16 needs N %% 16 == 0 (N=%d)", N);
-    if (launch_wide(epilogue, s, (const uint16_t*)A, lda, (const uint16_t*)W, (uint16_t*)C, ldc,
-                    (const uint16_t*)R, ldr, nullptr, M, N, K, ffn, 1))
-      return lsk_check_launch("lsk_gemm(bf16, wide)");
-    // whole-K workgroups
-    const int ns = tile_ns(N, M, epilogue);
-    const int ms = ms_for(M);
-    dispatch_bf16(ns, ms, epilogue, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, C, ldc, R, ldr,
-                  nullptr, nullptr, nullptr, M, N, K, ffn, K);
+    const int mw = launch_wide(epilogue, s, (const uint16_t*)A, lda, (const uint16_t*)W, (uint16_t*)C, ldc,
+                               (const uint16_t*)R, ldr, nullptr, nullptr, nullptr, M, N, K, ffn, 1);
+    if (mw > 0) {
+      const int rc = lsk_check_launch("lsk_gemm(bf16, wide)");
+      if (rc || mw == M) return rc;
+    }
+    // whole-K workgroups over rows [mw, M)
+    const int mr = M - mw;
+    const int ns = tile_ns(N, mr, epilogue);
+    const int ms = ms_for(mr);
+    dispatch_bf16(ns, ms, epilogue, N / (16 * ns), (mr + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, C, ldc, R, ldr,
+                  nullptr, nullptr, nullptr, M, N, K, ffn, K, false, mw);
     return lsk_check_launch("lsk_gemm(bf16)");
   }
   if (dtype == LSK_DTYPE_F32) {
@@ -751,13 +814,17 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
                   N % 16 == 0 && lda % 8 == 0,
               LSK_ESHAPE, "lsk_gemm_partial: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
-  if (launch_wide(EPI_PARTIAL, (hipStream_t)stream, (const uint16_t*)A, lda, (const uint16_t*)W, nullptr, 0, nullptr,
-                  0, P, M, N, K, 0, ks))
-    return lsk_check_launch("lsk_gemm_partial(wide)");
-  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks);
-  const int ms = ms_for(M);
-  dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (M + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,
-                ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, K / ks);
+  const int mw = launch_wide(EPI_PARTIAL, (hipStream_t)stream, (const uint16_t*)A, lda, (const uint16_t*)W, nullptr, 0,
+                             nullptr, 0, P, nullptr, nullptr, M, N, K, 0, ks);
+  if (mw > 0) {
+    const int rc = lsk_check_launch("lsk_gemm_partial(wide)");
+    if (rc || mw == M) return rc;
+  }
+  const int mr = M - mw;
+  const int ns = tile_ns(N, mr, EPI_PARTIAL, K / ks, ks);
+  const int ms = ms_for(mr);
+  dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), (mr + 16 * ms - 1) / (16 * ms), ks, (hipStream_t)stream, A, lda, W,
+                ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, K / ks, false, mw);
   return lsk_check_launch("lsk_gemm_partial");
 }
 
@@ -796,9 +863,13 @@ extern "C" int lsk_head_argmax(int dtype, const void* A, long lda, const void* W
               ws_bytes, 2 * half);
   float* av = (float*)workspace;
   int* ai = (int*)((char*)workspace + half);
-  const int ms = ms_for(M);
-  dispatch_bf16(4, ms, EPI_ARGMAX, nt, (M + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, logits, ldl, nullptr, 0,
-                nullptr, av, ai, M, N, K, 0, K);
+  // above 64 rows the wide tier (weights staged in LDS, 128 tokens per workgroup) takes every row
+  if (launch_wide(EPI_ARGMAX, s, (const uint16_t*)A, lda, (const uint16_t*)W, (uint16_t*)logits, ldl, nullptr, 0,
+                  nullptr, av, ai, M, N, K, 0, 1) != M) {
+    const int ms = ms_for(M);
+    dispatch_bf16(4, ms, EPI_ARGMAX, nt, (M + 16 * ms - 1) / (16 * ms), 1, s, A, lda, W, ldw, logits, ldl, nullptr, 0,
+                  nullptr, av, ai, M, N, K, 0, K);
+  }
   int rc = lsk_check_launch("lsk_head_argmax(gemm)");
   if (rc) return rc;
   argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);
@@ -814,7 +885,7 @@ template <int MS>
 static void launch_head_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, uint16_t* C,
                            long ldc, float* av, int* ai, int M, int N, int K, int nt) {
   gemm_bf16_kernel<4, MS, EPI_ARGMAX, gemm_unit<4, MS, EPI_ARGMAX>(), true><<<grid, 256, 0, s>>>(
-      A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, K, nt, 1);
+      A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, K, nt, 1, 0);
 }
 
 // Final norm into the workspace (fragment-major up to LSK_AF_MAX_TOKENS rows), then the head GEMM with its

@@ -565,3 +565,47 @@ def test_probe_matches_equal_the_closed_form(cuda, nc, nblk):
                       dev(blk, torch.int32), dev(jl, torch.int32), nc, nvt, out)
     assert out.cpu().tolist() == want
     assert 0 < want[nc] < nvt
+
+
+@pytest.mark.parametrize("M", [66, 150, 200, 288, 300])
+def test_gemm_wide_tier_and_remainder_are_bitwise_the_decode_kernel(cuda, M):
+    """Above 64 rows the wide tier (weights staged in LDS, 128 / 256 tokens per workgroup) covers the full token
+    blocks and the decode kernel the remaining rows (one partly filled block for larger remainders).  At shapes
+    large enough for the tier (>= 192 workgroups), every epilogue -- plain, residual, silu-mul, split-K partials,
+    LM-head argmax with its logits -- gives bitwise what the decode kernel gives row chunk by row chunk (<= 48 rows,
+    one token tile), so a token's result never depends on the batch it is packed in."""
+    lsk = _lsk()
+    g = _gen(M)
+    K = 512
+    a = torch.randn(M, K, generator=g).to(BF16).to(cuda)
+    w = lsk.PackedWeight(torch.randn(12288, K, generator=g).to(BF16).to(cuda))            # 192 row tiles
+    w13 = lsk.PackedWeight(torch.randn(2 * 14336, K, generator=g).to(BF16).to(cuda))       # 224 row tiles
+    wo = torch.randn(4096, 4096, generator=g).to(BF16)
+    wop = lsk.PackedWeight(wo.to(cuda))
+    a4 = torch.randn(M, 4096, generator=g).to(BF16).to(cuda)
+    r = torch.randn(M, 12288, generator=g).to(BF16).to(cuda)
+    head = torch.randn(16384, K, generator=g).to(BF16)
+    head[9000] = head[77]                                                                   # exact ties
+    headp = lsk.PackedWeight(head.to(cuda))
+    ns, ks = lsk.gemm_plan(4096, 4096)
+    ids_full = torch.empty(M, dtype=torch.long, device=cuda)
+    logit_full = torch.empty(M, 16384, dtype=BF16, device=cuda)
+    lsk.head_argmax(a, headp, ids_full, logits=logit_full)
+    full = {"none": lsk.gemm(a, w), "residual": lsk.gemm(a, w, residual=r, epilogue=lsk.EPI_RESIDUAL),
+            "silu": lsk.gemm(a, w13, epilogue=lsk.EPI_SILU_MUL), "partial": lsk.gemm_partial(a4, wop, ks)}
+    for lo in range(0, M, 48):
+        hi = min(M, lo + 48)
+        sub, sub4 = a[lo:hi].contiguous(), a4[lo:hi].contiguous()
+        assert torch.equal(lsk.gemm(sub, w), full["none"][lo:hi]), ("none", lo)
+        assert torch.equal(lsk.gemm(sub, w, residual=r[lo:hi].contiguous(), epilogue=lsk.EPI_RESIDUAL),
+                           full["residual"][lo:hi]), ("residual", lo)
+        assert torch.equal(lsk.gemm(sub, w13, epilogue=lsk.EPI_SILU_MUL), full["silu"][lo:hi]), ("silu", lo)
+        assert torch.equal(lsk.gemm_partial(sub4, wop, ks), full["partial"][:, lo:hi]), ("partial", lo)
+        ids = torch.empty(hi - lo, dtype=torch.long, device=cuda)
+        lg = torch.empty(hi - lo, 16384, dtype=BF16, device=cuda)
+        lsk.head_argmax(sub, headp, ids, logits=lg)
+        assert torch.equal(ids, ids_full[lo:hi]) and torch.equal(lg, logit_full[lo:hi]), ("head", lo)
+    # and against fp32 arithmetic: logits within bf16 rounding, ids = argmax of the returned logits (first on ties)
+    ref = a.float() @ head.to(cuda).float().t()
+    assert ((logit_full.float() - ref).abs() <= 2.0 ** -7 * ref.abs() + 1e-2).all()
+    assert torch.equal(ids_full, logit_full.float().argmax(-1))
