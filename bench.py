@@ -243,6 +243,44 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     return out
 
 
+def tokens_roofline(cfg, trace: list, k: int, head_tile: int) -> dict:
+    """Generated tokens/s the measured steps would reach if every kernel ran at its roofline: for each step,
+    sum over its launches of t_roof = max(algorithmic bytes / 8 TB/s, flops / 2.5166 PFLOP/s) -- per layer
+    the four projection GEMMs (weights + activations + outputs), attention (the unpadded KV of its blocks read
+    once + Q and O), the two RMSNorms and RoPE + append; per step the LM-head launches (drafts and verify tokens
+    share one when they fit one token tile, as the engine does) -- then committed tokens / total t_roof."""
+    dim, ffn, V = cfg.dim, cfg.intermediate_size, cfg.vocab_size
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    bw, fl = HBM_PEAK_GBS * 1e9, BF16_PEAK_TFLOPS * 1e12
+
+    def gemm(m, n, kk):
+        return max(2.0 * (n * kk + m * kk + m * n) / bw, 2.0 * m * n * kk / fl)
+
+    def layer(blocks):
+        m = sum(b[2] for b in blocks)
+        if m == 0:
+            return 0.0
+        kv = sum(b[1] + b[2] for b in blocks)
+        attn = (kv * kvd * 2 * 2 + m * qd * 2 * 2) / bw
+        small = (2 * 2 * m * dim * 2 + 2 * m * (qd + 2 * kvd) * 2) / bw
+        return gemm(m, qd + 2 * kvd, dim) + gemm(m, dim, qd) + gemm(m, 2 * ffn, dim) + gemm(m, dim, ffn) + attn + small
+
+    total, tokens = 0.0, 0
+    for st in trace:
+        total += k * layer(st["sh"])
+        if st["dp"]:
+            total += (cfg.n_layers - k) * layer(st["dp"])
+        nd, nv = int(st.get("n_draft", 0)), sum(b[2] for b in st["dp"])
+        heads = [nd + nv] if nv and nd + nv <= head_tile else [x for x in (nd, nv) if x]
+        total += sum(gemm(h, V, dim) for h in heads)
+        tokens += st["committed"]
+    return {"tokens_per_s": round(tokens / total, 1) if total > 0 else None, "t_roof_ms": round(1e3 * total, 3),
+            "steps": len(trace), "committed_tokens": tokens,
+            "definition": "committed tokens of the timed steps / sum over their launches of max(bytes / 8 TB/s, "
+                          "flops / 2.5166 PFLOP/s): projection GEMMs, attention (unpadded KV + Q + O), norms, RoPE + "
+                          "append, LM-head launches"}
+
+
 def summarize_kernels(prof: dict) -> dict:
     out = {}
     for name, p in prof.items():
@@ -365,6 +403,8 @@ def run_attention_bench(args):
         "kv_append_us": round(1e3 * t_append, 2), "kv_append_GBs": round(app_bytes / (t_append * 1e-3) / 1e9, 1),
         "rollback_us": round(1e3 * t_rb, 2), "rollback_bytes": int(B * 8),
     }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = attention_cpu_baseline(a, args)
     from thesis_amd.prof_summary import read_traffic
 
     traffic = read_traffic(ATTN_TRAFFIC_SUMMARY, "attention")
@@ -392,6 +432,52 @@ def run_attention_bench(args):
 
 
 # ----------------------------------------------------------------------------- CPU baseline
+
+def attention_cpu_baseline(a, args, every: int = 8) -> dict:
+    """The CPU oracle's verify attention (per-bucket masked SDPA over the cache, the reference's _attend,
+    solutions/packed.py:142-166) on a bounded sample of the microbenchmark -- every `every`-th request with its
+    cache rows, bf16 -- timed on the host cores; GB/s over the sample's algorithmic bytes, and the full
+    256-request layer's time extrapolated by bytes."""
+    from types import SimpleNamespace
+
+    from oracle.model import OBlock, attend, build_packed
+    from thesis_amd import _lsk
+
+    threads, affinity, quota = host_cores()
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    sel = np.arange(0, a.B, every)
+    Hq, Hkv, D = a.Hq, a.Hkv, a.D
+    kc = _lsk.k_from_frag(a.kc[sel].cpu())
+    vc = _lsk.v_from_blocked(a.vc[sel].cpu())
+    qs = torch.cat([a.q[int(a.offs[r]):int(a.offs[r] + a.T[r])].cpu() for r in sel])
+    S = kc.shape[2]
+    model = SimpleNamespace(rope_cos=torch.zeros(S, D), rope_sin=torch.zeros(S, D), dtype=torch.bfloat16,
+                            group=Hq // Hkv, q_size=Hq * D, cfg=SimpleNamespace(n_kv_heads=Hkv, head_dim=D),
+                            cache=SimpleNamespace(max_seq=S, k=[kc], v=[vc]), ordered=False)
+    blocks = [OBlock(j, int(a.ctx[r]), int(a.T[r])) for j, r in enumerate(sel)]
+    times = []
+    with torch.inference_mode():
+        for _ in range(4):
+            t0 = time.perf_counter()
+            pb = build_packed(model, blocks)
+            # q in the packed (bucket) order of pb
+            order = {(b.row, b.pos0): i for i, b in enumerate(blocks)}
+            starts = np.concatenate([[0], np.cumsum([b.T for b in blocks])])
+            q = torch.cat([qs[starts[order[(b.row, b.pos0)]]:starts[order[(b.row, b.pos0)] + 1]] for b in pb.blocks])
+            attend(model, 0, q, pb)
+            times.append(time.perf_counter() - t0)
+    torch.set_num_threads(prev)
+    t = float(np.median(times[1:]))
+    kv = float((a.ctx[sel] + a.T[sel]).sum()) * Hkv * D * 2 * 2 + float(a.T[sel].sum()) * Hq * D * 2 * 2
+    full = float((a.ctx + a.T).sum()) * Hkv * D * 2 * 2 + float(a.N) * Hq * D * 2 * 2
+    return {"value": round(kv / t / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "ms_per_layer_full_workload": round(1e3 * t * full / kv, 2),
+            "sample": f"CPU oracle (torch-CPU per-bucket masked SDPA, bf16) over every {every}th request "
+                      f"({len(sel)} of {a.B}, {kv / 1e9:.3f} GB algorithmic) on {threads} threads (affinity "
+                      f"{affinity}, cgroup quota {quota if quota else 'none'}); median of 3 after one warm-up: "
+                      f"{1e3 * t:.1f} ms; the full layer's time extrapolated by bytes"}
+
 
 def host_cores() -> tuple:
     """(threads to use, CPUs in the affinity mask, cgroup CPU quota or None): the host cores this process may
@@ -538,6 +624,12 @@ def main():
             "classes": {n: {k: replay[n][k] for k in ("launches", "avg_us", "t_roof_us", "frac", "bytes_per_launch",
                                                        "flops_per_launch")} for n in names}}
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
+    from thesis_amd import _lsk as _l
+
+    troof = tokens_roofline(cfg, trace, 8, _l.GEMM_TOKEN_TILE) if trace else None
+    if troof and troof["tokens_per_s"]:
+        troof["measured_tokens_per_s"] = round(committed / elapsed, 2)
+        troof["frac"] = round(committed / elapsed / troof["tokens_per_s"], 4)
 
     line = {
         "metric": METRIC, "value": round(committed / elapsed, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -548,7 +640,8 @@ def main():
                    "scheduler": "aspire (latency-aware)", "acceptance": "forced geometric p=0.3",
                    "cost_model": cost_model_source, "weights": "random init bf16",
                    "parallelism": "single GPU"},
-        "roofline": roofline, "gemm_roofline": gemm_roofline, "cpu_baseline": cpu, "verify_attn": attn,
+        "roofline": roofline, "gemm_roofline": gemm_roofline, "tokens_roofline": troof, "cpu_baseline": cpu,
+        "verify_attn": attn,
         "kernels": kernels,
         "steps_detail": {"committed_tokens": committed, "deep_steps": sum(1 for s in trace if s["dp"]),
                          "mean_shallow_rows": float(np.mean([len(s["sh"]) for s in trace])) if trace else None,

@@ -3,6 +3,7 @@
     python -m thesis_amd.prof_summary trace <prefix>_kernel_trace.csv [--bench bench.json] [--cmd "..."]
     python -m thesis_amd.prof_summary pmc <fetch>_counter_collection.csv <write>_counter_collection.csv
                                           --calib-mib 1024 [--bench bench.json] [--cmd "..."]
+    python -m thesis_amd.prof_summary gemm <probe>_kernel_trace.csv <probe stdout> [<counter CSVs> ...] [--cmd "..."]
 
 Both read the CSV files `rocprofv3 --output-format csv` writes.  Only dispatches after the calibration
 copy are counted: bench.py's --copy-calib-mib issues one plain lsk_copy_rows copy of a known size
@@ -228,6 +229,81 @@ def cmd_pmc(a):
     print("\n" + "\n".join(lines))
 
 
+GEMM_SHAPES = {"qkv": (6144, 4096), "o": (4096, 4096), "w13": (28672, 4096), "w2": (4096, 14336),
+               "head": (128256, 4096)}
+HBM_PEAK = 8.0e12
+BF16_PEAK = 2.5166e15
+
+
+def _probe_groups(rows, seq):
+    """Dispatch ids of the GEMM launches of each (class, M) group of a gemm_probe run: the dispatches after the
+    i-th 64 MiB marker copy belong to seq[i] (the sequence the probe printed)."""
+    out = defaultdict(list)
+    gi = -1
+    for d in sorted(rows):
+        s, gx = rows[d]
+        if s.startswith("copy_rows_kernel") and gx // 256 >= 4096:
+            gi += 1
+            continue
+        if 0 <= gi < len(seq) and s.startswith("gemm_"):
+            out[seq[gi]].append(d)
+    return out
+
+
+def cmd_gemm(a):
+    """MFMA work, roofline fraction and cache behaviour of the projection GEMMs per class and token count."""
+    seq = [(json.loads(l)["class"], json.loads(l)["M"]) for l in Path(a.sequence).read_text().splitlines()
+           if l.startswith("{")]
+    trace = {int(r["Dispatch_Id"]): r for r in _rows(a.trace)}
+    names = {d: (short_name(r["Kernel_Name"]), int(r["Grid_Size_X"])) for d, r in trace.items()}
+    groups = _probe_groups(names, seq)
+    counters = defaultdict(lambda: defaultdict(float))
+    cnames = {}
+    for path in a.counters:
+        for r in _rows(path):
+            d = int(r["Dispatch_Id"])
+            cnames.setdefault(path, {})[d] = (short_name(r["Kernel_Name"]), int(r["Grid_Size"]))
+            counters[(path, d)][r["Counter_Name"]] += float(r["Counter_Value"])
+    per = defaultdict(dict)
+    for path in a.counters:
+        for key, ds in _probe_groups(cnames[path], seq).items():
+            for d in ds:
+                for cn, v in counters[(path, d)].items():
+                    per[key][cn] = per[key].get(cn, 0.0) + v / len(ds)
+    print("# Projection GEMMs of the Llama3-8B layer shapes: MFMA work and roofline by token count\n")
+    print("Commands:\n")
+    for c in a.cmd.split(" ;; "):
+        print(f"    {c}")
+    print()
+    print("Per (class, M): the probe's launches on distinct weights (a GEMM call above 64 rows may be two launches: the "
+          "wide tier on the full token blocks and the decode kernel on the remainder).  t_roof = max(bytes / 8 TB/s, "
+          "flops / 2.5166 PFLOP/s) with bytes = 2 (K N + M K + M N); frac = t_roof / measured.  MFMA flops = "
+          "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 (the counter's unit); MFMA util = MFMA flops / (time x 2.5166 PFLOP/s), "
+          "the share of the dense bf16 peak the launch used.  L2 hit = TCC_HIT / (TCC_HIT + TCC_MISS).\n")
+    print("| class | M | kernel(s) | us per call | t_roof us | bound | frac | MFMA flops / algorithmic | MFMA util | "
+          "TFLOP/s | L2 hit |")
+    print("|---|---|---|---|---|---|---|---|---|---|---|")
+    for key in seq:
+        ds = groups.get(key)
+        if not ds:
+            continue
+        c, M = key
+        N, K = GEMM_SHAPES[c]
+        calls = a.reps
+        us = sum((int(trace[d]["End_Timestamp"]) - int(trace[d]["Start_Timestamp"])) for d in ds) / 1e3 / calls
+        flops = 2.0 * M * N * K
+        t_hbm, t_mfma = 2.0 * (K * N + M * K + M * N) / HBM_PEAK, flops / BF16_PEAK
+        t_roof = max(t_hbm, t_mfma) * 1e6
+        cn = per.get(key, {})
+        mops = cn.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512 * len(ds) / calls
+        hit, miss = cn.get("TCC_HIT_sum", 0.0), cn.get("TCC_MISS_sum", 0.0)
+        kern = sorted({names[d][0] for d in ds})
+        print(f"| {c} | {M} | {'; '.join('`' + k + '`' for k in kern)} | {us:.2f} | {t_roof:.2f} | "
+              f"{'hbm' if t_hbm >= t_mfma else 'mfma'} | {t_roof / us:.3f} | {mops / flops:.3f} | "
+              f"{mops / (us * 1e-6) / BF16_PEAK:.3f} | {flops / (us * 1e-6) / 1e12:.1f} | "
+              f"{hit / max(hit + miss, 1):.2f} |")
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = ap.add_subparsers(dest="mode", required=True)
@@ -246,8 +322,15 @@ def main(argv=None):
     p.add_argument("--cmd")
     p.add_argument("--title")
     p.add_argument("--subject", default="the decode steps")
+    gm = sub.add_parser("gemm")
+    gm.add_argument("trace")
+    gm.add_argument("sequence", help="stdout of the thesis_amd.gemm_probe run (its JSON lines)")
+    gm.add_argument("counters", nargs="*", help="counter_collection CSVs of the same probe sequence")
+    gm.add_argument("--reps", type=int, default=10)
+    gm.add_argument("--cmd", default="")
+    gm.set_defaults(fn=cmd_gemm)
     a = ap.parse_args(argv)
-    (cmd_trace if a.mode == "trace" else cmd_pmc)(a)
+    {"trace": cmd_trace, "pmc": cmd_pmc, "gemm": cmd_gemm}[a.mode](a)
 
 
 def read_traffic(path: Path, cls: str):
