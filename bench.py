@@ -494,8 +494,9 @@ def host_cores() -> tuple:
 
 
 def run_cpu_baseline(args, trace: list, k: int):
-    """The CPU oracle replays the GPU run's first timed steps (same segment shapes, bf16) on the host
-    cores until ~args.cpu_seconds have elapsed; tokens/s = tokens those steps committed / CPU time."""
+    """The CPU oracle replays the GPU run's timed steps (same segment shapes, bf16) on the host cores, in
+    order and again from the first when they run out, until ~args.cpu_seconds have elapsed; tokens/s = tokens
+    the replayed steps committed / CPU time."""
     from oracle.model import OBlock, OracleConfig, OracleLlama, build_packed, packed_layers
     from thesis_amd.common.model import PRESETS
 
@@ -511,8 +512,9 @@ def run_cpu_baseline(args, trace: list, k: int):
     log(f"[bench] CPU oracle model ready in {time.time() - t0:.1f}s ({threads} threads)")
     g = torch.Generator().manual_seed(0)
     spent, tokens, steps, n_deep = 0.0, 0, 0, 0
+    order = [st for _ in range(64) for st in trace]   # the timed steps, cycled (bounded) until the time is spent
     with torch.inference_mode():
-        for st in trace:
+        for st in order:
             ts = time.perf_counter()
             pb = build_packed(m, [OBlock(*b) for b in st["sh"]])
             x = m.embed(torch.randint(0, ocfg.vocab_size, (pb.n_tokens,), generator=g))
@@ -535,9 +537,9 @@ def run_cpu_baseline(args, trace: list, k: int):
     return {"value": round(tokens / spent, 2) if spent > 0 else None, "unit": "tokens/s", "cores": threads,
             "kind": "port",
             "sample": f"CPU oracle (torch-CPU restatement, bf16) on {threads} threads (CPUs in this process's "
-                      f"affinity mask: {affinity}; cgroup CPU quota: {quota if quota else 'none'}) replaying the "
-                      f"first {steps} timed engine steps ({n_deep} deep) of this run with the same packed segment "
-                      f"shapes; {tokens} committed tokens in {spent:.1f}s"}
+                      f"affinity mask: {affinity}; cgroup CPU quota: {quota if quota else 'none'}) replaying {steps} "
+                      f"engine steps ({n_deep} deep; the {len(trace)} timed steps of this run in order, cycled) "
+                      f"with the same packed segment shapes; {tokens} committed tokens in {spent:.1f}s"}
 
 
 # ----------------------------------------------------------------------------- main

@@ -19,15 +19,25 @@ from .engine import ARBatchEngine, DecodeEngine, SyncSpecEngine
 
 @dataclass
 class MethodSpec:
+    """One decoding method as the benchmark driver sees it.
+
+    `add_args(group)` declares the method's command-line options on an argparse group; `build(model, args,
+    batch_size, max_prompt_len, eos)` returns the ready `DecodeEngine`.  The remaining hooks have defaults:
+    `tag(args)` is appended to result file names (for example "-k8-g4"); `supports_sampling` says whether
+    temperature / top-k / top-p apply; `spec_slack` is how many cache positions a request may need past
+    its `max_new` budget (drafts that are later rolled back); `step_tokens(args)` bounds the tokens one
+    request adds in a single step, which sizes the per-step buffers; `params(args)` is the dictionary of
+    method settings stored next to the measured metrics."""
+
     name: str
     description: str
-    add_args: Callable                                   # (argparse group) -> None
-    build: Callable[..., DecodeEngine]                   # (model, args, batch_size, max_prompt_len, eos) -> engine
-    tag: Callable = field(default=lambda args: "")       # file-name tag, e.g. "-k8-g4"
+    add_args: Callable
+    build: Callable[..., DecodeEngine]
+    tag: Callable = field(default=lambda args: "")
     supports_sampling: bool = False
-    spec_slack: int = 0                                  # KV positions per request beyond max_new
-    step_tokens: Callable = field(default=lambda args: 1)  # max tokens per request in one step
-    params: Callable = field(default=lambda args: {})    # method parameters recorded with results
+    spec_slack: int = 0
+    step_tokens: Callable = field(default=lambda args: 1)
+    params: Callable = field(default=lambda args: {})
 
 
 METHODS: dict = {}
