@@ -113,12 +113,14 @@ int lsk_check_launch(const char* what);
 static inline size_t lsk_align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // ----------------------------------------------------------------------------- fragment-major activations
-// The layer loop keeps the GEMM inputs of launches of up to LSK_AF_MAX_TOKENS tokens in the packed weights'
-// fragment-major order: 16-token groups, each 16 x 32 block one 1 KiB fragment in MFMA lane order, so a wave's
-// activation load is one contiguous 1 KiB (8 full cache lines) instead of 16 half lines of 16 token rows.
-// Used where it measured faster: the qkv input (the attention RMSNorm output, 6 % faster qkv launches in the 8B
-// decode steps) and the o input (the attention output).  w13 and w2 read row-major inputs: fragment-major
-// stores of their producers cost more than the loads saved.
+// The layer loop keeps GEMM inputs in the packed weights' fragment-major order: 16-token groups, each 16 x 32
+// block one 1 KiB fragment in MFMA lane order, so a wave's activation load is one contiguous 1 KiB (8 full cache
+// lines) instead of 16 half lines of 16 token rows.  Every row tile of a GEMM re-reads its activations from L2,
+// and there a row-major fragment reads at about a third of the contiguous rate (measured on MI355X: ~9.5 vs
+// ~27 TB/s over all CUs).  Used for the qkv input (the attention RMSNorm output) and the o input (the attention
+// output) at every token count, for the head's normalised rows, and for the w13 input and the w2 input (w13's
+// silu-mul output) above LSK_AF_MAX_TOKENS tokens, where the wide tier's many row tiles re-read them; at up to
+// LSK_AF_MAX_TOKENS tokens those two measured faster row-major (the fragment-major stores cost more there).
 // Element (token r, column c) of a matrix of nks = columns / 32 k-steps sits at lsk_frag_off(r, c, nks).
 // Buffers hold whole 16-token groups; the padding tokens' values only reach discarded output columns.
 // Both layouts hold the same values, so every result is bitwise the same as with row-major activations.
@@ -131,6 +133,9 @@ __host__ __device__ __forceinline__ long lsk_frag_off(int r, int c, int nks) {
 int lsk_add_rmsnorm_impl(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w, float eps,
                          void* x_out, long ldxo, void* out, long ldo, int out_frag, int n_rows, int dim, void* stream);
 int lsk_gemm_partial_af(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream);
+// w13 with silu-mul over a fragment-major A; H row-major ([M, ffn]) or, with h_frag, fragment-major (whole
+// 16-token groups) for the w2 launch.
+int lsk_gemm_silu_af(const void* A, const void* W, void* H, int h_frag, int M, int ffn, int K, void* stream);
 int lsk_ragged_attn_impl(int dtype, const void* q, const void* kcache, const void* vcache, const int32_t* blocks,
                          const int32_t* works, int n_works, const int32_t* groups, int n_groups, int n_parts,
                          const int32_t* recs, int n_rounds, int n_slots, int rows_cap, void* out, int out_frag,

@@ -71,9 +71,11 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
                                                         const uint16_t* __restrict__ R, long ldr,
                                                         float* __restrict__ P, float* __restrict__ amax_v,
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
-                                                        int kslice, int n_tiles, int m_tiles, int m_lo) {
+                                                        int kslice, int n_tiles, int m_tiles, int m_lo,
+                                                        int c_nks) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
-  static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX, "fragment-major A: split-K partial and LM head");
+  static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL,
+                "fragment-major A: split-K partial, silu-mul and LM head");
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
 
@@ -110,7 +112,9 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
 #pragma unroll
   for (int t = 0; t < MS; ++t) {
     if constexpr (AF) {
-      arow[t] = A + ((long)(m0 / 16 + t) * nks + (k0 >> 5)) * 512 + 8 * lane;  // k-step j at + j * 512
+      // whole 16-token groups up to (M + 15) / 16; groups past it (last token tile) read the last one
+      const int grp = min(m0 / 16 + t, (M + 15) / 16 - 1);
+      arow[t] = A + ((long)grp * nks + (k0 >> 5)) * 512 + 8 * lane;  // k-step j at + j * 512
     } else {
       int m = m0 + 16 * t + l16;
       m = m < M - 1 ? m : M - 1;
@@ -227,9 +231,10 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
       }
     }
     return;
-  } else if (EPI == LSK_EPI_SILU_MUL && NS >= 2 && N % 8 == 0 && ldc % 8 == 0) {
+  } else if (EPI == LSK_EPI_SILU_MUL && NS >= 2 && N % 8 == 0 && (ldc % 8 == 0 || c_nks > 0)) {
     // 8 outputs per lane, one 16-byte store: a wave covers 16 tokens x 32 columns per pass (lane l: token
-    // 16 g + l % 16, columns 32 c + 8 (l / 16) .. +7), 8x fewer stores than one element per lane
+    // 16 g + l % 16, columns 32 c + 8 (l / 16) .. +7), 8x fewer stores than one element per lane.  c_nks > 0:
+    // C is fragment-major (the w2 launch's A operand); the 8 columns are one 16-byte slice of a fragment there.
     constexpr int FC = TN / 32;
     const int wv = tid >> 6;
     for (int f = wv; f < MS * FC; f += 4) {
@@ -244,7 +249,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
         const float o1 = rbf(silu_f(rbf(reduced(a0, ml, w0 + 1)))) * rbf(reduced(a0 + NS, ml, w0 + 1));
         pk[i >> 1] = (uint32_t)f2bf(o0) | ((uint32_t)f2bf(o1) << 16);
       }
-      *(uint4*)(C + (long)m * ldc + n) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      *(uint4*)(C + (c_nks > 0 ? lsk_frag_off(m, n, c_nks) : (long)m * ldc + n)) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
     }
   } else {
     for (int o = tid; o < TN * TM; o += 256) {
@@ -264,7 +269,7 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
         } else {
           outv = v;
         }
-        C[(long)m * ldc + n] = f2bf(outv);
+        C[c_nks > 0 ? lsk_frag_off(m, n, c_nks) : (long)m * ldc + n] = f2bf(outv);
       }
     }
   }
@@ -282,14 +287,15 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
 // so every output sees the same MFMA sequence and the same three adds: results are bitwise those of the
 // decode kernel, which keeps the batch invariance of the GEMM.  Covered shapes (launch_wide): N % 64 == 0 and
 // K slices of whole 128-k chunks (no tail k-steps).
-template <int NS, int MSW, int EPI, int NWV, int PF>
+template <int NS, int MSW, int EPI, int NWV, int PF, bool AF = false>
 __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* __restrict__ A, long lda,
                                                                 const uint16_t* __restrict__ W,
                                                                 uint16_t* __restrict__ C, long ldc,
                                                                 const uint16_t* __restrict__ R, long ldr,
                                                                 float* __restrict__ P, float* __restrict__ amax_v,
                                                                 int* __restrict__ amax_i, int M, int N, int K, int ffn,
-                                                                int kslice, int n_tiles, int m_blocks, int n_slices) {
+                                                                int kslice, int n_tiles, int m_blocks, int n_slices,
+                                                                int c_nks) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int NTH = 64 * NWV;
   constexpr int CHUNK_E = NT * 4 * 512;  // bf16 elements of one staged chunk (NT row groups x 4 k-steps)
@@ -328,7 +334,13 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
   for (int t = 0; t < MSW; ++t) {
     const int m = mb * TB + (wave * MSW + t) * 16 + l16;
     mrow[t] = m;
-    arow[t] = A + (long)(m < M - 1 ? m : M - 1) * lda + k0 + 8 * lg;
+    if constexpr (AF) {
+      // fragment-major A holds whole 16-token groups up to (M + 15) / 16; groups past it read the last one
+      const int grp = min(mb * TB / 16 + wave * MSW + t, (M + 15) / 16 - 1);
+      arow[t] = A + ((long)grp * nks + (k0 >> 5)) * 512 + 8 * lane;
+    } else {
+      arow[t] = A + (long)(m < M - 1 ? m : M - 1) * lda + k0 + 8 * lg;
+    }
   }
   lsk_f32x4 cur[NT][MSW], tot[NT][MSW];
 #pragma unroll
@@ -358,7 +370,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int t = 0; t < MSW; ++t) a[ks][t] = *(const lsk_bf16x8*)(arow[t] + c * 128 + ks * 32);
+      for (int t = 0; t < MSW; ++t)
+        a[ks][t] = *(const lsk_bf16x8*)(arow[t] + (AF ? (long)(c * 4 + ks) * 512 : (long)(c * 128 + ks * 32)));
   };
   auto comp = [&](const lsk_bf16x8 (&a)[4][MSW], int b) {
 #pragma unroll
@@ -493,7 +506,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
         uint2 pk;
         pk.x = (uint32_t)o[0] | ((uint32_t)o[1] << 16);
         pk.y = (uint32_t)o[2] | ((uint32_t)o[3] << 16);
-        *(uint2*)(C + (long)m * ldc + n) = pk;
+        // c_nks > 0: fragment-major C; columns n .. n + 3 (n % 4 == 0) stay within one 8-column slice
+        *(uint2*)(C + (c_nks > 0 ? lsk_frag_off(m, n, c_nks) : (long)m * ldc + n)) = pk;
       }
     }
   }
@@ -665,34 +679,44 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
                         int N, int K, int ffn, int kslice, int nt, int mt, int m_lo) {
   if (epi == LSK_EPI_RESIDUAL)
     gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                    ffn, kslice, nt, mt, m_lo);
+                                                                    ffn, kslice, nt, mt, m_lo, 0);
   else if (epi == LSK_EPI_SILU_MUL) {
     gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
-                                                                      K, ffn, kslice, nt, mt, m_lo);
+                                                                      K, ffn, kslice, nt, mt, m_lo, 0);
   } else if (epi == EPI_PARTIAL)
     gemm_bf16_kernel<NS, MS, EPI_PARTIAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                               kslice, nt, mt, m_lo);
+                                                               kslice, nt, mt, m_lo, 0);
   else if (epi == EPI_ARGMAX)
     gemm_bf16_kernel<NS, MS, EPI_ARGMAX><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                              kslice, nt, mt, m_lo);
+                                                              kslice, nt, mt, m_lo, 0);
   else
     gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                ffn, kslice, nt, mt, m_lo);
+                                                                ffn, kslice, nt, mt, m_lo, 0);
 }
 
 // Fragment-major activations: split-K partial launches only.
+// Fragment-major A: split-K partials, silu-mul (C row-major, or fragment-major with c_nks > 0) and the LM head.
 template <int NS, int MS>
-static void launch_bf16_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, float* P, int M,
-                           int N, int K, int kslice, int nt, int mt) {
-  gemm_bf16_kernel<NS, MS, EPI_PARTIAL, gemm_unit<NS, MS, EPI_PARTIAL>(), true><<<grid, 256, 0, s>>>(
-      A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, 0);
+static void launch_bf16_af(int epi, dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw,
+                           uint16_t* C, long ldc, int c_nks, float* P, float* av, int* ai, int M, int N, int K, int ffn,
+                           int kslice, int nt, int mt, int m_lo) {
+  if (epi == LSK_EPI_SILU_MUL)
+    gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL, gemm_unit<NS, MS, LSK_EPI_SILU_MUL>(), true><<<grid, 256, 0, s>>>(
+        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, nullptr, nullptr, M, N, K, ffn, kslice, nt, mt, m_lo, c_nks);
+  else if (epi == EPI_ARGMAX)
+    gemm_bf16_kernel<NS, MS, EPI_ARGMAX, gemm_unit<NS, MS, EPI_ARGMAX>(), true><<<grid, 256, 0, s>>>(
+        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, kslice, nt, mt, m_lo, 0);
+  else
+    gemm_bf16_kernel<NS, MS, EPI_PARTIAL, gemm_unit<NS, MS, EPI_PARTIAL>(), true><<<grid, 256, 0, s>>>(
+        A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, m_lo, 0);
 }
 
 // Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).  af: a split-K
 // partial launch with a fragment-major A.
 static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipStream_t s, const void* A, long lda,
                           const void* W, long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av,
-                          int* ai, int M, int N, int K, int ffn, int kslice, bool af = false, int m_lo = 0) {
+                          int* ai, int M, int N, int K, int ffn, int kslice, bool af = false, int m_lo = 0,
+                          int c_nks = 0) {
   const dim3 grid(mt > 1 ? (unsigned)(((nt + 7) / 8) * 8 * mt) : (unsigned)nt, 1, (unsigned)ks);
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)W;
@@ -701,7 +725,7 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 #define LSK_GEMM_CASE(NS_, MS_)                                                                                  \
   if (ns == NS_ && ms == MS_) {                                                                                  \
     if (af)                                                                                                      \
-      launch_bf16_af<NS_, MS_>(grid, s, a, w, ldw, P, M, N, K, kslice, nt, mt);                                  \
+      launch_bf16_af<NS_, MS_>(epi, grid, s, a, w, ldw, c, ldc, c_nks, P, av, ai, M, N, K, ffn, kslice, nt, mt, m_lo); \
     else                                                                                                         \
       launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt, \
                             m_lo);                                                                               \
@@ -722,7 +746,8 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 // it does not cover: N % 64 != 0 or K slices that are not whole 128-k chunks).  Both tiers give bitwise the same
 // sums, so how rows are split between them never changes a result.
 static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
-                       const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks) {
+                       const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks,
+                       bool af = false, int c_nks = 0) {
   if (M <= 64) return 0;
   if (N % 64 != 0 || (epi != EPI_PARTIAL && C != nullptr && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0)
     return 0;
@@ -738,17 +763,23 @@ static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, cons
   if ((long)n_tiles * m_blocks * ks < 192) return 0;
   const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * m_blocks * ks));
   const int kslice = K / ks;
-#define LSK_WIDE(MSW_, EPI_) \
-  gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, \
-                                                             kslice, n_tiles, m_blocks, ks)
+#define LSK_WIDE(MSW_, EPI_)                                                                                   \
+  do {                                                                                                          \
+    if (af)                                                                                                     \
+      gemm_wide_kernel<4, MSW_, EPI_, 8, 2, true><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, \
+                                                                      K, ffn, kslice, n_tiles, m_blocks, ks, c_nks); \
+    else                                                                                                        \
+      gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, \
+                                                                 ffn, kslice, n_tiles, m_blocks, ks, 0);        \
+  } while (0)
   if (silu) {
     if (tb == 256) LSK_WIDE(2, LSK_EPI_SILU_MUL);
     else LSK_WIDE(1, LSK_EPI_SILU_MUL);
   } else if (epi == EPI_PARTIAL) {
     LSK_WIDE(1, EPI_PARTIAL);
-  } else if (epi == LSK_EPI_RESIDUAL) {
+  } else if (epi == LSK_EPI_RESIDUAL && !af) {
     LSK_WIDE(1, LSK_EPI_RESIDUAL);
-  } else if (epi == LSK_EPI_NONE) {
+  } else if (epi == LSK_EPI_NONE && !af) {
     LSK_WIDE(1, LSK_EPI_NONE);
   } else if (epi == EPI_ARGMAX) {
     LSK_WIDE(1, EPI_ARGMAX);
@@ -828,17 +859,38 @@ extern "C" int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw
   return lsk_check_launch("lsk_gemm_partial");
 }
 
+// Fragment-major A (lsk_frag_off, whole 16-token groups): above 64 rows the wide tier takes its full token blocks
+// and the decode kernel the rest, exactly as lsk_gemm / lsk_gemm_partial / lsk_head_argmax split a row-major A,
+// with the same tiles (so the same sums).  c_nks > 0 (silu-mul): C fragment-major too.
+static void gemm_af(int epi, hipStream_t s, const void* A, const void* W, void* C, long ldc, int c_nks, float* P,
+                    float* av, int* ai, int M, int N, int K, int ffn, int ks) {
+  const int mw = launch_wide(epi, s, (const uint16_t*)A, 0, (const uint16_t*)W, (uint16_t*)C, ldc, nullptr, 0, P, av,
+                             ai, M, N, K, ffn, ks, true, c_nks);
+  if (mw == M) return;
+  const int mr = M - mw;
+  const int ms = ms_for(mr);
+  const int ns = epi == EPI_PARTIAL ? tile_ns(N, mr, EPI_PARTIAL, K / ks, ks, 48) : (epi == EPI_ARGMAX ? 4 : tile_ns(N, mr, epi));
+  dispatch_bf16(ns, ms, epi, N / (16 * ns), (mr + 16 * ms - 1) / (16 * ms), ks, s, A, 0, W, K, C, ldc, nullptr, 0, P,
+                av, ai, M, N, K, ffn, K / ks, true, mw, c_nks);
+}
+
 int lsk_gemm_partial_af(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream) {
   LSK_REQUIRE(A && W && P, LSK_EARG, "lsk_gemm_partial_af: null pointer");
-  LSK_REQUIRE(M >= 0 && M <= LSK_AF_MAX_TOKENS && N > 0 && N % 16 == 0 && K > 0 && ks >= 1 && K % ks == 0 &&
-                  (K / ks) % 32 == 0,
-              LSK_ESHAPE, "lsk_gemm_partial_af: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
+  LSK_REQUIRE(M >= 0 && N > 0 && N % 16 == 0 && K > 0 && ks >= 1 && K % ks == 0 && (K / ks) % 32 == 0, LSK_ESHAPE,
+              "lsk_gemm_partial_af: bad shape M=%d N=%d K=%d ks=%d", M, N, K, ks);
   if (M == 0) return 0;
-  const int ns = tile_ns(N, M, EPI_PARTIAL, K / ks, ks, 48);
-  const int ms = ms_for(M);
-  dispatch_bf16(ns, ms, EPI_PARTIAL, N / (16 * ns), 1, ks, (hipStream_t)stream, A, 0, W, K, nullptr, 0, nullptr, 0, P,
-                nullptr, nullptr, M, N, K, 0, K / ks, true);
+  gemm_af(EPI_PARTIAL, (hipStream_t)stream, A, W, nullptr, 0, 0, P, nullptr, nullptr, M, N, K, 0, ks);
   return lsk_check_launch("lsk_gemm_partial_af");
+}
+
+int lsk_gemm_silu_af(const void* A, const void* W, void* H, int h_frag, int M, int ffn, int K, void* stream) {
+  LSK_REQUIRE(A && W && H, LSK_EARG, "lsk_gemm_silu_af: null pointer");
+  LSK_REQUIRE(M >= 0 && ffn > 0 && ffn % 32 == 0 && K > 0 && K % 32 == 0, LSK_ESHAPE,
+              "lsk_gemm_silu_af: bad shape M=%d ffn=%d K=%d", M, ffn, K);
+  if (M == 0) return 0;
+  gemm_af(LSK_EPI_SILU_MUL, (hipStream_t)stream, A, W, H, ffn, h_frag ? ffn / 32 : 0, nullptr, nullptr, nullptr, M,
+          ffn, K, ffn, 1);
+  return lsk_check_launch("lsk_gemm_silu_af");
 }
 
 extern "C" size_t lsk_head_workspace_bytes(int M, int N) {
@@ -881,15 +933,8 @@ extern "C" size_t lsk_head_norm_workspace_bytes(int M, int N, int K) {
   return lsk_align_up(m16 * (size_t)K * 2, 256) + lsk_head_workspace_bytes(M, N);
 }
 
-template <int MS>
-static void launch_head_af(dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw, uint16_t* C,
-                           long ldc, float* av, int* ai, int M, int N, int K, int nt) {
-  gemm_bf16_kernel<4, MS, EPI_ARGMAX, gemm_unit<4, MS, EPI_ARGMAX>(), true><<<grid, 256, 0, s>>>(
-      A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, K, nt, 1, 0);
-}
-
-// Final norm into the workspace (fragment-major up to LSK_AF_MAX_TOKENS rows), then the head GEMM with its
-// per-tile argmax and the pick, as lsk_head_argmax.
+// Final norm into the workspace (fragment-major), then the head GEMM with its per-tile argmax and the pick, as
+// lsk_head_argmax.
 extern "C" int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const void* norm_w, float eps, const void* W,
                                     long ldw, int M, int N, int K, void* logits, long ldl, int64_t* out,
                                     const int64_t* dst_idx, void* workspace, size_t ws_bytes, void* stream) {
@@ -906,25 +951,14 @@ extern "C" int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const vo
   const size_t xn_bytes = lsk_align_up((size_t)(M + 15) / 16 * 16 * (size_t)K * 2, 256);
   uint16_t* xn = (uint16_t*)workspace;
   char* hw = (char*)workspace + xn_bytes;
-  const bool af = M <= LSK_AF_MAX_TOKENS;
-  int rc = lsk_add_rmsnorm_impl(dtype, h, ldh, nullptr, 0, norm_w, eps, nullptr, 0, xn, K, af ? 1 : 0, M, K, stream);
+  int rc = lsk_add_rmsnorm_impl(dtype, h, ldh, nullptr, 0, norm_w, eps, nullptr, 0, xn, K, 1, M, K, stream);
   if (rc) return rc;
-  if (!af)
-    return lsk_head_argmax(dtype, xn, K, W, ldw, M, N, K, logits, ldl, out, dst_idx, hw, ws_bytes - xn_bytes, stream);
   hipStream_t s = (hipStream_t)stream;
   const int nt = N / 64;
   const size_t half = lsk_align_up((size_t)M * nt * 4, 256);
   float* av = (float*)hw;
   int* ai = (int*)(hw + half);
-  const dim3 grid((unsigned)nt);
-  const uint16_t* w = (const uint16_t*)W;
-  uint16_t* c = (uint16_t*)logits;
-  switch (ms_for(M)) {  // one token tile: 16 * MS >= M
-    case 1: launch_head_af<1>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
-    case 2: launch_head_af<2>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
-    case 3: launch_head_af<3>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
-    default: launch_head_af<4>(grid, s, xn, w, ldw, c, ldl, av, ai, M, N, K, nt); break;
-  }
+  gemm_af(EPI_ARGMAX, s, xn, W, logits, ldl, 0, nullptr, av, ai, M, N, K, 0, 1);
   rc = lsk_check_launch("lsk_head_norm_argmax(gemm)");
   if (rc) return rc;
   argmax_tiles_kernel<<<M, 256, 0, s>>>(av, ai, nt, out, dst_idx);

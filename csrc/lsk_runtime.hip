@@ -84,7 +84,7 @@ Layout layout(const Model& m, int N, int n_parts) {
   L.qkv = take((size_t)N * (qd + 2 * kvd) * es);
   L.q = take((size_t)N * qd * es);
   L.attn = take(n16 * qd * es);
-  L.h = take((size_t)N * m.ffn * es);
+  L.h = take(n16 * m.ffn * es);  // whole 16-token groups (fragment-major above LSK_AF_MAX_TOKENS)
   L.part = take(n_parts > 0 ? lsk_attn_workspace_bytes(n_parts, m.n_kv_heads, m.head_dim) : 0);
   size_t gp = 0;
   if (m.dtype == LSK_DTYPE_BF16) {
@@ -234,10 +234,14 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
     // kernel reduces in slice order (RoPE + append; add + RMSNorm, which also materialises the residual
     // stream x).  Same rounding points as the unfused sequence.
     float* P = (float*)(ws + L.gpart);
-    // up to LSK_AF_MAX_TOKENS tokens, the qkv input (attention RMSNorm output) and the o input (attention
-    // output) are kept fragment-major
-    const int af = N <= LSK_AF_MAX_TOKENS && m->dim % 32 == 0;
-    const int af_o = N <= LSK_AF_MAX_TOKENS && qd % 32 == 0;
+    // GEMM inputs kept fragment-major (1 KiB contiguous per MFMA fragment; every row tile re-reads them from
+    // L2, where a row-major fragment -- 16 rows x 64 bytes -- reads at a third of the rate): the qkv input
+    // (attention RMSNorm output) and the o input (attention output) always; the w13 input (MLP RMSNorm output)
+    // and the w2 input (w13's silu-mul output) above LSK_AF_MAX_TOKENS tokens, where the wide tier re-reads
+    // them (at up to 64 tokens row-major measured faster for those two).
+    const int af = m->dim % 32 == 0;
+    const int af_o = qd % 32 == 0;
+    const int af_h = N > LSK_AF_MAX_TOKENS && m->dim % 32 == 0 && m->ffn % 64 == 0;
     const double norm_bytes_b = es_d * (2.0 * Nd * dimd + dimd);
     auto pbytes = [&](int ks, double width) { return 4.0 * ks * Nd * width; };
 #define LSK_PROF2(cls, b, f, call)                               \
@@ -277,12 +281,14 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
       const void* xi = (i == start) ? x_in : x_out;
       LSK_PROF2(LSK_PROF_NORM, norm_bytes_b + es_d * Nd * dimd + pbytes(m->ks_o, dimd), 4.0 * Nd * dimd,
                 lsk_add_rmsnorm_impl(m->dtype, xi, m->dim, P, m->ks_o, m->ffn_norm[i], m->eps, x_out, m->dim, xn,
-                                     m->dim, 0, N, m->dim, stream));
+                                     m->dim, af_h, N, m->dim, stream));
       LSK_PROF2(LSK_PROF_GEMM_W13, es_d * (2.0 * ffd * dimd + Nd * dimd + Nd * ffd), 4.0 * Nd * dimd * ffd,
-                lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
-                         LSK_EPI_SILU_MUL, m->ffn, stream));
+                af_h ? lsk_gemm_silu_af(xn, m->w13[i], h, 1, N, m->ffn, m->dim, stream)
+                     : lsk_gemm(m->dtype, xn, m->dim, m->w13[i], m->dim, h, m->ffn, nullptr, 0, N, m->ffn, m->dim,
+                                LSK_EPI_SILU_MUL, m->ffn, stream));
       LSK_PROF2(LSK_PROF_GEMM_W2, es_d * (dimd * ffd + Nd * ffd) + pbytes(m->ks_w2, dimd), 2.0 * Nd * ffd * dimd,
-                lsk_gemm_partial(h, m->ffn, m->w2[i], m->ffn, P, N, m->dim, m->ffn, m->ks_w2, stream));
+                af_h ? lsk_gemm_partial_af(h, m->w2[i], P, N, m->dim, m->ffn, m->ks_w2, stream)
+                     : lsk_gemm_partial(h, m->ffn, m->w2[i], m->ffn, P, N, m->dim, m->ffn, m->ks_w2, stream));
     }
     LSK_PROF2(LSK_PROF_NORM, 2.0 * es_d * Nd * dimd + pbytes(m->ks_w2, dimd), Nd * dimd,
               lsk_add_rmsnorm(m->dtype, x_out, m->dim, P, m->ks_w2, nullptr, m->eps, x_out, m->dim, nullptr, 0, N,
