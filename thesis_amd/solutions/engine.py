@@ -333,6 +333,10 @@ class EESDEngine:
         self._tally(committed, deep=True, n_deep=len(slots), verifiers=len(slots))
         return committed, done
 
+    def _verify_set(self, d, ctx, dec) -> np.ndarray:
+        V = self.sched.decide(d, ctx, dec, self.steps_since_deep) if dec.any() else np.zeros(self.B, dtype=bool)
+        return (V | (dec & (d >= self.cfg.d_max))) & dec & (d >= 1)
+
     def _spec_step(self):
         m, cfg, k = self.m, self.cfg, self.k
         Dm1 = self.Dm1
@@ -340,8 +344,14 @@ class EESDEngine:
         dec = self.state == DECODE
         d = self.d.copy()
         ctx = np.where(dec, self.pos + d, 0)
-        V = self.sched.decide(d, ctx, dec, self.steps_since_deep) if dec.any() else np.zeros(self.B, dtype=bool)
-        V = (V | (dec & (d >= cfg.d_max))) & dec & (d >= 1)
+        if self.m3 is None and self.exitc is None and dec.any():
+            return self._spec_step_early(dec, d, ctx, t0)
+        return self._spec_step_general(dec, d, ctx, t0)
+
+    def _spec_step_general(self, dec, d, ctx, t0):
+        m, cfg, k = self.m, self.cfg, self.k
+        Dm1 = self.Dm1
+        V = self._verify_set(d, ctx, dec)
         # M3 progress guarantee: with no decoding slot, pending prompts run both segments in this step
         flush = (not dec.any()) and bool((self.state == PREFILL).any())
         deep = bool(V.any()) or flush
@@ -436,6 +446,63 @@ class EESDEngine:
             _lsk.copy_rows(exh, ex_dst_t, h, ex_src_t, nex)               # exit_h[i, d_i] (all j of a probe) = h
         for (i, p, c, s0) in chunk_slices:
             self.pending[i].append((p, c, h[s0:s0 + c]))                  # layer-k states wait for the deep segment
+        return self._finish_step(V, d, deep, probe, chunks, h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, kb,
+                                 sb_slot, cap_sh, N, Dr)
+
+    def _spec_step_early(self, dec, d, ctx, t0):
+        """Steps without M2 probes or M3 chunks: the shallow segment (one token at pos + d per decoding slot,
+        whatever the verify set) is staged and launched first -- replayed as a graph when its shape repeats --
+        and the draft policy's host time overlaps it on the device.  Then the draft head and the deep segment
+        follow as in any step; every launch is the one the general path makes, in the same stream order."""
+        m, cfg, k, Dm1 = self.m, self.cfg, self.k, self.Dm1
+        dslots = np.flatnonzero(dec)
+        pb = build_packed_arrays(m, dslots, self.pos[dslots] + d[dslots], np.ones(len(dslots), dtype=np.int64),
+                                 cfg.bucketing, upload_meta=False)
+        N = pb.n_tokens
+        sl = dslots[pb.order]
+        sel = sl * Dm1 + d[sl]
+        self._count_kv(pb, k)
+        sb, exh = self._flat()
+        span = DeviceSpan(self.dev).open()
+        if self.graphs is not None and not _lsk.Profiler.enabled:
+            gkey = ("early", N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_rounds, pb.n_slots, pb.rows_cap, k)
+            (pb.meta, sel_t), gentry = self.graphs.stage(gkey, [pb.meta_host, sel])
+
+            def shallow_gpu():
+                xg = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+                _lsk.embed(m.embed_w, sel_t, xg, sb, sel_t)
+                hg = packed_layers(m, xg, pb, 0, k)
+                _lsk.copy_rows(exh, sel_t, hg, None, N)                  # exit_h[i, d_i] = h
+                return hg
+            self.graphs.run(gentry, lambda: m.buf_epoch, shallow_gpu)
+            h = gentry.out
+        else:
+            pb.meta, sel_t = upload_many([pb.meta_host, sel], self.dev)
+            x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+            _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
+            h = packed_layers(m, x, pb, 0, k)
+            _lsk.copy_rows(exh, sel_t, h, None, N)
+        t1 = time.perf_counter()
+        plan_ms = 1000 * (t1 - t0)
+        V = self._verify_set(d, ctx, dec)
+        deep = bool(V.any())
+        Dr = dec & ~V
+        drf_src = np.flatnonzero(Dr[sl])
+        drf_dst = sel[drf_src] + 1
+        nd = len(drf_src)
+        drf_src_t = drf_dst_t = None
+        if nd:
+            drf_src_t, drf_dst_t = upload_many([drf_src, drf_dst], self.dev)
+        plan_ms += 1000 * (time.perf_counter() - t1)
+        return self._finish_step(V, d, deep, False, [], h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, None, None,
+                                 None, N, Dr)
+
+    def _finish_step(self, V, d, deep, probe, chunks, h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, kb, sb_slot,
+                     cap_sh, N, Dr):
+        """After the shallow segment: the draft head, the deep segment with the step's LM-head launch and
+        greedy acceptance, the readback and the host bookkeeping."""
+        m = self.m
+        sb, _ = self._flat()
         n_verify = int((d[V] + 1).sum()) if deep else 0
         merge_heads = deep and not probe and nd + n_verify <= _lsk.GEMM_TOKEN_TILE
         if nd and not merge_heads:

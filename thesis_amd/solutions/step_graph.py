@@ -46,6 +46,7 @@ class _Entry:
         self.dev_views = [self.dev[o:o + a.nbytes].view(_NP_TO_TORCH[a.dtype]) for a, o in zip(arrays, self.offs)]
         self.ring: list = []                  # [(pinned host tensor, numpy views, event of its last copy)]
         self.graph: Optional[torch.cuda.CUDAGraph] = None
+        self.out = None                       # the step's result (graph memory once captured)
         self.epoch = -1
         self.seen = 0
 
@@ -92,9 +93,10 @@ class ShallowGraphs:
         e.load(arrays)                        # the device reads the copy in stream order, after the last replay
         return e.dev_views, e
 
-    def run(self, e: _Entry, epoch: Callable[[], int], step: Callable[[], None]) -> str:
+    def run(self, e: _Entry, epoch: Callable[[], int], step: Callable[[], object]) -> str:
         """Run one step of entry `e`: replay its graph, capture it (second sighting) or run it eagerly.
-        `epoch()` reads the model's buffer epoch.  Returns "replay", "capture" or "eager"."""
+        `epoch()` reads the model's buffer epoch.  Returns "replay", "capture" or "eager"; `e.out` is what
+        `step()` returned (for a replay: the captured run's result, whose memory the replay rewrites)."""
         if e.graph is not None and e.epoch != epoch():
             e.graph, e.seen = None, 0         # a buffer it writes or reads was reallocated
         if e.graph is not None:
@@ -103,16 +105,16 @@ class ShallowGraphs:
             return "replay"
         e.seen += 1
         if e.seen < 2:
-            step()
+            e.out = step()
             return "eager"
         before = epoch()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            step()
+            out = step()
         if epoch() != before:                 # the capture allocated a model buffer: never replay it
-            step()
+            e.out = step()
             return "eager"
-        e.graph, e.epoch = g, before
+        e.graph, e.epoch, e.out = g, before, out
         self.captures += 1
         g.replay()
         self.replays += 1
