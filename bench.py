@@ -149,9 +149,10 @@ def run_main(args):
 
 def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     """Average launch duration of each projection GEMM class (qkv, o and w2 as split-K partial launches, w13 =
-    [gate; up] with the silu-mul epilogue) over the launches the first `n_steps` timed steps made: the same
-    token counts (shallow segment through layers [0, k), deep segment through [k, L)) and each layer's own
-    weights, a class's launches issued back to back on the engine's stream between one pair of HIP events.
+    [gate; up] with the silu-mul epilogue, the LM head with its per-tile argmax) over the launches the first
+    `n_steps` timed steps made: the same token counts (shallow segment through layers [0, k), deep segment
+    through [k, L)), each layer's own weights and the activation layouts the layer loop uses, a class's launches
+    issued back to back on the engine's stream between one pair of HIP events.
     Events around every single launch would add their own dispatch overhead (a few microseconds) to each.
     Per class: algorithmic bytes (weights + activations + outputs, fp32 partials for the split-K classes) and
     flops per launch, and t_roof = max(bytes / HBM peak, flops / bf16 MFMA peak)."""
@@ -194,26 +195,46 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     if x.shape[0] < m_max:
         x = torch.empty(m_max, x.shape[1], dtype=model.dtype, device=model.device).normal_(generator=g)
     ids = torch.empty(m_max, dtype=torch.long, device=model.device)
-    head_ws = torch.empty(int(_lsk.load().lsk_head_workspace_bytes(m_max, c.vocab_size)), dtype=torch.uint8,
-                          device=model.device)
+    head_ws = torch.empty(int(_lsk.load().lsk_head_norm_workspace_bytes(m_max, c.vocab_size, c.dim)),
+                          dtype=torch.uint8, device=model.device)
+    # activations as the layer loop keeps them: fragment-major (whole 16-token groups) for the qkv and o inputs at
+    # every token count and for the w13 / w2 inputs above 64 tokens, row-major otherwise (the values are random
+    # either way; only the layout and the launch matter)
+    xf = x.view(-1)[:_lsk.frag_rows(x.shape[0]) * max(dim, qd, ffn)] if x.shape[0] % 16 == 0 else \
+        torch.empty(_lsk.frag_rows(x.shape[0]) * max(dim, qd, ffn), dtype=model.dtype,
+                    device=model.device).normal_(generator=g)
+    hf = torch.empty(_lsk.frag_rows(m_max) * ffn, dtype=model.dtype, device=model.device)
+    af_max = 64                                # lsk_forward_layers' LSK_AF_MAX_TOKENS
+
+    def w13(m, i):
+        if m > af_max:
+            return _lsk.gemm_silu_frag(xf, m, model.layers[i].w13, hf, True)
+        return _lsk.gemm(x[:m, :dim], model.layers[i].w13, h[:m], epilogue=_lsk.EPI_SILU_MUL)
+
+    def w2(m, i):
+        if m > af_max:
+            return _lsk.gemm_partial_frag(hf, m, model.layers[i].w2, ks["w2"], out=pv(dim, m, ks["w2"]))
+        return _lsk.gemm_partial(x[:m, :ffn], model.layers[i].w2, ks["w2"], out=pv(dim, m, ks["w2"]))
+
     classes = {
         # name: (launch(m, layer), bytes(m), flops(m), launch list)
-        "gemm_qkv": (lambda m, i: _lsk.gemm_partial(x[:m, :dim], model.layers[i].wqkv, ks["qkv"],
-                                                    out=pv(qkvd, m, ks["qkv"])),
+        "gemm_qkv": (lambda m, i: _lsk.gemm_partial_frag(xf, m, model.layers[i].wqkv, ks["qkv"],
+                                                         out=pv(qkvd, m, ks["qkv"])),
                      lambda m: es * (qkvd * dim + m * dim) + 4.0 * ks["qkv"] * m * qkvd,
                      lambda m: 2.0 * m * dim * qkvd),
-        "gemm_o": (lambda m, i: _lsk.gemm_partial(x[:m, :qd], model.layers[i].wo, ks["o"], out=pv(dim, m, ks["o"])),
+        "gemm_o": (lambda m, i: _lsk.gemm_partial_frag(xf, m, model.layers[i].wo, ks["o"], out=pv(dim, m, ks["o"])),
                    lambda m: es * (dim * qd + m * qd) + 4.0 * ks["o"] * m * dim,
                    lambda m: 2.0 * m * qd * dim),
-        "gemm_w13": (lambda m, i: _lsk.gemm(x[:m, :dim], model.layers[i].w13, h[:m], epilogue=_lsk.EPI_SILU_MUL),
+        "gemm_w13": (w13,
                      lambda m: es * (2.0 * ffn * dim + m * dim + m * ffn),
                      lambda m: 4.0 * m * dim * ffn),
-        "gemm_w2": (lambda m, i: _lsk.gemm_partial(x[:m, :ffn], model.layers[i].w2, ks["w2"], out=pv(dim, m, ks["w2"])),
+        "gemm_w2": (w2,
                     lambda m: es * (dim * ffn + m * ffn) + 4.0 * ks["w2"] * m * dim,
                     lambda m: 2.0 * m * ffn * dim),
-        # the final norm's output is the head's input; the launch is the LM-head GEMM with its fused per-tile
-        # argmax plus the pick over tiles (lsk_head_argmax)
-        "gemm_lm_head": (lambda m, i: _lsk.head_argmax(x[:m, :dim], model.lm_head_w, ids[:m], workspace=head_ws),
+        # the LM-head call as the engine makes it: final norm (its output fragment-major), the head GEMM with its
+        # fused per-tile argmax and the pick over tiles, one lsk_head_norm_argmax call
+        "gemm_lm_head": (lambda m, i: _lsk.head_norm_argmax(x[:m, :dim], model.norm_w, c.norm_eps, model.lm_head_w,
+                                                            ids[:m], workspace=head_ws),
                          lambda m: es * (V * dim + m * dim),
                          lambda m: 2.0 * m * dim * V, head_seq),
     }

@@ -893,6 +893,15 @@ int lsk_gemm_silu_af(const void* A, const void* W, void* H, int h_frag, int M, i
   return lsk_check_launch("lsk_gemm_silu_af");
 }
 
+extern "C" int lsk_gemm_partial_frag(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream) {
+  return lsk_gemm_partial_af(A, W, P, M, N, K, ks, stream);
+}
+
+extern "C" int lsk_gemm_silu_frag(const void* A, const void* W, void* H, int h_frag, int M, int ffn, int K,
+                                  void* stream) {
+  return lsk_gemm_silu_af(A, W, H, h_frag, M, ffn, K, stream);
+}
+
 extern "C" size_t lsk_head_workspace_bytes(int M, int N) {
   const size_t nt = (size_t)(N + 63) / 64;
   return lsk_align_up((size_t)M * nt * 4, 256) * 2;

@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 7
+#define LSK_ABI_VERSION 8
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -152,6 +152,16 @@ int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out);
  * the slices in order).  Replaces F.linear at solutions/packed.py:175 (wqkv), 182 (wo), 185 (w2). */
 int lsk_gemm_partial(const void* A, long lda, const void* W, long ldw, float* P, int M, int N, int K, int ks,
                      void* stream);
+
+/* Fragment-major A: A holds ceil(M/16)*16 rows x K in lsk_pack_weight's layout (16-token groups, each 16 x 32
+ * block one 1 KiB fragment in lane order; the padding rows only reach discarded outputs).  These are the GEMM
+ * launches lsk_forward_layers makes (its activations stay in that layout, so every row tile re-reads them as
+ * contiguous 1 KiB); results are bitwise those of lsk_gemm_partial / lsk_gemm with the same values row-major.
+ * lsk_gemm_silu_frag: w13 with the silu-mul epilogue, H [M, ffn] row-major (h_frag == 0, ldh = ffn) or
+ * fragment-major (h_frag != 0, ceil(M/16)*16 rows).  No reference counterpart: the layer runner's internal
+ * launches, exported so that measurements replay exactly those. */
+int lsk_gemm_partial_frag(const void* A, const void* W, float* P, int M, int N, int K, int ks, void* stream);
+int lsk_gemm_silu_frag(const void* A, const void* W, void* H, int h_frag, int M, int ffn, int K, void* stream);
 
 /* LM head + greedy pick (W packed, ldw == K): out[dst_idx ? dst_idx[m] : m] = argmax_n rnd(A[m] . W[n]) (first index on ties),
  * optionally also storing the bf16 logits [M, ldl].  workspace >= lsk_head_workspace_bytes(M, N).

@@ -609,3 +609,30 @@ def test_gemm_wide_tier_and_remainder_are_bitwise_the_decode_kernel(cuda, M):
     ref = a.float() @ head.to(cuda).float().t()
     assert ((logit_full.float() - ref).abs() <= 2.0 ** -7 * ref.abs() + 1e-2).all()
     assert torch.equal(ids_full, logit_full.float().argmax(-1))
+
+
+@pytest.mark.parametrize("M", [5, 40, 100, 288])
+def test_fragment_major_gemms_are_bitwise_the_row_major_ones(cuda, M):
+    """lsk_gemm_partial_frag / lsk_gemm_silu_frag -- the layer loop's launches, A fragment-major in whole
+    16-token groups (lsk_pack_weight's layout of the same values) -- give bitwise the row-major entry points'
+    results, in the decode tier (<= 64 rows) and in the wide tier with its remainder (above); the silu variant's
+    fragment-major h holds the row-major h's values."""
+    lsk = _lsk()
+    g = _gen(1000 + M)
+    K = 1024
+    m16 = lsk.frag_rows(M)
+    a = torch.randn(m16, K, generator=g).to(BF16).to(cuda)                 # rows >= M: the padding group
+    af = lsk.PackedWeight(a).data                                          # same values, fragment-major
+    w = lsk.PackedWeight(torch.randn(12288, K, generator=g).to(BF16).to(cuda))          # 192 row tiles
+    w13 = lsk.PackedWeight(torch.randn(2 * 12288, K, generator=g).to(BF16).to(cuda))     # 192 row tiles
+    ns, ks = lsk.gemm_plan(12288, K)
+    want = lsk.gemm_partial(a[:M].contiguous(), w, ks)
+    assert torch.equal(lsk.gemm_partial_frag(af, M, w, ks), want)
+    h_row = lsk.gemm(a[:M].contiguous(), w13, epilogue=lsk.EPI_SILU_MUL)
+    h1 = torch.empty(M, 12288, dtype=BF16, device=cuda)
+    assert torch.equal(lsk.gemm_silu_frag(af, M, w13, h1, False), h_row)
+    h2 = torch.full((m16 * 12288,), float("nan"), dtype=BF16, device=cuda)
+    lsk.gemm_silu_frag(af, M, w13, h2, True)
+    back = lsk.PackedWeight.__new__(lsk.PackedWeight)                      # view h2 as packed [m16, 12288]
+    back.shape, back.dtype, back.device, back.data = (m16, 12288), BF16, h2.device, h2
+    assert torch.equal(back.unpack()[:M], h_row)

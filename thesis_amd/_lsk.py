@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -61,6 +61,8 @@ _SIGS = {
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
     "lsk_segment_workspace_bytes": (_Z, [_L, _I, _I]),
+    "lsk_gemm_partial_frag": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
+    "lsk_gemm_silu_frag": (_I, [_P, _P, _P, _I, _I, _I, _I, _P]),
     "lsk_forward_layers": (_I, [_L, _P, _P, _I, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _P, _Z, _P,
                                 ctypes.c_double, ctypes.c_double, _P]),
     "lsk_prof_enable": (_I, [_I]),
@@ -557,6 +559,42 @@ def gemm_plan(N: int, K: int) -> tuple:
     ns, ks = ctypes.c_int(0), ctypes.c_int(0)
     _check(load().lsk_gemm_plan(N, K, ctypes.byref(ns), ctypes.byref(ks)), "lsk_gemm_plan")
     return ns.value, ks.value
+
+
+def frag_rows(m: int) -> int:
+    """Rows a fragment-major activation buffer of m tokens holds (whole 16-token groups)."""
+    return (m + 15) // 16 * 16
+
+
+def gemm_partial_frag(a_frag: torch.Tensor, m: int, w: torch.Tensor, ks: int,
+                      out: torch.Tensor | None = None) -> torch.Tensor:
+    """gemm_partial with A fragment-major (lsk_gemm_partial_frag): a_frag holds frag_rows(m) x K elements in
+    lsk_pack_weight's layout; fp32 K-slice partials [ks, m, N]."""
+    _dev(a_frag, w, out)
+    _check_weight(a_frag, w)
+    N, K = w.shape
+    if a_frag.dtype != torch.bfloat16 or a_frag.numel() < frag_rows(m) * K or not a_frag.is_contiguous():
+        raise LskError("gemm_partial_frag: a contiguous bf16 buffer of frag_rows(m) x K elements is needed")
+    if out is None:
+        out = torch.empty(ks, m, N, dtype=torch.float32, device=a_frag.device)
+    _check(load().lsk_gemm_partial_frag(_ptr(a_frag), _ptr(w), _ptr(out), m, N, K, ks, _stream()),
+           "lsk_gemm_partial_frag")
+    return out
+
+
+def gemm_silu_frag(a_frag: torch.Tensor, m: int, w: torch.Tensor, h: torch.Tensor, h_frag: bool) -> torch.Tensor:
+    """w13 + silu-mul with A fragment-major (lsk_gemm_silu_frag); h row-major [m, ffn] or, with h_frag,
+    fragment-major (frag_rows(m) x ffn elements)."""
+    _dev(a_frag, w, h)
+    _check_weight(a_frag, w)
+    ffn, K = w.shape[0] // 2, w.shape[1]
+    if a_frag.dtype != torch.bfloat16 or a_frag.numel() < frag_rows(m) * K or not a_frag.is_contiguous():
+        raise LskError("gemm_silu_frag: a contiguous bf16 buffer of frag_rows(m) x K elements is needed")
+    if h.numel() < (frag_rows(m) if h_frag else m) * ffn or not h.is_contiguous():
+        raise LskError("gemm_silu_frag: output too small")
+    _check(load().lsk_gemm_silu_frag(_ptr(a_frag), _ptr(w), _ptr(h), 1 if h_frag else 0, m, ffn, K, _stream()),
+           "lsk_gemm_silu_frag")
+    return h
 
 
 def gemm_partial(a: torch.Tensor, w: torch.Tensor, ks: int, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -7,7 +7,10 @@ For every token count M and class -- qkv (6144 x 4096, split-K partials), o (409
 issues `reps` launches on distinct random weights (two layers' worth, so repeated launches stream from HBM),
 after one marker copy of 64 MiB per group (lsk_copy_rows, 16 KiB rows), and prints the sequence as JSON lines
 ({"class", "M", "launches"}) so per-dispatch counters can be attributed: dispatches between two markers belong
-to the group printed in that position.
+to the group printed in that position.  The activations have the layer loop's layouts: fragment-major for
+qkv and o at every M and for w13 / w2 above 64 tokens (lsk_gemm_partial_frag, lsk_gemm_silu_frag), row-major
+otherwise; the LM head is the engine's lsk_head_norm_argmax call (its final norm writes the head's input
+fragment-major; only the GEMM kernels count in the summaries).
 """
 
 from __future__ import annotations
@@ -37,13 +40,16 @@ def main() -> None:
     weights = {c: [_lsk.PackedWeight(torch.empty(*shapes[c], dtype=torch.bfloat16, device=dev).normal_(generator=g))
                    for _ in range(1 if c == "head" else 2)] for c in classes}
     a = torch.empty(max(Ms), ffn, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    af = torch.empty(_lsk.frag_rows(max(Ms)) * ffn, dtype=torch.bfloat16, device=dev).normal_(generator=g)
+    norm_w = torch.ones(dim, dtype=torch.bfloat16, device=dev)
     src = torch.empty(4096, 16384, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
+    af_max = 64                                # lsk_forward_layers' LSK_AF_MAX_TOKENS
     for M in Ms:
         x = {c: a[:M, :shapes[c][1]].contiguous() for c in classes}
-        h = torch.empty(M, ffn, dtype=torch.bfloat16, device=dev)
+        h = torch.empty(_lsk.frag_rows(M) * ffn, dtype=torch.bfloat16, device=dev)
         ids = torch.empty(M, dtype=torch.long, device=dev)
-        ws = torch.empty(int(_lsk.load().lsk_head_workspace_bytes(M, V)), dtype=torch.uint8, device=dev)
+        ws = torch.empty(int(_lsk.load().lsk_head_norm_workspace_bytes(M, V, dim)), dtype=torch.uint8, device=dev)
         for c in classes:
             N, K = shapes[c]
             ks = _lsk.gemm_plan(N, K)[1]
@@ -53,9 +59,14 @@ def main() -> None:
             for r in range(args.reps):
                 w = weights[c][r % len(weights[c])]
                 if c == "w13":
-                    _lsk.gemm(x[c], w, h, epilogue=_lsk.EPI_SILU_MUL)
+                    if M > af_max:
+                        _lsk.gemm_silu_frag(af, M, w, h, True)
+                    else:
+                        _lsk.gemm(x[c], w, h[:M * ffn].view(M, ffn), epilogue=_lsk.EPI_SILU_MUL)
                 elif c == "head":
-                    _lsk.head_argmax(x[c], w, ids, workspace=ws)
+                    _lsk.head_norm_argmax(x[c], norm_w, 1e-5, w, ids, workspace=ws)
+                elif c in ("qkv", "o") or M > af_max:
+                    _lsk.gemm_partial_frag(af, M, w, ks, out=P)
                 else:
                     _lsk.gemm_partial(x[c], w, ks, out=P)
             torch.cuda.synchronize()
