@@ -32,6 +32,8 @@
 //   SILU_MUL  C = rnd(rnd(silu(rnd(g))) * rnd(u))         g, u = rows n and ffn + n of W (w13)
 //   PARTIAL   P[s][m][n] = acc over K slice s (fp32), reduced later in slice order
 //   ARGMAX    per (token, 16*NS-row tile): max of rnd(acc) and its first index (LM head + greedy pick)
+#include <type_traits>
+
 #include "lsk_common.h"
 #include "../include/lsk.h"
 
@@ -287,6 +289,11 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
 // so every output sees the same MFMA sequence and the same three adds: results are bitwise those of the
 // decode kernel, which keeps the batch invariance of the GEMM.  Covered shapes (launch_wide): N % 64 == 0 and
 // K slices of whole 128-k chunks (no tail k-steps).
+//
+// Token groups: block mb of a launch covers the 16-token groups [mb tbg, min((mb + 1) tbg, ceil(M / 16))), dealt
+// to the NWV waves in order, the first (count % NWV) waves one more (waves w and w + 4 share a SIMD, so the extra
+// groups land on different SIMDs).  MSW is the most groups a wave holds (tbg <= NWV MSW); a wave multiplies only
+// its own groups, so a block's MFMA work follows its real token count.
 template <int NS, int MSW, int EPI, int NWV, int PF, bool AF = false>
 __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* __restrict__ A, long lda,
                                                                 const uint16_t* __restrict__ W,
@@ -295,13 +302,12 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
                                                                 float* __restrict__ P, float* __restrict__ amax_v,
                                                                 int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                                 int kslice, int n_tiles, int m_blocks, int n_slices,
-                                                                int c_nks) {
+                                                                int c_nks, int tbg) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int NTH = 64 * NWV;
   constexpr int CHUNK_E = NT * 4 * 512;  // bf16 elements of one staged chunk (NT row groups x 4 k-steps)
   constexpr int LPT = CHUNK_E / (NTH * 8);
   static_assert(LPT >= 1 && CHUNK_E % (NTH * 8) == 0, "staging split");
-  constexpr int TB = NWV * MSW * 16;    // tokens per workgroup
   __shared__ __attribute__((aligned(16))) uint16_t wl[2][CHUNK_E];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -328,17 +334,22 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
     wsrc[j] = W + ((long)group_of(g) * nks + (k0 >> 5) + ks) * 512 + 8 * l;
     wdst[j] = (g * 4 + ks) * 512 + 8 * l;
   }
+  // this wave's token groups [g0, g0 + ng) (ng <= MSW); group slots t >= ng load a valid group and store nothing
+  const int gtot = (M + 15) / 16, gb0 = mb * tbg;
+  const int gb = min(tbg, gtot - gb0);
+  const int ng = __builtin_amdgcn_readfirstlane(gb / NWV + (wave < gb % NWV ? 1 : 0));
+  const int g0 = gb0 + wave * (gb / NWV) + min(wave, gb % NWV);
   const uint16_t* arow[MSW];
   int mrow[MSW];
 #pragma unroll
   for (int t = 0; t < MSW; ++t) {
-    const int m = mb * TB + (wave * MSW + t) * 16 + l16;
-    mrow[t] = m;
+    const int grp = min(g0 + min(t, max(ng - 1, 0)), gtot - 1);
+    mrow[t] = t < ng ? (g0 + t) * 16 + l16 : INT_MAX;
     if constexpr (AF) {
-      // fragment-major A holds whole 16-token groups up to (M + 15) / 16; groups past it read the last one
-      const int grp = min(mb * TB / 16 + wave * MSW + t, (M + 15) / 16 - 1);
+      // fragment-major A holds whole 16-token groups up to (M + 15) / 16
       arow[t] = A + ((long)grp * nks + (k0 >> 5)) * 512 + 8 * lane;
     } else {
+      const int m = grp * 16 + l16;
       arow[t] = A + (long)(m < M - 1 ? m : M - 1) * lda + k0 + 8 * lg;
     }
   }
@@ -366,24 +377,29 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
     for (int j = 0; j < LPT; ++j) *(lsk_i32x4*)(&wl[b][wdst[j]]) = r[j];
   };
   lsk_bf16x8 af[2][4][MSW];
-  auto load_a = [&](lsk_bf16x8 (&a)[4][MSW], int c) {
+  // na_c: std::integral_constant holding this wave's group count (the loops below are unrolled per count)
+  auto load_a = [&](lsk_bf16x8 (&a)[4][MSW], int c, auto na_c) {
+    constexpr int NA = decltype(na_c)::value;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-      for (int t = 0; t < MSW; ++t)
+      for (int t = 0; t < NA; ++t)
         a[ks][t] = *(const lsk_bf16x8*)(arow[t] + (AF ? (long)(c * 4 + ks) * 512 : (long)(c * 128 + ks * 32)));
   };
-  auto comp = [&](const lsk_bf16x8 (&a)[4][MSW], int b) {
+  auto comp = [&](const lsk_bf16x8 (&a)[4][MSW], int b, auto na_c) {
+    constexpr int NA = decltype(na_c)::value;
+    if constexpr (NA > 0) {
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      lsk_bf16x8 wf[NT];
+      for (int ks = 0; ks < 4; ++ks) {
+        lsk_bf16x8 wf[NT];
 #pragma unroll
-      for (int g = 0; g < NT; ++g) wf[g] = *(const lsk_bf16x8*)(&wl[b][(g * 4 + ks) * 512 + 8 * lane]);
+        for (int g = 0; g < NT; ++g) wf[g] = *(const lsk_bf16x8*)(&wl[b][(g * 4 + ks) * 512 + 8 * lane]);
 #pragma unroll
-      for (int g = 0; g < NT; ++g)
+        for (int g = 0; g < NT; ++g)
 #pragma unroll
-        for (int t = 0; t < MSW; ++t)
-          cur[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g], a[ks][t], cur[g][t], 0, 0, 0);
+          for (int t = 0; t < NA; ++t)
+            cur[g][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[g], a[ks][t], cur[g][t], 0, 0, 0);
+      }
     }
   };
   int cls = 0;
@@ -404,32 +420,41 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
       }
     ++cls;
   };
-  // prologue: chunks 0 .. PF-1 of the sequence in flight, chunk 0 in LDS buffer 0
+  // Every wave stages weights and meets every barrier; the group count only selects how many token groups it
+  // loads and multiplies (a wave-uniform branch around whole copies of the loop, same barriers in each).
+  auto run = [&](auto na_c) {
+    // prologue: chunks 0 .. PF-1 of the sequence in flight, chunk 0 in LDS buffer 0
 #pragma unroll
-  for (int j = 0; j < PF; ++j)
-    if (j < nfull) issue(stg[j], chunk_at(j));
-  if (nfull > 0) {
-    load_a(af[0], chunk_at(0));
-    put(stg[0], 0);
-  }
-  __syncthreads();
-  // sequence index i (i0 a multiple of 2 PF, so i % 2 == u % 2 and i % PF == u % PF): fold the classes that
-  // ended before i, multiply chunk i from LDS buffer i % 2, refill register slot i % PF with chunk i + PF, move
-  // chunk i + 1 from its register slot into the other LDS buffer
-  for (int i0 = 0; i0 < nfull; i0 += 2 * PF) {
+    for (int j = 0; j < PF; ++j)
+      if (j < nfull) issue(stg[j], chunk_at(j));
+    if (nfull > 0) {
+      load_a(af[0], chunk_at(0), na_c);
+      put(stg[0], 0);
+    }
+    __syncthreads();
+    // sequence index i (i0 a multiple of 2 PF, so i % 2 == u % 2 and i % PF == u % PF): fold the classes that
+    // ended before i, multiply chunk i from LDS buffer i % 2, refill register slot i % PF with chunk i + PF, move
+    // chunk i + 1 from its register slot into the other LDS buffer
+    for (int i0 = 0; i0 < nfull; i0 += 2 * PF) {
 #pragma unroll
-    for (int u = 0; u < 2 * PF; ++u) {
-      const int i = i0 + u;
-      if (i < nfull) {
-        while (cls < 3 && i >= cum[cls + 1]) fold();
-        if (i + 1 < nfull) load_a(af[(u + 1) & 1], chunk_at(i + 1));
-        comp(af[u & 1], u & 1);
-        if (i + PF < nfull) issue(stg[u % PF], chunk_at(i + PF));
-        if (i + 1 < nfull) put(stg[(u + 1) % PF], (u + 1) & 1);
-        __syncthreads();
+      for (int u = 0; u < 2 * PF; ++u) {
+        const int i = i0 + u;
+        if (i < nfull) {
+          while (cls < 3 && i >= cum[cls + 1]) fold();
+          if (i + 1 < nfull) load_a(af[(u + 1) & 1], chunk_at(i + 1), na_c);
+          comp(af[u & 1], u & 1, na_c);
+          if (i + PF < nfull) issue(stg[u % PF], chunk_at(i + PF));
+          if (i + 1 < nfull) put(stg[(u + 1) % PF], (u + 1) & 1);
+          __syncthreads();
+        }
       }
     }
-  }
+  };
+  static_assert(MSW >= 1 && MSW <= 3, "group counts per wave");
+  if (ng == MSW) run(std::integral_constant<int, MSW>{});
+  else if (ng == MSW - 1) run(std::integral_constant<int, (MSW > 1 ? MSW - 1 : 0)>{});
+  else if (MSW == 3 && ng == 1) run(std::integral_constant<int, 1>{});
+  else run(std::integral_constant<int, 0>{});
   while (cls < 4) fold();
   // epilogue: lane holds rows 16 g + 4 lg + i of its token group t, token l16
   if constexpr (EPI == EPI_ARGMAX) {
@@ -736,58 +761,115 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 #undef LSK_GEMM_CASE
 }
 
-// Wide-M tier selection (measured on MI355X at the 8B layer shapes, against the decode kernel's 64-token
-// tiles).  A workgroup covers TB = 128 tokens (256 for silu-mul above 128).  Above 64 tokens the tier covers the
-// full TB-token blocks and the decode kernel the remaining rows when they fit one of its token tiles (<= 64 rows:
-// one more pass over the weights, where another wide block would cost a full block's MFMA work); larger
-// remainders, and M <= TB, go in one partly filled wide block.  The LM head (argmax epilogue) always takes whole
-// blocks: a decode pass over its 1 GB of weights costs more than the empty rows of a block.  The launch needs
-// >= 192 workgroups to stream the weights.  Returns the rows [0, covered) the tier took (0: none; also for shapes
-// it does not cover: N % 64 != 0 or K slices that are not whole 128-k chunks).  Both tiers give bitwise the same
-// sums, so how rows are split between them never changes a result.
+// Wide-M tier selection.  Above 64 tokens every row goes through the wide tier in one launch.  A configuration
+// is a tile width (64 rows; silu-mul also 32 + 32) and a block count nb: the token groups are dealt evenly to nb
+// blocks of tbg groups, and within a block to the 8 waves, so a wave holds at most msw = ceil(tbg / 8) groups
+// (register budget: 3, or 2 for the 64 + 64-row silu-mul tile, whose gate and up accumulators take twice the
+// registers).  Each weight tile is streamed from HBM once per launch; the blocks of a tile run side by side on
+// one XCD and re-read it from that XCD's L2.
+//
+// The configuration minimises a cost fitted to MI355X measurements at the 8B layer shapes (M = 66..512, qkv /
+// o / w2 / w13 / LM head): workgroup rounds ceil(WGs / 256) x max(2.5, 0.83 + g) x rows / 64, where g is the most
+// token groups the two waves of one SIMD hold (MFMA work) and 2.5 the floor a workgroup's weight stream sets;
+// x 0.9 when a msw = 1 kernel fits two workgroups per CU (more memory parallelism), x 1.1 for the 32 + 32-row
+// silu-mul tile (twice the activation reads).  The launch needs >= 192
+// workgroups to stream the weights.  Returns the rows the tier took: M, or 0 where it does not apply (M <= 64,
+// N % 64 != 0, or K slices that are not whole 128-k chunks).  Both tiers give bitwise the same sums, so neither
+// the tier nor the configuration ever changes a result.
+struct WideCfg {
+  int ns, m_blocks, tbg, msw;
+};
+
+static WideCfg wide_config(int epi, int M, int N, int ks) {
+  const bool silu = epi == LSK_EPI_SILU_MUL;
+  const int gtot = (M + 15) / 16;
+  WideCfg best{0, 0, 0, 0};
+  double best_cost = 0.0;
+  for (int ns = 4; ns >= 2; ns -= 2) {
+    if (ns == 2 && !silu) break;
+    const int msw_max = (silu && ns == 4) ? 2 : 3;
+    const int nb_min = (gtot + 8 * msw_max - 1) / (8 * msw_max);
+    for (int nb = nb_min; nb <= nb_min + 2; ++nb) {
+      const int tbg = (gtot + nb - 1) / nb, m_blocks = (gtot + tbg - 1) / tbg, msw = (tbg + 7) / 8;
+      const int q = tbg / 8, r = tbg % 8;
+      const int g = 2 * q + (r > 0) + (r > 4);
+      const long wgs = (long)(N / (16 * ns)) * m_blocks * ks;
+      // >= 192 workgroups; the 64 + 64-row silu-mul tile only at msw = 2 (at msw = 1 the 32 + 32 tile, two
+      // workgroups per CU, always costs less)
+      if (wgs < 192 || (silu && ns == 4 && msw == 1)) continue;
+      const bool two_per_cu = msw == 1 && wgs > 256;
+      double cost = (double)((wgs + 255) / 256) * fmax(2.5, 0.83 + g) * ns / 4.0;
+      if (two_per_cu) cost *= 0.9;
+      if (silu && ns == 2) cost *= 1.1;
+      if (best.ns == 0 || cost < best_cost) {
+        best = WideCfg{ns, m_blocks, tbg, msw};
+        best_cost = cost;
+      }
+    }
+  }
+  return best;
+}
+
+template <int NS, int MSW, int EPI>
+static void launch_wide_kernel(dim3 grid, hipStream_t s, bool af, const uint16_t* A, long lda, const uint16_t* W,
+                               uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
+                               int N, int K, int ffn, int kslice, int n_tiles, int m_blocks, int ks, int c_nks,
+                               int tbg) {
+  if constexpr (EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL) {
+    if (af) {
+      gemm_wide_kernel<NS, MSW, EPI, 8, 2, true><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
+                                                                      kslice, n_tiles, m_blocks, ks, c_nks, tbg);
+      return;
+    }
+  }
+  gemm_wide_kernel<NS, MSW, EPI, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, kslice,
+                                                            n_tiles, m_blocks, ks, 0, tbg);
+}
+
 static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
                        const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks,
                        bool af = false, int c_nks = 0) {
   if (M <= 64) return 0;
   if (N % 64 != 0 || (epi != EPI_PARTIAL && C != nullptr && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0)
     return 0;
-  const bool silu = epi == LSK_EPI_SILU_MUL;
-  const int tb = (silu && M > 128) ? 256 : 128;
-  const int rem = M % tb;
-  int m_blocks = (M + tb - 1) / tb, covered = M;
-  if (epi != EPI_ARGMAX && M > tb && rem != 0 && rem <= 64) {
-    m_blocks = M / tb;
-    covered = m_blocks * tb;
-  }
-  const int n_tiles = N / 64;
-  if ((long)n_tiles * m_blocks * ks < 192) return 0;
-  const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * m_blocks * ks));
+  if (af && (epi == LSK_EPI_RESIDUAL || epi == LSK_EPI_NONE)) return 0;
+  // the tier streams the weights with >= 192 workgroups: 64-row tiles x the fewest blocks must reach that
+  const int gtot = (M + 15) / 16, cap = 8 * (epi == LSK_EPI_SILU_MUL ? 2 : 3);
+  if ((long)(N / 64) * ((gtot + cap - 1) / cap) * ks < 192) return 0;
+  const WideCfg cfg = wide_config(epi, M, N, ks);
+  if (cfg.ns == 0) return 0;
+  const int n_tiles = N / (16 * cfg.ns);
+  const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * cfg.m_blocks * ks));
   const int kslice = K / ks;
-#define LSK_WIDE(MSW_, EPI_)                                                                                   \
-  do {                                                                                                          \
-    if (af)                                                                                                     \
-      gemm_wide_kernel<4, MSW_, EPI_, 8, 2, true><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, \
-                                                                      K, ffn, kslice, n_tiles, m_blocks, ks, c_nks); \
-    else                                                                                                        \
-      gemm_wide_kernel<4, MSW_, EPI_, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, \
-                                                                 ffn, kslice, n_tiles, m_blocks, ks, 0);        \
+#define LSK_WIDE(NS_, MSW_, EPI_)                                                                                  \
+  launch_wide_kernel<NS_, MSW_, EPI_>(grid, s, af, A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, kslice, n_tiles, \
+                                      cfg.m_blocks, ks, c_nks, cfg.tbg)
+#define LSK_WIDE_MSW(NS_, EPI_)                 \
+  do {                                          \
+    if (cfg.msw == 1)                           \
+      LSK_WIDE(NS_, 1, EPI_);                   \
+    else if (cfg.msw == 2)                      \
+      LSK_WIDE(NS_, 2, EPI_);                   \
+    else                                        \
+      LSK_WIDE(NS_, 3, EPI_);                   \
   } while (0)
-  if (silu) {
-    if (tb == 256) LSK_WIDE(2, LSK_EPI_SILU_MUL);
-    else LSK_WIDE(1, LSK_EPI_SILU_MUL);
+  if (epi == LSK_EPI_SILU_MUL) {
+    if (cfg.ns == 2) LSK_WIDE_MSW(2, LSK_EPI_SILU_MUL);
+    else LSK_WIDE(4, 2, LSK_EPI_SILU_MUL);
   } else if (epi == EPI_PARTIAL) {
-    LSK_WIDE(1, EPI_PARTIAL);
-  } else if (epi == LSK_EPI_RESIDUAL && !af) {
-    LSK_WIDE(1, LSK_EPI_RESIDUAL);
-  } else if (epi == LSK_EPI_NONE && !af) {
-    LSK_WIDE(1, LSK_EPI_NONE);
+    LSK_WIDE_MSW(4, EPI_PARTIAL);
+  } else if (epi == LSK_EPI_RESIDUAL) {
+    LSK_WIDE_MSW(4, LSK_EPI_RESIDUAL);
+  } else if (epi == LSK_EPI_NONE) {
+    LSK_WIDE_MSW(4, LSK_EPI_NONE);
   } else if (epi == EPI_ARGMAX) {
-    LSK_WIDE(1, EPI_ARGMAX);
+    LSK_WIDE_MSW(4, EPI_ARGMAX);
   } else {
     return 0;
   }
+#undef LSK_WIDE_MSW
 #undef LSK_WIDE
-  return covered;
+  return M;
 }
 
 extern "C" int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* C, long ldc,

@@ -567,13 +567,16 @@ def test_probe_matches_equal_the_closed_form(cuda, nc, nblk):
     assert 0 < want[nc] < nvt
 
 
-@pytest.mark.parametrize("M", [66, 150, 200, 288, 300])
-def test_gemm_wide_tier_and_remainder_are_bitwise_the_decode_kernel(cuda, M):
-    """Above 64 rows the wide tier (weights staged in LDS, 128 / 256 tokens per workgroup) covers the full token
-    blocks and the decode kernel the remaining rows (one partly filled block for larger remainders).  At shapes
-    large enough for the tier (>= 192 workgroups), every epilogue -- plain, residual, silu-mul, split-K partials,
-    LM-head argmax with its logits -- gives bitwise what the decode kernel gives row chunk by row chunk (<= 48 rows,
-    one token tile), so a token's result never depends on the batch it is packed in."""
+@pytest.mark.parametrize("M", [66, 150, 200, 288, 300, 400, 600, 800])
+def test_gemm_wide_tier_is_bitwise_the_decode_kernel(cuda, M):
+    """Above 64 rows the wide tier (weights staged in LDS) takes every row: token groups dealt to one or more
+    blocks and, within a block, evenly to the 8 waves (1 to 3 groups each), with 64-row tiles or, for silu-mul,
+    32 + 32-row tiles, as its cost model picks.  These M reach every configuration at these shapes: 1, 2 and 3
+    groups per wave in one block, 2 and 3 in several blocks, both silu-mul tiles (66: 1 group; 150, 200: 2; 288,
+    300: 3; 400, 600: several blocks; 800: the 32 + 32 silu-mul tile in several blocks).  Every epilogue -- plain,
+    residual, silu-mul, split-K partials, LM-head argmax with its logits -- gives bitwise what the decode kernel
+    gives row chunk by row chunk (<= 48 rows, one token tile), so a token's result never depends on the batch it is
+    packed in."""
     lsk = _lsk()
     g = _gen(M)
     K = 512
@@ -615,7 +618,7 @@ def test_gemm_wide_tier_and_remainder_are_bitwise_the_decode_kernel(cuda, M):
 def test_fragment_major_gemms_are_bitwise_the_row_major_ones(cuda, M):
     """lsk_gemm_partial_frag / lsk_gemm_silu_frag -- the layer loop's launches, A fragment-major in whole
     16-token groups (lsk_pack_weight's layout of the same values) -- give bitwise the row-major entry points'
-    results, in the decode tier (<= 64 rows) and in the wide tier with its remainder (above); the silu variant's
+    results, in the decode tier (<= 64 rows) and in the wide tier (above); the silu variant's
     fragment-major h holds the row-major h's values."""
     lsk = _lsk()
     g = _gen(1000 + M)

@@ -275,8 +275,8 @@ def cmd_gemm(a):
     for c in a.cmd.split(" ;; "):
         print(f"    {c}")
     print()
-    print("Per (class, M): the probe's launches on distinct weights (a GEMM call above 64 rows may be two launches: the "
-          "wide tier on the full token blocks and the decode kernel on the remainder).  t_roof = max(bytes / 8 TB/s, "
+    print("Per (class, M): the probe's launches on distinct weights (one launch per GEMM call: the decode kernel up "
+          "to 64 rows, the wide tier above).  t_roof = max(bytes / 8 TB/s, "
           "flops / 2.5166 PFLOP/s) with bytes = 2 (K N + M K + M N); frac = t_roof / measured.  MFMA flops = "
           "SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 (the counter's unit); MFMA util = MFMA flops / (time x 2.5166 PFLOP/s), "
           "the share of the dense bf16 peak the launch used.  L2 hit = TCC_HIT / (TCC_HIT + TCC_MISS).\n")
