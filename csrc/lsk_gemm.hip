@@ -158,7 +158,9 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
         for (int t = 0; t < MS; ++t)
           acc[a][t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[ks][a], af[ks][t], acc[a][t], 0, 0, 0);
   };
-  // two register buffers: the next unit is in flight while the current one is multiplied
+  // two register buffers: the next unit is in flight while the current one is multiplied.  (A branch-free form of
+  // this loop -- every load unconditional, the last units peeled off, scheduling barriers keeping each unit's loads
+  // ahead of the previous unit's MFMAs -- gets exact wait counts but measured 1-2 % slower per layer stack.)
   if (my_u > 0) load(wA, aA, 0);
   int i = 0;
   for (; i + 2 <= my_u; i += 2) {
@@ -434,17 +436,22 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
     __syncthreads();
     // sequence index i (i0 a multiple of 2 PF, so i % 2 == u % 2 and i % PF == u % PF): fold the classes that
     // ended before i, multiply chunk i from LDS buffer i % 2, refill register slot i % PF with chunk i + PF, move
-    // chunk i + 1 from its register slot into the other LDS buffer
+    // chunk i + 1 from its register slot into the other LDS buffer.  The prefetches past the last chunk reload the
+    // last one (in bounds, never used): every iteration issues the same loads, so the compiler's wait counts stay
+    // exact (a conditional prefetch made it wait for the next chunk's loads before this chunk's MFMAs; measured
+    // 6-28 % slower).  The 64 + 64-row silu-mul tile at 2 groups per wave keeps the conditional form: it is at the
+    // register limit, and the earlier loads of the unconditional form spill.
+    constexpr bool exact = !(NT * MSW >= 16);
     for (int i0 = 0; i0 < nfull; i0 += 2 * PF) {
 #pragma unroll
       for (int u = 0; u < 2 * PF; ++u) {
         const int i = i0 + u;
         if (i < nfull) {
           while (cls < 3 && i >= cum[cls + 1]) fold();
-          if (i + 1 < nfull) load_a(af[(u + 1) & 1], chunk_at(i + 1), na_c);
+          if (exact || i + 1 < nfull) load_a(af[(u + 1) & 1], chunk_at(min(i + 1, nfull - 1)), na_c);
           comp(af[u & 1], u & 1, na_c);
-          if (i + PF < nfull) issue(stg[u % PF], chunk_at(i + PF));
-          if (i + 1 < nfull) put(stg[(u + 1) % PF], (u + 1) & 1);
+          if (exact || i + PF < nfull) issue(stg[u % PF], chunk_at(min(i + PF, nfull - 1)));
+          if (exact || i + 1 < nfull) put(stg[(u + 1) % PF], (u + 1) & 1);
           __syncthreads();
         }
       }
