@@ -163,11 +163,15 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
       }
     }
   };
-  // K / V fragments come through buffer loads over the item's (row, KV head) stripe of S * D elements: the
-  // descriptor and every uniform offset live in SGPRs, a lane adds one 32-bit offset, so no 64-bit per-lane
-  // addresses occupy VGPRs.  Non-temporal (aux 2): each byte is read once per launch.
-  auto stripe = [&](const uint16_t* base) {
-    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, S * D * 2, LSK_BUFFER_RSRC_WORD3);
+  // K / V fragments come through buffer loads over the item's (row, KV head) stripe: the descriptor and every
+  // uniform offset live in SGPRs, a lane adds one 32-bit offset, so no 64-bit per-lane addresses occupy VGPRs.
+  // Non-temporal (aux 2): each byte is read once per launch.  The descriptor's range ends at the 32-position block
+  // holding the item's last position (kv_hi - 1): a step past it reads as zeros without touching memory, so the
+  // next step's loads are issued unconditionally -- with them under `if (more)` the compiler's wait counts merged
+  // the two paths and every step's K.Q waited for the next step's V loads too.
+  auto stripe = [&](const uint16_t* base, int hi) {
+    const int blocks_end = min(S, (hi + ATTN_STEP - 1) / ATTN_STEP * ATTN_STEP);
+    return __builtin_amdgcn_make_buffer_rsrc((void*)base, (short)0, blocks_end * D * 2, LSK_BUFFER_RSRC_WORD3);
   };
   auto ldkv = [&](__amdgpu_buffer_rsrc_t rs, int vo, int so) -> lsk_bf16x8 {
     return __builtin_bit_cast(lsk_bf16x8, __builtin_amdgcn_raw_buffer_load_b128(rs, vo, so, 2));
@@ -193,11 +197,9 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   auto issue_first = [&](const Item& it) {
     q_load(it);
     const int sb = first_step(it);
-    const auto kr = stripe(kbase_of(it)), vr = stripe(vbase_of(it));
-    if (sb < it.kv_hi) {
-      load_k(kr, sb);
-      load_v(vr, sb);
-    }
+    const auto kr = stripe(kbase_of(it), it.kv_hi), vr = stripe(vbase_of(it), it.kv_hi);
+    load_k(kr, sb);  // (a wave with no step in the item reads zeros past the range)
+    load_v(vr, sb);
   };
 
   Item cur = fetch(0);
@@ -211,7 +213,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
   for (int r = 0; cur.nrows > 0; ++r) {
     const int nq = (cur.nrows + 15) >> 4;  // column tiles in use (wave-uniform)
     const int kv_hi = cur.kv_hi;
-    const auto kb = stripe(kbase_of(cur)), vb = stripe(vbase_of(cur));
+    const auto kb = stripe(kbase_of(cur), kv_hi), vb = stripe(vbase_of(cur), kv_hi);
     int qpos[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
@@ -231,7 +233,6 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
     }
     for (int sb = first_step(cur); sb < kv_hi; sb += STRIDE) {
       const int sn = sb + STRIDE;
-      const bool more = sn < kv_hi;
       const bool full = sb + ATTN_STEP - 1 <= full_lim;  // wave-uniform: no position of the step is masked
       lsk_bf16x8 pb[QT];
       float alpha[QT];
@@ -281,7 +282,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
           m_run[qt] = m_new;
         }
       }
-      if (more) load_k(kb, sn);  // the next step's K streams in during this step's P.V
+      load_k(kb, sn);  // the next step's K streams in during this step's P.V (zeros past the range)
 #pragma unroll
       for (int qt = 0; qt < QT; ++qt) {
         if (qt < nq) {
@@ -295,7 +296,7 @@ __global__ __launch_bounds__(64 * ATTN_WAVES, 1) void attn_bf16_kernel(
           }
         }
       }
-      if (more) load_v(vb, sn);
+      load_v(vb, sn);
     }
     // the next item's Q and first K / V loads fly while this item is merged
     const Item done = cur;
