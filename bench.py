@@ -181,15 +181,13 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     def pv(n, m, kk):
         return part[:kk * m * n].view(kk, m, n)
 
-    # LM-head calls of the same steps: one call for the drafts and the verify tokens when they fit one GEMM
-    # token tile (the engine merges them), else one each
+    # LM-head calls of the same steps: in a deep step one call for the drafts and the verify tokens (the engine
+    # merges them), in a shallow step one for the drafts
     head_seq = []
     for st in trace[:n_steps]:
         nd, nv = int(st.get("n_draft", len(st["sh"]))), sum(b[2] for b in st["dp"])
-        if nv and nd + nv <= _lsk.GEMM_TOKEN_TILE:
+        if nd + nv:
             head_seq.append((nd + nv, None))
-        else:
-            head_seq += [(mm, None) for mm in (nd, nv) if mm]
     V = c.vocab_size
     m_max = max(m_max, max((m for m, _ in head_seq), default=1))
     if x.shape[0] < m_max:
@@ -264,12 +262,12 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     return out
 
 
-def tokens_roofline(cfg, trace: list, k: int, head_tile: int) -> dict:
+def tokens_roofline(cfg, trace: list, k: int) -> dict:
     """Generated tokens/s the measured steps would reach if every kernel ran at its roofline: for each step,
     sum over its launches of t_roof = max(algorithmic bytes / 8 TB/s, flops / 2.5166 PFLOP/s) -- per layer
     the four projection GEMMs (weights + activations + outputs), attention (the unpadded KV of its blocks read
-    once + Q and O), the two RMSNorms and RoPE + append; per step the LM-head launches (drafts and verify tokens
-    share one when they fit one token tile, as the engine does) -- then committed tokens / total t_roof."""
+    once + Q and O), the two RMSNorms and RoPE + append; per step the LM-head launch (drafts and verify tokens
+    share one, as the engine does) -- then committed tokens / total t_roof."""
     dim, ffn, V = cfg.dim, cfg.intermediate_size, cfg.vocab_size
     qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
     bw, fl = HBM_PEAK_GBS * 1e9, BF16_PEAK_TFLOPS * 1e12
@@ -292,8 +290,8 @@ def tokens_roofline(cfg, trace: list, k: int, head_tile: int) -> dict:
         if st["dp"]:
             total += (cfg.n_layers - k) * layer(st["dp"])
         nd, nv = int(st.get("n_draft", 0)), sum(b[2] for b in st["dp"])
-        heads = [nd + nv] if nv and nd + nv <= head_tile else [x for x in (nd, nv) if x]
-        total += sum(gemm(h, V, dim) for h in heads)
+        if nd + nv:
+            total += gemm(nd + nv, V, dim)
         tokens += st["committed"]
     return {"tokens_per_s": round(tokens / total, 1) if total > 0 else None, "t_roof_ms": round(1e3 * total, 3),
             "steps": len(trace), "committed_tokens": tokens,
@@ -649,7 +647,7 @@ def main():
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
     from thesis_amd import _lsk as _l
 
-    troof = tokens_roofline(cfg, trace, 8, _l.GEMM_TOKEN_TILE) if trace else None
+    troof = tokens_roofline(cfg, trace, 8) if trace else None
     if troof and troof["tokens_per_s"]:
         troof["measured_tokens_per_s"] = round(committed / elapsed, 2)
         troof["frac"] = round(committed / elapsed / troof["tokens_per_s"], 4)

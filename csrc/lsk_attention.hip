@@ -644,6 +644,11 @@ static int rows_cap_for(const int32_t* blocks, int nb, int group, int split, int
     return n * n_kv_heads;
   };
   if (items_at(ATTN_ROWS) >= 2L * n_slots) return ATTN_ROWS;  // several items per workgroup: fewest bytes wins
+  // every block fits one 16-row item: all caps give the same items, and the one-tile kernel's estimate is the
+  // smallest (the wider kernels add a per-item cost), so the loop below would pick 16
+  bool small = true;
+  for (int b = 0; b < nb && small; ++b) small = (long)blocks[b * 4 + 2] * group <= 16;
+  if (small) return 16;
   thread_local std::vector<double> cost;
   thread_local std::vector<double> load;
   const double pos_bytes = 4.0 * head_dim;  // K and V, bf16, one KV head

@@ -364,7 +364,8 @@ def pack_segment(rows: np.ndarray, pos0: np.ndarray, T: np.ndarray, group: int, 
         if rc == -2:
             raise ValueError(lib.lsk_last_error().decode())
         _check(rc, "lsk_pack_segment")
-        return buf[:int(cnt[5])].copy(), tuple(int(c) for c in cnt)
+        c = cnt.tolist()
+        return buf[:c[5]].copy(), tuple(c)
     raise LskError("lsk_pack_segment: metadata buffer")
 
 

@@ -198,6 +198,7 @@ class EESDEngine:
         m.allocate_cache(B, max_prompt + self.max_new + self.cfg.d_max + 40)
         self.seq_buf = torch.zeros(B, self.Dm1, dtype=torch.long, device=self.dev)
         self.exit_h = torch.zeros(B, self.Dm1, m.cfg.dim, dtype=m.dtype, device=self.dev)
+        self._flat_views = (self.seq_buf.view(-1), self.exit_h.view(-1, m.cfg.dim))
         self.state = np.zeros(B, dtype=np.int64)        # FREE / PREFILL / DECODE
         self.pos = np.zeros(B, dtype=np.int64)          # committed length = position of the current input token
         self.d = np.zeros(B, dtype=np.int64)            # drafts held
@@ -244,7 +245,8 @@ class EESDEngine:
         return self._commit(slot, [first])
 
     def _flat(self):
-        return self.seq_buf.view(-1), self.exit_h.view(-1, self.exit_h.shape[-1])
+        """(seq_buf flat, exit_h as rows): views made once with the buffers (a step's host path is latency)."""
+        return self._flat_views
 
     # ------------------------------------------------------------------ assignment / prefill
     def _piggyback(self, req: Request) -> bool:
@@ -504,16 +506,17 @@ class EESDEngine:
         m = self.m
         sb, _ = self._flat()
         n_verify = int((d[V] + 1).sum()) if deep else 0
-        merge_heads = deep and not probe and nd + n_verify <= _lsk.GEMM_TOKEN_TILE
+        merge_heads = deep and not probe
         if nd and not merge_heads:
             hx = m.buffer("x_draft", (nd, m.cfg.dim), m.dtype)
             _lsk.copy_rows(hx, None, h, drf_src_t, nd)
             m.head_argmax(hx, out=sb, dst_idx=drf_dst_t)                  # seq_buf[i, d_i + 1] = draft
         readback, n_v_tok, vinfo, cfin = None, 0, ([], [], []), []
         if deep:
-            # the drafts are first read next step, so when the rows fit one GEMM token tile their head shares
-            # the verify head's launch (one pass over the LM head weights per step); the batch-invariant GEMM
-            # gives every row the same result either way
+            # the drafts are first read next step, so their head shares the verify head's launch: one pass over
+            # the LM head weights per step (above 64 rows the wide tier still reads them once: 65-128 rows cost
+            # ~270 us on MI355X against ~340-370 us for two launches); the batch-invariant GEMM gives every row
+            # the same result either way
             draft = (h, drf_src_t, drf_dst_t, nd) if merge_heads else (h, None, None, 0)
             probe_ctx = (pb, kb, sb_slot, cap_sh) if probe else None
             readback, n_v_tok, vinfo, cfin = self._deep(V, d, draft, probe_ctx)

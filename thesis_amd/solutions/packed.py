@@ -206,7 +206,7 @@ def build_packed_arrays(model, rows, pos0, T, bucketing: str = "exact", tags: Op
                      nb=nb, n_works=nw, n_groups=ng, n_parts=n_parts, n_rounds=n_rounds, n_slots=n_slots,
                      rows_cap=rows_cap, _model=model, meta_host=meta, kv_read=kv_read, kv_read_padded=kv_padded,
                      kv_gathered=kv_gathered, _bucketing=bucketing)
-    if bucketing == "exact" and nb:
+    if bucketing == "exact" and nb and Ts[0] != Ts[-1]:            # (Ts ascending: equal ends = one bucket)
         pb._bounds = np.concatenate([[0], np.flatnonzero(np.diff(Ts)) + 1, [nb]])
     else:
         pb._bounds = np.array([0, nb]) if nb else np.array([0])
