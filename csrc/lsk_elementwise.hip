@@ -615,3 +615,53 @@ extern "C" int lsk_kv_rollback(int64_t* kv_len, const int32_t* slots, const int6
   kv_rollback_kernel<<<(nv + 63) / 64, 64, 0, (hipStream_t)stream>>>(kv_len, slots, accepted, nv);
   return lsk_check_launch("lsk_kv_rollback");
 }
+
+// ----------------------------------------------------------------------------- segment planned ahead of acceptance
+// A decode segment planned before the previous step's acceptance is known: every block in cache row vslots[j]
+// was planned at the position it has if all vdrafts[j] drafts of that verifier are accepted, and acc[j] (the
+// greedy acceptance's output, still on the device) is the accepted count, so the block's actual position is
+// acc[j] - vdrafts[j] (<= 0) away.  The kernel moves those blocks in the segment's metadata (lsk_pack_segment's
+// layout): each token's position, each block's pos0, and each work record's pos0 and, for the record that ends
+// at its rows' last position (the last KV split), kv_hi.  Valid when the shift never changes a block's number
+// of KV splits; the caller checks that when it plans.  One workgroup: a decode segment's metadata is small.
+__global__ __launch_bounds__(256) void shift_positions_kernel(int32_t* __restrict__ meta, int N, int nb, int nw,
+                                                              int ng, int n_recs, int group,
+                                                              const int64_t* __restrict__ acc,
+                                                              const int32_t* __restrict__ vslots,
+                                                              const int32_t* __restrict__ vdrafts, int nv) {
+  auto delta_of = [&](int row) {
+    for (int j = 0; j < nv; ++j)
+      if (vslots[j] == row) return (int)acc[j] - vdrafts[j];
+    return 0;
+  };
+  auto fix = [&](int32_t* r) {  // [q_start, row0, nrows | kvh << 8, kv_lo, kv_hi, part, pos0, crow]
+    const int dl = delta_of(r[7]);
+    if (dl == 0) return;
+    const int end_old = r[6] + (r[1] + (r[2] & 255) - 1) / group + 1;
+    if (r[4] == end_old) r[4] += dl;
+    r[6] += dl;
+  };
+  const int32_t* rows_h = meta;
+  int32_t* pos_h = meta + N;
+  int32_t* blk = meta + 2L * N;
+  int32_t* works = blk + 4L * nb;
+  int32_t* recs = works + 8L * nw + 8L * ng;
+  for (int t = threadIdx.x; t < N; t += blockDim.x) pos_h[t] += delta_of(rows_h[t]);
+  for (int b = threadIdx.x; b < nb; b += blockDim.x) blk[4L * b + 1] += delta_of(blk[4L * b + 3]);
+  for (int w = threadIdx.x; w < nw; w += blockDim.x) fix(works + 8L * w);
+  for (int r = threadIdx.x; r < n_recs; r += blockDim.x)
+    if ((recs[8L * r + 2] & 255) > 0) fix(recs + 8L * r);
+}
+
+extern "C" int lsk_shift_segment_positions(int32_t* meta, int n_tokens, int nb, int n_works, int n_groups,
+                                           int n_recs, int group, const int64_t* accepted, const int32_t* vslots,
+                                           const int32_t* vdrafts, int nv, void* stream) {
+  LSK_REQUIRE(n_tokens >= 0 && nb >= 0 && n_works >= 0 && n_groups >= 0 && n_recs >= 0 && group > 0 && nv >= 0,
+              LSK_ESHAPE, "lsk_shift_segment_positions: bad shape");
+  LSK_REQUIRE((meta != nullptr || n_tokens == 0) && (nv == 0 || (accepted && vslots && vdrafts)), LSK_EARG,
+              "lsk_shift_segment_positions: null pointer");
+  if (nv == 0 || n_tokens == 0) return 0;
+  shift_positions_kernel<<<1, 256, 0, (hipStream_t)stream>>>(meta, n_tokens, nb, n_works, n_groups, n_recs, group,
+                                                             accepted, vslots, vdrafts, nv);
+  return lsk_check_launch("lsk_shift_segment_positions");
+}

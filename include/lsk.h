@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 8
+#define LSK_ABI_VERSION 9
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -226,6 +226,17 @@ int lsk_probe_matches(const int64_t* pred, const int64_t* Yv, const int64_t* acc
 /* Pointer rollback: kv_len[slots[j]] += accepted[j] + 1; moves no KV.
  * Replaces solutions/engine.py:381-384 (pos += a + 1; d = 0) for a device-resident length array. */
 int lsk_kv_rollback(int64_t* kv_len, const int32_t* slots, const int64_t* accepted, int nv, void* stream);
+
+/* No counterpart in the reference (it plans each step after the previous one's readback).  Moves the blocks of a
+   decode segment that was planned before the previous step's acceptance was read back: every block in cache row
+   vslots[j] was planned at the position it has if all vdrafts[j] drafts are accepted; accepted[j] (device, the
+   greedy acceptance's acc_out) gives the actual one.  meta: the segment's metadata as lsk_pack_segment writes it
+   (device; n_tokens, nb, n_works, n_groups from its counts, n_recs = n_slots * n_rounds); group = query heads per
+   KV head.  Updates each token's position, each block's pos0 and the work records' pos0 / final kv_hi in place.
+   The caller guarantees the move never changes a block's number of KV splits. */
+int lsk_shift_segment_positions(int32_t* meta, int n_tokens, int nb, int n_works, int n_groups, int n_recs, int group,
+                                const int64_t* accepted, const int32_t* vslots, const int32_t* vdrafts, int nv,
+                                void* stream);
 
 /* ---- native layer-range runner (solutions/packed.py:169-196, packed_layer / packed_layers) ----
  * A model handle holds host copies of per-layer device pointers (weights [out, in]: packed for bf16,

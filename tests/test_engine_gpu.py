@@ -474,7 +474,8 @@ def test_rollback_moves_no_kv(cuda):
 
 def test_shallow_steps_do_not_synchronise(cuda, monkeypatch):
     """No device->host read and no event / stream / device synchronisation in shallow steps (graph-replayed ones
-    included); exactly one read per deep step (tests/test_eesd.py:199-223)."""
+    included); exactly one host wait per deep step, the readback (tests/test_eesd.py:199-223): an asynchronous
+    copy into pinned memory and one event wait, after the next step's shallow segment was launched ahead."""
     from thesis_amd.solutions.cost_model import synthetic_cost_model
     from thesis_amd.solutions.engine import EESDEngine, EngineConfig, Request
 
@@ -516,8 +517,24 @@ def test_shallow_steps_do_not_synchronise(cuda, monkeypatch):
         eng.step()
         kind = eng.records[n_rec].kind
         kinds.append(kind)
-        if eng.graphs.captures > captures:          # capturing a graph (once per shape) synchronises by itself
-            calls = [c for c in calls if not c.endswith("synchronize")]
+        if eng.graphs.captures > captures:          # capturing a graph (once per shape) synchronises the device
+            calls = [c for c in calls if c != "cuda.synchronize"]
         replayed += eng.graphs.replays - replays
         assert len(calls) == (0 if kind == "shallow" else 1), (kind, calls)
     assert "shallow" in kinds and "deep" in kinds and replayed > 0
+
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("forced", [None, 0.3])
+def test_launch_ahead_shallow_segments_change_no_token(cuda, dtype, forced):
+    """Launching each deep step's successor shallow segment before the readback (planned at the verifiers'
+    upper-bound positions, moved back on the device) gives the tokens of steps that plan after the readback, and
+    the launched-ahead segments really run."""
+    ocfg = small_cfg()
+    _, g = _pair(ocfg, dtype, std=0.1)
+    prompts = _prompts(6, ocfg.vocab_size, seed=11)
+    kw = dict(sched="aspire", k=2, gamma=4, d_max=6, forced_accept_p=forced, forced_seed=3)
+    plain, _, _ = _run_gpu(g, prompts, 3, 30, launch_ahead=False, **kw)
+    ahead, eng, _ = _run_gpu(g, prompts, 3, 30, launch_ahead=True, **kw)
+    assert ahead == plain
+    assert eng.ahead_used > 0

@@ -639,3 +639,53 @@ def test_fragment_major_gemms_are_bitwise_the_row_major_ones(cuda, M):
     back = lsk.PackedWeight.__new__(lsk.PackedWeight)                      # view h2 as packed [m16, 12288]
     back.shape, back.dtype, back.device, back.data = (m16, 12288), BF16, h2.device, h2
     assert torch.equal(back.unpack()[:M], h_row)
+
+
+@pytest.mark.parametrize("split", [4096, 128])
+def test_shifted_segment_metadata_equals_a_plan_at_the_actual_positions(cuda, split):
+    """A decode segment planned at its verifiers' upper-bound positions (all drafts accepted) and moved back on the
+    device by lsk_shift_segment_positions holds the metadata of a plan made at the actual positions: the same
+    tokens, positions and blocks, the same work records, and schedule records that are those works once per KV
+    head (the slots they land on may differ: the schedule was costed at the bound).  With 128-position splits the
+    blocks span several KV splits and only the last one's end moves."""
+    lsk = _lsk()
+    rng = np.random.default_rng(split)
+    B, Hkv, group, D, n_slots = 24, 8, 4, 128, 256
+    rows = np.arange(B, dtype=np.int64)
+    base = rng.integers(100, 1500, size=B).astype(np.int64)
+    vs = np.sort(rng.choice(B, size=10, replace=False))
+    dr = rng.integers(1, 9, size=len(vs)).astype(np.int64)            # drafts held by each verifier
+    acc = np.array([rng.integers(0, d + 1) for d in dr], dtype=np.int64)
+    if split == 128:                                                   # keep every verifier inside one split count
+        for j, i in enumerate(vs):
+            lo, hi = base[i] + 2, base[i] + dr[j] + 2
+            if (lo + split - 1) // split != (hi + split - 1) // split:
+                base[i] = base[i] // split * split + 5                  # KV ends base + 7 .. base + 15
+    est = base + 1
+    est[vs] += dr                                                       # upper bound: all drafts accepted
+    actual = est.copy()
+    actual[vs] -= dr - acc
+    T = np.ones(B, dtype=np.int64)
+    args = (group, split, Hkv, D, n_slots, 0, B, 4096, 4096)
+    meta_e, cnt_e = lsk.pack_segment(rows, est, T, *args)
+    meta_a, cnt_a = lsk.pack_segment(rows, actual, T, *args)
+    N, nw, ng = cnt_e[0], cnt_e[1], cnt_e[2]
+    assert (N, nw, ng) == tuple(cnt_a[:3])
+    dev = torch.as_tensor(meta_e).to(cuda)
+    acc_t = torch.as_tensor(acc).to(cuda)
+    lsk.shift_segment_positions(dev, N, B, nw, ng, n_slots * cnt_e[4], group, acc_t,
+                                torch.as_tensor(vs.astype(np.int32)).to(cuda),
+                                torch.as_tensor(dr.astype(np.int32)).to(cuda), len(vs))
+    got = dev.cpu().numpy()
+    head = 2 * N + 4 * B
+    assert np.array_equal(got[:head], meta_a[:head])                  # rows, positions, blocks
+    w_got = got[head:head + 8 * nw].reshape(-1, 8)
+    w_ref = meta_a[head:head + 8 * nw].reshape(-1, 8)
+    key = lambda a: sorted(map(tuple, a.tolist()))                    # noqa: E731
+    assert key(w_got) == key(w_ref)
+    if split == 128:
+        assert nw > B                                                 # several splits per block
+    r_got = got[head + 8 * nw + 8 * ng:].reshape(-1, 8)
+    r_ref = meta_a[head + 8 * nw + 8 * ng:].reshape(-1, 8)
+    live = lambda r: r[(r[:, 2] & 255) > 0]                           # noqa: E731
+    assert key(live(r_got)) == key(live(r_ref))

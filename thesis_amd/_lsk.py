@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -57,6 +57,7 @@ _SIGS = {
     "lsk_argmax": (_I, [_I, _P, _L, _I, _I, _P, _P, _P]),
     "lsk_greedy_accept": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _P, _P, _P, _P]),
     "lsk_kv_rollback": (_I, [_P, _P, _P, _I, _P]),
+    "lsk_shift_segment_positions": (_I, [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _I, _P]),
     "lsk_probe_matches": (_I, [_P, _P, _P, _P, _P, _I, _I, _P, _P]),
     "lsk_model_create": (_L, [_I, _I, _I, _I, _I, _I, _I, _I, _F] + [_P] * 8 + [_I, _I, _P, _P, _I]),
     "lsk_model_destroy": (_I, [_L]),
@@ -465,6 +466,17 @@ def probe_matches(pred, Yv, acc, blk_i32, jl_i32, nc: int, nvt: int, out) -> Non
 def kv_rollback(kv_len, slots, accepted, nv):
     _dev(kv_len, slots, accepted)
     _check(load().lsk_kv_rollback(_ptr(kv_len), _ptr(slots), _ptr(accepted), nv, _stream()), "lsk_kv_rollback")
+
+
+def shift_segment_positions(meta, n_tokens: int, nb: int, n_works: int, n_groups: int, n_recs: int, group: int,
+                            accepted, vslots, vdrafts, nv: int) -> None:
+    """lsk_shift_segment_positions on a segment's device metadata `meta` (int32, pack_segment's layout; n_recs =
+    n_slots * n_rounds of its plan): blocks in cache row vslots[j] planned vdrafts[j] - accepted[j] positions ahead
+    move back to their actual positions (accepted: the device acc_out of greedy_accept)."""
+    _dev(meta, accepted, vslots, vdrafts)
+    _check(load().lsk_shift_segment_positions(_ptr(meta), n_tokens, nb, n_works, n_groups, n_recs, group,
+                                              _ptr(accepted), _ptr(vslots), _ptr(vdrafts), nv, _stream()),
+           "lsk_shift_segment_positions")
 
 
 # ----------------------------------------------------------------------------- layer-range runner

@@ -45,7 +45,7 @@ from ..common.driver import MeasureWindow, PoissonArrivals, run_arrivals, run_po
 from ..common.engine import commit_tokens
 from ..common.timing import DeviceSpan
 from .exit_select import ExitController
-from .packed import Block, build_packed, build_packed_arrays, packed_layers, upload, upload_many
+from .packed import Block, _attn_work, build_packed, build_packed_arrays, packed_layers, upload, upload_many
 from .prefill import M3Planner
 from .schedulers import make_scheduler
 from .step_graph import ShallowGraphs
@@ -94,6 +94,7 @@ class EngineConfig:
     forced_accept_p: Optional[float] = None
     forced_seed: int = 0
     graphs: bool = True
+    launch_ahead: bool = True          # launch the next shallow segment before a deep step's readback
 
     def check(self, n_layers: int) -> None:
         """ValueError for option combinations the engine cannot run."""
@@ -132,6 +133,18 @@ class Request:
     pf_dp: int = 0                  # prompt tokens already through every layer (M3)
     piggybacked: int = 0            # prompt tokens carried by decode steps (M3)
     key: int = -1                   # assignment counter: the forced-acceptance stream of the request
+
+
+_RB_HOST: list = []
+
+
+def _pinned_readback(n: int) -> torch.Tensor:
+    """n int64 of a process-wide pinned buffer for step readbacks (grown, never freed: pinned memory released
+    while a graph is being captured would record on the capturing stream).  Engines in one process read back
+    one after another (each waits for its copy before the next step)."""
+    if not _RB_HOST or _RB_HOST[0].numel() < n:
+        _RB_HOST[:] = [torch.empty(max(n, 1024), dtype=torch.long, pin_memory=True)] + _RB_HOST
+    return _RB_HOST[0][:n]
 
 
 @dataclass
@@ -219,6 +232,9 @@ class EESDEngine:
                             cfg.knee_safety) if cfg.prefill == "m3" else None
         self.forced = ForcedAcceptance(cfg.forced_accept_p, cfg.forced_seed) if cfg.forced_accept_p else None
         self.graphs = ShallowGraphs(self.dev) if cfg.graphs and spec else None
+        self.launch_ahead = cfg.launch_ahead and spec
+        self._ahead = None                 # the shallow segment _launch_ahead started for the next step
+        self.ahead_used = 0                # steps that ran the shallow segment launched ahead of the readback
 
     # ------------------------------------------------------------------ bookkeeping
     def _log(self, kind, span, **kw) -> StepEntry:
@@ -346,8 +362,9 @@ class EESDEngine:
         dec = self.state == DECODE
         d = self.d.copy()
         ctx = np.where(dec, self.pos + d, 0)
+        ahead, self._ahead = self._ahead, None
         if self.m3 is None and self.exitc is None and dec.any():
-            return self._spec_step_early(dec, d, ctx, t0)
+            return self._spec_step_early(dec, d, ctx, t0, ahead)
         return self._spec_step_general(dec, d, ctx, t0)
 
     def _spec_step_general(self, dec, d, ctx, t0):
@@ -451,41 +468,23 @@ class EESDEngine:
         return self._finish_step(V, d, deep, probe, chunks, h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, kb,
                                  sb_slot, cap_sh, N, Dr)
 
-    def _spec_step_early(self, dec, d, ctx, t0):
+    def _spec_step_early(self, dec, d, ctx, t0, ahead=None):
         """Steps without M2 probes or M3 chunks: the shallow segment (one token at pos + d per decoding slot,
         whatever the verify set) is staged and launched first -- replayed as a graph when its shape repeats --
-        and the draft policy's host time overlaps it on the device.  Then the draft head and the deep segment
-        follow as in any step; every launch is the one the general path makes, in the same stream order."""
-        m, cfg, k, Dm1 = self.m, self.cfg, self.k, self.Dm1
+        and the draft policy's host time overlaps it on the device.  After a deep step it was launched before that
+        step's readback (_launch_ahead), so the device never waits for the host between steps.  Then the draft
+        head and the deep segment follow as in any step; every launch is the one the general path makes, in the
+        same stream order."""
         dslots = np.flatnonzero(dec)
-        pb = build_packed_arrays(m, dslots, self.pos[dslots] + d[dslots], np.ones(len(dslots), dtype=np.int64),
-                                 cfg.bucketing, upload_meta=False)
-        N = pb.n_tokens
-        sl = dslots[pb.order]
-        sel = sl * Dm1 + d[sl]
-        self._count_kv(pb, k)
-        sb, exh = self._flat()
-        span = DeviceSpan(self.dev).open()
-        if self.graphs is not None and not _lsk.Profiler.enabled:
-            gkey = ("early", N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_rounds, pb.n_slots, pb.rows_cap, k)
-            (pb.meta, sel_t), gentry = self.graphs.stage(gkey, [pb.meta_host, sel])
-
-            def shallow_gpu():
-                xg = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
-                _lsk.embed(m.embed_w, sel_t, xg, sb, sel_t)
-                hg = packed_layers(m, xg, pb, 0, k)
-                _lsk.copy_rows(exh, sel_t, hg, None, N)                  # exit_h[i, d_i] = h
-                return hg
-            self.graphs.run(gentry, lambda: m.buf_epoch, shallow_gpu)
-            h = gentry.out
+        sh = self._take_ahead(ahead, dslots, d)
+        if sh is None:
+            sh = self._shallow_early(dslots, self.pos[dslots] + d[dslots], d)
+            plan_ms = 1000 * (time.perf_counter() - t0)
         else:
-            pb.meta, sel_t = upload_many([pb.meta_host, sel], self.dev)
-            x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
-            _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
-            h = packed_layers(m, x, pb, 0, k)
-            _lsk.copy_rows(exh, sel_t, h, None, N)
+            plan_ms = sh["plan_ms"] + 1000 * (time.perf_counter() - t0)
+        pb, sl, sel, h, N, span = sh["pb"], sh["sl"], sh["sel"], sh["h"], sh["N"], sh["span"]
+        self._count_kv(pb, self.k)
         t1 = time.perf_counter()
-        plan_ms = 1000 * (t1 - t0)
         V = self._verify_set(d, ctx, dec)
         deep = bool(V.any())
         Dr = dec & ~V
@@ -498,6 +497,109 @@ class EESDEngine:
         plan_ms += 1000 * (time.perf_counter() - t1)
         return self._finish_step(V, d, deep, False, [], h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, None, None,
                                  None, N, Dr)
+
+    def _shallow_early(self, dslots, positions, dnext, shift=None) -> dict:
+        """Plan, stage and launch the early path's shallow segment: one token per slot of dslots at `positions`,
+        input seq_buf[i, dnext[i]], exit state to exit_h[i, dnext[i]].  shift = (accepted device tensor, vslots
+        device int32, vdrafts device int32, nv): the plan's positions are upper bounds for those slots, corrected
+        on the device (lsk_shift_segment_positions) before the segment runs."""
+        m, k, Dm1 = self.m, self.k, self.Dm1
+        pb = build_packed_arrays(m, dslots, positions, np.ones(len(dslots), dtype=np.int64), self.cfg.bucketing,
+                                 upload_meta=False)
+        N = pb.n_tokens
+        sl = dslots[pb.order]
+        sel = sl * Dm1 + dnext[sl]
+        sb, exh = self._flat()
+        span = DeviceSpan(self.dev).open()
+
+        def shift_meta():
+            if shift is not None:
+                acc_t, vslots_t, vdrafts_t, nv = shift
+                _lsk.shift_segment_positions(pb.meta, N, pb.nb, pb.n_works, pb.n_groups, pb.n_slots * pb.n_rounds,
+                                             m.group, acc_t, vslots_t, vdrafts_t, nv)
+        if self.graphs is not None and not _lsk.Profiler.enabled:
+            gkey = ("early", N, pb.nb, pb.n_works, pb.n_groups, pb.n_parts, pb.n_rounds, pb.n_slots, pb.rows_cap, k)
+            (pb.meta, sel_t), gentry = self.graphs.stage(gkey, [pb.meta_host, sel])
+            shift_meta()
+
+            def shallow_gpu():
+                xg = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+                _lsk.embed(m.embed_w, sel_t, xg, sb, sel_t)
+                hg = packed_layers(m, xg, pb, 0, k)
+                _lsk.copy_rows(exh, sel_t, hg, None, N)                  # exit_h[i, d_i] = h
+                return hg
+            self.graphs.run(gentry, lambda: m.buf_epoch, shallow_gpu)
+            h = gentry.out
+        else:
+            pb.meta, sel_t = upload_many([pb.meta_host, sel], self.dev)
+            shift_meta()
+            x = m.buffer("x_in", (N, m.cfg.dim), m.dtype)
+            _lsk.embed(m.embed_w, sel_t, x, sb, sel_t)
+            h = packed_layers(m, x, pb, 0, k)
+            _lsk.copy_rows(exh, sel_t, h, None, N)
+        return {"pb": pb, "sl": sl, "sel": sel, "h": h, "N": N, "span": span}
+
+    def _launch_ahead(self, V, d, vslots, acc_t) -> None:
+        """At the end of a deep step, before its readback: launch the next step's shallow segment (the early
+        path's), so the device runs it while the host reads the acceptance back and plans.  Every decoding slot
+        gets one token; a verifier's next position depends on its accepted count, so the segment is planned at
+        its upper bound (all d drafts accepted) and moved back on the device from greedy_accept's output.  Skipped
+        when a verifier's possible positions straddle a KV split (the plan's shape would depend on the count) or
+        the upper bound leaves the cache.  A slot whose request finishes at this readback computes one unused
+        token; its cache row is free until a new request's prefill rewrites it."""
+        if not self.launch_ahead or self.m3 is not None or self.exitc is not None or self.cfg.mode == "ar":
+            return
+        if self.dev.type != "cuda" or not vslots:
+            return
+        t0 = time.perf_counter()
+        dec = self.state == DECODE
+        dslots = np.flatnonzero(dec)
+        if not len(dslots):
+            return
+        m = self.m
+        vs = np.asarray(vslots, dtype=np.int64)
+        dnext = self.d.copy()                                              # drafting slots: d + 1 already
+        dnext[vs] = 0
+        est = self.pos + d + 1                                             # every slot's next position (upper bound)
+        split = m.cache.attn_split
+        lo_end, hi_end = self.pos[vs] + 2, self.pos[vs] + d[vs] + 2        # a verifier's possible KV ends
+        if ((lo_end + split - 1) // split != (hi_end + split - 1) // split).any():
+            return
+        if int(est[dslots].max()) + 1 > min(m.cache.max_seq, m.rope_cos.shape[0]):
+            return
+        vslots_t, vdrafts_t = upload_many([vs.astype(np.int32), d[vs].astype(np.int32)], self.dev)
+        sh = self._shallow_early(dslots, est[dslots], dnext, (acc_t, vslots_t, vdrafts_t, len(vs)))
+        sh.update(slots=dslots, reqs=[self.req[i] for i in dslots], est=est.copy(), vslots=vs, vdrafts=d[vs].copy(),
+                  plan_ms=1000 * (time.perf_counter() - t0))
+        self._ahead = sh
+
+    def _take_ahead(self, sh, dslots, d):
+        """The shallow segment _launch_ahead started for this step (sh), when it covers every decoding slot with
+        the request it was planned for.  Otherwise (a slot started decoding since, or a freed slot took a new
+        request) the step plans its own segment, which rewrites the same values for the slots both cover; the
+        ahead segment's other writes lie at positions its row's next request writes before reading.  Its host
+        copies of the positions are set to the actual ones."""
+        if sh is None or "acc" not in sh:
+            return None
+        planned = dict(zip(sh["slots"].tolist(), sh["reqs"]))
+        if any(planned.get(i, None) is not self.req[i] for i in dslots.tolist()):
+            return None
+        actual = self.pos + d
+        want = sh["est"].copy()
+        want[sh["vslots"]] -= sh["vdrafts"] - sh["acc"]
+        if not np.array_equal(actual[dslots], want[dslots]):
+            raise RuntimeError("launch-ahead shallow segment: planned positions disagree with the committed ones")
+        pb = sh["pb"]
+        pos = actual[sh["sl"]]
+        meta, cnt = _lsk.pack_segment(pb.blk_rows, pos, pb.blk_T, self.m.group, self.m.cache.attn_split,
+                                      self.m.cfg.n_kv_heads, self.m.cfg.head_dim, pb.n_slots,
+                                      0 if self.cfg.bucketing == "exact" else 1, self.m.cache.max_batch,
+                                      self.m.cache.max_seq, self.m.rope_cos.shape[0])
+        pb.blk_pos0, pb.pos_h = pos, np.repeat(pos, pb.blk_T)              # T = 1: one position per block
+        pb.kv_read, pb.kv_read_padded, pb.kv_gathered = cnt[6], cnt[7], cnt[8]
+        _attn_work(pb, self.m, cnt[6], cnt[9])
+        self.ahead_used += 1
+        return sh
 
     def _finish_step(self, V, d, deep, probe, chunks, h, nd, drf_src_t, drf_dst_t, span, plan_ms, pb, kb, sb_slot,
                      cap_sh, N, Dr):
@@ -519,7 +621,8 @@ class EESDEngine:
             # the same result either way
             draft = (h, drf_src_t, drf_dst_t, nd) if merge_heads else (h, None, None, 0)
             probe_ctx = (pb, kb, sb_slot, cap_sh) if probe else None
-            readback, n_v_tok, vinfo, cfin = self._deep(V, d, draft, probe_ctx)
+            rb_dev, n_v_tok, vinfo, cfin = self._deep(V, d, draft, probe_ctx)
+            readback = self._readback(rb_dev)
         span.close()
         n_chunk = sum(c[2] for c in chunks)
         self._log("probe" if probe else ("deep" if deep else "shallow"), span, n_sh=N, n_dp=n_v_tok, n_chunk=n_chunk,
@@ -539,10 +642,13 @@ class EESDEngine:
             self.steps_since_deep += 1
             self._tally(0, deep=False, plan_ms=plan_ms)
             return 0, []
-        rb = readback.tolist()
         vslots, vstarts, vT = vinfo
         nv = len(vslots)
+        self._launch_ahead(V, d, vslots, rb_dev[:nv])
+        rb = readback()
         acc = np.array(rb[:nv], dtype=np.int64)
+        if self._ahead is not None:
+            self._ahead["acc"] = acc
         Y = rb[nv:nv + n_v_tok]
         accepted = np.zeros(self.B, dtype=np.int64)
         committed, done = 0, []
@@ -710,7 +816,22 @@ class EESDEngine:
                 for (p0, c, _) in self.pending[i]:
                     self.req[i].pf_dp = p0 + c
                 self.pending[i] = []
-        return rb.cpu(), nvt, (slots_a.tolist(), vstarts_a.tolist(), T_a.tolist()), cfin
+        return rb, nvt, (slots_a.tolist(), vstarts_a.tolist(), T_a.tolist()), cfin
+
+    def _readback(self, rb: torch.Tensor) -> Callable[[], list]:
+        """Start copying the step's device results to the host; the returned call waits for them (a list)."""
+        if rb.device.type != "cuda":
+            return rb.tolist
+        n = rb.numel()
+        host = _pinned_readback(n)
+        host.copy_(rb, non_blocking=True)
+        done = torch.cuda.Event()
+        done.record()
+
+        def wait() -> list:
+            done.synchronize()
+            return host.tolist()
+        return wait
 
     def _probe_counts(self, probe_ctx, cands, slots_a, T_a, vtok_t, x_k, cap_dp, Yv, rb, nv, nvt, blk_t, jl_t, out):
         """Agreement of every candidate exit with Y on the correct-prefix positions (solutions/engine.py:491-514):

@@ -17,6 +17,7 @@ launches (embedding, k layers, exit-state copy, draft head) replay as one captur
 
 from __future__ import annotations
 
+import gc
 from typing import Callable, Optional
 
 import numpy as np
@@ -109,8 +110,17 @@ class ShallowGraphs:
             return "eager"
         before = epoch()
         g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            out = step()
+        # no cyclic garbage collection inside the capture: a collected object holding device resources (pinned
+        # buffers of asynchronous copies, events) can issue a stream operation from its destructor, which the
+        # capturing stream refuses (the process aborts)
+        gc_was = gc.isenabled()
+        gc.disable()
+        try:
+            with torch.cuda.graph(g):
+                out = step()
+        finally:
+            if gc_was:
+                gc.enable()
         if epoch() != before:                 # the capture allocated a model buffer: never replay it
             e.out = step()
             return "eager"
