@@ -532,6 +532,15 @@ def test_committed_mi355x_calibration_is_the_default_and_fits_its_measurements()
         rows = list(csv.DictReader(f))
     assert len(rows) >= 90
     assert max(abs(float(r["roofline"]) - float(r["ms"])) / float(r["ms"]) for r in rows) < 0.4
+    # the other committed shapes load as their presets' defaults too; their linear fits (the ASPIRE 3-parameter
+    # model) stay within 25 % of every validation step
+    for name in ("llama2-7b", "llama3.2-1b"):
+        cm, src = default_cost_model(PRESETS[name])
+        assert isinstance(cm, RooflineCostModel) and f"calibrated on MI355X ({name})" in src
+        with open(calibration_path(name).with_name(f"{name}_mi355x_validation.csv")) as f:
+            rows = list(csv.DictReader(f))
+        assert len(rows) >= 90
+        assert max(abs(float(r["linear"]) - float(r["ms"])) / float(r["ms"]) for r in rows) < 0.25
 
 
 def test_config_parsing_old_and_new_formats(tmp_path):
