@@ -519,14 +519,14 @@ def host_cores() -> tuple:
     return (min(affinity, quota) if quota else affinity), affinity, quota
 
 
-def run_cpu_baseline(args, trace: list, k: int):
+def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch: int = 0, cache_len: int = 0):
     """The CPU oracle replays the GPU run's timed steps (same segment shapes, bf16) on the host cores, in
     order and again from the first when they run out, until ~args.cpu_seconds have elapsed; tokens/s = tokens
     the replayed steps committed / CPU time."""
     from oracle.model import OBlock, OracleConfig, OracleLlama, build_packed, packed_layers
     from thesis_amd.common.model import PRESETS
 
-    c = PRESETS["llama3-8b"]
+    c = PRESETS[preset]
     ocfg = OracleConfig(c.vocab_size, c.dim, c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.intermediate_size,
                         c.norm_eps, c.rope_theta, c.max_position_embeddings)
     threads, affinity, quota = host_cores()
@@ -534,7 +534,7 @@ def run_cpu_baseline(args, trace: list, k: int):
     torch.set_num_threads(threads)
     t0 = time.time()
     m = OracleLlama.synthetic(ocfg, dtype=torch.bfloat16, seed=args.seed, max_seq=2048)
-    m.allocate_cache(args.batch, 1024 + args.max_new + 8 + 40)
+    m.allocate_cache(batch or args.batch, cache_len or 1024 + args.max_new + 8 + 40)
     log(f"[bench] CPU oracle model ready in {time.time() - t0:.1f}s ({threads} threads)")
     g = torch.Generator().manual_seed(0)
     spent, tokens, steps, n_deep = 0.0, 0, 0, 0
@@ -608,6 +608,11 @@ def run_1b_b64(args) -> None:
     troof = tokens_roofline(cfg, eng.trace, k)
     if troof["tokens_per_s"]:
         troof["frac"] = round(committed / elapsed / troof["tokens_per_s"], 4)
+    trace = eng.trace
+    del model, eng
+    torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, k, "llama3.2-1b", B,
+                                                             plen + args.max_new + 8 + 40)
     emit({"metric": "generated tokens/s at 1 GPU (Llama3.2-1B shape, B=64)", "value": round(committed / elapsed, 2),
           "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
           "ms_per_step": round(1e3 * elapsed / args.steps, 3), "higher_is_better": True, "dtype": "bf16",
@@ -615,8 +620,8 @@ def run_1b_b64(args) -> None:
           "config": {"workload": "llama3.2-1b-shape packed self-speculative decode", "B": B, "prompt_len": plen,
                      "max_new": args.max_new, "exit_layer": k, "draft_len": 6, "scheduler": "fixed",
                      "acceptance": "forced geometric p=0.3", "weights": "random init bf16"},
-          "tokens_roofline": troof, "committed_tokens": committed,
-          "deep_steps": sum(1 for st in eng.trace if st["dp"])}, args.out)
+          "tokens_roofline": troof, "cpu_baseline": cpu, "committed_tokens": committed,
+          "deep_steps": sum(1 for st in trace if st["dp"])}, args.out)
 
 
 def run_7b_poisson(args) -> None:
