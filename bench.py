@@ -181,9 +181,15 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     g = torch.Generator(device=model.device).manual_seed(1)
     x = torch.empty(m_max, max(dim, qd, ffn), dtype=model.dtype, device=model.device).normal_(generator=g)
     h = torch.empty(m_max, ffn, dtype=model.dtype, device=model.device)
-    ks = {"qkv": _lsk.gemm_plan(qkvd, dim)[1], "o": _lsk.gemm_plan(dim, qd)[1], "w2": _lsk.gemm_plan(dim, ffn)[1]}
-    part = torch.empty(max(ks["qkv"] * qkvd, ks["o"] * dim, ks["w2"] * dim) * m_max, dtype=torch.float32,
-                       device=model.device)
+    ks = {"o": _lsk.gemm_plan(dim, qd)[1], "w2": _lsk.gemm_plan(dim, ffn)[1]}
+    part = torch.empty(max(ks["o"] * dim, ks["w2"] * dim) * m_max, dtype=torch.float32, device=model.device)
+    # the fused qkv + RoPE + append launch writes q and one scratch cache row (positions 0 .. m - 1)
+    s_kv = (m_max + 31) // 32 * 32
+    q_rep = torch.empty(m_max, c.n_heads, c.head_dim, dtype=model.dtype, device=model.device)
+    kc_rep = torch.zeros(1, c.n_kv_heads, s_kv // 32, c.head_dim // 16, 64, 8, dtype=model.dtype, device=model.device)
+    vc_rep = torch.zeros(1, c.n_kv_heads, s_kv // 32, c.head_dim, 32, dtype=model.dtype, device=model.device)
+    rows_rep = torch.zeros(m_max, dtype=torch.int32, device=model.device)
+    pos_rep = torch.arange(m_max, dtype=torch.int32, device=model.device)
 
     def pv(n, m, kk):
         return part[:kk * m * n].view(kk, m, n)
@@ -223,9 +229,9 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
 
     classes = {
         # name: (launch(m, layer), bytes(m), flops(m), launch list)
-        "gemm_qkv": (lambda m, i: _lsk.gemm_partial_frag(xf, m, model.layers[i].wqkv, ks["qkv"],
-                                                         out=pv(qkvd, m, ks["qkv"])),
-                     lambda m: es * (qkvd * dim + m * dim) + 4.0 * ks["qkv"] * m * qkvd,
+        "gemm_qkv": (lambda m, i: _lsk.gemm_qkv_rope(xf, model.layers[i].wqkv, m, q_rep[:m], kc_rep, vc_rep,
+                                                     model.rope_cos, model.rope_sin, rows_rep[:m], pos_rep[:m]),
+                     lambda m: es * (qkvd * dim + m * dim + m * qkvd) + 8.0 * m * c.head_dim,  # + fp32 cos / sin rows
                      lambda m: 2.0 * m * dim * qkvd),
         "gemm_o": (lambda m, i: _lsk.gemm_partial_frag(xf, m, model.layers[i].wo, ks["o"], out=pv(dim, m, ks["o"])),
                    lambda m: es * (dim * qd + m * qd) + 4.0 * ks["o"] * m * dim,
@@ -272,9 +278,10 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
 def tokens_roofline(cfg, trace: list, k: int) -> dict:
     """Generated tokens/s the measured steps would reach if every kernel ran at its roofline: for each step,
     sum over its launches of t_roof = max(algorithmic bytes / 8 TB/s, flops / 2.5166 PFLOP/s) -- per layer
-    the four projection GEMMs (weights + activations + outputs), attention (the unpadded KV of its blocks read
-    once + Q and O), the two RMSNorms and RoPE + append; per step the LM-head launch (drafts and verify tokens
-    share one, as the engine does) -- then committed tokens / total t_roof."""
+    the four projection GEMMs (weights + activations + outputs; RoPE and the KV append ride the qkv GEMM's
+    output), attention (the unpadded KV of its blocks read once + Q and O) and the two RMSNorms; per step the
+    LM-head launch (drafts and verify tokens share one, as the engine does) -- then committed tokens / total
+    t_roof."""
     dim, ffn, V = cfg.dim, cfg.intermediate_size, cfg.vocab_size
     qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
     bw, fl = HBM_PEAK_GBS * 1e9, BF16_PEAK_TFLOPS * 1e12
@@ -288,7 +295,7 @@ def tokens_roofline(cfg, trace: list, k: int) -> dict:
             return 0.0
         kv = sum(b[1] + b[2] for b in blocks)
         attn = (kv * kvd * 2 * 2 + m * qd * 2 * 2) / bw
-        small = (2 * 2 * m * dim * 2 + 2 * m * (qd + 2 * kvd) * 2) / bw
+        small = (2 * 2 * m * dim * 2 + 8 * m * cfg.head_dim) / bw       # two norms; fp32 RoPE table rows
         return gemm(m, qd + 2 * kvd, dim) + gemm(m, dim, qd) + gemm(m, 2 * ffn, dim) + gemm(m, dim, ffn) + attn + small
 
     total, tokens = 0.0, 0
@@ -303,8 +310,8 @@ def tokens_roofline(cfg, trace: list, k: int) -> dict:
     return {"tokens_per_s": round(tokens / total, 1) if total > 0 else None, "t_roof_ms": round(1e3 * total, 3),
             "steps": len(trace), "committed_tokens": tokens,
             "definition": "committed tokens of the timed steps / sum over their launches of max(bytes / 8 TB/s, "
-                          "flops / 2.5166 PFLOP/s): projection GEMMs, attention (unpadded KV + Q + O), norms, RoPE + "
-                          "append, LM-head launches"}
+                          "flops / 2.5166 PFLOP/s): projection GEMMs (RoPE + append fused into qkv), attention "
+                          "(unpadded KV + Q + O), norms, LM-head launches"}
 
 
 def summarize_kernels(prof: dict) -> dict:

@@ -90,6 +90,22 @@ template <> struct Elem<uint16_t> {
   static __device__ __forceinline__ float round(float v) { return rbf(v); }
 };
 
+// One RoPE rotation pair (common/model.py:143-150 with the cos / sin rows cast to the model dtype first,
+// solutions/packed.py:106-107): x1 = x[j], x2 = x[j + half] of one head at the position whose fp32 table rows are
+// ct / st;  o1 = rnd(x1 c1) + rnd(-x2 s1),  o2 = rnd(x2 c2) + rnd(x1 s2)  with c, s rounded to T and one T rounding
+// after each multiply (the caller's store rounds the add).  Shared by the RoPE + append kernel and the qkv GEMM's
+// fused epilogue, so both give the same bits.
+template <typename T>
+__device__ __forceinline__ void rope_pair(float x1, float x2, const float* ct, const float* st, int j, int half,
+                                          float& o1, float& o2) {
+  const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
+  const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
+  const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
+  const float a2 = Elem<T>::round(x2 * c2), b2 = Elem<T>::round(x1 * s2);
+  o1 = a1 + b1;
+  o2 = a2 + b2;
+}
+
 // ----------------------------------------------------------------------------- host side
 // Error reporting: every C-ABI entry returns 0 on success, a negative code for an argument
 // error detected on the host before any launch, or a positive hipError_t.  The text of the

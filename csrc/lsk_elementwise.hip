@@ -256,13 +256,8 @@ __global__ void rope_append_kernel(const T* __restrict__ qkv, const float* __res
     const int row = rows[t], p = pos[t];
     if (row < 0 || row >= max_batch || p < 0 || p >= max_seq || p >= tab_len) return;  // host validates too
     if (h < Hq + Hkv) {
-      const float* ct = cos_tab + (long)p * D;
-      const float* st = sin_tab + (long)p * D;
-      const float c1 = Elem<T>::round(ct[j]), c2 = Elem<T>::round(ct[j + half]);
-      const float s1 = Elem<T>::round(st[j]), s2 = Elem<T>::round(st[j + half]);
-      const float a1 = Elem<T>::round(x1 * c1), b1 = Elem<T>::round((-x2) * s1);
-      const float a2 = Elem<T>::round(x2 * c2), b2 = Elem<T>::round(x1 * s2);
-      const float o1 = a1 + b1, o2 = a2 + b2;
+      float o1, o2;
+      rope_pair<T>(x1, x2, cos_tab + (long)p * D, sin_tab + (long)p * D, j, half, o1, o2);
       if (h < Hq) {
         T* dst = q_out + ((long)t * Hq + h) * D;
         Elem<T>::st(dst + j, o1);

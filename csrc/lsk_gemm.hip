@@ -39,6 +39,52 @@
 
 #define EPI_PARTIAL 3
 #define EPI_ARGMAX 4
+#define EPI_QKV 5
+
+// Fused qkv epilogue (EPI_QKV): the qkv projection's output goes straight to RoPE and the caches instead of through
+// K-slice partials and the RoPE + append kernel.  The weight is packed with its q and k row groups RoPE-paired
+// (lsk_pack_weight_qkv): within each head of D rows (G = D / 16 groups) packed group 2 j holds dims 16 j .. 16 j + 15
+// and packed group 2 j + 1 dims D / 2 + 16 j .. (the rotation partners), so a tile of two (or four) row groups holds
+// whole rotation pairs and one lane owns both values of a pair.  v rows keep their order.
+struct QkvRope {
+  uint16_t* q;            // [N, Hq, D] RoPE-rotated queries
+  uint16_t* kc;           // K cache, fragment-major 32-position blocks (k_cache_offset)
+  uint16_t* vc;           // V cache, transposed 32-position blocks
+  const float* cos_tab;   // [tab_len, D] fp32
+  const float* sin_tab;
+  const int32_t* rows;    // [N] cache row of each token
+  const int32_t* pos;     // [N] position of each token
+  int hq, hkv, d, max_batch, max_seq, tab_len;
+};
+
+// Token m's values x_lo, x_hi of packed row groups G (even) and G + 1, row w16 of each: a RoPE pair for q / k (stored
+// rotated to q or the K cache), two v dims 16 apart otherwise (stored to the V cache), with the RoPE + append
+// kernel's arithmetic (rope_pair) and indexing.
+__device__ __forceinline__ void qkv_rope_store(const QkvRope& qa, int m, int G, int w16, float x_lo, float x_hi) {
+  const int D = qa.d, GH = D >> 4, half = D >> 1;
+  const int row = qa.rows[m], p = qa.pos[m];
+  if (row < 0 || row >= qa.max_batch || p < 0 || p >= qa.max_seq || p >= qa.tab_len) return;  // host validates too
+  const int kg = (qa.hq + qa.hkv) * GH;
+  if (G < kg) {
+    const int h = G / GH, d1 = 16 * ((G - h * GH) >> 1) + w16;
+    float o1, o2;
+    rope_pair<uint16_t>(x_lo, x_hi, qa.cos_tab + (long)p * D, qa.sin_tab + (long)p * D, d1, half, o1, o2);
+    if (h < qa.hq) {
+      uint16_t* dst = qa.q + ((long)m * qa.hq + h) * D;
+      dst[d1] = f2bf(o1);
+      dst[d1 + half] = f2bf(o2);
+    } else {
+      uint16_t* dst = qa.kc + ((long)row * qa.hkv + (h - qa.hq)) * (long)qa.max_seq * D;
+      dst[k_cache_offset<uint16_t>(p, d1, D)] = f2bf(o1);
+      dst[k_cache_offset<uint16_t>(p, d1 + half, D)] = f2bf(o2);
+    }
+  } else {
+    const int gv = G - kg, h = gv / GH, d1 = 16 * (gv - h * GH) + w16;
+    uint16_t* dst = qa.vc + ((long)row * qa.hkv + h) * (long)D * qa.max_seq + (long)(p >> 5) * 32 * D + (p & 31);
+    dst[(long)d1 * 32] = f2bf(x_lo);
+    dst[(long)(d1 + 16) * 32] = f2bf(x_hi);
+  }
+}
 
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + lsk_exp(-x)); }
 
@@ -74,10 +120,11 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
                                                         float* __restrict__ P, float* __restrict__ amax_v,
                                                         int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                         int kslice, int n_tiles, int m_tiles, int m_lo,
-                                                        int c_nks) {
+                                                        int c_nks, QkvRope qa) {
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
-  static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL,
-                "fragment-major A: split-K partial, silu-mul and LM head");
+  static_assert(!AF || EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL || EPI == EPI_QKV,
+                "fragment-major A: split-K partial, silu-mul, LM head and the fused qkv");
+  static_assert(EPI != EPI_QKV || (AF && NS % 2 == 0), "fused qkv: fragment-major A, whole rotation pairs per tile");
   constexpr int E = NT * MS * 256;  // partial-sum floats per wave
   __shared__ __attribute__((aligned(16))) float red[4 * E];
 
@@ -235,6 +282,14 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
       }
     }
     return;
+  } else if constexpr (EPI == EPI_QKV) {
+    // a thread per (row-group pair, token, row of the group): one RoPE pair (q / k) or two v values
+    for (int o = tid; o < (NS / 2) * TM * 16; o += 256) {
+      const int w16 = o & 15, r2 = o >> 4, ml = r2 % TM, pp = r2 / TM;
+      const int m = m0 + ml;
+      if (m >= M) continue;
+      qkv_rope_store(qa, m, n0 / 16 + 2 * pp, w16, rbf(reduced(2 * pp, ml, w16)), rbf(reduced(2 * pp + 1, ml, w16)));
+    }
   } else if (EPI == LSK_EPI_SILU_MUL && NS >= 2 && N % 8 == 0 && (ldc % 8 == 0 || c_nks > 0)) {
     // 8 outputs per lane, one 16-byte store: a wave covers 16 tokens x 32 columns per pass (lane l: token
     // 16 g + l % 16, columns 32 c + 8 (l / 16) .. +7), 8x fewer stores than one element per lane.  c_nks > 0:
@@ -304,7 +359,8 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
                                                                 float* __restrict__ P, float* __restrict__ amax_v,
                                                                 int* __restrict__ amax_i, int M, int N, int K, int ffn,
                                                                 int kslice, int n_tiles, int m_blocks, int n_slices,
-                                                                int c_nks, int tbg) {
+                                                                int c_nks, int tbg, QkvRope qa) {
+  static_assert(EPI != EPI_QKV || (AF && NS % 2 == 0), "fused qkv: fragment-major A, whole rotation pairs per tile");
   constexpr int NT = (EPI == LSK_EPI_SILU_MUL) ? 2 * NS : NS;
   constexpr int NTH = 64 * NWV;
   constexpr int CHUNK_E = NT * 4 * 512;  // bf16 elements of one staged chunk (NT row groups x 4 k-steps)
@@ -510,6 +566,20 @@ __global__ __launch_bounds__(64 * NWV, 1) void gemm_wide_kernel(const uint16_t* 
     }
     return;
   }
+  if constexpr (EPI == EPI_QKV) {
+    // lane: rows 4 lg + i of row groups 2 pp (low half of each RoPE pair) and 2 pp + 1 (high half), token mrow[t]
+#pragma unroll
+    for (int t = 0; t < MSW; ++t) {
+      const int m = mrow[t];
+      if (m >= M) continue;
+#pragma unroll
+      for (int pp = 0; pp < NS / 2; ++pp)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          qkv_rope_store(qa, m, n0 / 16 + 2 * pp, 4 * lg + i, rbf(tot[2 * pp][t][i]), rbf(tot[2 * pp + 1][t][i]));
+    }
+    return;
+  }
 #pragma unroll
   for (int t = 0; t < MSW; ++t) {
     const int m = mrow[t];
@@ -646,15 +716,22 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
 // ----------------------------------------------------------------------------- weight packing
 // One thread per 16-byte lane slice: packed element offset 8 * o, o = (g * nks + j) * 64 + l  <->  row
 // 16 g + l % 16, columns 32 j + 8 (l / 16) .. +7 of the row-major matrix.  Both directions are pure copies.
+// gh > 0 (a fused qkv weight, lsk_pack_weight_qkv): within each of the first paired_groups row groups' heads of gh
+// groups, packed group 2 r holds source group r and packed group 2 r + 1 source group gh / 2 + r (RoPE partners).
 template <bool PACK>
 __global__ __launch_bounds__(256) void pack_weight_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
-                                                          long ld, int nks, long n_slices) {
+                                                          long ld, int nks, long n_slices, int gh, int paired_groups) {
   const long o = (long)blockIdx.x * 256 + threadIdx.x;
   if (o >= n_slices) return;
   const int l = (int)(o & 63);
   const long f = o >> 6;
   const long g = f / nks, j = f - g * nks;
-  const long rm = (16 * g + (l & 15)) * ld + 32 * j + 8 * (l >> 4);  // row-major element offset
+  long sg = g;  // source row group
+  if (gh > 0 && g < paired_groups) {
+    const long h = g / gh, r = g - h * gh;
+    sg = h * gh + ((r & 1) ? gh / 2 + (r >> 1) : (r >> 1));
+  }
+  const long rm = (16 * sg + (l & 15)) * ld + 32 * j + 8 * (l >> 4);  // row-major element offset
   if (PACK)
     *(uint4*)(dst + 8 * o) = *(const uint4*)(src + rm);
   else
@@ -711,19 +788,19 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
                         int N, int K, int ffn, int kslice, int nt, int mt, int m_lo) {
   if (epi == LSK_EPI_RESIDUAL)
     gemm_bf16_kernel<NS, MS, LSK_EPI_RESIDUAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                    ffn, kslice, nt, mt, m_lo, 0);
+                                                                    ffn, kslice, nt, mt, m_lo, 0, QkvRope{});
   else if (epi == LSK_EPI_SILU_MUL) {
     gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N,
-                                                                      K, ffn, kslice, nt, mt, m_lo, 0);
+                                                                      K, ffn, kslice, nt, mt, m_lo, 0, QkvRope{});
   } else if (epi == EPI_PARTIAL)
     gemm_bf16_kernel<NS, MS, EPI_PARTIAL><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                               kslice, nt, mt, m_lo, 0);
+                                                               kslice, nt, mt, m_lo, 0, QkvRope{});
   else if (epi == EPI_ARGMAX)
     gemm_bf16_kernel<NS, MS, EPI_ARGMAX><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                              kslice, nt, mt, m_lo, 0);
+                                                              kslice, nt, mt, m_lo, 0, QkvRope{});
   else
     gemm_bf16_kernel<NS, MS, LSK_EPI_NONE><<<grid, 256, 0, s>>>(A, lda, W, ldw, C, ldc, R, ldr, P, av, ai, M, N, K,
-                                                                ffn, kslice, nt, mt, m_lo, 0);
+                                                                ffn, kslice, nt, mt, m_lo, 0, QkvRope{});
 }
 
 // Fragment-major activations: split-K partial launches only.
@@ -731,16 +808,21 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
 template <int NS, int MS>
 static void launch_bf16_af(int epi, dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw,
                            uint16_t* C, long ldc, int c_nks, float* P, float* av, int* ai, int M, int N, int K, int ffn,
-                           int kslice, int nt, int mt, int m_lo) {
+                           int kslice, int nt, int mt, int m_lo, const QkvRope& qa) {
   if (epi == LSK_EPI_SILU_MUL)
     gemm_bf16_kernel<NS, MS, LSK_EPI_SILU_MUL, gemm_unit<NS, MS, LSK_EPI_SILU_MUL>(), true><<<grid, 256, 0, s>>>(
-        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, nullptr, nullptr, M, N, K, ffn, kslice, nt, mt, m_lo, c_nks);
+        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, nullptr, nullptr, M, N, K, ffn, kslice, nt, mt, m_lo, c_nks,
+        QkvRope{});
   else if (epi == EPI_ARGMAX)
     gemm_bf16_kernel<NS, MS, EPI_ARGMAX, gemm_unit<NS, MS, EPI_ARGMAX>(), true><<<grid, 256, 0, s>>>(
-        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, kslice, nt, mt, m_lo, 0);
-  else
+        A, 0, W, ldw, C, ldc, nullptr, 0, nullptr, av, ai, M, N, K, 0, kslice, nt, mt, m_lo, 0, QkvRope{});
+  else if (epi == EPI_QKV) {
+    if constexpr (NS % 2 == 0)
+      gemm_bf16_kernel<NS, MS, EPI_QKV, gemm_unit<NS, MS, EPI_QKV>(), true><<<grid, 256, 0, s>>>(
+          A, 0, W, ldw, nullptr, 0, nullptr, 0, nullptr, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, m_lo, 0, qa);
+  } else
     gemm_bf16_kernel<NS, MS, EPI_PARTIAL, gemm_unit<NS, MS, EPI_PARTIAL>(), true><<<grid, 256, 0, s>>>(
-        A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, m_lo, 0);
+        A, 0, W, ldw, nullptr, 0, nullptr, 0, P, nullptr, nullptr, M, N, K, 0, kslice, nt, mt, m_lo, 0, QkvRope{});
 }
 
 // Launch over nt row tiles x mt token tiles x ks K slices (the tile mapping is in the kernel).  af: a split-K
@@ -748,7 +830,7 @@ static void launch_bf16_af(int epi, dim3 grid, hipStream_t s, const uint16_t* A,
 static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipStream_t s, const void* A, long lda,
                           const void* W, long ldw, void* C, long ldc, const void* R, long ldr, float* P, float* av,
                           int* ai, int M, int N, int K, int ffn, int kslice, bool af = false, int m_lo = 0,
-                          int c_nks = 0) {
+                          int c_nks = 0, const QkvRope& qa = QkvRope{}) {
   const dim3 grid(mt > 1 ? (unsigned)(((nt + 7) / 8) * 8 * mt) : (unsigned)nt, 1, (unsigned)ks);
   const uint16_t* a = (const uint16_t*)A;
   const uint16_t* w = (const uint16_t*)W;
@@ -757,7 +839,7 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 #define LSK_GEMM_CASE(NS_, MS_)                                                                                  \
   if (ns == NS_ && ms == MS_) {                                                                                  \
     if (af)                                                                                                      \
-      launch_bf16_af<NS_, MS_>(epi, grid, s, a, w, ldw, c, ldc, c_nks, P, av, ai, M, N, K, ffn, kslice, nt, mt, m_lo); \
+      launch_bf16_af<NS_, MS_>(epi, grid, s, a, w, ldw, c, ldc, c_nks, P, av, ai, M, N, K, ffn, kslice, nt, mt, m_lo, qa); \
     else                                                                                                         \
       launch_bf16<NS_, MS_>(epi, grid, s, a, lda, w, ldw, c, ldc, r, ldr, P, av, ai, M, N, K, ffn, kslice, nt, mt, \
                             m_lo);                                                                               \
@@ -793,7 +875,7 @@ static WideCfg wide_config(int epi, int M, int N, int ks) {
   WideCfg best{0, 0, 0, 0};
   double best_cost = 0.0;
   for (int ns = 4; ns >= 2; ns -= 2) {
-    if (ns == 2 && !silu) break;
+    if (ns == 2 && !silu && epi != EPI_QKV) break;
     const int msw_max = (silu && ns == 4) ? 2 : 3;
     const int nb_min = (gtot + 8 * msw_max - 1) / (8 * msw_max);
     for (int nb = nb_min; nb <= nb_min + 2; ++nb) {
@@ -807,7 +889,7 @@ static WideCfg wide_config(int epi, int M, int N, int ks) {
       const bool two_per_cu = msw == 1 && wgs > 256;
       double cost = (double)((wgs + 255) / 256) * fmax(2.5, 0.83 + g) * ns / 4.0;
       if (two_per_cu) cost *= 0.9;
-      if (silu && ns == 2) cost *= 1.1;
+      if ((silu || epi == EPI_QKV) && ns == 2) cost *= 1.1;
       if (best.ns == 0 || cost < best_cost) {
         best = WideCfg{ns, m_blocks, tbg, msw};
         best_cost = cost;
@@ -821,28 +903,31 @@ template <int NS, int MSW, int EPI>
 static void launch_wide_kernel(dim3 grid, hipStream_t s, bool af, const uint16_t* A, long lda, const uint16_t* W,
                                uint16_t* C, long ldc, const uint16_t* R, long ldr, float* P, float* av, int* ai, int M,
                                int N, int K, int ffn, int kslice, int n_tiles, int m_blocks, int ks, int c_nks,
-                               int tbg) {
-  if constexpr (EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL) {
+                               int tbg, const QkvRope& qa) {
+  if constexpr (EPI == EPI_PARTIAL || EPI == EPI_ARGMAX || EPI == LSK_EPI_SILU_MUL || EPI == EPI_QKV) {
     if (af) {
       gemm_wide_kernel<NS, MSW, EPI, 8, 2, true><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
-                                                                      kslice, n_tiles, m_blocks, ks, c_nks, tbg);
+                                                                      kslice, n_tiles, m_blocks, ks, c_nks, tbg, qa);
       return;
     }
   }
-  gemm_wide_kernel<NS, MSW, EPI, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, kslice,
-                                                            n_tiles, m_blocks, ks, 0, tbg);
+  if constexpr (EPI != EPI_QKV)
+    gemm_wide_kernel<NS, MSW, EPI, 8, 2><<<grid, 512, 0, s>>>(A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn,
+                                                              kslice, n_tiles, m_blocks, ks, 0, tbg, QkvRope{});
 }
 
 static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
                        const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks,
-                       bool af = false, int c_nks = 0) {
+                       bool af = false, int c_nks = 0, const QkvRope& qa = QkvRope{}) {
   if (M <= 64) return 0;
   if (N % 64 != 0 || (epi != EPI_PARTIAL && C != nullptr && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0)
     return 0;
   if (af && (epi == LSK_EPI_RESIDUAL || epi == LSK_EPI_NONE)) return 0;
-  // the tier streams the weights with >= 192 workgroups: 64-row tiles x the fewest blocks must reach that
+  if (epi == EPI_QKV && !af) return 0;
+  // the tier streams the weights with >= 192 workgroups: 64-row tiles (32-row for the fused qkv, which has no K
+  // split) x the fewest blocks must reach that
   const int gtot = (M + 15) / 16, cap = 8 * (epi == LSK_EPI_SILU_MUL ? 2 : 3);
-  if ((long)(N / 64) * ((gtot + cap - 1) / cap) * ks < 192) return 0;
+  if ((long)(N / (epi == EPI_QKV ? 32 : 64)) * ((gtot + cap - 1) / cap) * ks < 192) return 0;
   const WideCfg cfg = wide_config(epi, M, N, ks);
   if (cfg.ns == 0) return 0;
   const int n_tiles = N / (16 * cfg.ns);
@@ -850,7 +935,7 @@ static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, cons
   const int kslice = K / ks;
 #define LSK_WIDE(NS_, MSW_, EPI_)                                                                                  \
   launch_wide_kernel<NS_, MSW_, EPI_>(grid, s, af, A, lda, W, C, ldc, R, ldr, P, av, ai, M, N, K, ffn, kslice, n_tiles, \
-                                      cfg.m_blocks, ks, c_nks, cfg.tbg)
+                                      cfg.m_blocks, ks, c_nks, cfg.tbg, qa)
 #define LSK_WIDE_MSW(NS_, EPI_)                 \
   do {                                          \
     if (cfg.msw == 1)                           \
@@ -871,6 +956,9 @@ static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, cons
     LSK_WIDE_MSW(4, LSK_EPI_NONE);
   } else if (epi == EPI_ARGMAX) {
     LSK_WIDE_MSW(4, EPI_ARGMAX);
+  } else if (epi == EPI_QKV) {
+    if (cfg.ns == 2) LSK_WIDE_MSW(2, EPI_QKV);
+    else LSK_WIDE_MSW(4, EPI_QKV);
   } else {
     return 0;
   }
@@ -1063,7 +1151,8 @@ extern "C" int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const vo
   return lsk_check_launch("lsk_head_norm_argmax(pick)");
 }
 
-static int pack_common(bool pack, const void* src, void* dst, long ld, int N, int K, void* stream) {
+static int pack_common(bool pack, const void* src, void* dst, long ld, int N, int K, void* stream, int gh = 0,
+                       int paired_groups = 0) {
   const char* what = pack ? "lsk_pack_weight" : "lsk_unpack_weight";
   LSK_REQUIRE(src && dst && src != dst, LSK_EARG, "%s: null or aliased pointers", what);
   LSK_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0 && ld >= K && ld % 8 == 0, LSK_ESHAPE,
@@ -1072,10 +1161,10 @@ static int pack_common(bool pack, const void* src, void* dst, long ld, int N, in
   const unsigned grid = (unsigned)((n_slices + 255) / 256);
   if (pack)
     pack_weight_kernel<true><<<grid, 256, 0, (hipStream_t)stream>>>((const uint16_t*)src, (uint16_t*)dst, ld, K / 32,
-                                                                    n_slices);
+                                                                    n_slices, gh, paired_groups);
   else
     pack_weight_kernel<false><<<grid, 256, 0, (hipStream_t)stream>>>((const uint16_t*)src, (uint16_t*)dst, ld, K / 32,
-                                                                     n_slices);
+                                                                     n_slices, gh, paired_groups);
   return lsk_check_launch(what);
 }
 
@@ -1085,4 +1174,60 @@ extern "C" int lsk_pack_weight(const void* W, long ldw, void* Wp, int N, int K, 
 
 extern "C" int lsk_unpack_weight(const void* Wp, void* W, long ldw, int N, int K, void* stream) {
   return pack_common(false, Wp, W, ldw, N, K, stream);
+}
+
+// Fused qkv weight [q (n_heads D rows); k (n_kv_heads D); v (n_kv_heads D)] x K: fragment-major with the q and k row
+// groups RoPE-paired (see QkvRope), the storage lsk_gemm_qkv_rope reads.
+static int qkv_pack_args(const char* what, int n_heads, int n_kv_heads, int head_dim, int* N, int* gh, int* paired) {
+  LSK_REQUIRE(n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && head_dim % 32 == 0, LSK_ESHAPE,
+              "%s: head_dim %d must be a multiple of 32 (whole RoPE-paired row groups)", what, head_dim);
+  *N = (n_heads + 2 * n_kv_heads) * head_dim;
+  *gh = head_dim / 16;
+  *paired = (n_heads + n_kv_heads) * *gh;
+  return 0;
+}
+
+extern "C" int lsk_pack_weight_qkv(const void* W, long ldw, void* Wp, int n_heads, int n_kv_heads, int head_dim, int K,
+                                   void* stream) {
+  int N, gh, paired;
+  const int rc = qkv_pack_args("lsk_pack_weight_qkv", n_heads, n_kv_heads, head_dim, &N, &gh, &paired);
+  if (rc) return rc;
+  return pack_common(true, W, Wp, ldw, N, K, stream, gh, paired);
+}
+
+extern "C" int lsk_unpack_weight_qkv(const void* Wp, void* W, long ldw, int n_heads, int n_kv_heads, int head_dim,
+                                     int K, void* stream) {
+  int N, gh, paired;
+  const int rc = qkv_pack_args("lsk_unpack_weight_qkv", n_heads, n_kv_heads, head_dim, &N, &gh, &paired);
+  if (rc) return rc;
+  return pack_common(false, Wp, W, ldw, N, K, stream, gh, paired);
+}
+
+// qkv projection + RoPE + KV append in one GEMM (bf16).  A: the normalised rows fragment-major (lsk_frag_off,
+// whole 16-token groups); W: lsk_pack_weight_qkv storage.  No K split: each output's sum runs over all of K in the
+// decode kernel's chunk-class order in both tiers (batch invariant).  Writes q_out [M, n_heads, head_dim] (rotated),
+// the K cache (rotated) and the V cache at (rows[m], pos[m]), with the RoPE + append kernel's arithmetic.
+extern "C" int lsk_gemm_qkv_rope(const void* A, const void* W, int M, int n_heads, int n_kv_heads, int head_dim, int K,
+                                 void* q_out, void* kcache, void* vcache, const float* cos_tab, const float* sin_tab,
+                                 int tab_len, const int32_t* rows, const int32_t* pos, int max_batch, int max_seq,
+                                 void* stream) {
+  LSK_REQUIRE(A && W && q_out && kcache && vcache && cos_tab && sin_tab && rows && pos, LSK_EARG,
+              "lsk_gemm_qkv_rope: null pointer");
+  int N, gh, paired;
+  int rc = qkv_pack_args("lsk_gemm_qkv_rope", n_heads, n_kv_heads, head_dim, &N, &gh, &paired);
+  if (rc) return rc;
+  LSK_REQUIRE(M >= 0 && K > 0 && K % 32 == 0 && max_batch > 0 && max_seq > 0 && max_seq % 32 == 0 && tab_len > 0,
+              LSK_ESHAPE, "lsk_gemm_qkv_rope: bad shape M=%d K=%d max_seq=%d", M, K, max_seq);
+  if (M == 0) return 0;
+  const QkvRope qa{(uint16_t*)q_out, (uint16_t*)kcache, (uint16_t*)vcache, cos_tab, sin_tab, rows, pos, n_heads,
+                   n_kv_heads, head_dim, max_batch, max_seq, tab_len};
+  hipStream_t s = (hipStream_t)stream;
+  const int mw = launch_wide(EPI_QKV, s, (const uint16_t*)A, 0, (const uint16_t*)W, nullptr, 0, nullptr, 0, nullptr,
+                             nullptr, nullptr, M, N, K, 0, 1, true, 0, qa);
+  if (mw < M) {
+    const int mr = M - mw, ms = ms_for(mr);
+    dispatch_bf16(2, ms, EPI_QKV, N / 32, (mr + 16 * ms - 1) / (16 * ms), 1, s, A, 0, W, K, nullptr, 0, nullptr, 0,
+                  nullptr, nullptr, nullptr, M, N, K, 0, K, true, mw, 0, qa);
+  }
+  return lsk_check_launch("lsk_gemm_qkv_rope");
 }

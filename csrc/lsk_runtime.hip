@@ -4,8 +4,9 @@
 //
 // Per layer (same op order and rounding points as solutions/packed.py:175-185):
 //   xn   = rmsnorm(x, attn_norm)                      lsk_rmsnorm
-//   qkv  = xn Wqkv^T                                  lsk_gemm NONE
-//   q, cache[k, v] = rope(q), rope(k), v              lsk_rope_append
+//   qkv  = xn Wqkv^T                                  lsk_gemm NONE            (fp32)
+//   q, cache[k, v] = rope(q), rope(k), v              lsk_rope_append          (fp32)
+//   q, cache[k, v] = rope / append of xn Wqkv^T       lsk_gemm_qkv_rope        (bf16: one launch)
 //   attn = ragged attention(q, cache)                 lsk_ragged_attn (+ split combine)
 //   x    = x + attn Wo^T                              lsk_gemm RESIDUAL
 //   xn   = rmsnorm(x, ffn_norm)                       lsk_rmsnorm
@@ -81,7 +82,7 @@ Layout layout(const Model& m, int N, int n_parts) {
   };
   const size_t n16 = (size_t)(N + 15) / 16 * 16;  // xn, attn: whole 16-token groups (fragment-major use)
   L.xn = take(n16 * m.dim * es);
-  L.qkv = take((size_t)N * (qd + 2 * kvd) * es);
+  L.qkv = take(m.dtype == LSK_DTYPE_BF16 ? 0 : (size_t)N * (qd + 2 * kvd) * es);  // bf16: fused into the qkv GEMM
   L.q = take((size_t)N * qd * es);
   L.attn = take(n16 * qd * es);
   L.h = take(n16 * m.ffn * es);  // whole 16-token groups (fragment-major above LSK_AF_MAX_TOKENS)
@@ -160,8 +161,15 @@ extern "C" long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, 
   int ns;
   m->ks_qkv = m->ks_o = m->ks_w2 = 1;
   if (dtype == LSK_DTYPE_BF16) {
-    const int qd = n_heads * head_dim, kvd = n_kv_heads * head_dim;
-    lsk_gemm_plan(qd + 2 * kvd, dim, &ns, &m->ks_qkv);
+    // bf16: the qkv projection runs fused with RoPE + append (lsk_gemm_qkv_rope, no K split, wqkv in
+    // lsk_pack_weight_qkv storage); o and w2 leave K-slice partials for the next add + RMSNorm
+    const int qd = n_heads * head_dim;
+    if (dim % 32 != 0 || head_dim % 32 != 0) {
+      delete m;
+      LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_model_create: bf16 needs dim and head_dim multiples of 32 (got %d, %d)",
+                  dim, head_dim);
+    }
+    m->ks_qkv = 0;
     lsk_gemm_plan(dim, qd, &ns, &m->ks_o);
     lsk_gemm_plan(dim, ffn, &ns, &m->ks_w2);
   }
@@ -264,13 +272,12 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
           if (e != hipSuccess) { lsk_set_error("lsk_forward_layers: capture %s", hipGetErrorString(e)); return (int)e; }
         }
       }
-      LSK_PROF2(LSK_PROF_GEMM_QKV, es_d * (qkvd * dimd + Nd * dimd) + pbytes(m->ks_qkv, qkvd), 2.0 * Nd * dimd * qkvd,
-                af ? lsk_gemm_partial_af(xn, m->wqkv[i], P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream)
-                   : lsk_gemm_partial(xn, m->dim, m->wqkv[i], m->dim, P, N, qd + 2 * kvd, m->dim, m->ks_qkv, stream));
-      LSK_PROF2(LSK_PROF_ROPE, pbytes(m->ks_qkv, qkvd) + es_d * Nd * qkvd, 6.0 * Nd * (qd + kvd),
-                lsk_rope_append_partial(m->dtype, P, m->ks_qkv, q, m->kc[i], m->vc[i], m->cos_tab, m->sin_tab,
-                                        m->tab_len, rows, pos, N, m->n_heads, m->n_kv_heads, m->head_dim,
-                                        m->max_batch, m->max_seq, stream));
+      // qkv projection, RoPE and the KV append in one launch (q rotated into `q`, K / V into this layer's cache)
+      LSK_PROF2(LSK_PROF_GEMM_QKV, es_d * (qkvd * dimd + Nd * dimd + Nd * qkvd) + 8.0 * Nd * m->head_dim,
+                2.0 * Nd * dimd * qkvd,
+                lsk_gemm_qkv_rope(xn, m->wqkv[i], N, m->n_heads, m->n_kv_heads, m->head_dim, m->dim, q, m->kc[i],
+                                  m->vc[i], m->cos_tab, m->sin_tab, m->tab_len, rows, pos, m->max_batch, m->max_seq,
+                                  stream));
       LSK_PROF2(LSK_PROF_ATTN, attn_bytes, attn_flops,
                 lsk_ragged_attn_impl(m->dtype, q, m->kc[i], m->vc[i], blocks, works, n_works, groups, n_groups,
                                      n_parts, recs, n_rounds, n_slots, rows_cap, attn, af_o, m->n_heads,

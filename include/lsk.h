@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 9
+#define LSK_ABI_VERSION 10
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -187,6 +187,24 @@ int lsk_head_norm_argmax(int dtype, const void* h, long ldh, const void* norm_w,
 int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w, float eps,
                     void* x_out, long ldxo, void* out, long ldo, int n_rows, int dim, void* stream);
 
+/* Fused qkv projection + RoPE + KV append (bf16): replaces F.linear(x, wqkv) at solutions/packed.py:175 together
+ * with apply_rope (common/model.py:143-150, solutions/packed.py:176-179) and the KV write (solutions/packed.py:
+ * 180-181).  A: the normalised rows fragment-major (lsk_frag_off, ceil(M/16)*16 rows x K); W: lsk_pack_weight_qkv
+ * storage.  Writes q_out [M, n_heads, head_dim] (rotated), the K cache (rotated) and the V cache at (rows[m],
+ * pos[m]), with lsk_rope_append's arithmetic on rnd(the full-K sum).  head_dim % 32 == 0, max_seq % 32 == 0. */
+int lsk_gemm_qkv_rope(const void* A, const void* W, int M, int n_heads, int n_kv_heads, int head_dim, int K,
+                      void* q_out, void* kcache, void* vcache, const float* cos_tab, const float* sin_tab, int tab_len,
+                      const int32_t* rows, const int32_t* pos, int max_batch, int max_seq, void* stream);
+
+/* lsk_pack_weight for the fused [q; k; v] weight ((n_heads + 2 n_kv_heads) head_dim rows x K) that
+ * lsk_gemm_qkv_rope reads: within each q and k head the 16-row groups are stored RoPE-paired (dims 16j..16j+15,
+ * then their partners head_dim/2 + 16j ..), v rows in order.  Pure copies; unpacking restores the [out, in]
+ * tensor (common/model.py:259-276).  No reference counterpart (storage format only). */
+int lsk_pack_weight_qkv(const void* W, long ldw, void* Wp, int n_heads, int n_kv_heads, int head_dim, int K,
+                        void* stream);
+int lsk_unpack_weight_qkv(const void* Wp, void* W, long ldw, int n_heads, int n_kv_heads, int head_dim, int K,
+                          void* stream);
+
 /* lsk_rope_append reading qkv as rnd(sum_{s<ks} P[s]) from fp32 partials [ks][N][(Hq+2Hkv)D]. */
 int lsk_rope_append_partial(int dtype, const float* partials, int ks, void* q_out, void* kcache, void* vcache,
                             const float* cos_tab, const float* sin_tab, int tab_len, const int32_t* rows,
@@ -239,8 +257,9 @@ int lsk_shift_segment_positions(int32_t* meta, int n_tokens, int nb, int n_works
                                 void* stream);
 
 /* ---- native layer-range runner (solutions/packed.py:169-196, packed_layer / packed_layers) ----
- * A model handle holds host copies of per-layer device pointers (weights [out, in]: packed for bf16,
- * row-major for fp32,
+ * A model handle holds host copies of per-layer device pointers (weights [out, in]: packed for bf16 --
+ * wqkv in lsk_pack_weight_qkv storage, the others lsk_pack_weight; dim and head_dim multiples of 32 -- row-major
+ * for fp32,
  * KV caches [B, Hkv, S, D], fp32 RoPE tables [tab_len, D]); it owns no device memory.
  * Returns a handle > 0, or a negative error code. */
 long lsk_model_create(int dtype, int n_layers, int dim, int n_heads, int n_kv_heads, int head_dim, int ffn, int vocab,

@@ -270,8 +270,10 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
     c = lambda t: t.contiguous().cuda()  # noqa: E731
     rows, pos = opb.rows.to(torch.int32), opb.pos.to(torch.int32)
     q_gpu = torch.empty(N, cfg.n_heads, cfg.head_dim, dtype=BF16, device="cuda")
-    _lsk.rope_append(_lsk.gemm(c(xn1), glw.wqkv), q_gpu, g.cache.kstore[0], g.cache.vb[0], g.rope_cos, g.rope_sin,
-                     c(rows), c(pos), cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)
+    xn1_f = torch.zeros(_lsk.frag_rows(N), xn1.shape[1], dtype=BF16, device="cuda")
+    xn1_f[:N] = c(xn1)                              # the layer loop's fused qkv + RoPE + append launch
+    _lsk.gemm_qkv_rope(_lsk.PackedWeight(xn1_f).data, glw.wqkv, N, q_gpu, g.cache.kstore[0], g.cache.vb[0],
+                       g.rope_cos, g.rope_sin, c(rows), c(pos))
     kv_same = (float((g.cache.k[0].cpu() == o.cache.k[0]).float().mean()),
                float((g.cache.v[0].cpu() == o.cache.v[0]).float().mean()))
     stages = {

@@ -689,3 +689,43 @@ def test_shifted_segment_metadata_equals_a_plan_at_the_actual_positions(cuda, sp
     r_ref = meta_a[head + 8 * nw + 8 * ng:].reshape(-1, 8)
     live = lambda r: r[(r[:, 2] & 255) > 0]                           # noqa: E731
     assert key(live(r_got)) == key(live(r_ref))
+
+
+@pytest.mark.parametrize("M", [5, 32, 48, 64, 100, 288])
+@pytest.mark.parametrize("heads", [(32, 8, 128), (8, 8, 64)])
+def test_fused_qkv_rope_writes_what_the_unfused_path_writes(cuda, M, heads):
+    """lsk_gemm_qkv_rope -- the qkv projection with RoPE and the KV append in its epilogue, the weight's q / k row
+    groups RoPE-paired -- writes bitwise what the qkv GEMM without a K split (lsk_gemm_partial, ks = 1) followed by
+    lsk_rope_append_partial writes: the rotated q, the K cache and the V cache (every other cache slot untouched),
+    in the decode tier (<= 64 rows) and in the wide tier (above, GQA shape); unpacking the paired storage gives the
+    weight back."""
+    lsk = _lsk()
+    Hq, Hkv, D = heads
+    g = _gen(2000 + M + D)
+    K, N, B, S = 1024, (Hq + 2 * Hkv) * D, 4, 512
+    m16 = lsk.frag_rows(M)
+    a = torch.randn(m16, K, generator=g).to(BF16).to(cuda)
+    af = lsk.PackedWeight(a).data                                          # fragment-major A, same values
+    wd = (torch.randn(N, K, generator=g) * 0.05).to(BF16).to(cuda)
+    wp = lsk.PackedWeight(wd, qkv_heads=heads)
+    assert torch.equal(wp.unpack(), wd)
+    with pytest.raises(lsk.LskError):
+        lsk.gemm_partial(a[:M].contiguous(), wp, 1)                        # paired storage: fused GEMM only
+    cos = torch.randn(S, D, generator=g).to(cuda)
+    sin = torch.randn(S, D, generator=g).to(cuda)
+    perm = torch.randperm(B * S, generator=g)[:M]                         # distinct (row, position) per token
+    rows = (perm // S).to(torch.int32).to(cuda)
+    pos = (perm % S).to(torch.int32).to(cuda)
+    k0 = lsk.k_to_frag(torch.randn(B, Hkv, S, D, generator=g).to(BF16)).to(cuda)
+    v0 = lsk.v_to_blocked(torch.randn(B, Hkv, S, D, generator=g).to(BF16)).to(cuda)
+    k1, v1, k2, v2 = k0.clone(), v0.clone(), k0.clone(), v0.clone()
+    q1 = torch.empty(M, Hq, D, dtype=BF16, device=cuda)
+    q2 = torch.empty(M, Hq, D, dtype=BF16, device=cuda)
+    P = lsk.gemm_partial(a[:M].contiguous(), lsk.PackedWeight(wd), 1)
+    lsk.rope_append_partial(P, q1, k1, v1, cos, sin, rows, pos, Hq, Hkv, D)
+    lsk.gemm_qkv_rope(af, wp, M, q2, k2, v2, cos, sin, rows, pos)
+    torch.cuda.synchronize()
+    assert torch.equal(q2.view(torch.int16), q1.view(torch.int16))
+    assert torch.equal(k2.view(torch.int16), k1.view(torch.int16))
+    assert torch.equal(v2.view(torch.int16), v1.view(torch.int16))
+    assert not torch.equal(k2, k0) and not torch.equal(v2, v0)

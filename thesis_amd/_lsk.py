@@ -21,7 +21,7 @@ DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -43,6 +43,9 @@ _SIGS = {
                                     _P]),
     "lsk_pack_weight": (_I, [_P, _L, _P, _I, _I, _P]),
     "lsk_unpack_weight": (_I, [_P, _P, _L, _I, _I, _P]),
+    "lsk_pack_weight_qkv": (_I, [_P, _L, _P, _I, _I, _I, _I, _P]),
+    "lsk_unpack_weight_qkv": (_I, [_P, _P, _L, _I, _I, _I, _I, _P]),
+    "lsk_gemm_qkv_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
     "lsk_gemm_plan": (_I, [_I, _I, _P, _P]),
     "lsk_gemm_partial": (_I, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _P]),
@@ -192,9 +195,11 @@ def _dev(*ts):
 class PackedWeight:
     """A bf16 weight matrix [N, K] (F.linear's [out, in]) in the GEMM kernels' fragment-major storage
     (lsk_pack_weight): every 16-row x 32-column MFMA fragment is 1 KiB contiguous in lane order, so each
-    wave's weight load is one contiguous 1 KiB stream.  `unpack()` returns the [N, K] tensor (a copy)."""
+    wave's weight load is one contiguous 1 KiB stream.  `unpack()` returns the [N, K] tensor (a copy).
+    qkv_heads=(n_heads, n_kv_heads, head_dim): a fused [q; k; v] weight stored for the fused qkv + RoPE GEMM
+    (lsk_pack_weight_qkv, q and k row groups RoPE-paired); only `gemm_qkv_rope` reads it."""
 
-    def __init__(self, w: torch.Tensor):
+    def __init__(self, w: torch.Tensor, qkv_heads: tuple | None = None):
         _dev(w)
         if w.dtype != torch.bfloat16 or w.dim() != 2 or w.stride(1) != 1:
             raise LskError("PackedWeight: a 2-D bf16 tensor with unit column stride is needed")
@@ -202,8 +207,16 @@ class PackedWeight:
         self.shape = (N, K)
         self.dtype = w.dtype
         self.device = w.device
+        self.qkv_heads = tuple(qkv_heads) if qkv_heads is not None else None
         self.data = torch.empty(N * K, dtype=w.dtype, device=w.device)
-        _check(load().lsk_pack_weight(_ptr(w), w.stride(0), _ptr(self.data), N, K, _stream()), "lsk_pack_weight")
+        if self.qkv_heads is None:
+            _check(load().lsk_pack_weight(_ptr(w), w.stride(0), _ptr(self.data), N, K, _stream()), "lsk_pack_weight")
+        else:
+            hq, hkv, d = self.qkv_heads
+            if N != (hq + 2 * hkv) * d:
+                raise LskError(f"PackedWeight: {N} rows do not match qkv heads {self.qkv_heads}")
+            _check(load().lsk_pack_weight_qkv(_ptr(w), w.stride(0), _ptr(self.data), hq, hkv, d, K, _stream()),
+                   "lsk_pack_weight_qkv")
 
     def data_ptr(self) -> int:
         return self.data.data_ptr()
@@ -223,7 +236,12 @@ class PackedWeight:
     def unpack(self) -> torch.Tensor:
         N, K = self.shape
         out = torch.empty(N, K, dtype=self.dtype, device=self.device)
-        _check(load().lsk_unpack_weight(_ptr(self.data), _ptr(out), K, N, K, _stream()), "lsk_unpack_weight")
+        if getattr(self, "qkv_heads", None) is None:
+            _check(load().lsk_unpack_weight(_ptr(self.data), _ptr(out), K, N, K, _stream()), "lsk_unpack_weight")
+        else:
+            hq, hkv, d = self.qkv_heads
+            _check(load().lsk_unpack_weight_qkv(_ptr(self.data), _ptr(out), K, hq, hkv, d, K, _stream()),
+                   "lsk_unpack_weight_qkv")
         return out
 
     def __repr__(self) -> str:
@@ -243,6 +261,9 @@ def _check_weight(a: torch.Tensor, w) -> None:
         raise LskError("bf16 GEMMs read packed weights: wrap the [out, in] tensor in PackedWeight")
     if a.dtype != torch.bfloat16 and isinstance(w, PackedWeight):
         raise LskError("packed weights are bf16 only")
+    if isinstance(w, PackedWeight) and getattr(w, "qkv_heads", None) is not None:
+        raise LskError("a qkv weight packed for the fused qkv + RoPE GEMM is read by gemm_qkv_rope only (its rows are "
+                       "RoPE-paired); PackedWeight(w.unpack()) gives the plain storage")
 
 
 # ----------------------------------------------------------------------------- ops
@@ -666,6 +687,21 @@ def add_rmsnorm(x: torch.Tensor, partials: torch.Tensor | None, w: torch.Tensor 
     _check(load().lsk_add_rmsnorm(dtype_code(x.dtype), _ptr(x), x.stride(0), _ptr(partials), ks, _ptr(w), float(eps),
                                   _ptr(x_out), x_out.stride(0) if x_out is not None else 0, _ptr(out),
                                   out.stride(0) if out is not None else 0, n, dim, _stream()), "lsk_add_rmsnorm")
+
+
+def gemm_qkv_rope(a_frag: torch.Tensor, w: "PackedWeight", M: int, q_out, kcache, vcache, cos_tab, sin_tab,
+                  rows_i32, pos_i32) -> None:
+    """Fused qkv projection + RoPE + KV append (lsk_gemm_qkv_rope): a_frag holds the normalised rows fragment-major
+    (frag_rows(M) * K elements), w a PackedWeight packed with qkv_heads; writes q_out [M, Hq, D] and the caches."""
+    _dev(a_frag, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32)
+    if not isinstance(w, PackedWeight) or w.qkv_heads is None:
+        raise LskError("gemm_qkv_rope reads a PackedWeight packed with qkv_heads (lsk_pack_weight_qkv)")
+    _check_kcache(q_out.dtype, kcache)
+    hq, hkv, d = w.qkv_heads
+    B, _, S, _ = k_dims(kcache)
+    _check(load().lsk_gemm_qkv_rope(_ptr(a_frag), _ptr(w), M, hq, hkv, d, w.shape[1], _ptr(q_out), _ptr(kcache),
+                                    _ptr(vcache), _ptr(cos_tab), _ptr(sin_tab), cos_tab.shape[0], _ptr(rows_i32),
+                                    _ptr(pos_i32), B, S, _stream()), "lsk_gemm_qkv_rope")
 
 
 def rope_append_partial(partials, q_out, kcache, vcache, cos_tab, sin_tab, rows_i32, pos_i32, n_heads, n_kv_heads,

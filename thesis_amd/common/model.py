@@ -138,7 +138,8 @@ def build_rope_cache(cfg: ModelConfig, max_seq: int, device) -> tuple[Tensor, Te
 @dataclass
 class LayerWeights:
     """One layer's weights (common/model.py:161-168).  The four projections are GEMM weights: a
-    `_lsk.PackedWeight` for bf16 (`.unpack()` -> [out, in]), the row-major tensor for fp32."""
+    `_lsk.PackedWeight` for bf16 (`.unpack()` -> [out, in]; wqkv packed for the fused qkv + RoPE GEMM when the
+    head shape is given), the row-major tensor for fp32."""
     wqkv: object
     wo: object
     w13: object
@@ -148,9 +149,14 @@ class LayerWeights:
 
     @classmethod
     def from_dense(cls, wqkv: Tensor, wo: Tensor, w13: Tensor, w2: Tensor, attn_norm: Tensor,
-                   ffn_norm: Tensor) -> "LayerWeights":
+                   ffn_norm: Tensor, qkv_heads: tuple | None = None) -> "LayerWeights":
+        """qkv_heads = (n_heads, n_kv_heads, head_dim): a bf16 wqkv is stored for the fused qkv + RoPE GEMM."""
         g = _lsk.as_gemm_weight
-        return cls(g(wqkv), g(wo), g(w13), g(w2), attn_norm, ffn_norm)
+        if qkv_heads is not None and wqkv.dtype == torch.bfloat16:
+            pq = _lsk.PackedWeight(wqkv, qkv_heads=qkv_heads)
+        else:
+            pq = g(wqkv)
+        return cls(pq, g(wo), g(w13), g(w2), attn_norm, ffn_norm)
 
 
 _INPLACE_DUNDERS = {"__setitem__", "__iadd__", "__isub__", "__imul__", "__itruediv__", "__ifloordiv__",
@@ -333,7 +339,8 @@ class LayerSkipLlama:
             layers.append(LayerWeights.from_dense(wqkv.contiguous(), take(p + "self_attn.o_proj.weight"),
                                                   w13.contiguous(), take(p + "mlp.down_proj.weight"),
                                                   take(p + "input_layernorm.weight"),
-                                                  take(p + "post_attention_layernorm.weight")))
+                                                  take(p + "post_attention_layernorm.weight"),
+                                                  (cfg.n_heads, cfg.n_kv_heads, cfg.head_dim)))
             del wqkv, w13
         embed = take("model.embed_tokens.weight")
         norm = take("model.norm.weight")
@@ -373,7 +380,7 @@ class LayerSkipLlama:
 
         layers = [LayerWeights.from_dense(mat(qd + 2 * kvd, cfg.dim), mat(cfg.dim, qd),
                                           mat(2 * cfg.intermediate_size, cfg.dim), mat(cfg.dim, cfg.intermediate_size),
-                                          ones(cfg.dim), ones(cfg.dim))
+                                          ones(cfg.dim), ones(cfg.dim), (cfg.n_heads, cfg.n_kv_heads, cfg.head_dim))
                   for _ in range(cfg.n_layers)]
         embed = mat(cfg.vocab_size, cfg.dim)
         lm_head = _lsk.as_gemm_weight(embed if cfg.tie_word_embeddings else mat(cfg.vocab_size, cfg.dim))

@@ -117,11 +117,15 @@ def trace_ops(m) -> dict:
 
 def _layer_gemms(m) -> list:
     """(weight, input width, K slices) of the four projections of layer 0 as the bf16 layer runner launches
-    them: qkv, o and w2 as K-slice partials (the plan's slice count), w13 with the silu-mul epilogue (0)."""
+    them: qkv fused with RoPE + append (-1), o and w2 as K-slice partials (the plan's slice count), w13 with the
+    silu-mul epilogue (0)."""
     lw, c = m.layers[0], m.cfg
     out = []
     for w, k in ((lw.wqkv, c.dim), (lw.wo, m.q_size), (lw.w13, c.dim), (lw.w2, c.intermediate_size)):
-        ks = 0 if w is lw.w13 else (_lsk.gemm_plan(w.shape[0], k)[1] if m.dtype == torch.bfloat16 else 1)
+        if w is lw.wqkv and getattr(w, "qkv_heads", None) is not None:
+            ks = -1
+        else:
+            ks = 0 if w is lw.w13 else (_lsk.gemm_plan(w.shape[0], k)[1] if m.dtype == torch.bfloat16 else 1)
         out.append((w, k, ks))
     return out
 
@@ -132,16 +136,27 @@ def measure_flops_eff(m, ns=N_GRID) -> dict:
     shapes = _layer_gemms(m)
     params = sum(w.shape[0] * w.shape[1] for w, _, _ in shapes)
     rows = []
+    c = m.cfg
+    if any(ks < 0 for _, _, ks in shapes):           # scratch cache row for the fused qkv launch (positions 0 .. n-1)
+        s_kv = (max(ns) + 31) // 32 * 32
+        kc = torch.zeros(1, c.n_kv_heads, s_kv // 32, c.head_dim // 16, 64, 8, dtype=m.dtype, device=m.device)
+        vc = torch.zeros(1, c.n_kv_heads, s_kv // 32, c.head_dim, 32, dtype=m.dtype, device=m.device)
+        rows_s = torch.zeros(max(ns), dtype=torch.int32, device=m.device)
+        pos_s = torch.arange(max(ns), dtype=torch.int32, device=m.device)
     with torch.inference_mode():
         for n in ns:
-            xs = [torch.randn(n, k, device=m.device, dtype=m.dtype) for _, k, _ in shapes]
-            outs = [torch.empty(n, w.shape[0] // 2, device=m.device, dtype=m.dtype) if ks == 0 else
+            xs = [torch.randn(_lsk.frag_rows(n) * k if ks < 0 else n * k, device=m.device, dtype=m.dtype).view(
+                -1 if ks < 0 else n, *(() if ks < 0 else (k,))) for _, k, ks in shapes]
+            outs = [torch.empty(n, c.n_heads, c.head_dim, device=m.device, dtype=m.dtype) if ks < 0 else
+                    torch.empty(n, w.shape[0] // 2, device=m.device, dtype=m.dtype) if ks == 0 else
                     (torch.empty(ks, n, w.shape[0], device=m.device) if m.dtype == torch.bfloat16 else
                      torch.empty(n, w.shape[0], device=m.device, dtype=m.dtype)) for w, _, ks in shapes]
 
             def run():
                 for (w, _, ks), x, o in zip(shapes, xs, outs):
-                    if ks == 0:
+                    if ks < 0:
+                        _lsk.gemm_qkv_rope(x, w, n, o, kc, vc, m.rope_cos, m.rope_sin, rows_s[:n], pos_s[:n])
+                    elif ks == 0:
                         _lsk.gemm(x, w, out=o, epilogue=_lsk.EPI_SILU_MUL)
                     elif m.dtype == torch.bfloat16:
                         _lsk.gemm_partial(x, w, ks, out=o)
