@@ -803,8 +803,8 @@ static void launch_bf16(int epi, dim3 grid, hipStream_t s, const uint16_t* A, lo
                                                                 ffn, kslice, nt, mt, m_lo, 0, QkvRope{});
 }
 
-// Fragment-major activations: split-K partial launches only.
-// Fragment-major A: split-K partials, silu-mul (C row-major, or fragment-major with c_nks > 0) and the LM head.
+// Fragment-major A: split-K partials, silu-mul (C row-major, or fragment-major with c_nks > 0), the LM head and
+// the fused qkv + RoPE + KV append.
 template <int NS, int MS>
 static void launch_bf16_af(int epi, dim3 grid, hipStream_t s, const uint16_t* A, const uint16_t* W, long ldw,
                            uint16_t* C, long ldc, int c_nks, float* P, float* av, int* ai, int M, int N, int K, int ffn,

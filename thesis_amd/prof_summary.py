@@ -31,7 +31,7 @@ REQ_SIZE_WEIGHTS = {"TCC_EA0_RDREQ_32B_sum": 32.0, "TCC_EA0_RDREQ_64B_sum": 64.0
 MARKER_MIN_WGS = 4096           # calibration copy: >= 4096 rows of 16 KiB; engine copies have <= a few hundred
 
 # kernel short name -> class of the decode step (names of the per-class HIP-event profiler in bench.py)
-_EPI = {"0": "gemm", "1": "gemm_residual", "2": "gemm_w13", "3": "gemm_partial", "4": "gemm_lm_head"}
+_EPI = {"0": "gemm", "1": "gemm_residual", "2": "gemm_w13", "3": "gemm_partial", "4": "gemm_lm_head", "5": "gemm_qkv"}
 
 
 def short_name(name: str) -> str:
@@ -49,8 +49,9 @@ def short_name(name: str) -> str:
 
 
 def classify(short: str, grid_x_threads=None) -> str:
-    """Kernel class; the split-K GEMMs of qkv and of o / w2 are told apart by their grid's x extent
-    (weight row tiles), which the counter CSV does not carry (it reports the total grid)."""
+    """Kernel class.  The bf16 qkv projection has its own epilogue (RoPE + KV append, 5); the split-K partial
+    launches of o / w2 (and of qkv where it is launched as a plain partial GEMM) are told apart by their grid's x
+    extent (weight row tiles), which the counter CSV does not carry (it reports the total grid)."""
     m = re.match(r"gemm_bf16_kernel<(\d+), (\d+), (\d+)(?:, (?:\d+|true|false))*>", short)
     if m:
         cls = _EPI.get(m.group(3), "gemm")
