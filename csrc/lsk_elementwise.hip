@@ -47,127 +47,168 @@ __device__ __forceinline__ float wave_sum(float v) {
 // x_new = rnd(x + rnd(sum_s P[s]))   (x + F.linear(...) with the GEMM's K-slice partials, s in order;
 //                                     KS = 0: x_new = x)
 // out   = w * (x_new * rsqrt(mean(x_new^2) + eps)).to(dtype)      (common/model.py:153-156)
-// One 256-thread workgroup per row, 8 consecutive elements per thread per pass (16-byte loads).  The sum
-// of squares is accumulated per thread in element order, reduced per wave by an xor tree and across the
-// four waves in index order, so a row's result never depends on the other rows of the call.
-template <typename T>
-struct Vec8;
+// One workgroup per row: NW waves, EPT consecutive elements per thread per pass (pass p, thread t: elements
+// (p * 64 NW + t) EPT .. + EPT - 1), NP passes.  The sum of squares is accumulated per thread in element order,
+// reduced per wave by an xor tree and across the waves in index order, so a row's result never depends on the
+// other rows of the call.  fp32: 4 waves x 8 elements (the order the fp32 oracle restates); bf16: 8 waves x 4
+// elements, twice the waves streaming the row (a row of 4096 with four fp32 partials: 4.6 -> 3.6 us per launch
+// at 16-48 rows, graph-timed on MI355X).  The pass count, the partial count and which outputs exist are
+// template arguments, so every load of a row is issued before the first add.
+template <typename T, int N>
+struct VecN;
 template <>
-struct Vec8<uint16_t> {
+struct VecN<uint16_t, 4> {
   static __device__ __forceinline__ void ld(const uint16_t* p, float* v) {
-    const uint4 u = *(const uint4*)p;
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(w[i] << 16);
-      v[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-    }
+    const uint2 u = *(const uint2*)p;
+    v[0] = __uint_as_float(u.x << 16);
+    v[1] = __uint_as_float(u.x & 0xffff0000u);
+    v[2] = __uint_as_float(u.y << 16);
+    v[3] = __uint_as_float(u.y & 0xffff0000u);
   }
   static __device__ __forceinline__ void st(uint16_t* p, const float* v) {
-    uint4 u;
+    uint2 u;
     u.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
     u.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-    u.z = (uint32_t)f2bf(v[4]) | ((uint32_t)f2bf(v[5]) << 16);
-    u.w = (uint32_t)f2bf(v[6]) | ((uint32_t)f2bf(v[7]) << 16);
-    *(uint4*)p = u;
+    *(uint2*)p = u;
   }
 };
 template <>
-struct Vec8<float> {
+struct VecN<float, 4> {
   static __device__ __forceinline__ void ld(const float* p, float* v) {
-    const float4 a = *(const float4*)p, b = *(const float4*)(p + 4);
-    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+    const float4 a = *(const float4*)p;
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
   }
-  static __device__ __forceinline__ void st(float* p, const float* v) {
-    *(float4*)p = make_float4(v[0], v[1], v[2], v[3]);
-    *(float4*)(p + 4) = make_float4(v[4], v[5], v[6], v[7]);
+  static __device__ __forceinline__ void st(float* p, const float* v) { *(float4*)p = make_float4(v[0], v[1], v[2], v[3]); }
+};
+template <typename T>
+struct VecN<T, 8> {
+  static __device__ __forceinline__ void ld(const T* p, float* v) {
+    VecN<T, 4>::ld(p, v);
+    VecN<T, 4>::ld(p + 4, v + 4);
+  }
+  static __device__ __forceinline__ void st(T* p, const float* v) {
+    VecN<T, 4>::st(p, v);
+    VecN<T, 4>::st(p + 4, v + 4);
   }
 };
 
-#define NORM_MAX_PASSES 4  // dim <= 4 * 256 * 8 = 8192
+template <typename T> struct NormShape;
+template <> struct NormShape<float> { static constexpr int NW = 4, EPT = 8; };
+template <> struct NormShape<uint16_t> { static constexpr int NW = 8, EPT = 4; };
+#define NORM_PASS_ELEMS 2048  // 64 NW EPT for both shapes
+#define NORM_MAX_DIM 8192     // 4 passes
 
-// KSC: the number of K-slice partials as a compile-time constant (all of a thread's partial loads are issued
-// before the first add; the adds keep slice order), or -1 for a run-time count.
-template <typename T, int KSC>
+// KSC: the number of K-slice partials (0: none), or -1 for a run-time count KS.  XO / NO: x_out / out are written.
 // x and x_out may be the same rows (the layer runner updates the residual stream in place), so neither is
-// declared __restrict__; every thread reads its 8 elements of a row before it writes them.
-__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const T* x, long ldx, const float* __restrict__ P,
-                                                          int KS, long pstride, const T* __restrict__ w,
-                                                          T* x_out, long ldxo, T* __restrict__ out,
-                                                          long ldo, int out_nks, int dim, float eps) {
+// declared __restrict__; every thread reads its elements of a row before it writes them.
+template <typename T, int KSC, int NP, bool XO, bool NO>
+__global__ __launch_bounds__(64 * NormShape<T>::NW) void add_rmsnorm_kernel(
+    const T* x, long ldx, const float* __restrict__ P, int KS, long pstride, const T* __restrict__ w, T* x_out,
+    long ldxo, T* __restrict__ out, long ldo, int out_nks, int dim, float eps) {
+  constexpr int NW = NormShape<T>::NW, EPT = NormShape<T>::EPT, NTH = 64 * NW;
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
-  float v[NORM_MAX_PASSES][8], wv[NORM_MAX_PASSES][8];
+  float v[NP][EPT], wv[NP][EPT];
   float ss = 0.f;
 #pragma unroll
-  for (int p = 0; p < NORM_MAX_PASSES; ++p) {
-    const int j = (p * 256 + tid) * 8;
+  for (int p = 0; p < NP; ++p) {
+    const int j = (p * NTH + tid) * EPT;
     if (j < dim) {
-      if (out != nullptr) Vec8<T>::ld(w + j, wv[p]);  // issued with the row's loads: no second round trip
-      Vec8<T>::ld(x + (long)row * ldx + j, v[p]);
-      if (KS > 0) {
-        float acc[8];
+      if constexpr (NO) VecN<T, EPT>::ld(w + j, wv[p]);  // issued with the row's loads: no second round trip
+      VecN<T, EPT>::ld(x + (long)row * ldx + j, v[p]);
+      if constexpr (KSC != 0) {
+        float acc[EPT];
         const float* pr = P + (long)row * dim + j;
         if constexpr (KSC > 0) {
-          float pv[KSC][8];
+          float pv[KSC][EPT];
 #pragma unroll
-          for (int s2 = 0; s2 < KSC; ++s2) Vec8<float>::ld(pr + s2 * pstride, pv[s2]);
+          for (int s2 = 0; s2 < KSC; ++s2) VecN<float, EPT>::ld(pr + s2 * pstride, pv[s2]);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = pv[0][i];
+          for (int i = 0; i < EPT; ++i) acc[i] = pv[0][i];
 #pragma unroll
           for (int s2 = 1; s2 < KSC; ++s2)
 #pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pv[s2][i];
+            for (int i = 0; i < EPT; ++i) acc[i] = acc[i] + pv[s2][i];
         } else {
+          VecN<float, EPT>::ld(pr, acc);
+          for (int s2 = 1; s2 < KS; ++s2) {
+            float pv[EPT];
+            VecN<float, EPT>::ld(pr + s2 * pstride, pv);
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[i] = pr[i];
-          for (int s2 = 1; s2 < KS; ++s2)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] = acc[i] + pr[s2 * pstride + i];
+            for (int i = 0; i < EPT; ++i) acc[i] = acc[i] + pv[i];
+          }
         }
 #pragma unroll
-        for (int i = 0; i < 8; ++i) v[p][i] = Elem<T>::round(v[p][i] + Elem<T>::round(acc[i]));
+        for (int i = 0; i < EPT; ++i) v[p][i] = Elem<T>::round(v[p][i] + Elem<T>::round(acc[i]));
       }
-      if (x_out != nullptr) Vec8<T>::st(x_out + (long)row * ldxo + j, v[p]);  // x_new (= x when KS == 0)
+      if constexpr (XO) VecN<T, EPT>::st(x_out + (long)row * ldxo + j, v[p]);  // x_new (= x when KS == 0)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ss += v[p][i] * v[p][i];
+      for (int i = 0; i < EPT; ++i) ss += v[p][i] * v[p][i];
     }
   }
-  if (out == nullptr) return;
-  ss = wave_sum(ss);
-  __shared__ float red[4];
-  const int wave = tid >> 6;
-  if ((tid & 63) == 0) red[wave] = ss;
-  __syncthreads();
-  const float tot = ((red[0] + red[1]) + red[2]) + red[3];
-  const float mean = tot / (float)dim;
-  const float r = 1.0f / sqrtf(mean + eps);
+  if constexpr (NO) {
+    ss = wave_sum(ss);
+    __shared__ float red[NW];
+    const int wave = tid >> 6;
+    if ((tid & 63) == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = red[0];
 #pragma unroll
-  for (int p = 0; p < NORM_MAX_PASSES; ++p) {
-    const int j = (p * 256 + tid) * 8;
-    if (j < dim) {
-      float o[8];
+    for (int i = 1; i < NW; ++i) tot = tot + red[i];
+    const float mean = tot / (float)dim;
+    const float r = 1.0f / sqrtf(mean + eps);
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = wv[p][i] * Elem<T>::round(v[p][i] * r);
-      // out_nks > 0: fragment-major output (the 8 elements at j stay one 16-byte slice)
-      Vec8<T>::st(out + (out_nks > 0 ? lsk_frag_off(row, j, out_nks) : (long)row * ldo + j), o);
+    for (int p = 0; p < NP; ++p) {
+      const int j = (p * NTH + tid) * EPT;
+      if (j < dim) {
+        float o[EPT];
+#pragma unroll
+        for (int i = 0; i < EPT; ++i) o[i] = wv[p][i] * Elem<T>::round(v[p][i] * r);
+        // out_nks > 0: fragment-major output (EPT elements at j stay inside one 16-byte slice of 8)
+        VecN<T, EPT>::st(out + (out_nks > 0 ? lsk_frag_off(row, j, out_nks) : (long)row * ldo + j), o);
+      }
     }
   }
+}
+
+template <typename T, int KSC, int NP>
+static void launch_add_rmsnorm_np(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
+                                  void* x_out, long ldxo, void* out, long ldo, int out_nks, int n_rows, int dim,
+                                  float eps, hipStream_t s) {
+  const dim3 grid(n_rows), block(64 * NormShape<T>::NW);
+  if (x_out == nullptr && out == nullptr) return;  // nothing to write
+#define LSK_NORM_LAUNCH(XO_, NO_)                                                                                   \
+  add_rmsnorm_kernel<T, KSC, NP, XO_, NO_><<<grid, block, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w,  \
+                                                                  (T*)x_out, ldxo, (T*)out, ldo, out_nks, dim, eps)
+  if (x_out != nullptr && out != nullptr) LSK_NORM_LAUNCH(true, true);
+  else if (out != nullptr) LSK_NORM_LAUNCH(false, true);
+  else LSK_NORM_LAUNCH(true, false);
+#undef LSK_NORM_LAUNCH
+}
+
+template <typename T, int KSC>
+static void launch_add_rmsnorm_ks(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
+                                  void* x_out, long ldxo, void* out, long ldo, int out_nks, int n_rows, int dim,
+                                  float eps, hipStream_t s) {
+  const int np = (dim + NORM_PASS_ELEMS - 1) / NORM_PASS_ELEMS;
+  if (np == 1) launch_add_rmsnorm_np<T, KSC, 1>(x, ldx, P, KS, pstride, w, x_out, ldxo, out, ldo, out_nks, n_rows, dim, eps, s);
+  else if (np == 2) launch_add_rmsnorm_np<T, KSC, 2>(x, ldx, P, KS, pstride, w, x_out, ldxo, out, ldo, out_nks, n_rows, dim, eps, s);
+  else launch_add_rmsnorm_np<T, KSC, 4>(x, ldx, P, KS, pstride, w, x_out, ldxo, out, ldo, out_nks, n_rows, dim, eps, s);
 }
 
 template <typename T>
 static void launch_add_rmsnorm(const void* x, long ldx, const float* P, int KS, long pstride, const void* w,
                                void* x_out, long ldxo, void* out, long ldo, int out_nks, int n_rows, int dim,
                                float eps, hipStream_t s) {
-#define LSK_NORM_LAUNCH(KSC_)                                                                                    \
-  add_rmsnorm_kernel<T, KSC_><<<n_rows, 256, 0, s>>>((const T*)x, ldx, P, KS, pstride, (const T*)w, (T*)x_out, \
-                                                     ldxo, (T*)out, ldo, out_nks, dim, eps)
-  if (KS == 4) LSK_NORM_LAUNCH(4);
-  else if (KS == 2) LSK_NORM_LAUNCH(2);
-  else if (KS == 8) LSK_NORM_LAUNCH(8);
-  else if (KS == 1) LSK_NORM_LAUNCH(1);
-  else LSK_NORM_LAUNCH(-1);
-#undef LSK_NORM_LAUNCH
+#define LSK_NORM_KS(KSC_) \
+  launch_add_rmsnorm_ks<T, KSC_>(x, ldx, P, KS, pstride, w, x_out, ldxo, out, ldo, out_nks, n_rows, dim, eps, s)
+  if (KS == 0) LSK_NORM_KS(0);
+  else if (KS == 4) LSK_NORM_KS(4);
+  else if (KS == 2) LSK_NORM_KS(2);
+  else if (KS == 8) LSK_NORM_KS(8);
+  else if (KS == 1) LSK_NORM_KS(1);
+  else LSK_NORM_KS(-1);
+#undef LSK_NORM_KS
 }
 
 extern "C" int lsk_add_rmsnorm(int dtype, const void* x, long ldx, const float* partials, int ks, const void* w,
@@ -181,7 +222,7 @@ int lsk_add_rmsnorm_impl(int dtype, const void* x, long ldx, const float* partia
                          void* stream) {
   LSK_REQUIRE(x != nullptr && (ks == 0 || partials != nullptr) && (out == nullptr || w != nullptr), LSK_EARG,
               "lsk_add_rmsnorm: null pointer");
-  LSK_REQUIRE(n_rows >= 0 && dim > 0 && dim % 8 == 0 && dim <= NORM_MAX_PASSES * 256 * 8 && ldx >= dim && ks >= 0 &&
+  LSK_REQUIRE(n_rows >= 0 && dim > 0 && dim % 8 == 0 && dim <= NORM_MAX_DIM && ldx >= dim && ks >= 0 &&
                   ldx % 8 == 0 && (out == nullptr || (ldo >= dim && ldo % 8 == 0)) &&
                   (x_out == nullptr || (ldxo >= dim && ldxo % 8 == 0)),
               LSK_ESHAPE, "lsk_add_rmsnorm: bad shape n_rows=%d dim=%d", n_rows, dim);
