@@ -535,6 +535,36 @@ def test_add_rmsnorm_without_partials_stores_x_out(cuda):
     assert torch.equal(xi, x)
 
 
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("ks,dim", [(1, 512), (2, 2056), (3, 4096), (8, 8192), (4, 2048)])
+def test_add_rmsnorm_slice_counts_and_widths(cuda, dtype, ks, dim):
+    """Every launch shape of the add + RMSNorm kernel (compile-time slice counts 1 / 2 / 4 / 8 and the run-time
+    count, one to four passes including a partly filled last pass): x_new = rnd(x + rnd(sum_s P[s])) bitwise,
+    the norm equal to the plain RMSNorm of x_new bitwise (same per-row order), and within one rounding of
+    common/model.py:153-156 evaluated by the oracle."""
+    lsk = _lsk()
+    g = _gen(100 + ks)
+    n = 11
+    x = torch.randn(n, dim, generator=g).to(dtype)
+    P = torch.randn(ks, n, dim, generator=g)
+    w = (1 + 0.1 * torch.randn(dim, generator=g)).to(dtype)
+    xd, wd = x.to(cuda), w.to(cuda)
+    xo, xn = torch.empty(n, dim, dtype=dtype, device=cuda), torch.empty(n, dim, dtype=dtype, device=cuda)
+    lsk.add_rmsnorm(xd, P.to(cuda), wd, 1e-5, x_out=xo, out=xn)
+    acc = P[0].clone()
+    for s in range(1, ks):
+        acc = acc + P[s]
+    x_new = (x.float() + acc.to(dtype).float()).to(dtype)
+    assert torch.equal(xo.cpu(), x_new)
+    assert torch.equal(xn, lsk.rmsnorm(xo, wd, 1e-5))
+    ref = o_rms_norm(x_new, w, 1e-5)
+    ulp = 2.0 ** -7 if dtype == BF16 else 2.0 ** -20
+    assert ((xn.cpu().float() - ref.float()).abs() <= ulp * ref.float().abs() + 1e-6).all()
+    xi = xd.clone()                                              # x_out only, in place: the residual update
+    lsk.add_rmsnorm(xi, P.to(cuda), None, 1e-5, x_out=xi)
+    assert torch.equal(xi.cpu(), x_new)
+
+
 @pytest.mark.parametrize("nc,nblk", [(1, 3), (5, 40), (7, 64)])
 def test_probe_matches_equal_the_closed_form(cuda, nc, nblk):
     """M2 agreement counts (solutions/engine.py:491-514): out[c] = #{t : pred[c, t] == Y[t] and jl[t] <= acc[blk[t]]},
