@@ -1,6 +1,6 @@
 // Native layer-range runner of the packed forward (solutions/packed.py:169-196: packed_layer /
 // packed_layers).  One call issues every kernel of layers [start, end) on one stream, so the host
-// pays one C call per segment instead of ~9 launches per layer from Python.
+// pays one C call per segment instead of ~8 launches per layer from Python.
 //
 // Per layer (same op order and rounding points as solutions/packed.py:175-185):
 //   xn   = rmsnorm(x, attn_norm)                      lsk_rmsnorm

@@ -177,10 +177,10 @@ def synthetic_cost_model(cfg, kind: str = "roofline"):
 
 def mi355x_cost_model(cfg, bw_frac: float = 0.7, flops_frac: float = 0.5, t_op_ms: float = 0.004):
     """MI355X: HBM3E 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s, scaled by the fractions the kernels reach.
-    Launch terms follow this build's layer runner: 9 launches per layer (norm, QKV, RoPE+append,
+    Launch terms follow this build's bf16 layer runner: 8 launches per layer (norm, QKV with RoPE + KV append,
     attention, combine, O, norm, W13, W2), 3 per head (norm, GEMM, argmax), ~4 per segment."""
     dims = ModelDims.from_config(cfg)
-    gpu = GPUParams(bw=8.0e9 * bw_frac, flops=2.5166e12, t_op=t_op_ms, n_op_layer=9, n_op_bucket=0, n_op_head=3,
+    gpu = GPUParams(bw=8.0e9 * bw_frac, flops=2.5166e12, t_op=t_op_ms, n_op_layer=8, n_op_bucket=0, n_op_head=3,
                     n_op_segment=4, meta={"source": "MI355X peaks x achieved fractions", "bw_frac": bw_frac,
                                           "flops_frac": flops_frac},
                     flops_eff=2.5166e12 * flops_frac)
