@@ -59,6 +59,18 @@ def test_argument_errors_are_reported_on_the_host():
     assert lib.lsk_pack_weight(8, 64, 16, 40, 64, None) == -2                          # N % 16 != 0
     assert lib.lsk_unpack_weight(8, 16, 64, 64, 48, None) == -2                        # K % 32 != 0
     assert lib.lsk_rmsnorm(1, 8, 8, 8, 4, 7, 1e-5, 7, 7, None) == -2                 # dim % 8 != 0
+    # fused qkv + RoPE + KV append: pointers, head shapes and cache shape are checked before any launch
+    q = lib.lsk_gemm_qkv_rope
+    assert q(None, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -1         # null A
+    assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, None, 8, 2, 64, None) == -1         # null rows
+    assert q(8, 8, 4, 32, 8, 80, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2             # head_dim % 32
+    assert q(8, 8, 4, 0, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2             # no q heads
+    assert q(8, 8, 4, 32, 8, 128, 4000, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2           # K % 32
+    assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 48, None) == -2           # max_seq % 32
+    assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 0, 8, 8, 2, 64, None) == -2            # empty RoPE table
+    assert q(8, 8, 0, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == 0            # M = 0: no launch
+    assert lib.lsk_pack_weight_qkv(8, 4096, 8, 32, 8, 80, 4096, None) == -2                   # head_dim % 32
+    assert lib.lsk_unpack_weight_qkv(8, 8, 4096, 32, 0, 128, 4096, None) == -2                 # no kv heads
     assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, 8, 1, 1, 48, 8, 32, 8, 96, 64, 0.1, None, 0,
                                None) == -3                                            # head_dim 96
     assert lib.lsk_ragged_attn(1, 8, 8, 8, 8, 8, 1, None, 0, 0, None, 0, 0, 48, 8, 32, 8, 128, 64, 0.1, None, 0,
