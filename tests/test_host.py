@@ -65,7 +65,7 @@ def test_argument_errors_are_reported_on_the_host():
     assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, None, 8, 2, 64, None) == -1         # null rows
     assert q(8, 8, 4, 32, 8, 80, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2             # head_dim % 32
     assert q(8, 8, 4, 0, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2             # no q heads
-    assert q(8, 8, 4, 32, 8, 128, 4000, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2           # K % 32
+    assert q(8, 8, 4, 32, 8, 128, 4010, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == -2           # K % 32
     assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 48, None) == -2           # max_seq % 32
     assert q(8, 8, 4, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 0, 8, 8, 2, 64, None) == -2            # empty RoPE table
     assert q(8, 8, 0, 32, 8, 128, 4096, 8, 8, 8, 8, 8, 64, 8, 8, 2, 64, None) == 0            # M = 0: no launch
