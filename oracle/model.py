@@ -18,7 +18,10 @@ points of its eager ops kept in place (so a bf16 oracle rounds where the referen
   qo_indptr        solutions/packed.py:199-201
 
 OracleLlama(ordered=True) (fp32) evaluates the reductions in the fixed order of oracle/ordered.py, the
-fp32 kernels' order, so the fp32 engine is compared with it bit for bit.
+fp32 kernels' order, so the fp32 engine is compared with it bit for bit.  OracleLlama(attention="blocked")
+(bf16) runs attention in the bf16 kernel's softmax blocking (ordered.attend_bf16_blocked: 32-position steps dealt
+to 8 waves, P rounded to bf16 at each step's running max, waves then position splits merged in order); every
+other op keeps the reference's eager bf16 rounding points.
 
 Pinned by (tests/test_oracle.py): HF transformers LlamaForCausalLM golden logits / hidden states
 (tests/golden/hf_tiny.npz), fp64 brute-force per-token attention, packed == per-block forward,
@@ -180,12 +183,18 @@ class OracleLlama:
     """CPU LayerSkip-Llama; same attributes as the reference model object where the packed path reads them."""
 
     def __init__(self, cfg: OracleConfig, weights: dict, dtype=torch.float32, max_seq: int = 512,
-                 ordered: bool = False):
-        """ordered=True (fp32 only): the reductions run in the fixed order of oracle/ordered.py."""
+                 ordered: bool = False, attention: str = "sdpa"):
+        """ordered=True (fp32 only): the reductions run in the fixed order of oracle/ordered.py.
+        attention="blocked" (bf16 only): attention in the bf16 kernel's softmax blocking
+        (ordered.attend_bf16_blocked); "sdpa": torch's scaled_dot_product_attention, as the reference."""
         if ordered and dtype != torch.float32:
             raise ValueError("the ordered oracle is fp32 only")
+        if attention not in ("sdpa", "blocked") or (attention == "blocked" and dtype != torch.bfloat16):
+            raise ValueError(f"attention={attention!r} (sdpa, or blocked for bf16)")
         self.cfg, self.dtype, self.device = cfg, dtype, torch.device("cpu")
         self.ordered = ordered
+        self.attention = attention
+        self.attn_split = 2048
         self.group = cfg.n_heads // cfg.n_kv_heads
         self.q_size = cfg.n_heads * cfg.head_dim
         self.kv_size = cfg.n_kv_heads * cfg.head_dim
@@ -253,6 +262,8 @@ class OracleLlama:
         if max_seq > self.rope_cos.shape[0]:
             self.rope_cos, self.rope_sin = rope_tables(self.cfg, max_seq)
         self.cache = OracleCache(self.cfg, max_batch, max_seq, self.dtype)
+        # the bf16 kernel's position splits: 4096 positions once the cache holds >= 1024 (row, KV head) stripes
+        self.attn_split = 4096 if max_batch * self.cfg.n_kv_heads >= 1024 else 2048
         return self.cache
 
     def embed(self, ids: torch.Tensor) -> torch.Tensor:
@@ -376,6 +387,10 @@ def attend(model, i: int, q: torch.Tensor, pb: OPacked) -> torch.Tensor:
     if getattr(model, "ordered", False):
         o = O.attend(O.t2n(q), O.t2n(model.cache.k[i]), O.t2n(model.cache.v[i]), pb.rows, pb.pos, model.group)
         return O.n2t(o.reshape(q.shape[0], model.q_size))
+    if getattr(model, "attention", "sdpa") == "blocked":
+        o = O.attend_bf16_blocked(O.t2n(q), O.t2n(model.cache.k[i]), O.t2n(model.cache.v[i]), pb.rows, pb.pos,
+                                  model.group, model.attn_split)
+        return O.n2t(o.reshape(q.shape[0], model.q_size)).to(q.dtype)
     G, Hkv, D = model.group, model.cfg.n_kv_heads, model.cfg.head_dim
     ck, cv = model.cache.k[i], model.cache.v[i]
     out = torch.empty(q.shape[0], model.q_size, dtype=q.dtype)

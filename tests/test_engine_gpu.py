@@ -99,15 +99,25 @@ def test_packed_forward_fp32_is_bit_exact_against_the_ordered_oracle(cuda, which
 
 
 def test_packed_forward_bf16_logits_within_tolerance(cuda):
-    """bf16 bar: per-row ||dlogits||_2 / ||logits||_2 <= 2e-2 after 4 layers against the bf16 oracle
-    (bf16 carries ~3.9e-3 relative rounding per op; the oracle rounds at the reference's points)."""
+    """bf16, four layers with a 24-token prefix prefilled through the same path on both sides: per-row
+    ||dlogits||_2 / ||logits||_2 <= 2e-2 against the bf16 oracle with the reference's SDPA, and on average at most
+    0.75 x that against the oracle with the kernel's softmax blocking (measured 5.1e-3 vs 9.6e-3 mean: over four
+    layers the rare one-ulp differences of the GEMMs' summation order cascade, see the one-layer test)."""
+    from oracle.model import OracleLlama, random_weights
+
     o, g = _pair(small_cfg(), BF16)
-    o.allocate_cache(4, 128)
-    g.allocate_cache(4, 128)
+    ob = OracleLlama(small_cfg(), random_weights(small_cfg(), seed=0, std=0.05), dtype=BF16, max_seq=1024,
+                     attention="blocked")
+    for m in (o, g, ob):
+        m.allocate_cache(4, 128)
     blocks = [(0, 24, 1), (1, 24, 4), (2, 24, 2), (3, 24, 9)]
     _, _, lo, lg, _, _ = _ragged_forward(o, g, blocks)
+    lb = _oracle_ragged(ob, blocks)
     rel = ((lg.float() - lo.float()).norm(dim=-1) / lo.float().norm(dim=-1))
-    print(f"bf16 per-row relative L2 of logits: max {rel.max():.3e} mean {rel.mean():.3e}")
+    rel_b = ((lg.float() - lb.float()).norm(dim=-1) / lb.float().norm(dim=-1))
+    print(f"bf16 per-row relative L2 of logits: blocked-attention oracle max {rel_b.max():.3e} mean "
+          f"{rel_b.mean():.3e}; SDPA oracle max {rel.max():.3e} mean {rel.mean():.3e}")
+    assert rel_b.mean() <= 0.75 * rel.mean() and rel_b.max() < 2e-2
     assert rel.max() < 2e-2
 
 
@@ -197,7 +207,7 @@ ONE_LAYER_CFGS = {
 }
 
 
-def _one_layer_state(ocfg, seed, n_prefix=40):
+def _one_layer_state(ocfg, seed, n_prefix=40, std=0.05):
     """The same bf16 state on both sides: bf16 weights, a cached prefix of random bf16 K / V (written into the
     oracle's [B, Hkv, S, D] cache and copied into the kernels' layouts), bf16 input rows of ragged blocks."""
     from oracle.model import OBlock, OracleLlama, build_packed as obuild, random_weights
@@ -205,7 +215,7 @@ def _one_layer_state(ocfg, seed, n_prefix=40):
     from thesis_amd.common.model import LayerSkipLlama
     from thesis_amd.solutions.packed import Block, build_packed
 
-    w = random_weights(ocfg, seed=seed, std=0.05)
+    w = random_weights(ocfg, seed=seed, std=std)
     o = OracleLlama(ocfg, w, dtype=BF16, max_seq=1024)
     g = LayerSkipLlama.from_weights(to_model_config(ocfg), w, device="cuda", dtype=BF16, max_seq=1024)
     B = 6
@@ -239,10 +249,11 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
       * RMSNorm, qkv GEMM + RoPE + KV append, o GEMM + residual, w13 GEMM + silu-mul, w2 GEMM + residual:
         relative L2 <= 1e-4 (a tenth of the 1e-3 bar) and at most 2e-3 of the elements one rounding apart
         (fp32 summation order only);
-      * attention: both sides round the softmax weights to bf16 for the P.V product, at different running
-        maxima, so each is ~2e-3 from the exact result.  Bar: this build's distance to the fp64 brute force lies
-        within [0.75, 1.25] x the oracle's own (a dropped term or a missing rescale lands far outside), and the
-        two differ by at most 3e-3."""
+      * attention against the oracle with the kernel's softmax blocking (oracle/ordered.py attend_bf16_blocked):
+        the same bar, relative L2 <= 1e-4;
+      * attention against the reference's SDPA form: both round the softmax weights to bf16 for the P.V product,
+        at different running maxima, so each is ~2e-3 from the exact result.  Bar: this build's distance to the
+        fp64 brute force lies within [0.75, 1.25] x the SDPA oracle's own, and the two differ by at most 3e-3."""
     import math
     import torch.nn.functional as F
 
@@ -300,6 +311,11 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
                      dv(groups) if len(groups) else None, len(groups), n_parts, att_gpu, cfg.n_heads,
                      1.0 / math.sqrt(cfg.head_dim), ws, dv(recs), n_rounds, n_slots, cap)
     exact = brute_attention(q, o.cache.k[0], o.cache.v[0], opb.rows.tolist(), opb.pos.tolist(), o.group)
+    o.attention = "blocked"                                   # the kernel's softmax blocking, restated
+    with torch.inference_mode():
+        att_blk = attend(o, 0, q, opb)
+    o.attention = "sdpa"
+    stages["attention (blocked)"] = _rel(att_gpu, att_blk)
     d_ours, d_oracle, d_pair = _rel(att_gpu, exact)[0], _rel(att, exact)[0], _rel(att_gpu, att)[0]
     print(f"[{which}] " + "; ".join(f"{k} relL2 {r:.2e} differ {f:.1e}" for k, (r, f) in stages.items())
           + f"; K/V equal {kv_same[0]:.5f}/{kv_same[1]:.5f}; attention relL2 to exact: this build {d_ours:.3e}, "
@@ -311,22 +327,38 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
     assert d_pair <= 3e-3
 
 
+@pytest.mark.parametrize("std", [0.02, 0.05])
+@pytest.mark.parametrize("seed", [3, 4, 5])
 @pytest.mark.parametrize("which", list(ONE_LAYER_CFGS))
-def test_one_layer_bf16_logits_against_the_bf16_oracle(cuda, which):
+def test_one_layer_bf16_logits_against_the_bf16_oracle(cuda, which, seed, std):
     """The whole layer end to end (packed_layers, then the final norm + LM head) against the bf16 oracle from the
-    same state.  Every stage but attention agrees to ~1e-5 (test above); the attention's bf16 softmax weights
-    differ in rounding on the two sides (each ~2e-3 from exact), which carries into the logits: measured
-    4.6e-3 (head_dim 64) and 6.6e-3 (head_dim 128) per-row relative L2.  Bar: 1e-2, and the greedy tokens agree
-    on every row whose top-2 logit margin exceeds that noise."""
+    same state, at the configurations' HF-style init (std 0.02) and at std 0.05.
+      * Oracle with the kernel's softmax blocking (attention="blocked"; every other op at the reference's eager
+        bf16 rounding points): relative L2 of the logits tensor <= 1e-3 at std 0.02 (1.5e-3 at std 0.05), and most
+        rows bitwise equal (median row 0).  A row differs only where one upstream bf16 rounding fell the other way
+        (the MFMA's fp32 summation order is not restated; ~1e-4 of a GEMM's outputs): that one-ulp change moves
+        the MLP's inputs by about their own rounding step and cascades into 10^2 one-ulp differences of that row's
+        hidden state, 1-4e-3 of its logits.  Bar per row: 5e-3.
+      * Oracle with the reference's SDPA: the two attentions round the softmax weights to bf16 at different running
+        maxima (each ~2e-3 from exact), which carries into every row's logits (measured 1.6-6e-3).  Bar: 1e-2, and
+        the greedy tokens agree on every row whose top-2 logit margin exceeds that noise."""
     from oracle.model import packed_layer as olayer
     from thesis_amd.solutions.packed import packed_layers
 
-    o, g, opb, gpb, x = _one_layer_state(small_cfg(**ONE_LAYER_CFGS[which]), seed=3)
+    o, g, opb, gpb, x = _one_layer_state(small_cfg(**ONE_LAYER_CFGS[which]), seed=seed, std=std)
     with torch.inference_mode():
         lo = o.head(olayer(o, 0, x, opb)).float()
+        o.attention = "blocked"                               # rewrites the same K / V, then attends blocked
+        lb = o.head(olayer(o, 0, x, opb)).float()
     lg = g.head(packed_layers(g, x.cuda(), gpb, 0, 1)).cpu().float()
     rel = (lg - lo).norm(dim=-1) / lo.norm(dim=-1)
-    print(f"[{which}] one bf16 layer, logits per-row relative L2: max {rel.max():.3e} mean {rel.mean():.3e}")
+    rel_b = (lg - lb).norm(dim=-1) / lb.norm(dim=-1)
+    tot_b = float((lg - lb).norm() / lb.norm())
+    print(f"[{which} seed {seed} std {std}] one bf16 layer, logits relative L2: blocked-attention oracle whole "
+          f"{tot_b:.3e} per-row max {rel_b.max():.3e} median {rel_b.median():.3e} rows bitwise equal "
+          f"{int((rel_b == 0).sum())}/{len(rel_b)}; SDPA oracle per-row max {rel.max():.3e} mean {rel.mean():.3e}")
+    assert tot_b <= (1e-3 if std <= 0.02 else 1.5e-3)
+    assert rel_b.median() <= 1e-5 and rel_b.max() <= 5e-3
     assert rel.max() <= 1e-2
     top2 = lo.topk(2, dim=-1).values
     clear = (top2[:, 0] - top2[:, 1]) > 4 * (lg - lo).abs().max(dim=-1).values

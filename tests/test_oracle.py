@@ -308,3 +308,105 @@ def test_ordered_checks_catch_planted_mistakes(monkeypatch):
     nrm = O.rms_norm(a, np.ones(700, np.float32), 1e-5)
     plain_ms = np.float32(1) / np.sqrt((a * a).sum(axis=1, dtype=np.float32) / np.float32(700) + np.float32(1e-5))
     assert np.allclose(nrm, a * plain_ms[:, None], rtol=1e-5) and not np.array_equal(nrm, a * plain_ms[:, None])
+
+
+# ----------------------------------------------------------------------------- blocked bf16 attention
+
+def _exact_attention_case(seed=0, D=64, G=4, Hkv=2, split=512, ctx=(37, 300, 700, 1100, 1535)):
+    """Inputs on which every step of the blocked bf16 softmax is exact: with scale_log2 = 1 and one-hot queries a
+    score is one integer K entry in [-6, 0], so every p, alpha and merge weight is a power of two 2^-k (k <= 6, bf16
+    exact) and every partial O / L is a multiple of 2^-6 below 2^13 (exact in fp32).  The scores rise within a wave
+    (round 0 in [-6, -3], later rounds in [-6, -2]), one wave per split sees -1, and one position of the second
+    split scores 0, so the running-max rescale, the wave merge weights and the split merge weights all matter."""
+    rng = np.random.default_rng(seed)
+    n = max(ctx)
+    S = ((n + 63) // 64 + 1) * 64
+    K = rng.integers(-6, -2, size=(1, Hkv, S, D)).astype(np.float32)
+    pos_in = np.arange(S) % split
+    later = pos_in >= 256
+    K[:, :, later] = rng.integers(-6, -1, size=(1, Hkv, int(later.sum()), D))
+    wave = (pos_in // 32) % 8
+    hot = later & (wave == (np.arange(S) // split) % 8)
+    K[:, :, hot] = rng.integers(-6, 0, size=(1, Hkv, int(hot.sum()), D))
+    K[:, :, split + 300] = 0.0
+    V = rng.integers(-4, 5, size=(1, Hkv, S, D)).astype(np.float32)
+    N = len(ctx)
+    q = np.zeros((N, Hkv * G, D), np.float32)
+    hot_dim = rng.integers(0, D, size=(N, Hkv * G))
+    q[np.arange(N)[:, None], np.arange(Hkv * G)[None, :], hot_dim] = 1.0
+    pos = np.array(ctx) - 1
+    return q, K, V, np.zeros(N, np.int64), pos, G, split
+
+
+def _exact_base2(q, K, V, rows, pos, G):
+    """Textbook softmax in base 2 over the scores q . k (scale_log2 = 1), fp64, then rounded fp32 -> bf16."""
+    import oracle.ordered as O
+
+    N, Hq, D = q.shape
+    out = np.zeros((N, Hq, D), np.float64)
+    for t in range(N):
+        for h in range(Hq):
+            s = K[rows[t], h // G, :pos[t] + 1].astype(np.float64) @ q[t, h].astype(np.float64)
+            w = np.exp2(s - s.max())
+            out[t, h] = (w @ V[rows[t], h // G, :pos[t] + 1].astype(np.float64)) / w.sum()
+    return O.bf16_round(out.astype(np.float32))
+
+
+def test_blocked_bf16_attention_is_exact_where_every_step_is_exact():
+    """Known answer: on the exact inputs the blocked softmax (several waves, rounds and position splits) equals the
+    base-2 textbook result bit for bit, for a single-split and a four-split context alike.  Planted mistakes -- no
+    alpha rescale of the running output, waves and splits summed without their weights -- change the result."""
+    import oracle.ordered as O
+
+    q, K, V, rows, pos, G, split = _exact_attention_case()
+    want = _exact_base2(q, K, V, rows, pos, G)
+    got = O.attend_bf16_blocked(q, K, V, rows, pos, G, split, scale_log2=1.0)
+    assert np.array_equal(got, want)
+    for kw in (dict(rescale=False), dict(weigh_waves=False)):
+        bad = O.attend_bf16_blocked(q, K, V, rows, pos, G, split, scale_log2=1.0, **kw)
+        assert not np.array_equal(bad, want), kw
+        assert (bad != want).mean() > 0.05, kw
+    # the same inputs with no split at all (one wave chain over the whole context) agree too
+    assert np.array_equal(O.attend_bf16_blocked(q, K, V, rows, pos, G, 1 << 20, scale_log2=1.0), want)
+
+
+def _random_attention_case(seed, D, G=4, Hkv=2, ctx=(1, 9, 64, 257, 600, 2100, 4500)):
+    rng = np.random.default_rng(seed)
+    S = (max(ctx) + 63) // 64 * 64
+    bf = lambda a: torch.from_numpy(a.astype(np.float32)).to(torch.bfloat16)  # noqa: E731
+    K = bf(rng.normal(size=(2, Hkv, S, D)))
+    V = bf(rng.normal(size=(2, Hkv, S, D)))
+    q = bf(rng.normal(size=(len(ctx), Hkv * G, D)))
+    rows = np.arange(len(ctx)) % 2
+    pos = np.array(ctx) - 1
+    return q, K, V, rows, pos, G
+
+
+@pytest.mark.parametrize("D", [64, 128])
+def test_blocked_bf16_attention_sits_at_the_bf16_rounding_floor(D):
+    """Random bf16 inputs, contexts of 1 to 4500 positions (up to three 2048-position splits): the blocked form is
+    as far from the fp64 brute force as the reference's eager bf16 SDPA is (within [0.75, 1.25] x: both round the
+    softmax weights to bf16), and within 3e-3 of it.  Planted mistakes land outside: weights kept in fp32 (no bf16
+    rounding of P or of the output) sit far closer to exact, a dropped rescale or unweighted merges far above."""
+    import torch.nn.functional as F
+
+    import oracle.ordered as O
+
+    q, K, V, rows, pos, G = _random_attention_case(3, D)
+    exact = om.brute_attention(q.float(), K.float(), V.float(), rows, pos, G).view(len(pos), -1, D).numpy()
+    sdpa = np.zeros_like(exact)
+    for t in range(len(pos)):
+        kk = K[rows[t], :, :pos[t] + 1].repeat_interleave(G, 0)
+        vv = V[rows[t], :, :pos[t] + 1].repeat_interleave(G, 0)
+        sdpa[t] = F.scaled_dot_product_attention(q[t][:, None], kk, vv)[:, 0].float().numpy()
+    args = (q.float().numpy(), K.float().numpy(), V.float().numpy(), rows, pos, G, 2048)
+    got = O.attend_bf16_blocked(*args)
+    rel = lambda a: float(np.linalg.norm(a - exact) / np.linalg.norm(exact))  # noqa: E731
+    d_blk, d_sdpa = rel(got), rel(sdpa)
+    assert 0.75 * d_sdpa <= d_blk <= 1.25 * d_sdpa, (d_blk, d_sdpa)
+    assert float(np.linalg.norm(got - sdpa) / np.linalg.norm(sdpa)) <= 3e-3
+    assert rel(O.attend_bf16_blocked(*args, rescale=False)) > 10 * d_sdpa
+    assert rel(O.attend_bf16_blocked(*args, weigh_waves=False)) > 10 * d_sdpa
+    import unittest.mock as um
+    with um.patch.object(O, "bf16_round", lambda x: np.asarray(x, np.float32)):
+        assert rel(O.attend_bf16_blocked(*args)) < 0.1 * d_sdpa
