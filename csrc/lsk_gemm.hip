@@ -916,19 +916,37 @@ static void launch_wide_kernel(dim3 grid, hipStream_t s, bool af, const uint16_t
                                                               kslice, n_tiles, m_blocks, ks, 0, tbg, QkvRope{});
 }
 
-static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
-                       const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks,
-                       bool af = false, int c_nks = 0, const QkvRope& qa = QkvRope{}) {
-  if (M <= 64) return 0;
-  if (N % 64 != 0 || (epi != EPI_PARTIAL && C != nullptr && ldc % 4 != 0) || K % ks != 0 || (K / ks) % 128 != 0)
-    return 0;
-  if (af && (epi == LSK_EPI_RESIDUAL || epi == LSK_EPI_NONE)) return 0;
-  if (epi == EPI_QKV && !af) return 0;
+// Whether the wide tier takes a launch (ns == 0: no) and its configuration.  c_ok: the output's row stride
+// allows the tier's 4-element stores.
+static WideCfg wide_plan(int epi, int M, int N, int K, int ks, bool af, bool c_ok) {
+  const WideCfg none{0, 0, 0, 0};
+  if (M <= 64 || ks <= 0) return none;
+  if (N % 64 != 0 || !c_ok || K % ks != 0 || (K / ks) % 128 != 0) return none;
+  if (af && (epi == LSK_EPI_RESIDUAL || epi == LSK_EPI_NONE)) return none;
+  if (epi == EPI_QKV && !af) return none;
   // the tier streams the weights with >= 192 workgroups: 64-row tiles (32-row for the fused qkv, which has no K
   // split) x the fewest blocks must reach that
   const int gtot = (M + 15) / 16, cap = 8 * (epi == LSK_EPI_SILU_MUL ? 2 : 3);
-  if ((long)(N / (epi == EPI_QKV ? 32 : 64)) * ((gtot + cap - 1) / cap) * ks < 192) return 0;
-  const WideCfg cfg = wide_config(epi, M, N, ks);
+  if ((long)(N / (epi == EPI_QKV ? 32 : 64)) * ((gtot + cap - 1) / cap) * ks < 192) return none;
+  return wide_config(epi, M, N, ks);
+}
+
+extern "C" int lsk_gemm_wide_config(int epilogue, int M, int N, int K, int ks, int af, int* cfg) {
+  LSK_REQUIRE(cfg != nullptr, LSK_EARG, "lsk_gemm_wide_config: null pointer");
+  LSK_REQUIRE(epilogue >= LSK_EPI_NONE && epilogue <= EPI_QKV, LSK_EARG, "lsk_gemm_wide_config: epilogue %d",
+              epilogue);
+  const WideCfg c = wide_plan(epilogue, M, N, K, ks, af != 0, true);
+  cfg[0] = c.ns;
+  cfg[1] = c.m_blocks;
+  cfg[2] = c.tbg;
+  cfg[3] = c.msw;
+  return 0;
+}
+
+static int launch_wide(int epi, hipStream_t s, const uint16_t* A, long lda, const uint16_t* W, uint16_t* C, long ldc,
+                       const uint16_t* R, long ldr, float* P, float* av, int* ai, int M, int N, int K, int ffn, int ks,
+                       bool af = false, int c_nks = 0, const QkvRope& qa = QkvRope{}) {
+  const WideCfg cfg = wide_plan(epi, M, N, K, ks, af, epi == EPI_PARTIAL || C == nullptr || ldc % 4 == 0);
   if (cfg.ns == 0) return 0;
   const int n_tiles = N / (16 * cfg.ns);
   const dim3 grid((unsigned)(((n_tiles + 7) / 8) * 8 * cfg.m_blocks * ks));

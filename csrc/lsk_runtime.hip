@@ -238,9 +238,9 @@ extern "C" int lsk_forward_layers(long handle, const void* x_in, void* x_out, in
   int rc;
   const double es_d = (double)es, Nd = N, dimd = m->dim, qkvd = qd + 2 * kvd, ffd = m->ffn;
   if (m->dtype == LSK_DTYPE_BF16) {
-    // bf16 flow: the small-N projections (qkv, o, w2) leave fp32 K-slice partials in P that the next
-    // kernel reduces in slice order (RoPE + append; add + RMSNorm, which also materialises the residual
-    // stream x).  Same rounding points as the unfused sequence.
+    // bf16 flow: the qkv projection is one launch with RoPE and the KV append in its epilogue (no K split);
+    // the o and w2 projections leave fp32 K-slice partials in P that the next add + RMSNorm reduces in slice
+    // order (it also materialises the residual stream x).  Same rounding points as the unfused sequence.
     float* P = (float*)(ws + L.gpart);
     // GEMM inputs kept fragment-major (1 KiB contiguous per MFMA fragment; every row tile re-reads them from
     // L2, where a row-major fragment -- 16 rows x 64 bytes -- reads at a third of the rate): the qkv input

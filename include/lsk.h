@@ -23,7 +23,7 @@
 extern "C" {
 #endif
 
-#define LSK_ABI_VERSION 10
+#define LSK_ABI_VERSION 11
 
 #define LSK_EPI_NONE 0     /* C = rnd(A W^T)                                   */
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
@@ -146,6 +146,13 @@ int lsk_gemm(int dtype, const void* A, long lda, const void* W, long ldw, void* 
  * order) and ns, the 16-row-group tile width the rule is based on.  Chosen from (N, K) only, so the
  * reduction order never depends on the token count M; each launch picks its own tile width from M. */
 int lsk_gemm_plan(int N, int K, int* ns_out, int* ks_out);
+
+/* Configuration the wide-M tier (the bf16 GEMM path above 64 tokens) picks for a launch: cfg[4] = {ns (16-row
+ * groups per tile; 0: the tier does not take the launch), blocks, 16-token groups per block, groups per wave}.
+ * epilogue: LSK_EPI_*, or 3 = K-slice partials (lsk_gemm_partial), 4 = LM head + argmax, 5 = fused qkv + RoPE +
+ * KV append; af: fragment-major A.  A query only (no launch): for tests and measurement tools to know which
+ * kernel configuration a token count reaches.  Part of the lsk_gemm* family above (solutions/packed.py:175-185). */
+int lsk_gemm_wide_config(int epilogue, int M, int N, int K, int ks, int af, int* cfg);
 
 /* bf16 GEMM into fp32 K-slice partials (W packed, ldw == K): P[s][m][n] = sum over k in slice s of A[m][k] W[n][k], s < ks
  * (ks must equal lsk_gemm_plan's for this shape to keep the canonical reduction order; the consumer adds

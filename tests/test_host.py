@@ -852,3 +852,150 @@ def test_open_loop_driver_on_a_stub_engine():
                         lambda i, t: (i, t), admit, arr, 6, lambda: None)
     assert eng.released == 6 and [r[0] for r in eng.order[:6]] == list(range(6))
     assert all(a[1] <= b[1] for a, b in zip(eng.order, eng.order[1:])) and left >= 0
+
+
+def test_graph_capture_runs_with_the_cyclic_collector_disabled(monkeypatch):
+    """ShallowGraphs.run captures a step with Python's cyclic garbage collector off (a collected object holding a
+    pinned buffer or an event can issue a stream operation from its destructor, which a capturing stream refuses)
+    and restores the collector afterwards, also when the step raises; a collector the caller had disabled stays
+    disabled.  torch.cuda.graph / CUDAGraph are replaced by recording stand-ins, so this runs on the CPU."""
+    import contextlib
+    import gc
+
+    from thesis_amd.solutions import step_graph
+
+    events = []
+
+    class FakeGraph:
+        def replay(self):
+            events.append("replay")
+
+    @contextlib.contextmanager
+    def fake_capture(g):
+        events.append("capture-begin")
+        yield
+        events.append("capture-end")
+
+    monkeypatch.setattr(torch.cuda, "CUDAGraph", FakeGraph)
+    monkeypatch.setattr(torch.cuda, "graph", fake_capture)
+    sg = step_graph.ShallowGraphs("cpu")
+
+    def entry():
+        return SimpleNamespace(graph=None, epoch=-1, seen=0, out=None)
+
+    seen_gc = []
+
+    def step():
+        seen_gc.append(gc.isenabled())
+        return "out"
+
+    was = gc.isenabled()
+    try:
+        gc.enable()
+        e = entry()
+        assert sg.run(e, lambda: 0, step) == "eager" and seen_gc == [True]       # first sighting: eager
+        assert sg.run(e, lambda: 0, step) == "capture" and seen_gc == [True, False]
+        assert gc.isenabled() and events == ["capture-begin", "capture-end", "replay"]
+        assert sg.run(e, lambda: 0, step) == "replay" and len(seen_gc) == 2
+
+        def boom():
+            seen_gc.append(gc.isenabled())
+            raise RuntimeError("step failed")
+
+        e2 = entry()
+        e2.seen = 1
+        with pytest.raises(RuntimeError, match="step failed"):
+            sg.run(e2, lambda: 0, boom)
+        assert seen_gc[-1] is False and gc.isenabled() and e2.graph is None
+
+        gc.disable()
+        e3 = entry()
+        e3.seen = 1
+        sg.run(e3, lambda: 0, step)
+        assert seen_gc[-1] is False and not gc.isenabled()
+    finally:
+        if was:
+            gc.enable()
+        else:
+            gc.disable()
+
+
+def test_bf16_runner_refuses_a_wqkv_without_the_rope_paired_packing():
+    """The bf16 layer runner's fused qkv + RoPE launch reads wqkv packed RoPE-paired for the model's heads; a plain
+    packing (or another head split) is refused before any device work, instead of permuting q / k rows."""
+    from thesis_amd import _lsk
+
+    w = torch.zeros(3 * 64, 64, dtype=torch.bfloat16)
+    for bad in (w, SimpleNamespace(qkv_heads=None), SimpleNamespace(qkv_heads=(2, 1, 32))):
+        lw = SimpleNamespace(wqkv=bad)
+        with pytest.raises(_lsk.LskError, match="RoPE|qkv_heads"):
+            _lsk.NativeModel(torch.bfloat16, 1, 64, 1, 1, 64, 128, 16, 1e-5, [lw], [], [], None, None)
+
+
+class _FakeSlots:
+    """SlotOps over a scripted sequence of steps: step i finishes the slots listed in finishes[i]."""
+
+    def __init__(self, n_slots, finishes):
+        self.n_slots, self.finishes, self.i = n_slots, list(finishes), 0
+        self.released, self.admitted = [], []
+
+    def admit(self, slot, index, prompt):
+        self.admitted.append((slot, index))
+        return False
+
+    def advance(self):
+        out = self.finishes[self.i] if self.i < len(self.finishes) else []
+        self.i += 1
+        return list(out)
+
+    def release(self, slot):
+        self.released.append(slot)
+
+    def busy(self):
+        return self.i < len(self.finishes)
+
+
+def test_measure_window_rules_of_the_two_engines():
+    """DecodeEngine rule (common/engine.py:224-247): a request finishing in the step where warm-up ends is not
+    evaluated, and after the stop reason the step's other completions are left unrecorded.  EESD rule
+    (solutions/engine.py:582-604): completions count by the state when they are accounted, and the step's other
+    completions are still released and counted.  A throughput of None (no measured time) skips the convergence
+    test."""
+    from thesis_amd.common.driver import MeasureWindow, run_pool
+
+    # warm-up of 2; the first step finishes 3 requests, the second 2, the third 3
+    script = [[0, 1, 2], [3, 0], [1, 2, 3]]
+    w = MeasureWindow(warmup=2, max_eval=3, converge=False, per_step=True)
+    ops = _FakeSlots(4, script)
+    stop = run_pool(ops, list(range(8)), True, w, lambda: 1.0, drain_after_stop=False)
+    # step 1: two warm-up completions, the third finishes in the warm-up step (not evaluated); step 2: 2 evaluated;
+    # step 3: the 3rd evaluated completion stops the run and the remaining two are not released
+    assert (w.warm_done, w.evaluated, stop) == (2, 3, "max_eval_samples")
+    assert ops.released == [0, 1, 2, 3, 0, 1]
+    w = MeasureWindow(warmup=2, max_eval=3, converge=False)
+    ops = _FakeSlots(4, script)
+    stop = run_pool(ops, list(range(8)), True, w, lambda: 1.0)
+    # step 1: the third completion is already evaluated; step 2 reaches 3 with its last completion
+    assert (w.warm_done, w.evaluated, stop) == (2, 3, "max_eval_samples")
+    assert ops.released == [0, 1, 2, 3, 0]
+    # no measured time: the convergence test waits (no anchor); then a constant rate converges after `window`
+    rates = iter([None, None, 5.0, 5.0, 5.0, 5.0])
+    w = MeasureWindow(warmup=0, window=3)
+    got = [w.completed(lambda: next(rates)) for _ in range(6)]
+    assert got == [None] * 5 + ["converged"]
+
+
+def test_fused_qkv_token_counts_reach_every_wide_configuration():
+    """The token counts of the fused qkv GPU test reach both wide-tier tile widths (32- and 64-row tiles, ns 2 / 4)
+    and one to three token groups per wave at the GQA shape, and both widths at the 64-dim MHA shape, by the
+    library's own configuration rule (lsk_gemm_wide_config)."""
+    from thesis_amd import _lsk
+    from test_kernels_gpu import FUSED_QKV_MS
+
+    _lsk.load()
+    for heads, need in (((32, 8, 128), {(2, 1), (2, 2), (2, 3), (4, 2), (4, 3)}), ((8, 8, 64), {(2, 2), (4, 2)})):
+        N = (heads[0] + 2 * heads[1]) * heads[2]
+        got = {(c[0], c[3]) for c in (_lsk.gemm_wide_config(_lsk.EPI_QKV_ROPE, M, N, 1024) for M in FUSED_QKV_MS)
+               if c[0]}
+        assert need <= got, (heads, sorted(got))
+        assert _lsk.gemm_wide_config(_lsk.EPI_QKV_ROPE, 64, N, 1024)[0] == 0       # <= 64 rows: decode tier

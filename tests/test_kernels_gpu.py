@@ -763,14 +763,18 @@ def test_shifted_segment_metadata_equals_a_plan_at_the_actual_positions(cuda, sp
     assert key(live(r_got)) == key(live(r_ref))
 
 
-@pytest.mark.parametrize("M", [5, 32, 48, 64, 100, 288])
+FUSED_QKV_MS = [5, 32, 48, 64, 100, 160, 288, 600, 1200, 2000]   # wide tier: every (ns, msw) it picks for qkv
+
+
+@pytest.mark.parametrize("M", FUSED_QKV_MS)
 @pytest.mark.parametrize("heads", [(32, 8, 128), (8, 8, 64)])
 def test_fused_qkv_rope_writes_what_the_unfused_path_writes(cuda, M, heads):
     """lsk_gemm_qkv_rope -- the qkv projection with RoPE and the KV append in its epilogue, the weight's q / k row
     groups RoPE-paired -- writes bitwise what the qkv GEMM without a K split (lsk_gemm_partial, ks = 1) followed by
     lsk_rope_append_partial writes: the rotated q, the K cache and the V cache (every other cache slot untouched),
-    in the decode tier (<= 64 rows) and in the wide tier (above, GQA shape); unpacking the paired storage gives the
-    weight back."""
+    in the decode tier (<= 64 rows) and in the wide tier (every tile width and groups-per-wave count it picks for
+    these shapes, up to 2000-token prefill sizes: test_fused_qkv_token_counts_reach_every_wide_configuration);
+    unpacking the paired storage gives the weight back."""
     lsk = _lsk()
     Hq, Hkv, D = heads
     g = _gen(2000 + M + D)

@@ -19,9 +19,10 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "liblsk.so"
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
+EPI_PARTIAL, EPI_ARGMAX, EPI_QKV_ROPE = 3, 4, 5   # launch kinds known to lsk_gemm_wide_config
 ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 # name -> (restype, argtypes)
 _P, _I, _L, _F, _Z = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_float, ctypes.c_size_t
@@ -48,6 +49,7 @@ _SIGS = {
     "lsk_gemm_qkv_rope": (_I, [_P, _P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P]),
     "lsk_gemm": (_I, [_I, _P, _L, _P, _L, _P, _L, _P, _L, _I, _I, _I, _I, _I, _P]),
     "lsk_gemm_plan": (_I, [_I, _I, _P, _P]),
+    "lsk_gemm_wide_config": (_I, [_I, _I, _I, _I, _I, _I, _P]),
     "lsk_gemm_partial": (_I, [_P, _L, _P, _L, _P, _I, _I, _I, _I, _P]),
     "lsk_head_workspace_bytes": (_Z, [_I, _I]),
     "lsk_head_argmax": (_I, [_I, _P, _L, _P, _L, _I, _I, _I, _P, _L, _P, _P, _P, _Z, _P]),
@@ -514,6 +516,13 @@ class NativeModel:
 
     def __init__(self, dtype, n_layers, dim, n_heads, n_kv_heads, head_dim, ffn, vocab, eps, layers, kcache, vcache,
                  cos_tab, sin_tab):
+        if dtype == torch.bfloat16:
+            # the bf16 runner's fused qkv + RoPE launch reads wqkv in the RoPE-paired packing
+            for i, lw in enumerate(layers):
+                if not (isinstance(lw.wqkv, PackedWeight) and lw.wqkv.qkv_heads == (n_heads, n_kv_heads, head_dim)):
+                    raise LskError(f"layer {i}: bf16 wqkv must be a PackedWeight packed with qkv_heads="
+                                   f"{(n_heads, n_kv_heads, head_dim)} (got "
+                                   f"{getattr(lw.wqkv, 'qkv_heads', type(lw.wqkv).__name__)})")
         lib = load()
         _dev(cos_tab, sin_tab)
         _check_kcache(dtype, kcache[0])
@@ -593,6 +602,13 @@ def gemm_plan(N: int, K: int) -> tuple:
     ns, ks = ctypes.c_int(0), ctypes.c_int(0)
     _check(load().lsk_gemm_plan(N, K, ctypes.byref(ns), ctypes.byref(ks)), "lsk_gemm_plan")
     return ns.value, ks.value
+
+
+def gemm_wide_config(epilogue: int, M: int, N: int, K: int, ks: int = 1, af: bool = True) -> tuple:
+    """(ns, blocks, groups per block, groups per wave) the wide-M tier picks; ns == 0: the tier does not apply."""
+    cfg = (ctypes.c_int * 4)()
+    _check(load().lsk_gemm_wide_config(epilogue, M, N, K, ks, int(af), cfg), "lsk_gemm_wide_config")
+    return tuple(cfg)
 
 
 def frag_rows(m: int) -> int:

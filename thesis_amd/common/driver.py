@@ -47,14 +47,21 @@ class MeasureWindow:
     max_eval    measured completions that end the run ("max_eval_samples"); None: no cap
     threshold   relative distance from the anchor throughput that counts as stable
     window      consecutive stable completions that end the run ("converged")
+    per_step    a completion counts as measured by the window's state when its step began (the DecodeEngine
+                rule, common/engine.py:224-247: requests finishing in the step where warm-up ends are not
+                evaluated); False: by the state when it is accounted (the EESD rule, solutions/engine.py:588-600)
+    A throughput callable that returns None (no measured time yet) skips the convergence test.
     """
 
     def __init__(self, warmup: int = 0, min_eval: int = 0, max_eval: Optional[int] = None, threshold: float = 0.01,
-                 window: int = 4, converge: bool = True, on_start: Optional[Callable[[], None]] = None):
+                 window: int = 4, converge: bool = True, on_start: Optional[Callable[[], None]] = None,
+                 per_step: bool = False):
         self.warmup, self.min_eval, self.max_eval = warmup, min_eval, max_eval
         self.threshold, self.window, self.converge = threshold, window, converge
         self.on_start = on_start
+        self.per_step = per_step
         self.measuring = False
+        self.step_measured = False
         self.warm_done = 0
         self.evaluated = 0
         self._anchor: Optional[float] = None
@@ -62,6 +69,11 @@ class MeasureWindow:
         self.t_start: Optional[float] = None
         if warmup <= 0:
             self._start()
+        self.step_measured = self.measuring
+
+    def begin_step(self) -> None:
+        """Snapshot the measuring state for the completions of the step about to be accounted."""
+        self.step_measured = self.measuring
 
     def _start(self) -> None:
         self.measuring = True
@@ -71,14 +83,15 @@ class MeasureWindow:
 
     def completed(self, throughput: Callable[[], float]) -> Optional[str]:
         """Account one finished request; returns the stop reason when the window is full."""
-        if not self.measuring:
-            self.warm_done += 1
-            if self.warm_done >= self.warmup:
-                self._start()
+        if not (self.step_measured if self.per_step else self.measuring):
+            if not self.measuring:
+                self.warm_done += 1
+                if self.warm_done >= self.warmup:
+                    self._start()
             return None
         self.evaluated += 1
-        if self.converge and self.evaluated >= self.min_eval:
-            thr = throughput()
+        thr = throughput() if self.converge and self.evaluated >= self.min_eval else None
+        if thr is not None:
             if self._anchor is not None and abs(thr - self._anchor) < self.threshold * max(self._anchor, 1e-9):
                 self._stable += 1
             else:
@@ -106,9 +119,13 @@ class PromptPool:
 
 
 def run_pool(ops: SlotOps, prompts: list, cyclic: bool, window: MeasureWindow,
-             throughput: Callable[[], float], max_steps: Optional[int] = None) -> str:
+             throughput: Callable[[], Optional[float]], max_steps: Optional[int] = None,
+             drain_after_stop: bool = True) -> str:
     """Drive `ops` over the pool until it is exhausted, the window stops the run or `max_steps` engine steps
-    ran; returns the stop reason.  Requests finished by their first token are released without a step."""
+    ran; returns the stop reason.  Requests finished by their first token are released without a step.
+    drain_after_stop: the step's remaining finished requests are still released and accounted after the stop
+    reason is set (the EESD rule, solutions/engine.py:582-604); False: they are left unrecorded (the
+    DecodeEngine rule, common/engine.py:226-229)."""
     pool = PromptPool(prompts, cyclic)
     finished: deque = deque()
     for slot in range(ops.n_slots):
@@ -118,12 +135,15 @@ def run_pool(ops: SlotOps, prompts: list, cyclic: bool, window: MeasureWindow,
             finished.append(slot)
     steps, stop = 0, None
     while stop is None:
+        window.begin_step()
         if not finished:
             if not ops.busy():
                 return "pool_exhausted"
             finished.extend(ops.advance())
             steps += 1
         while finished:
+            if stop is not None and not drain_after_stop:
+                break
             slot = finished.popleft()
             ops.release(slot)
             reason = window.completed(throughput)

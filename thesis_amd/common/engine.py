@@ -142,14 +142,13 @@ class _EngineSlots:
         if measured:
             self.tokens += committed
             self.ms += step_ms
-        self._measured_step = measured
         return [i for i, s in enumerate(eng.slots) if not s.idle and s.finish_reason is not None]
 
     def release(self, slot: int) -> None:
         s = self.eng.slots[slot]
         rec = {"pid": s.pid, "prompt_idx": s.prompt_idx, "prompt_len": s.prompt_len, "generated": len(s.output),
                "finish_reason": s.finish_reason, "decode_ms": s.decode_ms,
-               "measured": bool(getattr(self, "_measured_step", self.window.measuring))}
+               "measured": bool(self.window.step_measured)}
         if self.keep:
             rec["tokens"] = list(s.output)
         if self.eng.probe is not None:
@@ -157,8 +156,8 @@ class _EngineSlots:
         self.completions.append(rec)
         s.idle = True
 
-    def throughput(self) -> float:
-        return self.tokens / (self.ms / 1000) if self.ms > 0 else 0.0
+    def throughput(self) -> Optional[float]:
+        return self.tokens / (self.ms / 1000) if self.ms > 0 else None
 
 
 class DecodeEngine:
@@ -232,8 +231,8 @@ class DecodeEngine:
         max_eval = (max(cfg.max_eval_samples, min_eval) if cfg.converge else cfg.max_eval_samples) if cyclic else None
         ops = _EngineSlots(self, cfg.keep_outputs)
         ops.window = window = MeasureWindow(warm, min_eval, max_eval, cfg.converge_threshold, cfg.converge_window,
-                                            converge=cyclic and cfg.converge)
-        stop = run_pool(ops, prompts, cyclic, window, ops.throughput, cfg.max_steps)
+                                            converge=cyclic and cfg.converge, per_step=True)
+        stop = run_pool(ops, prompts, cyclic, window, ops.throughput, cfg.max_steps, drain_after_stop=False)
         wall = (_now() - window.t_start) if window.t_start is not None else 0.0
         measured = [r for r in self.records if r.measured]
         by_kind = {}
