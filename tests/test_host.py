@@ -999,3 +999,28 @@ def test_fused_qkv_token_counts_reach_every_wide_configuration():
                if c[0]}
         assert need <= got, (heads, sorted(got))
         assert _lsk.gemm_wide_config(_lsk.EPI_QKV_ROPE, 64, N, 1024)[0] == 0       # <= 64 rows: decode tier
+
+
+class _ToyTokenizer:
+    """decode(ids): one character per id; ids in `nl` decode to a newline."""
+
+    def __init__(self, nl):
+        self.nl = set(nl)
+
+    def decode(self, ids, skip_special_tokens=False):
+        return "".join("\n" if i in self.nl else chr(65 + i % 26) for i in ids)
+
+
+def test_stop_checker_cuts_after_the_token_completing_the_first_stop():
+    """The cut keeps the token that completes the first stop string (tests/test_engine.py:98-105 of the reference):
+    a stop spanning two tokens, one completed inside a multi-token commit, and a stop made of the commit alone."""
+    from thesis_amd.common.data import StopChecker
+
+    sc = StopChecker(_ToyTokenizer({9}), ("\nB",))              # "\n" (id 9) followed by id 1 ("B")
+    out = [3, 4, 9, 5, 9, 1, 7, 9, 1]
+    assert sc(out[:4], 4) is None
+    assert sc(out[:6], 2) == 6
+    assert sc(out[:5], 1) is None
+    assert sc(out[:7], 7) == 6
+    assert StopChecker(_ToyTokenizer({9}), ("\n",))([1, 2, 9, 9], 3) == 3
+    assert not StopChecker(_ToyTokenizer(set()), ())
