@@ -12,7 +12,8 @@ through layers [0, 8) + draft head, plus, when the scheduler verifies, a packed 
   (p = 0.3).  Prompts are prefilled before the timed region; weights, KV cache and metadata are in HBM.
 value = committed (generated) tokens over the K timed steps / wall time of those steps.
 
-Other workloads (`--workload`, each prints its own JSON line; the default line above is unchanged):
+Other workloads (`--workload`, each prints its own JSON line; the default run also measures both, bounded -- 60
+timed steps, 24 measured requests, 8 s CPU samples -- under the "workloads" key of its line):
   1b-b64      Llama3.2-1B shape, bf16, B = 64, prompts of 512, 256 new tokens, exit layer 6, draft length 6,
               forced geometric acceptance (p = 0.3); shallow and deep rows in one packed forward per step.
   7b-poisson  Llama2-7B shape (MHA, vocab 32000), bf16, B = 128 slots, Poisson arrivals at 8 requests/s,
@@ -168,9 +169,12 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     c = model.cfg
     seq = []
     for st in trace[:n_steps]:
-        seq += [(len(st["sh"]), i) for i in range(k)]
+        if st["sh"]:
+            seq += [(sum(b[2] for b in st["sh"]), i) for i in range(k)]
         if st["dp"]:
             seq += [(sum(b[2] for b in st["dp"]), i) for i in range(k, c.n_layers)]
+        for b in st.get("pf", ()):                  # a separate prefill: each chunk through every layer
+            seq += [(b[2], i) for i in range(c.n_layers)]
     if not seq:
         return {}
     es = model.dtype.itemsize
@@ -199,6 +203,8 @@ def replay_gemms(model, trace: list, k: int, n_steps: int) -> dict:
     head_seq = []
     for st in trace[:n_steps]:
         nd, nv = int(st.get("n_draft", len(st["sh"]))), sum(b[2] for b in st["dp"])
+        if st.get("pf"):
+            nv = 1                                  # the prompt's last token
         if nd + nv:
             head_seq.append((nd + nv, None))
     V = c.vocab_size
@@ -280,8 +286,8 @@ def tokens_roofline(cfg, trace: list, k: int) -> dict:
     sum over its launches of t_roof = max(algorithmic bytes / 8 TB/s, flops / 2.5166 PFLOP/s) -- per layer
     the four projection GEMMs (weights + activations + outputs; RoPE and the KV append ride the qkv GEMM's
     output), attention (the unpadded KV of its blocks read once + Q and O) and the two RMSNorms; per step the
-    LM-head launch (drafts and verify tokens share one, as the engine does) -- then committed tokens / total
-    t_roof."""
+    LM-head launch (drafts and verify tokens share one, as the engine does); a separate prefill's chunks through
+    every layer -- then committed tokens / total t_roof."""
     dim, ffn, V = cfg.dim, cfg.intermediate_size, cfg.vocab_size
     qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
     bw, fl = HBM_PEAK_GBS * 1e9, BF16_PEAK_TFLOPS * 1e12
@@ -303,7 +309,11 @@ def tokens_roofline(cfg, trace: list, k: int) -> dict:
         total += k * layer(st["sh"])
         if st["dp"]:
             total += (cfg.n_layers - k) * layer(st["dp"])
+        for b in st.get("pf", ()):                   # a separate prefill chunk runs every layer
+            total += cfg.n_layers * layer([b])
         nd, nv = int(st.get("n_draft", 0)), sum(b[2] for b in st["dp"])
+        if st.get("pf"):
+            nv = 1
         if nd + nv:
             total += gemm(nd + nv, V, dim)
         tokens += st["committed"]
@@ -526,10 +536,12 @@ def host_cores() -> tuple:
     return (min(affinity, quota) if quota else affinity), affinity, quota
 
 
-def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch: int = 0, cache_len: int = 0):
+def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch: int = 0, cache_len: int = 0,
+                     row_mod: int = 0):
     """The CPU oracle replays the GPU run's timed steps (same segment shapes, bf16) on the host cores, in
     order and again from the first when they run out, until ~args.cpu_seconds have elapsed; tokens/s = tokens
-    the replayed steps committed / CPU time."""
+    the replayed steps committed / CPU time.  row_mod > 0: cache rows are taken modulo row_mod (a smaller host
+    cache for many-slot workloads; the blocks' shapes, hence the work, are unchanged)."""
     from oracle.model import OBlock, OracleConfig, OracleLlama, build_packed, packed_layers
     from thesis_amd.common.model import PRESETS
 
@@ -541,7 +553,10 @@ def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch
     torch.set_num_threads(threads)
     t0 = time.time()
     m = OracleLlama.synthetic(ocfg, dtype=torch.bfloat16, seed=args.seed, max_seq=2048)
-    m.allocate_cache(batch or args.batch, cache_len or 1024 + args.max_new + 8 + 40)
+    m.allocate_cache(row_mod or batch or args.batch, cache_len or 1024 + args.max_new + 8 + 40)
+    if row_mod:
+        trace = [{**st, **{key: [(r % row_mod, p0, T) for (r, p0, T) in st.get(key, ())] for key in ("sh", "dp", "pf")}}
+                 for st in trace]
     log(f"[bench] CPU oracle model ready in {time.time() - t0:.1f}s ({threads} threads)")
     g = torch.Generator().manual_seed(0)
     spent, tokens, steps, n_deep = 0.0, 0, 0, 0
@@ -549,9 +564,10 @@ def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch
     with torch.inference_mode():
         for st in order:
             ts = time.perf_counter()
-            pb = build_packed(m, [OBlock(*b) for b in st["sh"]])
-            x = m.embed(torch.randint(0, ocfg.vocab_size, (pb.n_tokens,), generator=g))
-            h = packed_layers(m, x, pb, 0, k)
+            if st["sh"]:
+                pb = build_packed(m, [OBlock(*b) for b in st["sh"]])
+                x = m.embed(torch.randint(0, ocfg.vocab_size, (pb.n_tokens,), generator=g))
+                h = packed_layers(m, x, pb, 0, k)
             if st["n_draft"]:
                 m.head(h[:st["n_draft"]]).argmax(-1)
             if st["dp"]:
@@ -560,6 +576,11 @@ def run_cpu_baseline(args, trace: list, k: int, preset: str = "llama3-8b", batch
                 hd = packed_layers(m, xd, pbd, k, ocfg.n_layers)
                 m.head(hd).argmax(-1)
                 n_deep += 1
+            for b in st.get("pf", ()):
+                pbp = build_packed(m, [OBlock(*b)])
+                hp = packed_layers(m, m.embed(torch.randint(0, ocfg.vocab_size, (b[2],), generator=g)), pbp, 0,
+                                   ocfg.n_layers)
+                m.head(hp[-1:]).argmax(-1)
             spent += time.perf_counter() - ts
             tokens += st["committed"]
             steps += 1
@@ -585,9 +606,44 @@ def emit(line: dict, out) -> None:
         Path(out).write_text(txt + "\n")
 
 
-def run_1b_b64(args) -> None:
+def gemm_rooflines(replay: dict, traffic_path=None) -> tuple:
+    """(roofline of the w13 GEMM class, gemm_roofline over every projection class) from replay_gemms' figures."""
+    if not replay or "gemm_w13" not in replay:
+        return None, None
+    w13 = replay["gemm_w13"]
+    b, us = w13["bytes_per_launch"], w13["avg_us"]
+    ach = b / (us * 1e-6) / 1e9
+    traffic = None
+    if traffic_path is not None:
+        from thesis_amd.prof_summary import read_traffic
+
+        traffic = read_traffic(traffic_path, "gemm_w13")
+    roofline = {"kernel": "gemm_w13 (gemm_bf16_kernel, silu-mul epilogue)", "bound": "hbm",
+                "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_launch_us": us,
+                "bytes_per_launch": b, "launches_timed": w13["launches"], "token_counts": replay["token_counts"]}
+    if traffic is not None:
+        roofline["traffic_source"] = str(Path(traffic_path).relative_to(ROOT))
+    names = [n for n in ("gemm_qkv", "gemm_o", "gemm_w13", "gemm_w2", "gemm_lm_head") if n in replay]
+
+    def agg(ns):
+        t_roof = sum(replay[n]["t_roof_us"] * replay[n]["launches"] for n in ns)
+        t_meas = sum(replay[n]["avg_us"] * replay[n]["launches"] for n in ns)
+        return round(t_roof / t_meas, 4)
+
+    gemm_roofline = {
+        "frac": agg(names), "frac_layer_gemms": agg([n for n in names if n != "gemm_lm_head"]),
+        "definition": "over the QKV / O / MLP / LM-head launches of the replayed steps: sum of t_roof over sum "
+                      "of measured launch time, t_roof = max(bytes / 8 TB/s, flops / 2.5166 PFLOP/s) per launch",
+        "classes": {n: {k: replay[n][k] for k in ("launches", "avg_us", "t_roof_us", "frac", "bytes_per_launch",
+                                                   "flops_per_launch")} for n in names}}
+    return roofline, gemm_roofline
+
+
+def run_1b_b64(args, emit_line: bool = True) -> dict:
     """Llama3.2-1B shape, bf16, B = 64 prompts of 512 tokens, exit layer 6, fixed draft length 6, forced geometric
-    acceptance (p = 0.3): `steps` engine steps after `warmup`, timed like the default workload."""
+    acceptance (p = 0.3): `steps` engine steps after `warmup`, timed like the default workload; the projection GEMMs
+    of the timed steps replayed for the roofline figures; the CPU oracle on a bounded sample."""
     from thesis_amd.common.data import synthetic_prompts
     from thesis_amd.common.model import PRESETS, LayerSkipLlama
     from thesis_amd.solutions.cost_model import default_cost_model
@@ -595,6 +651,7 @@ def run_1b_b64(args) -> None:
 
     torch.cuda.set_device(0)
     cfg, B, plen, k = PRESETS["llama3.2-1b"], 64, 512, 6
+    t0 = time.time()
     model = LayerSkipLlama.random(cfg, seed=args.seed, dtype=torch.bfloat16,
                                   max_seq=(plen + args.max_new + 8 + 63) // 64 * 64)
     prompts = synthetic_prompts(B, cfg.vocab_size, plen, plen, seed=args.seed + 1)
@@ -606,35 +663,62 @@ def run_1b_b64(args) -> None:
     eng.measuring = True
     for _ in range(args.warmup):
         engine_step(eng)
+    if args.copy_calib_mib > 0:
+        calibration_copy(args.copy_calib_mib)
     eng.trace = []
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     committed = sum(engine_step(eng) for _ in range(args.steps))
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t1
+    log(f"[bench] 1b-b64: {args.steps} steps in {elapsed * 1e3:.1f} ms, {committed} tokens "
+        f"({time.time() - t0:.1f}s with model build and prefill)")
+    prof = {}
+    if args.profile_steps > 0:                  # per-class kernel time with HIP events, after the timed steps
+        from thesis_amd import _lsk
+
+        saved = eng.trace
+        eng.trace = None
+        _lsk.Profiler.enable(True)
+        for _ in range(args.profile_steps):
+            if not (eng.state == 2).any():
+                break
+            engine_step(eng)
+        prof = _lsk.Profiler.collect()
+        _lsk.Profiler.enable(False)
+        eng.trace = saved
     troof = tokens_roofline(cfg, eng.trace, k)
     if troof["tokens_per_s"]:
+        troof["measured_tokens_per_s"] = round(committed / elapsed, 2)
         troof["frac"] = round(committed / elapsed / troof["tokens_per_s"], 4)
     trace = eng.trace
+    eng.trace = None
+    replay = replay_gemms(model, trace, k, args.replay_steps) if args.replay_steps > 0 else {}
+    roofline, gemm_roofline = gemm_rooflines(replay)
     del model, eng
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, k, "llama3.2-1b", B,
                                                              plen + args.max_new + 8 + 40)
-    emit({"metric": "generated tokens/s at 1 GPU (Llama3.2-1B shape, B=64)", "value": round(committed / elapsed, 2),
-          "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-          "ms_per_step": round(1e3 * elapsed / args.steps, 3), "higher_is_better": True, "dtype": "bf16",
-          "data": "synthetic",
-          "config": {"workload": "llama3.2-1b-shape packed self-speculative decode", "B": B, "prompt_len": plen,
-                     "max_new": args.max_new, "exit_layer": k, "draft_len": 6, "scheduler": "fixed",
-                     "acceptance": "forced geometric p=0.3", "weights": "random init bf16"},
-          "tokens_roofline": troof, "cpu_baseline": cpu, "committed_tokens": committed,
-          "deep_steps": sum(1 for st in trace if st["dp"])}, args.out)
+    line = {"metric": "generated tokens/s at 1 GPU (Llama3.2-1B shape, B=64)", "value": round(committed / elapsed, 2),
+            "unit": "tokens/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(1e3 * elapsed / args.steps, 3), "higher_is_better": True, "dtype": "bf16",
+            "data": "synthetic",
+            "config": {"workload": "llama3.2-1b-shape packed self-speculative decode", "B": B, "prompt_len": plen,
+                       "max_new": args.max_new, "exit_layer": k, "draft_len": 6, "scheduler": "fixed",
+                       "acceptance": "forced geometric p=0.3", "weights": "random init bf16"},
+            "roofline": roofline, "gemm_roofline": gemm_roofline, "tokens_roofline": troof, "cpu_baseline": cpu,
+            "committed_tokens": committed, "deep_steps": sum(1 for st in trace if st["dp"]),
+            "kernels": summarize_kernels(prof)}
+    if emit_line:
+        emit(line, args.out)
+    return line
 
 
-def run_7b_poisson(args) -> None:
+def run_7b_poisson(args, emit_line: bool = True) -> dict:
     """Llama2-7B shape, bf16, B = 128 slots fed by Poisson arrivals at 8 requests/s; prompts uniform in [256, 1024]
     ride the decode steps as 256-token prefill chunks (M3); exit layer 8, draft length 4, greedy acceptance.  The
-    first `poisson_warm` completions are warm-up; the run ends after `poisson_requests` more."""
+    first `poisson_warm` completions are warm-up; the run ends after `poisson_requests` more.  value = wall-clock
+    throughput; tokens_roofline.frac = the measured steps' roofline time over their GPU time."""
     from thesis_amd.common.data import synthetic_prompts
     from thesis_amd.common.model import PRESETS, LayerSkipLlama
     from thesis_amd.solutions.cost_model import default_cost_model
@@ -642,6 +726,7 @@ def run_7b_poisson(args) -> None:
 
     torch.cuda.set_device(0)
     cfg, B, k, rate = PRESETS["llama2-7b"], 128, 8, 8.0
+    t0 = time.time()
     model = LayerSkipLlama.random(cfg, seed=args.seed, dtype=torch.bfloat16,
                                   max_seq=(1024 + args.max_new + 8 + 63) // 64 * 64)
     n_req, warm = args.poisson_requests, args.poisson_warm
@@ -660,7 +745,10 @@ def run_7b_poisson(args) -> None:
     eng = EESDEngine(model, B, 1024, args.max_new, (), EngineConfig(sched="fixed", k=k, gamma=4, d_max=4,
                                                                      prefill="m3", m3_chunk_cap=256,
                                                                      prefill_chunk=256), cm)
+    eng.trace = []
     res = eng.run_poisson(prompts, rate, n_req, warm_requests=warm, seed=args.seed)
+    trace = [st for st in eng.trace if st.get("m")]
+    eng.trace = None
     m = res["metrics"]
     keys = ("wall_throughput_tok_s", "throughput_tok_s", "e2e_throughput_tok_s", "wall_s", "measured_tokens",
             "ttft_ms_mean", "ttft_ms_p99", "tpot_ms_mean", "tpot_ms_p99", "host_overhead_share",
@@ -671,15 +759,55 @@ def run_7b_poisson(args) -> None:
         if isinstance(v, dict):
             flat.update(v)
     flat.update({kk: v for kk, v in m.items() if not isinstance(v, dict)})
-    emit({"metric": "generated tokens/s at 1 GPU (Llama2-7B shape, B=128, Poisson 8 req/s)",
-          "value": round(flat.get("wall_throughput_tok_s") or 0.0, 2), "unit": "tokens/s", "n_gpus": 1,
-          "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
-          "config": {"workload": "llama2-7b-shape open-loop EESD with M3 prefill sharing", "B": B,
-                     "arrivals": f"Poisson {rate} req/s", "prompt_len": [256, 1024], "prefill_chunk": 256,
-                     "max_new": args.max_new, "exit_layer": k, "draft_len": 4, "scheduler": "fixed",
-                     "acceptance": "greedy", "cost_model": src, "requests": n_req, "warm_requests": warm,
-                     "weights": "random init bf16"},
-          "metrics": {kk: flat.get(kk) for kk in keys}}, args.out)
+    log(f"[bench] 7b-poisson: {flat.get('wall_throughput_tok_s')} tokens/s wall over {len(trace)} measured steps "
+        f"({time.time() - t0:.1f}s with model build)")
+    troof = tokens_roofline(cfg, trace, k)
+    gpu_ms = (flat.get("decode_ms") or 0.0) + (flat.get("prefill_ms") or 0.0)
+    if troof["t_roof_ms"] and gpu_ms:
+        troof["gpu_ms"] = round(gpu_ms, 3)
+        troof["frac"] = round(troof["t_roof_ms"] / gpu_ms, 4)
+        troof["definition"] += "; frac = roofline time of the measured steps and prefills / their GPU time"
+    replay = replay_gemms(model, trace, k, args.replay_steps) if args.replay_steps > 0 else {}
+    roofline, gemm_roofline = gemm_rooflines(replay)
+    del model, eng
+    torch.cuda.empty_cache()
+    cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, k, "llama2-7b", B,
+                                                             1024 + args.max_new + 8 + 40, row_mod=8)
+    line = {"metric": "generated tokens/s at 1 GPU (Llama2-7B shape, B=128, Poisson 8 req/s)",
+            "value": round(flat.get("wall_throughput_tok_s") or 0.0, 2), "unit": "tokens/s", "n_gpus": 1,
+            "higher_is_better": True, "dtype": "bf16", "data": "synthetic",
+            "config": {"workload": "llama2-7b-shape open-loop EESD with M3 prefill sharing", "B": B,
+                       "arrivals": f"Poisson {rate} req/s", "prompt_len": [256, 1024], "prefill_chunk": 256,
+                       "max_new": args.max_new, "exit_layer": k, "draft_len": 4, "scheduler": "fixed",
+                       "acceptance": "greedy", "cost_model": src, "requests": n_req, "warm_requests": warm,
+                       "weights": "random init bf16"},
+            "roofline": roofline, "gemm_roofline": gemm_roofline, "tokens_roofline": troof, "cpu_baseline": cpu,
+            "metrics": {kk: flat.get(kk) for kk in keys}}
+    if emit_line:
+        emit(line, args.out)
+    return line
+
+
+def run_extra_workloads(args) -> dict:
+    """The 1B B=64 and 7B open-loop configurations, bounded for the default run (its own step / request counts and a
+    shorter CPU sample), reported beside the headline."""
+    out = {}
+    sub = argparse.Namespace(**vars(args))
+    sub.steps, sub.warmup, sub.cpu_seconds = args.extra_steps, args.extra_warmup, args.extra_cpu_seconds
+    sub.poisson_requests, sub.out, sub.copy_calib_mib, sub.profile_steps = args.extra_requests, None, 0, 20
+    for name, fn in (("llama3.2-1b-b64", run_1b_b64), ("llama2-7b-poisson", run_7b_poisson)):
+        t0 = time.time()
+        out[name] = fn(sub, emit_line=False)
+        out[name]["seconds"] = round(time.time() - t0, 1)
+        gc_collect()
+    return out
+
+
+def gc_collect() -> None:
+    import gc
+
+    gc.collect()
+    torch.cuda.empty_cache()
 
 
 def main():
@@ -711,6 +839,12 @@ def main():
     ap.add_argument("--poisson-warm", type=int, default=8, help="7b-poisson: warm-up completions")
     ap.add_argument("--m3-knee", type=int, default=600,
                     help="7b-poisson: knee (tokens) of the cost model the M3 rule sees; 0 keeps the calibrated one")
+    ap.add_argument("--no-extra-workloads", action="store_true",
+                    help="default workload: skip the bounded 1b-b64 and 7b-poisson runs reported beside it")
+    ap.add_argument("--extra-steps", type=int, default=60, help="1b-b64 timed steps inside the default run")
+    ap.add_argument("--extra-warmup", type=int, default=10, help="1b-b64 warm-up steps inside the default run")
+    ap.add_argument("--extra-cpu-seconds", type=float, default=8.0, help="CPU sample of each extra workload")
+    ap.add_argument("--extra-requests", type=int, default=24, help="7b-poisson measured requests in the default run")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only: this build has no multi-GPU path (requested --gpus {args.gpus}); "
@@ -742,37 +876,10 @@ def main():
     attn = None if args.no_attn else run_attention_bench(args)
 
     # roofline of the largest kernel class of the decode step: the w13 GEMM (weight stream, HBM-bound at
-    # these token counts); its average launch duration comes from the back-to-back replay above
-    roofline = gemm_roofline = None
-    if replay:
-        from thesis_amd.prof_summary import read_traffic
-
-        w13 = replay["gemm_w13"]
-        b, us = w13["bytes_per_launch"], w13["avg_us"]
-        ach = b / (us * 1e-6) / 1e9
-        traffic = read_traffic(TRAFFIC_SUMMARY, "gemm_w13")
-        roofline = {"kernel": "gemm_w13 (gemm_bf16_kernel, silu-mul epilogue)", "bound": "hbm",
-                    "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_launch_us": us,
-                    "bytes_per_launch": b, "launches_timed": w13["launches"],
-                    "token_counts": replay["token_counts"]}
-        if traffic is not None:
-            roofline["traffic_source"] = str(TRAFFIC_SUMMARY.relative_to(ROOT))
-        # all four projection GEMM classes of the step: roofline time over measured time (the MFMA-utilisation
-        # figure where a GEMM is compute-bound; these token counts make every one of them HBM-bound)
-        names = [n for n in ("gemm_qkv", "gemm_o", "gemm_w13", "gemm_w2", "gemm_lm_head") if n in replay]
-
-        def agg(ns):
-            t_roof = sum(replay[n]["t_roof_us"] * replay[n]["launches"] for n in ns)
-            t_meas = sum(replay[n]["avg_us"] * replay[n]["launches"] for n in ns)
-            return round(t_roof / t_meas, 4)
-
-        gemm_roofline = {
-            "frac": agg(names), "frac_layer_gemms": agg([n for n in names if n != "gemm_lm_head"]),
-            "definition": "over the QKV / O / MLP / LM-head launches of the replayed steps: sum of t_roof over sum "
-                          "of measured launch time, t_roof = max(bytes / 8 TB/s, flops / 2.5166 PFLOP/s) per launch",
-            "classes": {n: {k: replay[n][k] for k in ("launches", "avg_us", "t_roof_us", "frac", "bytes_per_launch",
-                                                       "flops_per_launch")} for n in names}}
+    # these token counts); its average launch duration comes from the back-to-back replay above.  gemm_roofline:
+    # all four projection GEMM classes and the LM head, roofline time over measured time (the MFMA-utilisation
+    # figure where a GEMM is compute-bound; these token counts make every one of them HBM-bound)
+    roofline, gemm_roofline = gemm_rooflines(replay, TRAFFIC_SUMMARY)
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, 8)
     from thesis_amd import _lsk as _l
 
@@ -792,6 +899,7 @@ def main():
                    "parallelism": "single GPU"},
         "roofline": roofline, "gemm_roofline": gemm_roofline, "tokens_roofline": troof, "cpu_baseline": cpu,
         "verify_attn": attn,
+        "workloads": None if args.no_extra_workloads else run_extra_workloads(args),
         "kernels": kernels,
         "steps_detail": {"committed_tokens": committed, "deep_steps": sum(1 for s in trace if s["dp"]),
                          "mean_shallow_rows": float(np.mean([len(s["sh"]) for s in trace])) if trace else None,

@@ -665,7 +665,18 @@ __global__ __launch_bounds__(256) void shift_positions_kernel(int32_t* __restric
                                                               const int64_t* __restrict__ acc,
                                                               const int32_t* __restrict__ vslots,
                                                               const int32_t* __restrict__ vdrafts, int nv) {
+  // per-row shifts in LDS (rows below SHIFT_TAB; a row beyond it, which no cache this large holds, scans the list)
+  constexpr int SHIFT_TAB = 4096;
+  __shared__ int tab[SHIFT_TAB];
+  for (int i = threadIdx.x; i < SHIFT_TAB; i += blockDim.x) tab[i] = 0;
+  __syncthreads();
+  for (int j = threadIdx.x; j < nv; j += blockDim.x) {
+    const int row = vslots[j];
+    if (row >= 0 && row < SHIFT_TAB) tab[row] = (int)acc[j] - vdrafts[j];
+  }
+  __syncthreads();
   auto delta_of = [&](int row) {
+    if (row >= 0 && row < SHIFT_TAB) return tab[row];
     for (int j = 0; j < nv; ++j)
       if (vslots[j] == row) return (int)acc[j] - vdrafts[j];
     return 0;

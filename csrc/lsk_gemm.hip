@@ -775,10 +775,15 @@ static int ms_for(int M) { return M <= 16 ? 1 : (M <= 32 ? 2 : (M <= 48 ? 3 : 4)
 // activations (cheaper activation loads per workgroup) up to 48 tokens (qkv -0.35 us, o -0.24 us per launch).  The reduction
 // order of an output does not depend on NS or MS (only on K and the plan's KS), so the tile follows M
 // without breaking batch invariance.
+// Without a K split (silu-mul, plain and residual epilogues), a shape whose 64-row tiles would leave more than a
+// third of the CUs idle (fewer than 160 workgroups: the 1B MLP's 128) runs 32-row tiles instead.  Measured on
+// MI355X (back-to-back launches, cold weights): 1B w13 -12 % at 8 tokens to -26 % at 64; the 7B MLP (172
+// workgroups) ran 9-13 % slower with 32-row tiles, so it keeps 64.
 static int tile_ns(int n, int M, int epi, int kslice = 0, int ks = 1, int short_max = 32) {
   int ns = 4;
   while (ns > 1 && n % (16 * ns) != 0) ns >>= 1;
   if (ns == 4 && epi == EPI_PARTIAL && M <= short_max && kslice <= 1024 && (long)(n / 64) * ks < 512) ns = 2;
+  if (ns == 4 && epi != EPI_PARTIAL && epi != EPI_ARGMAX && n / 64 < 160 && n % 32 == 0) ns = 2;
   return ns;
 }
 
@@ -1243,7 +1248,12 @@ extern "C" int lsk_gemm_qkv_rope(const void* A, const void* W, int M, int n_head
   const int mw = launch_wide(EPI_QKV, s, (const uint16_t*)A, 0, (const uint16_t*)W, nullptr, 0, nullptr, 0, nullptr,
                              nullptr, nullptr, M, N, K, 0, 1, true, 0, qa);
   if (mw < M) {
-    const int mr = M - mw, ms = ms_for(mr);
+    // one K slice, 32-row tiles: a weight with fewer than 192 tiles (the 1B shape's 96) splits the tokens over
+    // two or more token tiles, so every CU streams (the weights are re-read from the XCD's L2): 1B qkv at 64
+    // tokens 11.9 -> 10.0 us on MI355X
+    const int mr = M - mw;
+    int ms = ms_for(mr);
+    while (ms > 1 && (long)(N / 32) * ((mr + 16 * ms - 1) / (16 * ms)) < 192) --ms;
     dispatch_bf16(2, ms, EPI_QKV, N / 32, (mr + 16 * ms - 1) / (16 * ms), 1, s, A, 0, W, K, nullptr, 0, nullptr, 0,
                   nullptr, nullptr, nullptr, M, N, K, 0, K, true, mw, 0, qa);
   }

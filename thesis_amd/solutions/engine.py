@@ -203,7 +203,10 @@ class EESDEngine:
         self.steps_since_deep = 0
         self.kv_bytes_per_pos = 2 * model.cfg.n_kv_heads * model.cfg.head_dim * model.dtype.itemsize
         self._keys = 0
-        self.trace: Optional[list] = None     # set to [] to log every step's segment shapes
+        # set to [] to log every step's segment shapes: {"sh": shallow blocks, "n_draft", "dp": deep blocks (verify
+        # blocks and M3 chunks), "committed", "m": measured, "pf": a separate prefill's chunks (entries of their own)}
+        self.trace: Optional[list] = None
+        self._dp_blocks: list = []
 
     def _allocate(self, max_prompt: int) -> None:
         """Cache rows for prompt + output + drafts + slack; device seq_buf / exit_h; host slot arrays."""
@@ -310,6 +313,10 @@ class EESDEngine:
         _lsk.copy_rows(sb.view(-1, 1), upload([slot * self.Dm1], self.dev), y0.view(-1, 1), None, 1)
         span.close()
         self._log("prefill", span, n_chunk=n)
+        if self.trace is not None:
+            pc = self.cfg.prefill_chunk
+            self.trace.append({"sh": [], "n_draft": 0, "dp": [], "committed": 1, "m": bool(self.measuring),
+                               "pf": [(slot, s0, min(pc, n - s0)) for s0 in range(0, n, pc)]})
         self.stats["separate_prefills"] += 1
         if self.measuring:
             self.stats["prefill_tokens"] += n
@@ -453,7 +460,7 @@ class EESDEngine:
             self.d[Dr] += 1
             if self.trace is not None:
                 self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
-                                   "n_draft": nd, "dp": [], "committed": 0})
+                                   "n_draft": nd, "dp": [], "committed": 0, "m": bool(self.measuring)})
             self.steps_since_deep += 1
             self._tally(0, deep=False, plan_ms=plan_ms)
             return 0, []
@@ -633,11 +640,9 @@ class EESDEngine:
         for (i, _, c) in chunks:
             self.req[i].piggybacked += c
         if self.trace is not None:
-            vs = np.flatnonzero(V)
             self.trace.append({"sh": list(zip(pb.blk_rows.tolist(), pb.blk_pos0.tolist(), pb.blk_T.tolist())),
-                               "n_draft": nd,
-                               "dp": list(zip(vs.tolist(), self.pos[vs].tolist(), (d[vs] + 1).tolist())),
-                               "committed": 0})
+                               "n_draft": nd, "dp": self._dp_blocks if deep else [], "committed": 0,
+                               "m": bool(self.measuring)})
         if not deep:
             self.steps_since_deep += 1
             self._tally(0, deep=False, plan_ms=plan_ms)
@@ -738,6 +743,8 @@ class EESDEngine:
         T = np.concatenate([d[vs] + 1, np.array(cT, dtype=np.int64)])
         pb = build_packed_arrays(m, rows, pos0, T, self.cfg.bucketing, upload_meta=False)
         self._count_kv(pb, L - k)
+        if self.trace is not None:                                        # the deep segment's blocks, chunks included
+            self._dp_blocks = list(zip(rows.tolist(), pos0.tolist(), T.tolist()))
         n = pb.n_tokens
         is_v = pb.order < nvb
         vb = np.flatnonzero(is_v)                                         # verify blocks in packed order
