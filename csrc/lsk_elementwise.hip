@@ -378,19 +378,32 @@ extern "C" int lsk_rope_append_partial(int dtype, const float* partials, int ks,
 // Plain KV append (no RoPE): kcache[row_t, h, pos_t] = k[t, h]; V cache (row_t, h, pos_t) = v[t, h]
 // (V in transposed 32-position blocks, [B, Hkv, S/32, D, 32]).
 // Used for inputs whose RoPE is already applied (solutions/packed.py:180-181 on its own).
+#define KV_APPEND_TOKENS 16
 template <typename T>
 __global__ __launch_bounds__(256) void kv_append_kernel(const T* __restrict__ k, const T* __restrict__ v,
                                                         T* __restrict__ kc, T* __restrict__ vc,
                                                         const int32_t* __restrict__ rows,
-                                                        const int32_t* __restrict__ pos, int Hkv, int D,
+                                                        const int32_t* __restrict__ pos, int N, int Hkv, int D,
                                                         int max_batch, int max_seq) {
-  const int t = blockIdx.x;
-  const int row = rows[t], p = pos[t];
-  if (row < 0 || row >= max_batch || p < 0 || p >= max_seq) return;
-  for (int e = threadIdx.x; e < Hkv * D; e += blockDim.x) {
-    const int hk = e / D, d = e - hk * D;
-    kc[((long)row * Hkv + hk) * (long)max_seq * D + k_cache_offset<T>(p, d, D)] = k[(long)t * Hkv * D + e];
-    vc[((long)row * Hkv + hk) * (long)D * max_seq + (long)(p >> 5) * 32 * D + d * 32 + (p & 31)] = v[(long)t * Hkv * D + e];
+  // A workgroup per (KV_APPEND_TOKENS tokens, KV head).  K: consecutive threads take consecutive d of one token
+  // (16-byte runs of the fragment-major block).  V^T: consecutive threads take consecutive tokens of one d row, so
+  // the positions of a verify block land side by side in the transposed 32-position block instead of one 2-byte
+  // write per 64-byte row (the input rows are re-read from L2, where the previous kernel left them).
+  const int t0 = blockIdx.x * KV_APPEND_TOKENS, hk = blockIdx.y;
+  const int nt = min(KV_APPEND_TOKENS, N - t0);
+  const int HD = Hkv * D;
+  for (int e = threadIdx.x; e < nt * D; e += blockDim.x) {
+    const int j = e / D, d = e - j * D;
+    const int t = t0 + j, row = rows[t], p = pos[t];
+    if (row < 0 || row >= max_batch || p < 0 || p >= max_seq) continue;
+    kc[((long)row * Hkv + hk) * (long)max_seq * D + k_cache_offset<T>(p, d, D)] = k[(long)t * HD + hk * D + d];
+  }
+  for (int e = threadIdx.x; e < nt * D; e += blockDim.x) {
+    const int d = e / nt, j = e - d * nt;
+    const int t = t0 + j, row = rows[t], p = pos[t];
+    if (row < 0 || row >= max_batch || p < 0 || p >= max_seq) continue;
+    vc[((long)row * Hkv + hk) * (long)D * max_seq + (long)(p >> 5) * 32 * D + d * 32 + (p & 31)] =
+        v[(long)t * HD + hk * D + d];
   }
 }
 
@@ -403,14 +416,15 @@ extern "C" int lsk_kv_append(int dtype, const void* k, const void* v, void* kcac
               LSK_ESHAPE, "lsk_kv_append: bad shape (bf16 needs head_dim %% 32 == 0; max_seq %% 32 == 0)");
   if (n_tokens == 0) return 0;
   hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((n_tokens + KV_APPEND_TOKENS - 1) / KV_APPEND_TOKENS, n_kv_heads);
   if (dtype == LSK_DTYPE_BF16)
-    kv_append_kernel<uint16_t><<<n_tokens, 256, 0, s>>>((const uint16_t*)k, (const uint16_t*)v, (uint16_t*)kcache,
-                                                        (uint16_t*)vcache, rows, pos, n_kv_heads, head_dim,
-                                                        max_batch, max_seq);
+    kv_append_kernel<uint16_t><<<grid, 256, 0, s>>>((const uint16_t*)k, (const uint16_t*)v, (uint16_t*)kcache,
+                                                    (uint16_t*)vcache, rows, pos, n_tokens, n_kv_heads, head_dim,
+                                                    max_batch, max_seq);
   else if (dtype == LSK_DTYPE_F32)
-    kv_append_kernel<float><<<n_tokens, 256, 0, s>>>((const float*)k, (const float*)v, (float*)kcache,
-                                                     (float*)vcache, rows, pos, n_kv_heads, head_dim, max_batch,
-                                                     max_seq);
+    kv_append_kernel<float><<<grid, 256, 0, s>>>((const float*)k, (const float*)v, (float*)kcache,
+                                                 (float*)vcache, rows, pos, n_tokens, n_kv_heads, head_dim, max_batch,
+                                                 max_seq);
   else
     LSK_REQUIRE(false, LSK_EUNSUPPORTED, "lsk_kv_append: dtype %d", dtype);
   return lsk_check_launch("lsk_kv_append");

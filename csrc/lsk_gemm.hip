@@ -283,9 +283,24 @@ __global__ __launch_bounds__(256, (gemm_occupancy<NS, MS, EPI, CK>())) void gemm
     }
     return;
   } else if constexpr (EPI == EPI_QKV) {
-    // a thread per (row-group pair, token, row of the group): one RoPE pair (q / k) or two v values
+    // a thread per (row-group pair, token, row of the group): one RoPE pair (q / k) or two v values.  q / k tiles:
+    // consecutive threads take consecutive rows (dims) of a token; v tiles (a 32-row tile never straddles the q / k
+    // to v boundary): consecutive tokens of a row, so a verify block's positions land side by side in the
+    // transposed V block
+    const bool vtile = n0 / 16 >= (qa.hq + qa.hkv) * (qa.d >> 4);
     for (int o = tid; o < (NS / 2) * TM * 16; o += 256) {
-      const int w16 = o & 15, r2 = o >> 4, ml = r2 % TM, pp = r2 / TM;
+      int w16, ml, pp;
+      if (vtile) {
+        ml = o % TM;
+        const int r2 = o / TM;
+        w16 = r2 & 15;
+        pp = r2 >> 4;
+      } else {
+        w16 = o & 15;
+        const int r2 = o >> 4;
+        ml = r2 % TM;
+        pp = r2 / TM;
+      }
       const int m = m0 + ml;
       if (m >= M) continue;
       qkv_rope_store(qa, m, n0 / 16 + 2 * pp, w16, rbf(reduced(2 * pp, ml, w16)), rbf(reduced(2 * pp + 1, ml, w16)));
