@@ -694,7 +694,7 @@ def run_1b_b64(args, emit_line: bool = True) -> dict:
     trace = eng.trace
     eng.trace = None
     replay = replay_gemms(model, trace, k, args.replay_steps) if args.replay_steps > 0 else {}
-    roofline, gemm_roofline = gemm_rooflines(replay)
+    roofline, gemm_roofline = gemm_rooflines(replay, ROOT / "profiles" / "decode_1b_b64_traffic.md")
     del model, eng
     torch.cuda.empty_cache()
     cpu = None if args.no_cpu_baseline else run_cpu_baseline(args, trace, k, "llama3.2-1b", B,
