@@ -881,9 +881,10 @@ static void dispatch_bf16(int ns, int ms, int epi, int nt, int mt, int ks, hipSt
 // o / w2 / w13 / LM head): workgroup rounds ceil(WGs / 256) x max(2.5, 0.83 + g) x rows / 64, where g is the most
 // token groups the two waves of one SIMD hold (MFMA work) and 2.5 the floor a workgroup's weight stream sets;
 // x 0.9 when a msw = 1 kernel fits two workgroups per CU (more memory parallelism), x 1.1 for the 32 + 32-row
-// silu-mul tile (twice the activation reads).  The launch needs >= 192
+// silu-mul tile (twice the activation reads), x 1.5 for the 32-row fused qkv tile (its rope epilogue and the
+// doubled activation reads; refitted over the 1B, 8B and 7B shapes at 96-512 tokens).  The launch needs >= 192
 // workgroups to stream the weights.  Returns the rows the tier took: M, or 0 where it does not apply (M <= 64,
-// N % 64 != 0, or K slices that are not whole 128-k chunks).  Both tiers give bitwise the same sums, so neither
+// N % 64 != 0, K slices that are not whole 128-k chunks, or too few weight tiles to spread).  Both tiers give bitwise the same sums, so neither
 // the tier nor the configuration ever changes a result.
 struct WideCfg {
   int ns, m_blocks, tbg, msw;
@@ -909,7 +910,7 @@ static WideCfg wide_config(int epi, int M, int N, int ks) {
       const bool two_per_cu = msw == 1 && wgs > 256;
       double cost = (double)((wgs + 255) / 256) * fmax(2.5, 0.83 + g) * ns / 4.0;
       if (two_per_cu) cost *= 0.9;
-      if ((silu || epi == EPI_QKV) && ns == 2) cost *= 1.1;
+      if (ns == 2) cost *= epi == EPI_QKV ? 1.5 : 1.1;
       if (best.ns == 0 || cost < best_cost) {
         best = WideCfg{ns, m_blocks, tbg, msw};
         best_cost = cost;
@@ -944,10 +945,12 @@ static WideCfg wide_plan(int epi, int M, int N, int K, int ks, bool af, bool c_o
   if (N % 64 != 0 || !c_ok || K % ks != 0 || (K / ks) % 128 != 0) return none;
   if (af && (epi == LSK_EPI_RESIDUAL || epi == LSK_EPI_NONE)) return none;
   if (epi == EPI_QKV && !af) return none;
-  // the tier streams the weights with >= 192 workgroups: 64-row tiles (32-row for the fused qkv, which has no K
-  // split) x the fewest blocks must reach that
-  const int gtot = (M + 15) / 16, cap = 8 * (epi == LSK_EPI_SILU_MUL ? 2 : 3);
-  if ((long)(N / (epi == EPI_QKV ? 32 : 64)) * ((gtot + cap - 1) / cap) * ks < 192) return none;
+  // too few weight tiles to spread: the narrowest tile (32 rows for the fused qkv and the silu-mul, 64 otherwise)
+  // x blocks of up to 24 row groups x K slices under 128 leaves the decode tier faster (measured over the 1B, 8B
+  // and 7B projections at 96-512 tokens)
+  const int gtot = (M + 15) / 16;
+  const int narrow = (epi == EPI_QKV || epi == LSK_EPI_SILU_MUL) ? 32 : 64;
+  if ((long)(N / narrow) * ((gtot + 23) / 24) * ks < 128) return none;
   return wide_config(epi, M, N, ks);
 }
 

@@ -987,13 +987,14 @@ def test_measure_window_rules_of_the_two_engines():
 
 def test_fused_qkv_token_counts_reach_every_wide_configuration():
     """The token counts of the fused qkv GPU test reach both wide-tier tile widths (32- and 64-row tiles, ns 2 / 4)
-    and one to three token groups per wave at the GQA shape, and both widths at the 64-dim MHA shape, by the
-    library's own configuration rule (lsk_gemm_wide_config)."""
+    with one to three token groups per wave (every pair the tier instantiates for qkv) over the GQA shape and the
+    64-dim MHA shape together, by the library's own configuration rule (lsk_gemm_wide_config)."""
     from thesis_amd import _lsk
     from test_kernels_gpu import FUSED_QKV_MS
 
     _lsk.load()
-    for heads, need in (((32, 8, 128), {(2, 1), (2, 2), (2, 3), (4, 2), (4, 3)}), ((8, 8, 64), {(2, 2), (4, 2)})):
+    for heads, need in (((32, 8, 128), {(2, 1), (4, 1), (4, 2), (4, 3)}),
+                        ((8, 8, 64), {(2, 2), (2, 3), (4, 2), (4, 3)})):
         N = (heads[0] + 2 * heads[1]) * heads[2]
         got = {(c[0], c[3]) for c in (_lsk.gemm_wide_config(_lsk.EPI_QKV_ROPE, M, N, 1024) for M in FUSED_QKV_MS)
                if c[0]}

@@ -763,7 +763,7 @@ def test_shifted_segment_metadata_equals_a_plan_at_the_actual_positions(cuda, sp
     assert key(live(r_got)) == key(live(r_ref))
 
 
-FUSED_QKV_MS = [5, 32, 48, 64, 100, 160, 288, 600, 1200, 2000]   # wide tier: every (ns, msw) it picks for qkv
+FUSED_QKV_MS = [5, 32, 48, 64, 100, 160, 288, 600, 1200, 1600, 2000, 2100]   # wide tier: every (ns, msw) it picks for qkv
 
 
 @pytest.mark.parametrize("M", FUSED_QKV_MS)
@@ -773,12 +773,12 @@ def test_fused_qkv_rope_writes_what_the_unfused_path_writes(cuda, M, heads):
     groups RoPE-paired -- writes bitwise what the qkv GEMM without a K split (lsk_gemm_partial, ks = 1) followed by
     lsk_rope_append_partial writes: the rotated q, the K cache and the V cache (every other cache slot untouched),
     in the decode tier (<= 64 rows) and in the wide tier (every tile width and groups-per-wave count it picks for
-    these shapes, up to 2000-token prefill sizes: test_fused_qkv_token_counts_reach_every_wide_configuration);
+    these shapes, up to 2100-token prefill sizes: test_fused_qkv_token_counts_reach_every_wide_configuration);
     unpacking the paired storage gives the weight back."""
     lsk = _lsk()
     Hq, Hkv, D = heads
     g = _gen(2000 + M + D)
-    K, N, B, S = 1024, (Hq + 2 * Hkv) * D, 4, 512
+    K, N, B, S = 1024, (Hq + 2 * Hkv) * D, 4, 1024
     m16 = lsk.frag_rows(M)
     a = torch.randn(m16, K, generator=g).to(BF16).to(cuda)
     af = lsk.PackedWeight(a).data                                          # fragment-major A, same values
