@@ -4,7 +4,9 @@ is lossless token for token against autoregressive decoding of the same model, i
   config 1  Llama3.2-1B shape, fp32, B = 4, prompts U[16, 128], 64 new tokens, exit 4, draft 4
   config 3  Llama3.2-1B shape, bf16, B = 64, prompts of 512, exit 6, draft 6 (32 new tokens here; the forced
             geometric acceptance run checks the rollback bookkeeping)
-  config 4  Llama3-8B shape, bf16, B = 32, prompts U[128, 1024], exit 8, aspire drafts in [2, 8] (24 new tokens)
+  config 4  Llama3-8B shape, bf16, B = 32, prompts U[128, 1024], exit 8, aspire drafts in [2, 8] (24 new tokens);
+            with the benchmark's forced acceptance (p = 0.3) every committed token is checked against a
+            teacher-forced prefill
   config 2  isolated verify attention + KV append + rollback at the microbenchmark's exact inputs: 256
             requests, GQA 32/8, head_dim 128, bf16 cache, lognormal contexts (median 1500, sigma 0.5, clipped to
             [64, 8192]), 1-9 query rows each, the production 4096-position splits (bench.AttentionInputs)
@@ -87,6 +89,57 @@ def test_config4_llama3_8b_bf16_aspire(cuda):
     sp, eng, _ = _run(m, prompts, 32, 1024, 24, sched="aspire", k=8, d_max=8, min_draft=2, initial_draft=3)
     assert sp == ar
     assert eng.stats["deep_steps"] > 0
+
+
+def _teacher_forced_argmax(m, seqs, k):
+    """Greedy tokens after every prefix of each sequence, from one prefill per sequence (cache row i, positions
+    0..len-1): (exit layer k through the shared final norm + LM head, the full model).  Entry j of both arrays is
+    the token predicted for position j + 1."""
+    from thesis_amd.solutions.packed import Block, pack_blocks, packed_layers
+
+    m.allocate_cache(len(seqs), m.cache.max_seq)
+    out = []
+    for i, s in enumerate(seqs):
+        pb = pack_blocks(m, [Block(i, 0, len(s))])
+        x = m.embed(torch.tensor(s, dtype=torch.long))
+        cap = {}
+        h = packed_layers(m, x, pb, 0, m.n_layers, cap, (k,))
+        out.append((m.head_argmax(cap[k]).cpu().numpy(), m.head_argmax(h).cpu().numpy()))
+    return out
+
+
+def test_config4_forced_acceptance_commits_only_model_tokens(cuda):
+    """The benchmark's own mode at config 4's shape: aspire drafts in [2, 8] with acceptance forced by the seeded
+    geometric draw (p = 0.3), so drafts the full model disagrees with are committed and rejected ones rolled back.
+    Checked against a teacher-forced prefill of each request's final sequence with the same weights: every AR token
+    is the full model's greedy token after its prefix (prefill and incremental decode give the same bits), and every
+    token of the forced run is the exit head's greedy token (an accepted draft) or the full model's (a correction)
+    after its own prefix, with both kinds present; any error in the rollback, the positions or the KV kept would
+    change the prefixes and break the match from there on."""
+    m = _model("llama3-8b", torch.bfloat16, 1152)
+    prompts = _prompts(32, m.cfg.vocab_size, 128, 1024, seed=13)
+    k = 8
+    ar, _, _ = _run(m, prompts, 32, 1024, 24, mode="ar", k=k)
+    fo, eng, _ = _run(m, prompts, 32, 1024, 24, sched="aspire", k=k, d_max=8, min_draft=2, initial_draft=3,
+                      forced_accept_p=0.3, forced_seed=7)
+    assert all(len(v) == 24 for v in fo.values())
+    assert eng.stats["deep_steps"] > 0 and 0 < eng.stats["accepted"] < eng.stats["drafted"]
+    ptok = {p.pid: list(p.tokens) for p in prompts}
+    pids = sorted(ar)
+    seqs_ar = [ptok[i] + list(ar[i]) for i in pids]
+    seqs_fo = [ptok[i] + list(fo[i]) for i in pids]
+    n_draft_only = n_full_only = 0
+    for i, (s, (_, full)) in zip(pids, zip(seqs_ar, _teacher_forced_argmax(m, seqs_ar, k))):
+        P = len(ptok[i])
+        assert np.array_equal(np.asarray(s[P:]), full[P - 1:len(s) - 1]), i
+    for i, (s, (ex, full)) in zip(pids, zip(seqs_fo, _teacher_forced_argmax(m, seqs_fo, k))):
+        P = len(ptok[i])
+        tok = np.asarray(s[P:])
+        e, f = ex[P - 1:len(s) - 1], full[P - 1:len(s) - 1]
+        assert ((tok == e) | (tok == f)).all(), (i, np.flatnonzero((tok != e) & (tok != f))[:5])
+        n_draft_only += int(((tok == e) & (tok != f)).sum())
+        n_full_only += int(((tok == f) & (tok != e)).sum())
+    assert n_draft_only > 0 and n_full_only > 0
 
 
 def test_config5_llama2_7b_bf16_m3_chunks(cuda):
