@@ -3,7 +3,7 @@ is lossless token for token against autoregressive decoding of the same model, i
 
   config 1  Llama3.2-1B shape, fp32, B = 4, prompts U[16, 128], 64 new tokens, exit 4, draft 4
   config 3  Llama3.2-1B shape, bf16, B = 64, prompts of 512, exit 6, draft 6 (32 new tokens here; the forced
-            geometric acceptance run checks the rollback bookkeeping)
+            geometric acceptance run's tokens are checked against a teacher-forced prefill)
   config 4  Llama3-8B shape, bf16, B = 32, prompts U[128, 1024], exit 8, aspire drafts in [2, 8] (24 new tokens);
             with the benchmark's forced acceptance (p = 0.3) every committed token is checked against a
             teacher-forced prefill
@@ -80,6 +80,8 @@ def test_config3_llama32_1b_bf16_b64(cuda):
                       forced_seed=3)
     assert all(len(v) == 32 for v in fo.values())
     assert eng.stats["accepted"] < eng.stats["drafted"]          # drafts were rejected and rolled back
+    # every forced-run token is the exit head's or the full model's greedy token after its own prefix
+    _check_forced_tokens(m, prompts, fo, 6)
 
 
 def test_config4_llama3_8b_bf16_aspire(cuda):
@@ -108,6 +110,23 @@ def _teacher_forced_argmax(m, seqs, k):
     return out
 
 
+def _check_forced_tokens(m, prompts, fo, k):
+    """Every generated token of a forced-acceptance run (fo: pid -> tokens) is the exit-k head's greedy token (an
+    accepted draft) or the full model's (a correction) after its own prefix, and both kinds occur."""
+    ptok = {p.pid: list(p.tokens) for p in prompts}
+    pids = sorted(fo)
+    seqs = [ptok[i] + list(fo[i]) for i in pids]
+    n_draft_only = n_full_only = 0
+    for i, (s, (ex, full)) in zip(pids, zip(seqs, _teacher_forced_argmax(m, seqs, k))):
+        P = len(ptok[i])
+        tok = np.asarray(s[P:])
+        e, f = ex[P - 1:len(s) - 1], full[P - 1:len(s) - 1]
+        assert ((tok == e) | (tok == f)).all(), (i, np.flatnonzero((tok != e) & (tok != f))[:5])
+        n_draft_only += int(((tok == e) & (tok != f)).sum())
+        n_full_only += int(((tok == f) & (tok != e)).sum())
+    assert n_draft_only > 0 and n_full_only > 0
+
+
 def test_config4_forced_acceptance_commits_only_model_tokens(cuda):
     """The benchmark's own mode at config 4's shape: aspire drafts in [2, 8] with acceptance forced by the seeded
     geometric draw (p = 0.3), so drafts the full model disagrees with are committed and rejected ones rolled back.
@@ -127,19 +146,10 @@ def test_config4_forced_acceptance_commits_only_model_tokens(cuda):
     ptok = {p.pid: list(p.tokens) for p in prompts}
     pids = sorted(ar)
     seqs_ar = [ptok[i] + list(ar[i]) for i in pids]
-    seqs_fo = [ptok[i] + list(fo[i]) for i in pids]
-    n_draft_only = n_full_only = 0
     for i, (s, (_, full)) in zip(pids, zip(seqs_ar, _teacher_forced_argmax(m, seqs_ar, k))):
         P = len(ptok[i])
         assert np.array_equal(np.asarray(s[P:]), full[P - 1:len(s) - 1]), i
-    for i, (s, (ex, full)) in zip(pids, zip(seqs_fo, _teacher_forced_argmax(m, seqs_fo, k))):
-        P = len(ptok[i])
-        tok = np.asarray(s[P:])
-        e, f = ex[P - 1:len(s) - 1], full[P - 1:len(s) - 1]
-        assert ((tok == e) | (tok == f)).all(), (i, np.flatnonzero((tok != e) & (tok != f))[:5])
-        n_draft_only += int(((tok == e) & (tok != f)).sum())
-        n_full_only += int(((tok == f) & (tok != e)).sum())
-    assert n_draft_only > 0 and n_full_only > 0
+    _check_forced_tokens(m, prompts, fo, k)
 
 
 def test_config5_llama2_7b_bf16_m3_chunks(cuda):
