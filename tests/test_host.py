@@ -1025,3 +1025,30 @@ def test_stop_checker_cuts_after_the_token_completing_the_first_stop():
     assert sc(out[:7], 7) == 6
     assert StopChecker(_ToyTokenizer({9}), ("\n",))([1, 2, 9, 9], 3) == 3
     assert not StopChecker(_ToyTokenizer(set()), ())
+
+
+def test_empty_inputs_return_before_any_launch():
+    """Every launching entry point accepts an empty input (no tokens, rows, verifiers or work items) and returns
+    0 without launching or touching memory: this container has no GPU, so a launch would fail, and the pointers
+    passed are not valid addresses."""
+    lib = _lsk().load()
+    P = 16                       # a non-null pointer that must never be dereferenced
+    assert lib.lsk_rmsnorm(1, P, P, P, 0, 64, 1e-5, 64, 64, None) == 0
+    assert lib.lsk_rope_append(1, P, P, P, P, P, P, 64, P, P, 0, 4, 2, 64, 2, 64, None) == 0
+    assert lib.lsk_kv_append(1, P, P, P, P, P, P, 0, 2, 64, 2, 64, None) == 0
+    assert lib.lsk_rope_append_partial(1, P, 2, P, P, P, P, P, 64, P, P, 0, 4, 2, 64, 2, 64, None) == 0
+    assert lib.lsk_ragged_attn(1, P, P, P, P, P, 0, P, 0, 0, P, 1, 1, 16, P, 4, 2, 64, 64, 0.125, P, 0, None) == 0
+    assert lib.lsk_gemm(1, P, 64, P, 64, P, 64, None, 0, 0, 64, 64, 0, 0, None) == 0
+    assert lib.lsk_gemm(0, P, 64, P, 64, P, 64, None, 0, 0, 64, 64, 0, 0, None) == 0
+    assert lib.lsk_gemm_partial(P, 64, P, 64, P, 0, 64, 64, 2, None) == 0
+    assert lib.lsk_gemm_partial_frag(P, P, P, 0, 64, 64, 2, None) == 0
+    assert lib.lsk_gemm_silu_frag(P, P, P, 1, 0, 64, 64, None) == 0
+    assert lib.lsk_head_argmax(1, P, 64, P, 64, 0, 128, 64, None, 0, P, None, P, 0, None) == 0
+    assert lib.lsk_add_rmsnorm(1, P, 64, P, 2, P, 1e-5, P, 64, P, 64, 0, 64, None) == 0
+    assert lib.lsk_embed(P, 100, 128, P, 8, P, P, P, 0, None) == 0
+    assert lib.lsk_copy_rows(P, P, 4, P, P, 4, 128, 0, None) == 0
+    assert lib.lsk_argmax(1, P, 128, 0, 128, P, None, None) == 0
+    assert lib.lsk_greedy_accept(P, P, 8, P, P, P, None, 0, P, P, P, None) == 0
+    assert lib.lsk_kv_rollback(P, P, P, 0, None) == 0
+    assert lib.lsk_shift_segment_positions(P, 4, 1, 1, 0, 1, 4, P, P, P, 0, None) == 0
+    assert lib.lsk_gemm_qkv_rope(P, P, 0, 32, 8, 128, 4096, P, P, P, P, P, 64, P, P, 2, 64, None) == 0
