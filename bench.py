@@ -847,7 +847,7 @@ def main():
     ap.add_argument("--extra-requests", type=int, default=24, help="7b-poisson measured requests in the default run")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only: this build has no multi-GPU path (requested --gpus {args.gpus}); "
+        print(f"bench.py runs on one GPU only: the package has no multi-GPU path (requested --gpus {args.gpus}); "
               "the packed forward would shard by request (data parallel over slots)", file=sys.stderr)
         sys.exit(2)
     if not torch.cuda.is_available():

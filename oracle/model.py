@@ -1,7 +1,7 @@
 """CPU oracle of the packed ragged LayerSkip-Llama forward (TEST INFRASTRUCTURE ONLY).
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this package, and
-only as the checker / CPU baseline: the product path (thesis_amd) never calls it.
+only as the reference for parity tests / CPU baseline: the product path (thesis_amd) never calls it.
 
 This is a from-scratch torch-CPU restatement of the reference's math, with the dtype rounding
 points of its eager ops kept in place (so a bf16 oracle rounds where the reference rounds):

@@ -175,7 +175,7 @@ def _oracle_ragged(o, blocks, seed=0):
 
 
 def test_bf16_logits_are_as_close_to_fp32_as_the_oracles_bf16(cuda):
-    """bf16 pinned to the bf16 noise floor: with the same bf16-rounded weights and inputs, this build's bf16
+    """bf16 pinned to the bf16 noise floor: with the same bf16-rounded weights and inputs, the HIP path's bf16
     logits are no farther from the fp32 restatement than the oracle's own bf16 restatement (the reference's
     eager bf16 rounding points) is.  A kernel that dropped a term or mis-rounded would sit far above it."""
     from oracle.model import OracleLlama, random_weights
@@ -195,7 +195,7 @@ def test_bf16_logits_are_as_close_to_fp32_as_the_oracles_bf16(cuda):
     rel = lambda a: ((a.float() - l32).norm(dim=-1) / l32.norm(dim=-1))  # noqa: E731
     d_ref, d_ours = rel(l16), rel(lg)
     print(f"relative L2 to fp32: oracle bf16 max {d_ref.max():.3e} mean {d_ref.mean():.3e}; "
-          f"this build bf16 max {d_ours.max():.3e} mean {d_ours.mean():.3e}")
+          f"HIP bf16 max {d_ours.max():.3e} mean {d_ours.mean():.3e}")
     assert d_ours.mean() <= 1.25 * d_ref.mean() and d_ours.max() <= 1.5 * d_ref.max()
     # two-sided: a kernel that skipped one of the reference's bf16 rounding points would sit closer to fp32
     assert d_ours.mean() >= 0.75 * d_ref.mean()
@@ -252,7 +252,7 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
       * attention against the oracle with the kernel's softmax blocking (oracle/ordered.py attend_bf16_blocked):
         the same bar, relative L2 <= 1e-4;
       * attention against the reference's SDPA form: both round the softmax weights to bf16 for the P.V product,
-        at different running maxima, so each is ~2e-3 from the exact result.  Bar: this build's distance to the
+        at different running maxima, so each is ~2e-3 from the exact result.  Bar: the HIP path's distance to the
         fp64 brute force lies within [0.75, 1.25] x the SDPA oracle's own, and the two differ by at most 3e-3."""
     import math
     import torch.nn.functional as F
@@ -318,7 +318,7 @@ def test_one_layer_bf16_stage_by_stage_against_the_bf16_oracle(cuda, which):
     stages["attention (blocked)"] = _rel(att_gpu, att_blk)
     d_ours, d_oracle, d_pair = _rel(att_gpu, exact)[0], _rel(att, exact)[0], _rel(att_gpu, att)[0]
     print(f"[{which}] " + "; ".join(f"{k} relL2 {r:.2e} differ {f:.1e}" for k, (r, f) in stages.items())
-          + f"; K/V equal {kv_same[0]:.5f}/{kv_same[1]:.5f}; attention relL2 to exact: this build {d_ours:.3e}, "
+          + f"; K/V equal {kv_same[0]:.5f}/{kv_same[1]:.5f}; attention relL2 to exact: HIP {d_ours:.3e}, "
             f"oracle {d_oracle:.3e}, between them {d_pair:.3e}")
     for name, (r, f) in stages.items():
         assert r <= 1e-4 and f <= 2e-3, (name, r, f)

@@ -6,7 +6,7 @@ W / P = bytes / parameters of one decoder layer, n = tokens through the layer, C
 read by attention, BW / F = bandwidth and bf16 GEMM throughput, t_op x n_op = launch overhead
 (solutions/cost_model.py:1-31).  `LinearCostModel` is the ASPIRE-style a + b n + c C variant.
 `mi355x_cost_model` fills the GPU parameters from MI355X's published peaks scaled by the fractions
-this build's kernels reach (measured by bench.py); `synthetic_cost_model` keeps the reference's
+the package's kernels reach (measured by bench.py); `synthetic_cost_model` keeps the reference's
 made-up constants for CPU tests (solutions/cost_model.py:220-227).
 """
 
@@ -177,7 +177,7 @@ def synthetic_cost_model(cfg, kind: str = "roofline"):
 
 def mi355x_cost_model(cfg, bw_frac: float = 0.7, flops_frac: float = 0.5, t_op_ms: float = 0.004):
     """MI355X: HBM3E 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s, scaled by the fractions the kernels reach.
-    Launch terms follow this build's bf16 layer runner: 8 launches per layer (norm, QKV with RoPE + KV append,
+    Launch terms follow the package's bf16 layer runner: 8 launches per layer (norm, QKV with RoPE + KV append,
     attention, combine, O, norm, W13, W2), 3 per head (norm, GEMM, argmax), ~4 per segment."""
     dims = ModelDims.from_config(cfg)
     gpu = GPUParams(bw=8.0e9 * bw_frac, flops=2.5166e12, t_op=t_op_ms, n_op_layer=8, n_op_bucket=0, n_op_head=3,
