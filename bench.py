@@ -357,7 +357,7 @@ class AttentionInputs:
 
     Hq, Hkv, D = 32, 8, 128
 
-    def __init__(self, seed: int, dev):
+    def __init__(self, seed: int, dev, split: int | None = None):
         from thesis_amd import _lsk
 
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
@@ -373,7 +373,8 @@ class AttentionInputs:
         self.v_new = torch.empty_like(self.k_new).normal_(generator=g)
         self.offs = offs = np.concatenate([[0], np.cumsum(T)[:-1]])
         self.blocks = np.stack([offs, ctx, T, np.arange(B)], axis=1).astype(np.int32)
-        self.split = _lsk.ATTN_SPLIT        # what KVCache uses for a cache of >= 1024 (row, KV head) stripes
+        # what KVCache uses for a cache of >= 1024 (row, KV head) stripes, unless a split is given
+        self.split = _lsk.ATTN_SPLIT if split is None else split
         self.n_slots = _lsk.cu_count(dev)
         self.rows_cap = _lsk.attn_rows_cap(self.blocks, Hq // Hkv, self.split, Hkv, D, self.n_slots)
         self.works, self.groups, self.n_parts = _lsk.attn_plan(self.blocks, Hq // Hkv, self.split, self.rows_cap)

@@ -29,7 +29,7 @@ extern "C" {
 #define LSK_EPI_RESIDUAL 1 /* C = rnd(R + rnd(A W^T))                          */
 #define LSK_EPI_SILU_MUL 2 /* C = rnd(rnd(silu(rnd(g))) * rnd(u)), [g;u] = A W^T */
 
-#define LSK_ATTN_SPLIT 4096 /* KV positions per flash-decoding split of large bf16 caches */
+#define LSK_ATTN_SPLIT 8192 /* KV positions per flash-decoding split of large bf16 caches */
 
 const char* lsk_last_error(void);
 int lsk_abi_version(void);

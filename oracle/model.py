@@ -262,8 +262,8 @@ class OracleLlama:
         if max_seq > self.rope_cos.shape[0]:
             self.rope_cos, self.rope_sin = rope_tables(self.cfg, max_seq)
         self.cache = OracleCache(self.cfg, max_batch, max_seq, self.dtype)
-        # the bf16 kernel's position splits: 4096 positions once the cache holds >= 1024 (row, KV head) stripes
-        self.attn_split = 4096 if max_batch * self.cfg.n_kv_heads >= 1024 else 2048
+        # the bf16 kernel's position splits: 8192 positions once the cache holds >= 1024 (row, KV head) stripes
+        self.attn_split = 8192 if max_batch * self.cfg.n_kv_heads >= 1024 else 2048
         return self.cache
 
     def embed(self, ids: torch.Tensor) -> torch.Tensor:

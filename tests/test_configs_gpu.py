@@ -9,7 +9,7 @@ is lossless token for token against autoregressive decoding of the same model, i
             teacher-forced prefill
   config 2  isolated verify attention + KV append + rollback at the microbenchmark's exact inputs: 256
             requests, GQA 32/8, head_dim 128, bf16 cache, lognormal contexts (median 1500, sigma 0.5, clipped to
-            [64, 8192]), 1-9 query rows each, the production 4096-position splits (bench.AttentionInputs)
+            [64, 8192]), 1-9 query rows each, the production split (bench.AttentionInputs) and 4096-position splits
   config 5  Llama2-7B shape (MHA, vocab 32000), bf16, exit 8, draft 4, 256-token prefill chunks piggybacked on
             the decode steps (M3); 16 slots and 24 requests of U[256, 1024] prompt tokens, 16 new tokens each,
             and the open-loop driver at B = 128 with Poisson arrivals at 8 requests/s
@@ -205,18 +205,24 @@ def _ubench_sample(a) -> list:
     return sorted(set(picks))
 
 
-def test_config2_verify_attention_microbench_matches_brute_force(cuda):
-    """The microbenchmark's attention launch (256 requests, 4096-position splits, contexts up to 8192, the rows
-    cap and schedule the benchmark uses) after its KV append: the appended rows equal the inputs bitwise, the
-    cached prefix [0, ctx) is untouched, sampled requests (longest, multi-split, split-crossing, ragged) match
-    the fp64 brute force at the kernel tests' bounds, and the rollback gives kv_len = ctx + accepted + 1."""
+@pytest.mark.parametrize("split", [None, 4096])
+def test_config2_verify_attention_microbench_matches_brute_force(cuda, split):
+    """The microbenchmark's attention launch (256 requests, contexts up to 8192, the rows cap and schedule the
+    benchmark uses) after its KV append, at the production split of this cache (8192 positions: every context
+    unsplit) and at 4096-position splits (two-split requests and the combine): the appended rows equal the
+    inputs bitwise, the cached prefix [0, ctx) is untouched, sampled requests (longest, multi-split,
+    split-crossing, ragged) match the fp64 brute force at the kernel tests' bounds, and the rollback gives
+    kv_len = ctx + accepted + 1."""
     import bench
     from oracle.model import brute_attention
     from thesis_amd import _lsk
 
-    a = bench.AttentionInputs(0, cuda)
+    a = bench.AttentionInputs(0, cuda, split)
     Hq, Hkv, D = a.Hq, a.Hkv, a.D
-    assert a.ctx.max() > a.split and a.n_parts > 0              # two-split requests, combine groups in the plan
+    if split is None:
+        assert a.split == _lsk.ATTN_SPLIT and a.ctx.max() + a.T.max() <= a.split and a.n_parts == 0
+    else:
+        assert a.ctx.max() > a.split and a.n_parts > 0          # two-split requests, combine groups in the plan
     sample = _ubench_sample(a)
     assert len(sample) >= 8
     before = {r: (a.kc[r:r + 1].clone(), a.vc[r:r + 1].clone()) for r in sample[:4]}

@@ -20,7 +20,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 EPI_NONE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
 EPI_PARTIAL, EPI_ARGMAX, EPI_QKV_ROPE = 3, 4, 5   # launch kinds known to lsk_gemm_wide_config
-ATTN_SPLIT = 4096         # LSK_ATTN_SPLIT
+ATTN_SPLIT = 8192         # LSK_ATTN_SPLIT
 ATTN_ROWS = 48            # query rows per attention work item (csrc/lsk_attention.hip ATTN_ROWS)
 ABI_VERSION = 11
 

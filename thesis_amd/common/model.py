@@ -244,9 +244,10 @@ class KVCache:
         self.v = _Decoded(self.vb_all, _lsk.v_from_blocked)
         # KV positions per flash-decoding split of the attention kernel, fixed for the cache's lifetime so that
         # a query's result never depends on the batch it is packed in.  Measured on MI355X: 256 requests x 8 KV
-        # heads with median-1500 contexts stream best with 4096-position splits (fewer work items, fewer
-        # prologues); a B = 32 decode batch runs unsplit up to 2048 positions, its launches using the
-        # deep-prefetch kernel.  The fp32 path does not split.
+        # heads with median-1500 contexts (up to 8192) stream best unsplit up to 8192 positions (2048-position
+        # splits 7 % and 4096-position splits 3 % slower: more work items, split partials and the combine
+        # launch); a B = 32 decode batch runs unsplit up to 2048 positions, its launches using the deep-prefetch
+        # kernel.  The fp32 path does not split.
         if dtype == torch.bfloat16:
             self.attn_split = _lsk.ATTN_SPLIT if max_batch * cfg.n_kv_heads >= 1024 else 2048
         else:
